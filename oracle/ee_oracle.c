@@ -1,0 +1,471 @@
+/*
+ * ee_oracle.c -- CPU restatement of the entropy-gated precision path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This file is the parity checker for the HIP
+ * kernels of the package; only tests/, __graft_entry__.smoke() and the
+ * cpu_baseline leg of bench.py may load it.  No product code path calls it.
+ *
+ * Every function restates the arithmetic of the reference implementation
+ * (Triton kernels + PyTorch launcher ops) at the level the reference fixes it:
+ *   - bit level for integer, fp16 and e4m3 work (codes, scales, int32
+ *     accumulators, the INT8 dequant epilogue, W8A16 dequantised weights);
+ *   - float64 for the f32-accumulated GEMMs and for the entropy, whose
+ *     summation order the reference leaves to the compiler (tl.dot, tl.sum).
+ * Citations: EE = "entropy-engine (1)/entropy-engine" of the reference tree.
+ *
+ * fp16 values travel as their uint16 bit patterns; e4m3 codes as uint8.
+ * Compile with -ffp-contract=off: every float operation below is meant to be
+ * one IEEE operation, rounded once, exactly as written.
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#define EO_API __attribute__((visibility("default")))
+
+/* ------------------------------------------------------------------------ */
+/* Scalar formats                                                            */
+/* ------------------------------------------------------------------------ */
+
+static inline uint32_t f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+static inline float u2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+
+/* IEEE binary16 -> binary32, exact. */
+EO_API float eo_f16_to_f32(uint16_t h) {
+    uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    uint32_t e = (h >> 10) & 0x1f, m = h & 0x3ffu;
+    if (e == 0x1f) return u2f(sign | 0x7f800000u | (m << 13));          /* inf / nan */
+    if (e == 0) {
+        if (m == 0) return u2f(sign);
+        /* subnormal: m * 2^-24, exact in binary32 */
+        float v = (float)m * 0x1p-24f;
+        return (sign ? -v : v);
+    }
+    return u2f(sign | ((e + 112u) << 23) | (m << 13));
+}
+
+/* Round-half-even of (mant >> shift) for shift in [1, 31]. */
+static inline uint32_t rne_shift(uint32_t mant, int shift) {
+    if (shift > 31) return 0;
+    uint32_t q = mant >> shift;
+    uint32_t rem = mant & ((1u << shift) - 1u);
+    uint32_t half = 1u << (shift - 1);
+    if (rem > half || (rem == half && (q & 1u))) q++;
+    return q;
+}
+
+/* IEEE binary32 -> binary16, round-to-nearest-even, subnormals, inf, nan.
+ * This is what every `.to(torch.float16)` / `.to(tl.float16)` on the path
+ * does (EE/python/kernels.py:109,215,233,245,336). */
+EO_API uint16_t eo_f32_to_f16(float f) {
+    uint32_t x = f2u(f);
+    uint16_t sign = (uint16_t)((x >> 16) & 0x8000u);
+    uint32_t ax = x & 0x7fffffffu;
+    if (ax > 0x7f800000u) return (uint16_t)(sign | 0x7e00u | ((ax >> 13) & 0x3ffu));
+    if (ax == 0x7f800000u) return (uint16_t)(sign | 0x7c00u);
+    if (ax >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u);               /* >= 65520 -> inf */
+    int E = (int)(ax >> 23) - 127;
+    if (E >= -14) {                                                          /* normal fp16 */
+        uint32_t mant = ax & 0x7fffffu;
+        uint32_t h = ((uint32_t)(E + 15) << 10) | (mant >> 13);
+        uint32_t rem = mant & 0x1fffu;
+        if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) h++;
+        return (uint16_t)(sign | h);
+    }
+    if ((ax >> 23) == 0) return sign;                                        /* f32 subnormal -> 0 */
+    /* fp16 subnormal: value / 2^-24 = M * 2^(E-23+24) = M >> (-1-E) */
+    uint32_t M = (ax & 0x7fffffu) | 0x800000u;
+    uint32_t q = rne_shift(M, -1 - E);
+    return (uint16_t)(sign | q);                                             /* q == 1024 -> min normal */
+}
+
+/* binary32 -> OCP e4m3fn code, round-to-nearest-even, saturating to +-448
+ * ("satfinite": the only e4m3 conversion mode PTX offers, which the Triton
+ * casts `.to(tl.float8e4nv)` at EE/python/kernels.py:160,166 lower to).
+ * NaN -> 0x7f | sign.  Inputs here are always binary16 values widened to
+ * binary32, so rounding from f32 equals rounding from f16. */
+EO_API uint8_t eo_e4m3_from_f32(float f) {
+    uint32_t x = f2u(f);
+    uint8_t sign = (uint8_t)((x >> 24) & 0x80u);
+    uint32_t ax = x & 0x7fffffffu;
+    if (ax > 0x7f800000u) return (uint8_t)(sign | 0x7fu);
+    if (u2f(ax) >= 448.0f) return (uint8_t)(sign | 0x7eu);                  /* saturate (incl. inf) */
+    int E = (int)(ax >> 23) - 127;
+    if ((ax >> 23) == 0) return sign;                                        /* f32 zero/subnormal */
+    uint32_t mant = ax & 0x7fffffu;
+    if (E >= -6) {                                                           /* e4m3 normal */
+        uint32_t q = rne_shift(mant, 20);                                    /* 3 mantissa bits */
+        int ee = E + 7;
+        if (q == 8u) { q = 0; ee++; }
+        /* ee <= 15; the >=448 test above removes the only overflowing case */
+        return (uint8_t)(sign | ((uint32_t)ee << 3) | q);
+    }
+    /* e4m3 subnormal: value / 2^-9 = M * 2^(E-23+9) = M >> (14-E) */
+    uint32_t M = mant | 0x800000u;
+    uint32_t q = rne_shift(M, 14 - E);                                       /* q == 8 -> min normal */
+    return (uint8_t)(sign | q);
+}
+
+EO_API float eo_e4m3_to_f32(uint8_t c) {
+    uint32_t e = (c >> 3) & 0xfu, m = c & 7u;
+    float v;
+    if ((c & 0x7fu) == 0x7fu) return NAN;
+    if (e == 0) v = (float)m * 0x1p-9f;
+    else v = ldexpf(1.0f + (float)m / 8.0f, (int)e - 7);
+    return (c & 0x80u) ? -v : v;
+}
+
+/* float -> int8 as `.to(torch.int8)` does it on the GPU (EE/python/
+ * kernels.py:338): truncate toward zero into int32 with saturation (NaN -> 0),
+ * then keep the low byte.  In-range quotients (|q| < 128) are plain
+ * truncation; the rest is implementation-defined in the reference and never
+ * appears in fixtures. */
+EO_API int8_t eo_i8_trunc(float q) {
+    int32_t v;
+    if (q != q) v = 0;
+    else if (q >= 2147483648.0f) v = INT32_MAX;
+    else if (q <= -2147483648.0f) v = INT32_MIN;
+    else v = (int32_t)q;
+    return (int8_t)(uint8_t)((uint32_t)v & 0xffu);
+}
+
+/* The reciprocals PyTorch's GPU `tensor / python_float` multiplies by: it
+ * computes opmath(1)/opmath(divisor) once on the host in float and then
+ * multiplies every element (ATen div_true for a CPU-scalar divisor). */
+static float inv_f32(float d) { volatile float one = 1.0f; return one / d; }
+
+/* ------------------------------------------------------------------------ */
+/* Quantisers                                                                */
+/* ------------------------------------------------------------------------ */
+
+/* a9: INT8 activation quantiser of triton_int8_gemm, EE/python/kernels.py:336-338
+ *   a_scale = (a.abs().amax(1) / 127.0).clamp(min=1e-8).to(f32)   -- fp16 math
+ *   a_int8  = (a / a_scale[:, None]).to(int8)                      -- f32 divide, trunc
+ * clamp(min=1e-8) is a no-op in fp16 (1e-8 rounds to 0). */
+EO_API void eo_quant_act_i8_dispatch(const uint16_t* A, int64_t M, int64_t K, int64_t lda,
+                                     int8_t* codes, int64_t ldc, float* scale) {
+    const float inv127 = inv_f32(127.0f);
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < M; ++i) {
+        const uint16_t* a = A + i * lda;
+        float amax = 0.0f;
+        for (int64_t k = 0; k < K; ++k) {
+            float v = fabsf(eo_f16_to_f32(a[k]));
+            if (v > amax || v != v) amax = v;
+            if (amax != amax) break;
+        }
+        float s = eo_f16_to_f32(eo_f32_to_f16(amax * inv127));
+        scale[i] = s;
+        for (int64_t k = 0; k < K; ++k) codes[i * ldc + k] = eo_i8_trunc(eo_f16_to_f32(a[k]) / s);
+    }
+}
+
+/* a15: round-based quantiser of the CubinEngine test, EE/test_cubin.py:93-103
+ *   a_scale = (a.float().abs().amax(1) / 127.0).clamp(min=1e-8)   -- f32
+ *   a_int8  = (a.float() / a_scale[:, None]).round().clamp(-127, 127).to(int8) */
+EO_API void eo_quant_act_i8_engine(const uint16_t* A, int64_t M, int64_t K, int64_t lda,
+                                   int8_t* codes, int64_t ldc, float* scale) {
+    const float inv127 = inv_f32(127.0f);
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < M; ++i) {
+        const uint16_t* a = A + i * lda;
+        float amax = 0.0f;
+        for (int64_t k = 0; k < K; ++k) {
+            float v = fabsf(eo_f16_to_f32(a[k]));
+            if (v > amax) amax = v;
+        }
+        float s = amax * inv127;
+        if (s < 1e-8f) s = 1e-8f;
+        scale[i] = s;
+        for (int64_t k = 0; k < K; ++k) {
+            float r = rintf(eo_f16_to_f32(a[k]) / s);
+            if (r > 127.0f) r = 127.0f;
+            if (r < -127.0f) r = -127.0f;
+            codes[i * ldc + k] = (r != r) ? 0 : (int8_t)r;        /* NaN -> 0 */
+        }
+    }
+}
+
+/* a11 + a12 (activation side): the FP8 tier's per-row codes.
+ *   a_scale = (a.abs().amax(1) / 448.0).clamp(min=1e-12).to(f32)  EE/python/kernels.py:361
+ *   inv     = (1.0 / a_scale).to(f16)                             :144
+ *   a8      = (a * inv).to(float8e4nv)   fp16 product, RNE, satfinite  :159-160
+ * The reference recomputes these codes inside every N-tile of its K loop; they
+ * are a pure function of the row, so computing them once is the same codes.
+ * fp16(1/s) is the same for a correctly rounded and a 2-ulp f32 divide for
+ * every fp16 s (checked exhaustively with exact rationals in tests/). */
+EO_API void eo_quant_act_f8(const uint16_t* A, int64_t M, int64_t K, int64_t lda,
+                            uint8_t* codes, int64_t ldc, float* scale) {
+    const float inv448 = inv_f32(448.0f);
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < M; ++i) {
+        const uint16_t* a = A + i * lda;
+        float amax = 0.0f;
+        for (int64_t k = 0; k < K; ++k) {
+            float v = fabsf(eo_f16_to_f32(a[k]));
+            if (v > amax || v != v) amax = v;
+            if (amax != amax) break;
+        }
+        float s = eo_f16_to_f32(eo_f32_to_f16(amax * inv448));
+        scale[i] = s;
+        volatile float one = 1.0f;
+        float inv16 = eo_f16_to_f32(eo_f32_to_f16(one / s));
+        for (int64_t k = 0; k < K; ++k) {
+            float p = eo_f16_to_f32(eo_f32_to_f16(eo_f16_to_f32(a[k]) * inv16));
+            codes[i * ldc + k] = eo_e4m3_from_f32(p);
+        }
+    }
+}
+
+/* a7: offline weight quantiser, EE/python/dispatch.py:43-48
+ *   w = W.float().t()   [K, N];  scale = (amax_k |w| / 127.0).clamp(min=1e-8)
+ *   code = (w / scale).round().clamp(-127, 127).to(int8)       -> [K, N]
+ * W is the nn.Linear weight [N, K] (fp16 bits, row stride ldw). */
+EO_API void eo_quant_weight_i8(const uint16_t* W, int64_t N, int64_t K, int64_t ldw,
+                               int8_t* B_kn, int64_t ldb, float* scale) {
+    const float inv127 = inv_f32(127.0f);
+#pragma omp parallel for schedule(static)
+    for (int64_t n = 0; n < N; ++n) {
+        const uint16_t* w = W + n * ldw;
+        float amax = 0.0f;
+        for (int64_t k = 0; k < K; ++k) {
+            float v = fabsf(eo_f16_to_f32(w[k]));
+            if (v > amax) amax = v;
+        }
+        float s = amax * inv127;
+        if (s < 1e-8f) s = 1e-8f;
+        scale[n] = s;
+        for (int64_t k = 0; k < K; ++k) {
+            float r = rintf(eo_f16_to_f32(w[k]) / s);
+            if (r > 127.0f) r = 127.0f;
+            if (r < -127.0f) r = -127.0f;
+            B_kn[k * ldb + n] = (r != r) ? 0 : (int8_t)r;
+        }
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* GEMMs                                                                     */
+/* ------------------------------------------------------------------------ */
+
+#define IB 8
+#define JB 256
+
+/* a10 core: exact int32 accumulators acc[m,n] = sum_k A[m,k] * B[k,n]
+ * (EE/python/kernels.py:81-98).  A int8 [M,K] (lda), B int8 [K,N] (ldb). */
+EO_API void eo_gemm_i8_acc(const int8_t* A, int64_t lda, const int8_t* B, int64_t ldb,
+                           int32_t* acc, int64_t ldacc, int64_t M, int64_t N, int64_t K) {
+    int64_t nib = (M + IB - 1) / IB, njb = (N + JB - 1) / JB;
+#pragma omp parallel for schedule(dynamic)
+    for (int64_t t = 0; t < nib * njb; ++t) {
+        int64_t i0 = (t / njb) * IB, j0 = (t % njb) * JB;
+        int64_t ni = (M - i0 < IB) ? M - i0 : IB, nj = (N - j0 < JB) ? N - j0 : JB;
+        int32_t c[IB][JB];
+        memset(c, 0, sizeof(c));
+        for (int64_t k = 0; k < K; ++k) {
+            const int8_t* b = B + k * ldb + j0;
+            for (int64_t r = 0; r < ni; ++r) {
+                int32_t a = A[(i0 + r) * lda + k];
+                if (!a) continue;
+                int32_t* cr = c[r];
+                for (int64_t j = 0; j < nj; ++j) cr[j] += a * (int32_t)b[j];
+            }
+        }
+        for (int64_t r = 0; r < ni; ++r)
+            memcpy(acc + (i0 + r) * ldacc + j0, c[r], (size_t)nj * sizeof(int32_t));
+    }
+}
+
+/* a10 epilogue, EE/python/kernels.py:104-110:
+ *   out = fp16( (f32(acc) * a_scale[m]) * b_scale[n] ), each step one RNE op. */
+EO_API void eo_epilogue_i8(const int32_t* acc, int64_t ldacc, const float* as, const float* bs,
+                           uint16_t* C, int64_t ldc, int64_t M, int64_t N) {
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < M; ++i)
+        for (int64_t j = 0; j < N; ++j) {
+            float v = (float)acc[i * ldacc + j];
+            v = v * as[i];
+            v = v * bs[j];
+            C[i * ldc + j] = eo_f32_to_f16(v);
+        }
+}
+
+/* Generic float64 GEMM: C[m,n] = sum_k a[m,k] * b[k,n], a [M,K] row-major,
+ * b [K,N] row-major, both already decoded to double. */
+static void gemm_f64(const double* a, const double* b, double* c, int64_t M, int64_t N, int64_t K) {
+    int64_t nib = (M + IB - 1) / IB, njb = (N + JB - 1) / JB;
+#pragma omp parallel for schedule(dynamic)
+    for (int64_t t = 0; t < nib * njb; ++t) {
+        int64_t i0 = (t / njb) * IB, j0 = (t % njb) * JB;
+        int64_t ni = (M - i0 < IB) ? M - i0 : IB, nj = (N - j0 < JB) ? N - j0 : JB;
+        double acc[IB][JB];
+        memset(acc, 0, sizeof(acc));
+        for (int64_t k = 0; k < K; ++k) {
+            const double* bk = b + k * N + j0;
+            for (int64_t r = 0; r < ni; ++r) {
+                double av = a[(i0 + r) * K + k];
+                if (av == 0.0) continue;
+                for (int64_t j = 0; j < nj; ++j) acc[r][j] += av * bk[j];
+            }
+        }
+        for (int64_t r = 0; r < ni; ++r)
+            memcpy(c + (i0 + r) * N + j0, acc[r], (size_t)nj * sizeof(double));
+    }
+}
+
+/* a12: FP8 GEMM in float64 from the e4m3 codes.  A8 = activation codes
+ * [M,K] (eo_quant_act_f8); the weight codes are e4m3(fp16(B_int8))
+ * (EE/python/kernels.py:165-166).  out = acc * a_scale[m] * b_scale[n]
+ * (:176), returned unrounded in float64 (the f32 order inside tl.dot is the
+ * compiler's).  A NaN code poisons its row as in the reference. */
+EO_API void eo_gemm_f8_f64(const uint8_t* A8, int64_t lda, const int8_t* B, int64_t ldb,
+                           const float* as, const float* bs, double* C,
+                           int64_t M, int64_t N, int64_t K) {
+    double* a = (double*)malloc(sizeof(double) * (size_t)(M * K));
+    double* b = (double*)malloc(sizeof(double) * (size_t)(K * N));
+    double lut[256];
+    for (int c = 0; c < 256; ++c) lut[c] = (double)eo_e4m3_to_f32((uint8_t)c);
+    for (int64_t i = 0; i < M; ++i)
+        for (int64_t k = 0; k < K; ++k) a[i * K + k] = lut[A8[i * lda + k]];
+    for (int64_t k = 0; k < K; ++k)
+        for (int64_t j = 0; j < N; ++j)
+            b[k * N + j] = lut[eo_e4m3_from_f32((float)B[k * ldb + j])];
+    /* NaN codes: a zero skip in gemm_f64 would drop them; mark rows first */
+    gemm_f64(a, b, C, M, N, K);
+    for (int64_t i = 0; i < M; ++i) {
+        int nanrow = 0;
+        for (int64_t k = 0; k < K; ++k) if (a[i * K + k] != a[i * K + k]) { nanrow = 1; break; }
+        for (int64_t j = 0; j < N; ++j)
+            C[i * N + j] = nanrow ? NAN : C[i * N + j] * (double)as[i] * (double)bs[j];
+    }
+    free(a); free(b);
+}
+
+/* a14: the W8A16 ("FP16") tier's dequantised weight, bit level,
+ * EE/python/kernels.py:215,232-233:
+ *   s16 = fp16(b_scale[n]);  w[k,n] = fp16( fp16(B_int8[k,n]) * s16 ). */
+EO_API void eo_dequant_w8a16(const int8_t* B, int64_t ldb, const float* bs, uint16_t* W16,
+                             int64_t ldw, int64_t K, int64_t N) {
+    for (int64_t k = 0; k < K; ++k)
+        for (int64_t j = 0; j < N; ++j) {
+            float s16 = eo_f16_to_f32(eo_f32_to_f16(bs[j]));
+            W16[k * ldw + j] = eo_f32_to_f16((float)B[k * ldb + j] * s16);
+        }
+}
+
+/* a14: W8A16 GEMM in float64: C = A(fp16) @ w (as above), unrounded
+ * (EE/python/kernels.py:220-246; tl.dot accumulates in f32). */
+EO_API void eo_gemm_w8a16_f64(const uint16_t* A, int64_t lda, const int8_t* B, int64_t ldb,
+                              const float* bs, double* C, int64_t M, int64_t N, int64_t K) {
+    double* a = (double*)malloc(sizeof(double) * (size_t)(M * K));
+    double* b = (double*)malloc(sizeof(double) * (size_t)(K * N));
+    for (int64_t i = 0; i < M; ++i)
+        for (int64_t k = 0; k < K; ++k) a[i * K + k] = eo_f16_to_f32(A[i * lda + k]);
+    for (int64_t k = 0; k < K; ++k)
+        for (int64_t j = 0; j < N; ++j) {
+            float s16 = eo_f16_to_f32(eo_f32_to_f16(bs[j]));
+            b[k * N + j] = eo_f16_to_f32(eo_f32_to_f16((float)B[k * ldb + j] * s16));
+        }
+    gemm_f64(a, b, C, M, N, K);
+    free(a); free(b);
+}
+
+/* ------------------------------------------------------------------------ */
+/* Softmax + entropy                                                         */
+/* ------------------------------------------------------------------------ */
+
+/* a1: fused softmax + Shannon entropy per row, EE/python/kernels.py:264-312,
+ * in float64.  Row r of X (fp16 bits, row stride ld) has S columns; with
+ * `causal`, columns c > (r % S) are -inf (:273,291-292).
+ *   m = max x;  s = x - m;  Z = sum e^s;  p = e^s / Z
+ *   H = ln Z - sum p * s        (terms with s = -inf contribute 0, :303)
+ * H is evaluated as ln(c0) + log1p(Z'/c0) - T/(c0 + Z') where c0 counts the
+ * entries equal to the max, Z' = sum over the others of e^s and
+ * T = sum e^s * s: every term is non-negative, so no digits cancel on
+ * nearly one-hot rows.  Outputs: H[r] (double), optionally P (double) and
+ * P16 (fp16 bits of the correctly rounded probability). */
+EO_API void eo_softmax_entropy(const uint16_t* X, int64_t R, int64_t S, int64_t ld, int causal,
+                               double* H, double* P, uint16_t* P16) {
+#pragma omp parallel for schedule(dynamic, 16)
+    for (int64_t r = 0; r < R; ++r) {
+        const uint16_t* x = X + r * ld;
+        int64_t nvalid = causal ? ((r % S) + 1 < S ? (r % S) + 1 : S) : S;
+        double m = -INFINITY;
+        for (int64_t c = 0; c < nvalid; ++c) {
+            double v = eo_f16_to_f32(x[c]);
+            if (v > m || v != v) m = v;
+            if (m != m) break;
+        }
+        double c0 = 0.0, z = 0.0, t = 0.0;
+        for (int64_t c = 0; c < nvalid; ++c) {
+            double v = eo_f16_to_f32(x[c]);
+            if (v == -INFINITY) continue;
+            double s = v - m;
+            if (s == 0.0) { c0 += 1.0; continue; }
+            double e = exp(s);
+            z += e;
+            t += e * s;
+        }
+        double Z = c0 + z;
+        double h = log(c0) + log1p(z / c0) - t / Z;
+        if (m != m || m == INFINITY || m == -INFINITY) h = NAN;
+        H[r] = h;
+        if (P || P16) {
+            for (int64_t c = 0; c < S; ++c) {
+                double p;
+                if (c >= nvalid) p = 0.0;
+                else {
+                    double v = eo_f16_to_f32(x[c]);
+                    p = (v == -INFINITY) ? 0.0 : exp(v - m) / Z;
+                    if (h != h) p = NAN;
+                }
+                if (P) P[r * S + c] = p;
+                if (P16) P16[r * S + c] = eo_f32_to_f16((float)p);
+            }
+        }
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* Routing                                                                   */
+/* ------------------------------------------------------------------------ */
+
+/* a4 + a6: tier of each row by the dispatcher's strict comparisons
+ * (EE/python/dispatch.py:74-79): INT8 (0) if H < tau_low, FP8 (1) if
+ * H < tau_high, else FP16 (2).  H is binary32 compared in double against
+ * double thresholds, as `.item()` vs Python floats does; NaN -> FP16.
+ * idx = stable partition [rows of tier 0 | tier 1 | tier 2], counts[3]. */
+EO_API void eo_route(const float* H, int64_t R, double tau_low, double tau_high,
+                     int32_t* tier, int32_t* idx, int32_t* counts) {
+    int64_t cnt[3] = {0, 0, 0};
+    for (int64_t r = 0; r < R; ++r) {
+        double h = (double)H[r];
+        int t = (h < tau_low) ? 0 : (h < tau_high) ? 1 : 2;
+        tier[r] = t;
+        cnt[t]++;
+    }
+    int64_t off[3] = {0, cnt[0], cnt[0] + cnt[1]};
+    for (int64_t r = 0; r < R; ++r) idx[off[tier[r]]++] = (int32_t)r;
+    for (int t = 0; t < 3; ++t) counts[t] = (int32_t)cnt[t];
+}
+
+/* ------------------------------------------------------------------------ */
+/* Array forms of the scalar conversions (used by the Python face)           */
+/* ------------------------------------------------------------------------ */
+
+EO_API void eo_f32_to_f16_n(const float* x, uint16_t* y, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) y[i] = eo_f32_to_f16(x[i]);
+}
+EO_API void eo_f16_to_f32_n(const uint16_t* x, float* y, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) y[i] = eo_f16_to_f32(x[i]);
+}
+EO_API void eo_e4m3_from_f32_n(const float* x, uint8_t* y, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) y[i] = eo_e4m3_from_f32(x[i]);
+}
+EO_API void eo_e4m3_to_f32_n(const uint8_t* x, float* y, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) y[i] = eo_e4m3_to_f32(x[i]);
+}
+EO_API void eo_i8_trunc_n(const float* x, int8_t* y, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) y[i] = eo_i8_trunc(x[i]);
+}
