@@ -1,0 +1,185 @@
+/*
+ * entropy_engine.h -- C ABI of the MI355X (gfx950) entropy-gated precision path.
+ *
+ * A host library (libentropy_engine.so) that loads gfx950 code objects
+ * (*.hsaco, listed in entropy_engine_meta.json) with hipModuleLoadData and
+ * launches them with hipModuleLaunchKernel.  It replaces the reference's
+ * CubinEngine (.cubin + CUDA Driver API, EE/csrc/engine.cpp) and the Triton
+ * launchers of EE/python/kernels.py.
+ *   EE = "entropy-engine (1)/entropy-engine" in the reference tree.
+ *
+ * Conventions
+ *  - Every call returns 0 (EE_OK) or a negative ee_status; the message of the
+ *    last failure on the calling thread is ee_last_error().
+ *  - All argument checks run before any HIP call, so a rejected call has no
+ *    side effect on the device.
+ *  - The caller owns every buffer (inputs, outputs, workspaces); the engine
+ *    owns only its loaded modules.  Pointers are device pointers on the
+ *    engine's device; "stream" is a hipStream_t (NULL = default stream).
+ *    Calls are asynchronous on that stream.
+ *  - fp16 tensors are passed as raw 16-bit storage; e4m3 codes as bytes (OCP
+ *    e4m3fn, max 448).  Leading dimensions are in elements.
+ *  - An ee_engine is immutable after creation: launches from several threads
+ *    are safe; create/destroy must not overlap its use.
+ */
+#ifndef ENTROPY_ENGINE_H
+#define ENTROPY_ENGINE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define EE_ABI_VERSION 1
+
+typedef struct ee_engine ee_engine;
+typedef struct ee_module_engine ee_module_engine;
+typedef void* ee_stream_t; /* hipStream_t */
+
+typedef enum {
+    EE_OK = 0,
+    EE_ERR_INVALID_ARG = -1, /* bad pointer, size, stride, alignment or dtype contract */
+    EE_ERR_IO = -2,          /* code object / meta file cannot be opened or read */
+    EE_ERR_META = -3,        /* meta JSON malformed or missing a key */
+    EE_ERR_HIP = -4,         /* a HIP runtime call failed */
+    EE_ERR_UNSUPPORTED = -5, /* shape outside what the kernels implement */
+    EE_ERR_NOT_FOUND = -6    /* kernel symbol missing from the code objects */
+} ee_status;
+
+/* Precision tiers: EE/python/dispatch.py:32-36 (PrecisionTier). */
+enum { EE_TIER_INT8 = 0, EE_TIER_FP8 = 1, EE_TIER_FP16 = 2 };
+
+/* Activation quantiser modes. */
+enum {
+    EE_QUANT_I8_DISPATCH = 0, /* EE/python/kernels.py:336-338: fp16 scale, truncating cast   */
+    EE_QUANT_I8_ENGINE = 1,   /* EE/test_cubin.py:93-103: f32 scale, round + clamp(+-127)    */
+    EE_QUANT_F8_ROW = 2       /* EE/python/kernels.py:361,144,159-160: e4m3 codes per row    */
+};
+
+/* GEMM kinds (the three tiers). */
+enum {
+    EE_GEMM_I8 = 0,  /* EE/python/kernels.py:50-110  int8 x int8 -> int32 -> fp16 */
+    EE_GEMM_F8 = 1,  /* EE/python/kernels.py:118-180 e4m3 x e4m3 -> f32 -> fp16   */
+    EE_GEMM_F16 = 2  /* EE/python/kernels.py:192-246 fp16 x fp16 (W8A16) -> fp16  */
+};
+
+const char* ee_last_error(void);
+int ee_abi_version(void);
+
+/* ---- engine lifetime ------------------------------------------------------
+ * Replaces load_cubin + CubinEngine construction (EE/csrc/engine.cpp:23-44,
+ * 73-104).  lib_dir holds entropy_engine_meta.json and the *.hsaco files it
+ * names; modules are loaded on the current device.  destroy unloads them
+ * (the reference leaks its CUmodule). */
+int ee_engine_create(const char* lib_dir, ee_engine** out);
+int ee_engine_destroy(ee_engine* eng);
+/* Tuning knobs (0 = automatic): "se_wpr" / "quant_wpr" waves per row (1,2,4). */
+int ee_engine_set_option(ee_engine* eng, const char* key, int64_t value);
+int ee_engine_device(const ee_engine* eng);
+
+/* ---- a1/a2: fused softmax + entropy ---------------------------------------
+ * Replaces fused_softmax_entropy_kernel + launcher (EE/python/kernels.py:
+ * 264-312, 416-450).  x: fp16 [rows, S] (row stride ld_x); p: fp16 probs
+ * [rows, S] (row stride ld_p) or NULL for entropy only; h: f32 [rows].
+ * causal: keep column c of row r iff c <= r % S (the reference's [B,H,S,S]
+ * rows).  tier: optional int32 [rows] = routing tier of h (strict compares
+ * against tau_low/tau_high in double, EE/python/dispatch.py:74-79). */
+int ee_softmax_entropy(ee_engine* eng, const void* x, void* p, float* h, int64_t rows, int32_t S,
+                       int64_t ld_x, int64_t ld_p, int32_t causal, int32_t* tier, double tau_low,
+                       double tau_high, ee_stream_t stream);
+
+/* ---- a9/a11/a15: activation quantisers -------------------------------------
+ * Replaces the PyTorch quantiser ops of triton_int8_gemm / triton_fp8_gemm
+ * (EE/python/kernels.py:336-338, 361 + in-kernel :144,159-160) and the
+ * CubinEngine test's quantiser (EE/test_cubin.py:93-103).
+ * x fp16 [M, K] -> codes (int8 or e4m3 bytes) [M, K] (row stride ld_c) + f32 scale [M].
+ * Routed form: with counts != NULL, rows r < counts[tier] are read from
+ * x[idx[off + r]] and written to codes/scale slot off + r, where
+ * off = counts[0] + ... + counts[tier-1]; M is then the upper bound. */
+int ee_quant_act(ee_engine* eng, const void* x, int64_t M, int64_t K, int64_t ld_x, int32_t mode,
+                 void* codes, int64_t ld_c, float* scale, const int32_t* idx, const int32_t* counts,
+                 int32_t tier, ee_stream_t stream);
+
+/* ---- a7: offline weight quantisation ----------------------------------------
+ * Replaces quantize_weights_int8 (EE/python/dispatch.py:43-48).  w: fp16
+ * nn.Linear weight [N, K]; writes int8 codes in GEMM operand order [N, K]
+ * (row stride ld_c) and f32 per-channel scale [N].  ee_transpose_i8 turns the
+ * codes into the reference's [K, N] buffer. */
+int ee_quant_weight_i8(ee_engine* eng, const void* w, int64_t N, int64_t K, int64_t ld_w,
+                       int8_t* codes_nk, int64_t ld_c, float* scale, ee_stream_t stream);
+
+/* dst[c, r] = src[r, c] for int8 [R, C]. */
+int ee_transpose_i8(ee_engine* eng, const int8_t* src, int64_t R, int64_t C, int64_t ld_src,
+                    int8_t* dst, int64_t ld_dst, ee_stream_t stream);
+/* FP8 tier weight codes e4m3(fp16(b)) of int8 codes (EE/python/kernels.py:166). */
+int ee_pack_b_f8(ee_engine* eng, const int8_t* codes_nk, int64_t N, int64_t K, int64_t ld_src,
+                 uint8_t* dst, int64_t ld_dst, ee_stream_t stream);
+/* W8A16 tier weights fp16(fp16(b) * fp16(scale[n])) (EE/python/kernels.py:215,233). */
+int ee_pack_b_f16(ee_engine* eng, const int8_t* codes_nk, const float* scale, int64_t N, int64_t K,
+                  int64_t ld_src, void* dst, int64_t ld_dst, ee_stream_t stream);
+
+/* ---- a10/a12/a14: the tier GEMMs --------------------------------------------
+ * Replaces gemm_{int8,fp8,fp16}_kernel and their launchers (EE/python/
+ * kernels.py:50-246, 330-409).  C[m, n] = sum_k A[m, k] * B[n, k]:
+ *   a: [M, K] int8 codes (I8), e4m3 codes (F8) or fp16 (F16), row stride lda;
+ *   b_nk: [N, K] same element type (weights in operand order), row stride ldb;
+ *   c: fp16, row stride ldc; a_scale [M], b_scale [N] f32 (I8/F8 only).
+ *   acc_out: optional int32 accumulators (I8 only), row stride ldc.
+ * Routed form: counts != NULL bounds M by counts[tier]; A row m is
+ * a[a_idx[off+m]] if a_idx else a[off+m]; a_scale at off+m; C row m is
+ * c[c_idx[off+m]] if c_idx else c[m].
+ * Contract: K * elem_size, lda * elem_size, ldb * elem_size multiples of 16
+ * bytes; a, b, b_scale 16-byte aligned; N and ldc multiples of 4; c 8-byte
+ * aligned.  K * elem_size a multiple of 128 selects the pipelined kernels. */
+int ee_gemm(ee_engine* eng, int32_t kind, const void* a, int64_t lda, const void* b_nk, int64_t ldb,
+            void* c, int64_t ldc, const float* a_scale, const float* b_scale, int32_t M, int32_t N,
+            int32_t K, const int32_t* a_idx, const int32_t* c_idx, const int32_t* counts, int32_t tier,
+            int32_t* acc_out, ee_stream_t stream);
+
+/* ---- a4/a6: per-row routing -------------------------------------------------
+ * New with no reference function: the reference picks one tier per call
+ * (EE/python/dispatch.py:68-82).  tier[r] by the same strict compares;
+ * idx = stable partition [INT8 rows | FP8 rows | FP16 rows]; counts[3]. */
+int ee_route(ee_engine* eng, const float* h, int64_t rows, double tau_low, double tau_high,
+             int32_t* tier, int32_t* idx, int32_t* counts, ee_stream_t stream);
+
+/* Row gather (scatter = 0: dst[r] = src[idx[off+r]]) or scatter
+ * (scatter = 1: dst[idx[off+r]] = src[r]) for r < counts[tier] (or rows). */
+int ee_row_copy(ee_engine* eng, const void* src, int64_t ld_src_bytes, void* dst, int64_t ld_dst_bytes,
+                int64_t rows, int64_t row_bytes, const int32_t* idx, const int32_t* counts, int32_t tier,
+                int32_t scatter, ee_stream_t stream);
+
+/* ---- routed linear: entropy-gated GEMM over a mixed batch -------------------
+ * One tier per row: INT8 rows quantised (EE_QUANT_I8_DISPATCH) and run on the
+ * I8 GEMM, FP8 rows on the F8 GEMM, FP16 rows on the W8A16 GEMM, outputs
+ * scattered back to their rows; no host synchronisation.  idx/counts come
+ * from ee_route.  ws_codes: bytes [M, K] (row stride K), ws_scale: f32 [M].
+ * b_i8 / b_f8 / b_f16: the three weight operands [N, K] (row stride K). */
+int ee_routed_linear(ee_engine* eng, const void* x, int64_t ld_x, int32_t M, int32_t K, int32_t N,
+                     const int32_t* idx, const int32_t* counts, const int8_t* b_i8, const uint8_t* b_f8,
+                     const void* b_f16, const float* b_scale, void* c, int64_t ldc, void* ws_codes,
+                     float* ws_scale, ee_stream_t stream);
+
+/* ---- CubinEngine counterpart (EE/csrc/engine.cpp:64-216) --------------------
+ * One code object + one GEMM function, launched on the caller's stream (the
+ * reference launched on the NULL stream, engine.cpp:160).  create mirrors the
+ * constructor (engine.cpp:73-104; num_warps counts wave64s); from_metadata
+ * reads "shared", "num_warps", "BLOCK_M", "BLOCK_N" from a meta JSON
+ * (engine.cpp:168-199).  forward mirrors engine.cpp:106-166 but takes B in
+ * operand order [N, K] and a caller-allocated fp16 C [M, N]. */
+int ee_module_engine_create(const char* code_object_path, const char* func_name, int32_t shared_mem,
+                            int32_t num_warps, int32_t block_m, int32_t block_n, ee_module_engine** out);
+int ee_module_engine_from_metadata(const char* code_object_path, const char* meta_json_path,
+                                   const char* func_name, ee_module_engine** out);
+int ee_module_engine_info(const ee_module_engine* me, int32_t* shared_mem, int32_t* num_warps,
+                          int32_t* block_m, int32_t* block_n);
+int ee_module_engine_forward(ee_module_engine* me, const int8_t* a, int64_t lda, const int8_t* b_nk,
+                             int64_t ldb, void* c, int64_t ldc, const float* a_scale, const float* b_scale,
+                             int32_t M, int32_t N, int32_t K, ee_stream_t stream);
+int ee_module_engine_destroy(ee_module_engine* me);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* ENTROPY_ENGINE_H */

@@ -42,7 +42,7 @@ _p = ctypes.c_void_p
 def build(force: bool = False) -> str:
     """Compile ee_oracle.c into oracle/_build/libee_oracle.so with make."""
     if force or not os.path.exists(_LIB_PATH):
-        subprocess.run(["make", "-s", "-B" if force else "-s", "-C", _HERE],
+        subprocess.run(["make", "-s"] + (["-B"] if force else []) + ["-C", _HERE],
                        check=True, stdout=subprocess.DEVNULL)
     return _LIB_PATH
 
@@ -75,6 +75,7 @@ def lib() -> ctypes.CDLL:
             "eo_e4m3_from_f32_n": ([_p, _p, _i64], None),
             "eo_e4m3_to_f32_n": ([_p, _p, _i64], None),
             "eo_i8_trunc_n": ([_p, _p, _i64], None),
+            "eo_num_threads": ([], ctypes.c_int),
         }
         for name, (args, res) in sigs.items():
             fn = getattr(L, name)
@@ -82,6 +83,11 @@ def lib() -> ctypes.CDLL:
             fn.restype = res
         _lib = L
     return _lib
+
+
+def num_threads() -> int:
+    """OpenMP threads the oracle's parallel loops use."""
+    return int(lib().eo_num_threads())
 
 
 def _ptr(a: np.ndarray) -> int:

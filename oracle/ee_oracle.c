@@ -469,3 +469,7 @@ EO_API void eo_e4m3_to_f32_n(const uint8_t* x, float* y, int64_t n) {
 EO_API void eo_i8_trunc_n(const float* x, int8_t* y, int64_t n) {
     for (int64_t i = 0; i < n; ++i) y[i] = eo_i8_trunc(x[i]);
 }
+
+/* Threads an OpenMP region of this library uses (the cpu_baseline "cores"). */
+#include <omp.h>
+EO_API int eo_num_threads(void) { return omp_get_max_threads(); }

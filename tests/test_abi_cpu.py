@@ -1,0 +1,167 @@
+"""CPU-only checks of the C-ABI boundary and the host-side logic.
+
+No GPU compute is launched here: the library must load, export every entry
+point include/entropy_engine.h declares, and reject bad engine / meta / code
+object inputs before its first HIP call.  The dispatcher's host logic runs on
+CPU tensors.
+"""
+import ctypes
+import json
+import os
+import re
+
+import pytest
+import torch
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "entropy_engine.h")
+PKG = os.path.join(ROOT, "triton-kernels-optimization_amd")
+
+
+@pytest.fixture(scope="module")
+def L():
+    from entropy_engine import _lib
+    return _lib.lib()
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(ee_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol(L):
+    syms = declared_symbols()
+    assert len(syms) >= 20
+    for s in syms:
+        assert hasattr(L, s), f"{s} declared in entropy_engine.h but not exported"
+    assert L.ee_abi_version() == 1
+
+
+def test_python_binding_covers_the_header():
+    from entropy_engine import _lib
+    assert set(declared_symbols()) == set(_lib.SIGNATURES)
+
+
+def _create(L, path):
+    out = ctypes.c_void_p()
+    rc = L.ee_engine_create(path if path is None else path.encode(), ctypes.byref(out))
+    return rc, L.ee_last_error().decode(), out.value
+
+
+def test_engine_create_errors(L, tmp_path):
+    from entropy_engine import _lib
+    rc, msg, h = _create(L, None)
+    assert rc == _lib.EE_ERR_INVALID_ARG and h is None
+    rc, msg, _ = _create(L, str(tmp_path / "nowhere"))
+    assert rc == _lib.EE_ERR_IO and "Could not open meta JSON" in msg
+    (tmp_path / "entropy_engine_meta.json").write_text("{ not json")
+    rc, msg, _ = _create(L, str(tmp_path))
+    assert rc == _lib.EE_ERR_META and "Malformed" in msg
+    (tmp_path / "entropy_engine_meta.json").write_text(json.dumps({"code_objects": {}, "kernels": {}}))
+    rc, msg, _ = _create(L, str(tmp_path))
+    assert rc == _lib.EE_ERR_META and "format" in msg
+    meta = {"format": "entropy-engine-meta/1", "code_objects": {"gemm": {"file": "gemm.hsaco"}},
+            "kernels": {"eek_gemm_i8": {"code_object": "gemm", "block": 256, "lds": 65536}}}
+    (tmp_path / "entropy_engine_meta.json").write_text(json.dumps(meta))
+    rc, msg, _ = _create(L, str(tmp_path))
+    assert rc == _lib.EE_ERR_IO and "Could not open code object" in msg
+    (tmp_path / "gemm.hsaco").write_bytes(b"not an elf at all")
+    rc, msg, _ = _create(L, str(tmp_path))
+    assert rc == _lib.EE_ERR_IO and "Not an ELF" in msg
+    del meta["kernels"]["eek_gemm_i8"]["lds"]
+    (tmp_path / "entropy_engine_meta.json").write_text(json.dumps(meta))
+    rc, msg, _ = _create(L, str(tmp_path))
+    assert rc == _lib.EE_ERR_META and "Missing key: lds" in msg
+
+
+def test_module_engine_errors(L, tmp_path):
+    """The reference's CubinEngine error surface (EE/csrc/engine.cpp:24-41,174-181)."""
+    from entropy_engine import _lib
+    out = ctypes.c_void_p()
+    rc = L.ee_module_engine_create(str(tmp_path / "x.hsaco").encode(), b"eek_gemm_i8", 65536, 4, 128, 128,
+                                   ctypes.byref(out))
+    assert rc == _lib.EE_ERR_IO and "Could not open code object file" in L.ee_last_error().decode()
+    rc = L.ee_module_engine_from_metadata(b"x.hsaco", str(tmp_path / "m.json").encode(), b"eek_gemm_i8",
+                                          ctypes.byref(out))
+    assert rc == _lib.EE_ERR_IO and "Could not open meta JSON" in L.ee_last_error().decode()
+    (tmp_path / "m.json").write_text(json.dumps({"shared": 65536, "num_warps": 4, "BLOCK_M": 128}))
+    rc = L.ee_module_engine_from_metadata(b"x.hsaco", str(tmp_path / "m.json").encode(), b"eek_gemm_i8",
+                                          ctypes.byref(out))
+    assert rc == _lib.EE_ERR_META and "Missing key: BLOCK_N" in L.ee_last_error().decode()
+    rc = L.ee_module_engine_create(b"x.hsaco", b"eek_gemm_i8", 65536, 0, 128, 128, ctypes.byref(out))
+    assert rc == _lib.EE_ERR_INVALID_ARG
+
+
+def test_null_engine_rejected(L):
+    from entropy_engine import _lib
+    assert L.ee_gemm(None, 0, None, 0, None, 0, None, 0, None, None, 1, 1, 16, None, None, None, 0, None,
+                     None) == _lib.EE_ERR_INVALID_ARG
+    assert L.ee_softmax_entropy(None, None, None, None, 1, 1, 1, 1, 0, None, 0.0, 0.0, None) == _lib.EE_ERR_INVALID_ARG
+    assert L.ee_route(None, None, 1, 0.0, 0.0, None, None, None, None) == _lib.EE_ERR_INVALID_ARG
+    assert L.ee_engine_set_option(None, b"se_wpr", 1) == _lib.EE_ERR_INVALID_ARG
+    assert L.ee_engine_destroy(None) == _lib.EE_OK
+
+
+def test_built_meta_lists_every_kernel_the_launcher_selects():
+    meta = json.load(open(os.path.join(PKG, "lib", "entropy_engine_meta.json")))
+    ks = meta["kernels"]
+    for v in range(1, 9):
+        for w in (1, 2, 4):
+            assert f"eek_softmax_entropy_v{v}_w{w}" in ks and f"eek_quant_v{v}_w{w}" in ks
+    for k in ("eek_softmax_entropy_generic", "eek_quant_generic", "eek_gemm_i8", "eek_gemm_f8", "eek_gemm_f16",
+              "eek_route", "eek_row_copy", "eek_transpose_i8", "eek_pack_b_f8", "eek_pack_b_f16"):
+        assert k in ks
+    assert ks["eek_gemm_i8"]["lds"] == 65536 and ks["eek_route"]["block"] == 1024
+    src = open(os.path.join(PKG, "csrc", "launcher", "ee_launcher.cpp")).read()
+    for name in re.findall(r'"(eek_[a-z0-9_]+)"', src):
+        assert name in ks or name.endswith("_v") or name.endswith("_generic") or name in src, name
+
+
+def test_product_has_no_cpu_path():
+    import entropy_engine as ee
+    a = torch.zeros((4, 16), dtype=torch.float16)
+    b = torch.zeros((16, 8), dtype=torch.int8)
+    s = torch.ones(8)
+    for fn in (ee.triton_int8_gemm, ee.triton_fp8_gemm, ee.triton_fp16_gemm):
+        with pytest.raises(ValueError, match="GPU tensors"):
+            fn(a, b, s)
+    with pytest.raises(ValueError, match="GPU tensors"):
+        ee.softmax_entropy(a)
+    # the product never imports the test oracle
+    for dirpath, _, files in os.walk(os.path.join(PKG, "entropy_engine")):
+        for f in files:
+            if f.endswith(".py"):
+                assert not re.search(r"^\s*(import|from)\s+oracle", open(os.path.join(dirpath, f)).read(), re.M), f
+
+
+def test_dispatcher_host_logic():
+    """EE/python/benchmark.py:180-218 on CPU tensors (the tier logic is host code)."""
+    from entropy_engine import PipelinedEntropyDispatcher, PrecisionTier
+    d = PipelinedEntropyDispatcher(tau_low=2.0, tau_high=3.5)
+    assert d.get_tier() == PrecisionTier.FP16
+    for v, t in ((1.0, PrecisionTier.INT8), (2.5, PrecisionTier.FP8), (4.0, PrecisionTier.FP16),
+                 (2.0, PrecisionTier.FP8), (3.5, PrecisionTier.FP16)):
+        d.submit_entropy(torch.tensor([v, v - 3.0]))
+        assert d.get_tier() == t
+    st = d.get_stats()
+    assert [st[k]["count"] for k in ("INT8", "FP8", "FP16")] == [1, 2, 2]
+    assert st["FP8"]["pct"] == pytest.approx(40.0)
+    d.reset_stats()
+    assert d.get_tier() == PrecisionTier.FP16 and d.get_stats()["FP16"]["count"] == 0   # default is not counted (dispatch.py:69-70)
+
+
+SWEEP = [(1.0, 2.0, 10, 20, 70), (1.5, 2.5, 20, 20, 60), (2.0, 3.0, 30, 20, 50), (2.0, 3.5, 30, 30, 40),
+         (2.5, 3.5, 40, 20, 40), (3.0, 4.0, 50, 20, 30), (3.5, 4.5, 60, 20, 20)]
+
+
+@pytest.mark.parametrize("tl,th,p0,p1,p2", SWEEP)
+def test_dispatcher_sweep_known_answers(tl, th, p0, p1, p2):
+    """NB:555-561: the dispatch sweep's tier percentages over simulated entropies."""
+    from entropy_engine import PipelinedEntropyDispatcher
+    d = PipelinedEntropyDispatcher(tau_low=tl, tau_high=th)
+    for e in [0.5, 1.0, 1.5, 2.0, 2.5, 3.0, 3.5, 4.0, 4.5, 5.0]:
+        d.submit_entropy(torch.tensor([e]))
+        d.get_tier()
+    st = d.get_stats()
+    assert [st[k]["pct"] for k in ("INT8", "FP8", "FP16")] == pytest.approx([p0, p1, p2])

@@ -1,0 +1,427 @@
+"""GPU parity: the HIP kernels (through the C ABI) against the CPU oracle.
+
+Bars (north star): int8 codes, int32 accumulators, INT8 fp16 outputs, e4m3
+codes, W8A16 weights and routing decisions bit-exact; entropy within 1e-5
+relative (absolute floor 1e-12 for rows whose entropy underflows); FP8 and
+W8A16 outputs within 1e-2 relative of a float64 recompute from the same codes
+(absolute floor 1e-3 x the output's RMS, for outputs that cancel to ~0);
+probabilities within one fp16 ulp of the correctly rounded value.
+Inputs are generated on the CPU from seeded numpy generators and copied to
+the device, so both sides see identical bits.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+ENT_RTOL = 1e-5
+ENT_ATOL = 1e-12
+F_RTOL = 1e-2
+F_ATOL_RMS = 1e-3
+
+
+@pytest.fixture(scope="module")
+def ee():
+    import entropy_engine
+    return entropy_engine
+
+
+def cuda(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def logits_rows(rng, R, S, scales=(0.25, 1.0, 4.0, 16.0)):
+    s = rng.choice(np.asarray(scales), R)
+    return (rng.standard_normal((R, S)) * s[:, None]).astype(np.float16)
+
+
+def check_entropy(h_gpu, h_ref):
+    h_gpu = np.asarray(h_gpu, np.float64)
+    err = np.abs(h_gpu - h_ref)
+    bad = err > ENT_RTOL * np.abs(h_ref) + ENT_ATOL
+    assert not bad.any(), f"{bad.sum()} rows off; worst rel {np.max(err / np.maximum(np.abs(h_ref), 1e-30)):.3e}"
+
+
+def check_probs(p_gpu, p_ref16):
+    a = p_gpu.view(np.uint16).astype(np.int32)
+    b = p_ref16.view(np.uint16).astype(np.int32)
+    assert np.abs(a - b).max() <= 1, "probabilities differ by more than one fp16 ulp"
+
+
+def check_close_f64(out16, ref64):
+    out = out16.astype(np.float64)
+    fin = np.isfinite(ref64)
+    rms = math.sqrt(np.mean(ref64[fin] ** 2)) if fin.any() else 0.0
+    err = np.abs(out[fin] - ref64[fin])
+    tol = F_RTOL * np.abs(ref64[fin]) + F_ATOL_RMS * rms
+    assert (err <= tol).all(), f"max err {err.max():.3e}; worst excess {(err - tol).max():.3e}"
+    assert np.array_equal(np.isnan(out), np.isnan(ref64))
+
+
+# ---------------------------------------------------------------------------- torch semantics
+
+def test_torch_gpu_scalar_division_is_reciprocal_multiply():
+    """The oracle assumes `tensor / python_float` on the GPU is t * f32(1/d)
+    (what the reference's launchers ran, EE/python/kernels.py:336,361 and
+    dispatch.py:46).  Checked here on every fp16 value and on f32 amaxes."""
+    x16 = np.arange(0, 0x7C00, dtype=np.uint16).view(np.float16)
+    t = cuda(x16)
+    for d in (127.0, 448.0):
+        inv = np.float32(1.0) / np.float32(d)
+        ref = (x16.astype(np.float32) * inv).astype(np.float16)
+        assert np.array_equal(host(t / d).view(np.uint16), ref.view(np.uint16)), d
+    x32 = x16.astype(np.float32)
+    inv = np.float32(1.0) / np.float32(127.0)
+    assert np.array_equal(host(cuda(x32) / 127.0).view(np.uint32), (x32 * inv).view(np.uint32))
+
+
+# ---------------------------------------------------------------------------- softmax + entropy
+
+@pytest.mark.parametrize("R,S", [(64, 4096), (48, 512), (33, 1000), (8, 14336), (5, 40000), (3, 8)])
+def test_softmax_entropy_rows(ee, orc, R, S):
+    rng = np.random.default_rng(R * 7919 + S)
+    X = logits_rows(rng, R, S)
+    H_ref, P_ref = orc.softmax_entropy(X)
+    p, h, _ = ee.softmax_entropy(cuda(X))
+    check_entropy(host(h), H_ref)
+    check_probs(host(p), P_ref)
+
+
+@pytest.mark.parametrize("wpr", [1, 2, 4])
+def test_softmax_entropy_every_row_split(ee, orc, wpr):
+    from entropy_engine import _lib
+    rng = np.random.default_rng(wpr)
+    X = logits_rows(rng, 40, 2048)
+    H_ref, P_ref = orc.softmax_entropy(X)
+    L = _lib.lib()
+    _lib.check(L.ee_engine_set_option(_lib.engine(), b"se_wpr", wpr))
+    try:
+        p, h, _ = ee.softmax_entropy(cuda(X))
+        check_entropy(host(h), H_ref)
+        check_probs(host(p), P_ref)
+    finally:
+        _lib.check(L.ee_engine_set_option(_lib.engine(), b"se_wpr", 0))
+
+
+def test_softmax_entropy_closed_forms(ee, orc):
+    S = 4096
+    X = np.zeros((6, S), np.float16)
+    X[1] = 3.5
+    X[2] = -np.inf; X[2, 17] = 1.0
+    X[3] = -np.inf; X[3, 5] = 2.0; X[3, 900] = 2.0
+    X[4] = -30000.0; X[4, 3] = 0.0
+    X[5] = np.arange(S) % 2
+    p, h, _ = ee.softmax_entropy(cuda(X))
+    h = host(h)
+    p = host(p)
+    assert h[0] == pytest.approx(math.log(S), rel=1e-6) and h[1] == pytest.approx(math.log(S), rel=1e-6)
+    assert h[2] == 0.0 and p[2, 17] == 1.0 and np.count_nonzero(p[2]) == 1
+    assert h[3] == pytest.approx(math.log(2), rel=1e-6)
+    assert h[4] == 0.0
+    H_ref, _ = orc.softmax_entropy(X)
+    check_entropy(h, H_ref)
+
+
+def test_softmax_entropy_causal_4d(ee, orc):
+    rng = np.random.default_rng(5)
+    L = rng.standard_normal((2, 4, 128, 128)).astype(np.float16)
+    probs, ent = ee.fused_softmax_entropy(cuda(L), causal=True)
+    P_ref, ent_ref = orc.fused_softmax_entropy(L, causal=True)
+    H_ref, _ = orc.softmax_entropy(L.reshape(-1, 128), causal=True)
+    _, h, _ = ee.softmax_entropy(cuda(L.reshape(-1, 128)), causal=True)
+    check_entropy(host(h), H_ref)
+    check_probs(host(probs).reshape(-1, 128), P_ref.reshape(-1, 128))
+    assert np.allclose(host(ent), ent_ref, rtol=1e-5)
+    # the reference test's own bound (EE/python/benchmark.py:174) against -sum p log(p + 1e-10)
+    pf = torch.softmax(torch.from_numpy(L).float().masked_fill(
+        ~torch.tril(torch.ones(128, 128)).bool(), float("-inf")), dim=-1)
+    ref_e = -(pf * torch.log(pf + 1e-10)).sum(-1).mean(dim=(1, 2)).numpy()
+    assert np.abs(host(ent) - ref_e).max() < 0.1
+
+
+def test_softmax_entropy_tiers_in_pass(ee, orc):
+    rng = np.random.default_rng(6)
+    X = logits_rows(rng, 300, 1024)
+    _, h, tier = ee.softmax_entropy(cuda(X), probs=False, thresholds=(0.41, 1.68))
+    t_ref, _, _ = orc.route(host(h), 0.41, 1.68)
+    assert np.array_equal(host(tier), t_ref)
+
+
+def test_softmax_entropy_full_size_properties(ee):
+    """BASELINE config 2's entropy shape [4096, 14336], log-uniform row scales:
+    H in [0, ln S] and probabilities summing to 1 within fp16 rounding."""
+    rng = np.random.default_rng(7)
+    R, S = 4096, 14336
+    sc = np.exp(rng.uniform(np.log(0.1), np.log(30.0), R)).astype(np.float32)
+    X = (torch.from_numpy(rng.standard_normal((R, S), dtype=np.float32)) * torch.from_numpy(sc)[:, None]).half()
+    p, h, _ = ee.softmax_entropy(X.cuda())
+    h = host(h)
+    assert np.all(h >= 0) and np.all(h <= math.log(S) * (1 + 1e-6))
+    sums = p.float().sum(dim=1)
+    assert torch.all((sums - 1).abs() < 5e-3).item()
+
+
+# ---------------------------------------------------------------------------- quantisers
+
+@pytest.mark.parametrize("mode", ["dispatcher", "engine", "fp8"])
+@pytest.mark.parametrize("M,K", [(64, 4096), (37, 1024), (9, 14336), (13, 1000), (6, 24)])
+def test_quant_codes_bit_exact(ee, orc, mode, M, K):
+    rng = np.random.default_rng(M * 31 + K)
+    A = rng.standard_normal((M, K)).astype(np.float16)
+    A[1] = 0
+    if M > 3:
+        A[3] *= np.float16(0.01)
+    codes, scale = ee.quantize_activations(cuda(A), mode)
+    if mode == "fp8":
+        ref_c, ref_s = orc.quant_act_f8(A)
+    else:
+        ref_c, ref_s = orc.quant_act_i8(A, mode)
+    assert np.array_equal(host(scale).view(np.uint32), ref_s.view(np.uint32))
+    assert np.array_equal(host(codes).view(np.uint8), ref_c.view(np.uint8))
+
+
+def test_e4m3_codes_every_fp16_value(ee, orc):
+    """A row whose amax is 448 has scale fp16(448/448) = 1 and inverse 1, so its
+    codes are e4m3(x) of the inputs themselves: all fp16 values |x| <= 448."""
+    h = np.arange(0, 0x7C00, dtype=np.uint16).view(np.float16)
+    h = h[h <= 448]
+    vals = np.concatenate([h, -h]).astype(np.float16)
+    K = 4096
+    n = (len(vals) + K - 2) // (K - 1)
+    A = np.zeros((n, K), np.float16)
+    A[:, 0] = 448
+    flat = A[:, 1:].reshape(-1)
+    flat[:len(vals)] = vals
+    A[:, 1:] = flat.reshape(n, K - 1)
+    codes, scale = ee.quantize_activations(cuda(A), "fp8")
+    assert np.all(host(scale) == 1.0)
+    ref = orc.e4m3_from_f32(A.astype(np.float32))
+    got = host(codes)
+    bad = np.argwhere(got != ref)
+    detail = [(float(A[i, j]), hex(int(A[i:i + 1, j:j + 1].view(np.uint16)[0, 0])), int(got[i, j]), int(ref[i, j]))
+              for i, j in bad[:12]]
+    assert len(bad) == 0, f"{len(bad)} codes differ (x, bits, gpu, oracle): {detail}"
+
+
+def test_quant_routed_slots(ee, orc):
+    rng = np.random.default_rng(8)
+    A = rng.standard_normal((50, 512)).astype(np.float16)
+    H = (rng.random(50) * 4).astype(np.float32)
+    tier, idx, counts = ee.route(cuda(H), 1.0, 2.0)
+    codes = torch.zeros((50, 512), dtype=torch.int8, device="cuda")
+    scale = torch.zeros(50, dtype=torch.float32, device="cuda")
+    ee.quantize_activations(cuda(A), "dispatcher", idx=idx, counts=counts, tier=1, out_codes=codes, out_scale=scale)
+    c = host(counts)
+    ix = host(idx)
+    off = int(c[0])
+    ref_c, ref_s = orc.quant_act_i8(A[ix[off:off + c[1]]], "dispatcher")
+    assert np.array_equal(host(codes)[off:off + c[1]], ref_c)
+    assert np.array_equal(host(scale)[off:off + c[1]], ref_s)
+    assert np.all(host(codes)[:off] == 0) and np.all(host(codes)[off + c[1]:] == 0)
+
+
+def test_quantize_weights_int8(ee, orc):
+    rng = np.random.default_rng(9)
+    W = (rng.standard_normal((384, 640)) * 0.02).astype(np.float16)
+    W[5] = 0
+    B, s = ee.quantize_weights_int8(cuda(W))
+    rB, rs = orc.quantize_weights_int8(W)
+    assert np.array_equal(host(B), rB)
+    assert np.array_equal(host(s).view(np.uint32), rs.view(np.uint32))
+
+
+# ---------------------------------------------------------------------------- GEMMs
+
+def weights(orc, rng, N, K, scale=0.02):
+    W = (rng.standard_normal((N, K)) * scale).astype(np.float16)
+    return orc.quantize_weights_int8(W)
+
+
+@pytest.mark.parametrize("M,K,N", [(256, 1024, 512), (200, 512, 260), (1, 4096, 128), (130, 4112, 4), (1024, 4096, 4096)])
+def test_int8_gemm_bit_exact(ee, orc, M, K, N):
+    rng = np.random.default_rng(M + K + N)
+    A = rng.standard_normal((M, K)).astype(np.float16)
+    B, bs = weights(orc, rng, N, K)
+    codes, a_s = orc.quant_act_i8(A, "dispatcher")
+    acc_ref = orc.gemm_i8_acc(codes, B)
+    out_ref = orc.epilogue_i8(acc_ref, a_s, bs)
+    pw = ee.prepare_weight(cuda(B), cuda(bs))
+    acc = torch.empty((M, N), dtype=torch.int32, device="cuda")
+    out = ee.gemm("int8", cuda(codes), pw.i8, cuda(a_s), cuda(bs), acc_out=acc)
+    assert np.array_equal(host(acc), acc_ref)
+    assert np.array_equal(host(out).view(np.uint16), out_ref.view(np.uint16))
+    # the reference launcher end to end (quantiser + GEMM)
+    full = ee.triton_int8_gemm(cuda(A), cuda(B), cuda(bs))
+    assert np.array_equal(host(full).view(np.uint16), out_ref.view(np.uint16))
+
+
+def test_int8_gemm_extreme_codes(ee, orc):
+    M, K, N = 128, 14336, 128
+    A = np.full((M, K), -127, np.int8)
+    A[::2] = 127
+    B = np.full((K, N), -127, np.int8)
+    acc = torch.empty((M, N), dtype=torch.int32, device="cuda")
+    pw = ee.prepare_weight(cuda(B), cuda(np.ones(N, np.float32)))
+    ee.gemm("int8", cuda(A), pw.i8, cuda(np.ones(M, np.float32)), cuda(np.ones(N, np.float32)), acc_out=acc)
+    assert np.array_equal(host(acc), orc.gemm_i8_acc(A, B))
+
+
+@pytest.mark.parametrize("M,K,N,sc", [(256, 1024, 512, 1.0), (96, 4096, 260, 0.1), (1024, 4096, 4096, 1.0)])
+def test_fp8_gemm(ee, orc, M, K, N, sc):
+    rng = np.random.default_rng(M * 3 + N)
+    A = (rng.standard_normal((M, K)) * sc).astype(np.float16)
+    A[2] = 0                                    # zero row -> NaN row, as the reference
+    B, bs = weights(orc, rng, N, K)
+    codes, a_s = orc.quant_act_f8(A)
+    ref = orc.gemm_f8_f64(codes, B, a_s, bs)
+    out = ee.triton_fp8_gemm(cuda(A), cuda(B), cuda(bs))
+    o = host(out)
+    assert np.all(np.isnan(o[2]))
+    check_close_f64(o, ref)
+    pw = ee.prepare_weight(cuda(B), cuda(bs))
+    assert np.array_equal(host(pw.f8), orc.e4m3_from_f32(B.T.astype(np.float32)))
+
+
+@pytest.mark.parametrize("M,K,N", [(256, 1024, 512), (77, 2048, 132), (1024, 4096, 4096)])
+def test_w8a16_gemm(ee, orc, M, K, N):
+    rng = np.random.default_rng(M * 5 + N)
+    A = rng.standard_normal((M, K)).astype(np.float16)
+    B, bs = weights(orc, rng, N, K)
+    pw = ee.prepare_weight(cuda(B), cuda(bs))
+    assert np.array_equal(host(pw.f16).view(np.uint16), orc.dequant_w8a16(B, bs).T.copy().view(np.uint16))
+    out = ee.triton_fp16_gemm(cuda(A), cuda(B), cuda(bs))
+    check_close_f64(host(out), orc.gemm_w8a16_f64(A, B, bs))
+
+
+def test_gemm_full_size_sampled_rows(ee, orc):
+    """BASELINE configs 1-2 at full size (M=4096, K=4096, N=14336): INT8 int32
+    accumulators bit-exact on 48 sampled rows (rows are independent)."""
+    rng = np.random.default_rng(11)
+    M, K, N = 4096, 4096, 14336
+    A = rng.standard_normal((M, K)).astype(np.float16)
+    B, bs = weights(orc, rng, N, K)
+    a, s = ee.quantize_activations(cuda(A), "dispatcher")
+    pw = ee.prepare_weight(cuda(B), cuda(bs))
+    acc = torch.empty((M, N), dtype=torch.int32, device="cuda")
+    ee.gemm("int8", a, pw.i8, s, pw.scale, acc_out=acc)
+    rows = np.sort(rng.choice(M, 48, replace=False))
+    codes, _ = orc.quant_act_i8(A[rows], "dispatcher")
+    assert np.array_equal(host(acc[torch.from_numpy(rows).cuda()]), orc.gemm_i8_acc(codes, B))
+
+
+# ---------------------------------------------------------------------------- routing
+
+@pytest.mark.parametrize("R", [1, 10, 1000, 4096, 70000])
+def test_route_matches_oracle(ee, orc, R):
+    rng = np.random.default_rng(R)
+    H = (rng.random(R) * 8).astype(np.float32)
+    H[: min(R, 3)] = np.float32(0.41)
+    tier, idx, counts = ee.route(cuda(H), 0.41, 1.68)
+    t_ref, i_ref, c_ref = orc.route(H, 0.41, 1.68)
+    assert np.array_equal(host(tier), t_ref)
+    assert np.array_equal(host(idx), i_ref)
+    assert np.array_equal(host(counts), c_ref)
+
+
+def test_route_reference_sweep(ee):
+    ent = cuda(np.float32([0.5, 1.0, 1.5, 2.0, 2.5, 3.0, 3.5, 4.0, 4.5, 5.0]))   # EE/python/benchmark.py:386
+    for (tl, th), pct in {(1.0, 2.0): [10, 20, 70], (2.0, 3.5): [30, 30, 40], (3.5, 4.5): [60, 20, 20]}.items():
+        _, _, counts = ee.route(ent, tl, th)                                       # NB:555-561
+        assert (host(counts) * 10).tolist() == pct
+
+
+def test_row_copy_gather_scatter(ee):
+    rng = np.random.default_rng(12)
+    X = rng.standard_normal((40, 72)).astype(np.float16)
+    idx = np.array(rng.permutation(40), np.int32)
+    g = ee.row_copy(cuda(X), cuda(idx))
+    assert np.array_equal(host(g), X[idx])
+    s = ee.row_copy(g, cuda(idx), scatter=True, out=torch.empty((40, 72), dtype=torch.float16, device="cuda"))
+    assert np.array_equal(host(s), X)
+
+
+@pytest.mark.parametrize("M,K,N", [(300, 1024, 256), (4096, 4096, 4096)])
+def test_routed_linear_equals_per_tier(ee, orc, M, K, N):
+    """scatter(gemm_t(gather(X)))[r] == gemm_t(X)[r] bit for bit, every tier."""
+    rng = np.random.default_rng(M + 1)
+    X = rng.standard_normal((M, K)).astype(np.float16)
+    B, bs = weights(orc, rng, N, K)
+    H = (rng.random(M) * 3).astype(np.float32)
+    pw = ee.prepare_weight(cuda(B), cuda(bs)).materialize()
+    x = cuda(X)
+    tier, idx, counts = ee.route(cuda(H), 0.41, 1.68)
+    out = ee.routed_linear(x, pw, idx, counts)
+    full = [ee.triton_int8_gemm(x, cuda(B), cuda(bs)), ee.triton_fp8_gemm(x, cuda(B), cuda(bs)),
+            ee.triton_fp16_gemm(x, cuda(B), cuda(bs))]
+    o = host(out).view(np.uint16)
+    t = host(tier)
+    assert sorted(set(t.tolist())) == [0, 1, 2]
+    for k in range(3):
+        ref = host(full[k]).view(np.uint16)
+        assert np.array_equal(o[t == k], ref[t == k]), f"tier {k}"
+
+
+# ---------------------------------------------------------------------------- dispatcher API
+
+def test_dispatcher_reference_answers(ee):
+    """EE/python/benchmark.py:180-218 on GPU tensors."""
+    d = ee.PipelinedEntropyDispatcher(tau_low=2.0, tau_high=3.5)
+    assert d.get_tier() == ee.PrecisionTier.FP16
+    for v, t in ((1.0, ee.PrecisionTier.INT8), (2.5, ee.PrecisionTier.FP8), (4.0, ee.PrecisionTier.FP16)):
+        d.submit_entropy(torch.tensor([v], device="cuda"))
+        assert d.get_tier() == t
+    st = d.get_stats()
+    assert [st[k]["count"] for k in ("INT8", "FP8", "FP16")] == [1, 1, 1]
+
+
+def test_dispatched_linear_tiers(ee, orc):
+    rng = np.random.default_rng(13)
+    lin = torch.nn.Linear(512, 384, bias=True).half()
+    with torch.no_grad():
+        lin.weight.copy_(torch.from_numpy((rng.standard_normal((384, 512)) * 0.02).astype(np.float16)))
+    lin = lin.cuda()
+    layer = ee.EntropyDispatchedLinear.from_linear(lin)
+    W = lin.weight.detach().cpu().numpy()
+    B, bs = orc.quantize_weights_int8(W)
+    assert np.array_equal(host(layer.weight_int8), B) and np.array_equal(host(layer.weight_scale), bs)
+    x = rng.standard_normal((2, 10, 512)).astype(np.float16)
+    y = layer(cuda(x), tier=ee.PrecisionTier.INT8)
+    assert y.shape == (2, 10, 384)
+    ref = orc.triton_int8_gemm(x.reshape(-1, 512), B, bs)
+    ref = (torch.from_numpy(ref) + lin.bias.detach().cpu().unsqueeze(0)).numpy()
+    assert np.array_equal(host(y).reshape(-1, 384).view(np.uint16), ref.view(np.uint16))
+    for tier, fn in ((ee.PrecisionTier.FP8, orc.triton_fp8_gemm_f64), (ee.PrecisionTier.FP16, orc.triton_fp16_gemm_f64)):
+        y = layer(cuda(x), tier=tier)
+        r = fn(x.reshape(-1, 512), B, bs) + lin.bias.detach().cpu().double().numpy()[None, :]
+        check_close_f64(host(y).reshape(-1, 384), r)
+
+
+def test_cubin_engine_counterpart(ee, orc):
+    """EE/test_cubin.py flow: round-based activation codes, int8 B [K, N], f32 scales."""
+    import os
+    from entropy_engine import engine as eng_mod
+    rng = np.random.default_rng(14)
+    M, K, N = 256, 1024, 512
+    A = rng.standard_normal((M, K)).astype(np.float16)
+    codes, a_s = orc.quant_act_i8(A, "engine")
+    g_codes, g_s = ee.quantize_activations(cuda(A), "engine")
+    assert np.array_equal(host(g_codes), codes) and np.array_equal(host(g_s), a_s)
+    B = rng.integers(-127, 127, (K, N), dtype=np.int8)
+    bs = (np.abs(rng.standard_normal(N)) * 0.01 + 0.001).astype(np.float32)
+    e = ee.CubinEngine.from_metadata(eng_mod.DEFAULT_CODE_OBJECT, eng_mod.DEFAULT_META, "gemm_int8_kernel")
+    out = e.forward(cuda(codes), cuda(B), cuda(a_s), cuda(bs))
+    assert out.dtype == torch.float16 and out.shape == (M, N)
+    assert np.array_equal(host(out).view(np.uint16), orc.gemm_i8(codes, B, a_s, bs).view(np.uint16))
+    with pytest.raises(RuntimeError, match="a must be int8"):
+        e.forward(cuda(A), cuda(B), cuda(a_s), cuda(bs))
+    with pytest.raises(RuntimeError, match="K mismatch"):
+        e.forward(cuda(codes[:, :512]), cuda(B), cuda(a_s), cuda(bs))
+    assert os.path.exists(eng_mod.DEFAULT_META)

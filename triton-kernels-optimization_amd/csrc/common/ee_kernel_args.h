@@ -1,0 +1,103 @@
+// ee_kernel_args.h -- kernel argument blocks shared by the gfx950 code objects
+// and the host launcher.  Every kernel takes exactly one of these structs by
+// value; the launcher passes it through hipModuleLaunchKernel's kernelParams.
+// Plain C layout (pointers and fixed-width integers only) so the host and the
+// device compilers agree on every offset.
+#pragma once
+#include <stdint.h>
+
+#include "entropy_engine.h"  // tier, quantiser-mode and GEMM-kind constants
+
+#define EE_WAVE 64
+#define EE_BLOCK 256
+
+// Row softmax + Shannon entropy.
+struct EeSoftmaxArgs {
+    const uint16_t* x;    // fp16 logits, rows of S, row stride ld_x (elements)
+    uint16_t* p;          // fp16 probabilities (nullable: entropy only)
+    float* h;             // f32 entropy per row
+    int32_t* tier;        // optional per-row precision tier (nullable)
+    int64_t rows;
+    int64_t ld_x;
+    int64_t ld_p;
+    int32_t S;
+    int32_t causal;       // 1: column c of row r is kept iff c <= r % S
+    double tau_low;       // tier thresholds, used when tier != nullptr
+    double tau_high;
+};
+
+// Per-row activation quantisation (optionally gathering routed rows);
+// mode is one of EE_QUANT_* (entropy_engine.h).
+struct EeQuantArgs {
+    const uint16_t* x;      // fp16 [*, K] activations, row stride ld_x
+    void* codes;            // int8 / e4m3 codes [rows, K], row stride ld_c
+    float* scale;           // f32 per output row
+    const int32_t* idx;     // optional source-row list (routing partition)
+    const int32_t* counts;  // optional device row counts per tier; output row
+                            // r goes to slot off + r (off = rows of lower tiers)
+    int64_t M;              // rows (upper bound when counts != nullptr)
+    int64_t K;
+    int64_t ld_x;
+    int64_t ld_c;
+    int32_t mode;
+    int32_t tier;           // which counts[] entry / idx segment (routing)
+};
+
+// Tiled GEMM on MFMA.  C[m, n] = sum_k A[m, k] * B[n, k]  (B packed K-contiguous).
+// kind (template argument of the kernel) is one of EE_GEMM_* (entropy_engine.h).
+struct EeGemmArgs {
+    const void* a;          // [M, K] int8 / e4m3 / fp16, row stride lda (elements)
+    const void* b;          // [N, K] same element type, row stride ldb
+    uint16_t* c;            // fp16 [*, N], row stride ldc
+    int32_t* acc;           // optional int32 accumulators (I8 only), row stride ldc
+    const float* a_scale;   // [M] (I8, F8)
+    const float* b_scale;   // [N] (I8, F8)
+    const int32_t* a_idx;   // optional: A row m is a[a_idx[off + m]] (else a[off + m])
+    const int32_t* c_idx;   // optional: C row m is c[c_idx[off + m]]
+    const int32_t* counts;  // optional device row counts per tier (M bound);
+                            // off = counts[0] + .. + counts[tier-1], else 0
+    int64_t lda;
+    int64_t ldb;
+    int64_t ldc;
+    int32_t M;              // rows (upper bound when counts != nullptr)
+    int32_t N;
+    int32_t K;
+    int32_t tier;
+};
+
+// Per-row routing: tier + stable partition of row indices.
+struct EeRouteArgs {
+    const float* h;
+    int32_t* tier;          // [rows]
+    int32_t* idx;           // [rows]: rows of tier 0, then tier 1, then tier 2
+    int32_t* counts;        // [3]
+    int64_t rows;
+    double tau_low;
+    double tau_high;
+};
+
+// Weight preparation (offline, once per layer).
+struct EeWeightArgs {
+    const void* src;        // see each kernel
+    void* dst;
+    void* dst2;
+    const float* scale;
+    int64_t R;              // rows of src
+    int64_t C;              // columns of src
+    int64_t ld_src;
+    int64_t ld_dst;
+};
+
+// Row copy (gather / scatter through a routing partition).
+struct EeRowCopyArgs {
+    const uint8_t* src;
+    uint8_t* dst;
+    const int32_t* idx;
+    const int32_t* counts;
+    int64_t rows;           // upper bound
+    int64_t row_bytes;
+    int64_t ld_src;         // bytes
+    int64_t ld_dst;         // bytes
+    int32_t tier;
+    int32_t scatter;        // 0: dst[r] = src[idx[r]]; 1: dst[idx[r]] = src[r]
+};

@@ -1,0 +1,551 @@
+// gemm.hip -- MFMA GEMMs of the three precision tiers for gfx950.
+//
+//   EE_GEMM_I8 : int8 x int8 -> int32 on v_mfma_i32_16x16x64_i8;
+//                C = fp16((f32(acc) * a_scale[m]) * b_scale[n])
+//                (EE/python/kernels.py:50-110)
+//   EE_GEMM_F8 : e4m3 x e4m3 -> f32 on v_mfma_f32_16x16x128_f8f6f4;
+//                C = fp16((acc * a_scale[m]) * b_scale[n])
+//                (EE/python/kernels.py:118-180; codes from quant.hip)
+//   EE_GEMM_F16: fp16 x fp16 -> f32 on v_mfma_f32_16x16x32_f16; C = fp16(acc)
+//                (EE/python/kernels.py:192-246; W8A16 weights pre-dequantised
+//                bit-exactly by eek_pack_b_f16)
+//
+// Operands: A [M, K] and B [N, K], both K-contiguous, which is the order the
+// MFMA register fragments want (16 consecutive K bytes per lane).
+// Tiling: a 256-thread workgroup computes a 128 x 128 tile of C; its four
+// wave64s each own a 64 x 64 quadrant as 4 x 4 MFMA 16x16 blocks.  K advances
+// in 128-byte stages.  LDS rows are 128 bytes; 16-byte chunk c of row r sits at
+// chunk c ^ (r & 7), so the eight lanes one ds_read_b128 pass serves hit eight
+// distinct 16-byte bank groups.
+//
+// eek_gemm_{i8,f8,f16}: four LDS stages (128 KB) filled by direct-to-LDS
+// global_load_lds_dwordx4 (no VGPR staging), three stages in flight while the
+// fourth is consumed: each wave waits only for its own oldest stage
+// (s_waitcnt vmcnt), then one s_barrier publishes it to the workgroup.
+// Needs K * elem_size to be a multiple of 128 bytes.
+// eek_gemm_{i8,f8,f16}_generic: two register-staged LDS buffers and a
+// zero-filled K tail, for K that is only a multiple of 16 bytes.
+//
+// The MFMA is issued with B as its first operand, so each lane ends up with
+// four consecutive columns of one row of C -> one 8-byte store per block.
+// Routing: with a device row count counts[tier] (off = rows of lower tiers),
+// A row m is a[a_idx[off + m]] (gather from the activations) or, without
+// a_idx, a[off + m] (the quantiser's partition slot), a_scale is read at
+// off + m, and C row m is c[c_idx[off + m]] (scatter).  The grid covers the
+// upper bound M and surplus workgroups exit at once.
+#include "../common/ee_device.h"
+
+#define BM 128
+#define BN 128
+#define BKB 128                         // K bytes per LDS stage
+#define LDS_STAGE ((BM + BN) * BKB)     // 32 KB
+#define NSTAGE 5                        // pipelined kernel: LDS stages (5 x 32 KB = all 160 KB)
+
+template <int KIND> struct AccT { typedef f32x4 type; };
+template <> struct AccT<EE_GEMM_I8> { typedef i32x4 type; };
+
+// 16-byte chunk c of LDS row r sits at chunk c ^ ((r >> 1) & 7).  gfx950's LDS
+// serves a ds_read_b128 in passes of 16 lanes over 64 banks: the 16 rows of a
+// pass then land on 16 distinct (row parity, chunk) bank groups.
+EE_DEV int swz(int row) { return (row >> 1) & 7; }
+EE_DEV uint32_t lds_off(int row, int chunk) { return (uint32_t)(row * BKB + ((chunk ^ swz(row)) << 4)); }
+
+EE_DEV i32x4 as_i32x4(u32x4 v) { return __builtin_bit_cast(i32x4, v); }
+EE_DEV f16x8 as_f16x8(u32x4 v) { return __builtin_bit_cast(f16x8, v); }
+
+// Workgroup -> tile.  Consecutive workgroup ids land on different XCDs
+// (round robin over 8); renumber so each XCD owns a contiguous run of tiles,
+// ordered M-fastest, so an XCD's L2 sees few distinct B column panels.
+EE_DEV void tile_of(int bid, int nblk, int tiles_m, int& tm, int& tn) {
+    int logical = bid;
+    if ((nblk & 7) == 0) logical = (bid & 7) * (nblk >> 3) + (bid >> 3);
+    tm = logical % tiles_m;
+    tn = logical / tiles_m;
+}
+
+// One 128-byte K stage from LDS into the 4 x 4 accumulator blocks of a wave.
+template <int KIND, typename acc_t>
+EE_DEV void mfma_stage(const uint8_t* s, acc_t (&acc)[4][4], int wm, int wn, int lane) {
+    const int fr = lane & 15, fg = lane >> 4;
+    if constexpr (KIND == EE_GEMM_F8) {
+        i32x8 af[4], bf[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int ra = wm * 64 + i * 16 + fr, rb = BM + wn * 64 + i * 16 + fr;
+            const u32x4 a0 = *(const u32x4*)(s + lds_off(ra, 2 * fg));
+            const u32x4 a1 = *(const u32x4*)(s + lds_off(ra, 2 * fg + 1));
+            const u32x4 b0 = *(const u32x4*)(s + lds_off(rb, 2 * fg));
+            const u32x4 b1 = *(const u32x4*)(s + lds_off(rb, 2 * fg + 1));
+            af[i] = i32x8{(int)a0[0], (int)a0[1], (int)a0[2], (int)a0[3], (int)a1[0], (int)a1[1], (int)a1[2], (int)a1[3]};
+            bf[i] = i32x8{(int)b0[0], (int)b0[1], (int)b0[2], (int)b0[3], (int)b1[0], (int)b1[1], (int)b1[2], (int)b1[3]};
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bf[j], af[i], acc[i][j], 0, 0, 0, 0, 0, 0);
+    } else {
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+            u32x4 af[4], bf[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                af[i] = *(const u32x4*)(s + lds_off(wm * 64 + i * 16 + fr, kk * 4 + fg));
+                bf[i] = *(const u32x4*)(s + lds_off(BM + wn * 64 + i * 16 + fr, kk * 4 + fg));
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    if constexpr (KIND == EE_GEMM_I8)
+                        acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(as_i32x4(bf[j]), as_i32x4(af[i]), acc[i][j],
+                                                                         0, 0, 0);
+                    else
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_f16x8(bf[j]), as_f16x8(af[i]),
+                                                                          acc[i][j], 0, 0, 0);
+                }
+        }
+    }
+}
+
+// Dequantising epilogue: lane holds C[m0 + wm*64 + i*16 + fr][n0 + wn*64 + j*16 + 4*fg + 0..3].
+template <int KIND, typename acc_t>
+EE_DEV void epilogue(const EeGemmArgs& g, const acc_t (&acc)[4][4], int m0, int n0, int M, int64_t off, int wm,
+                     int wn, int lane) {
+    const int fr = lane & 15, fg = lane >> 4;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int m = m0 + wm * 64 + i * 16 + fr;
+        if (m >= M) continue;
+        const int64_t crow = g.c_idx ? (int64_t)g.c_idx[off + m] : (int64_t)m;
+        const float as = (KIND == EE_GEMM_F16) ? 0.0f : g.a_scale[off + m];
+        uint16_t* cr = g.c + crow * g.ldc;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int n = n0 + wn * 64 + j * 16 + 4 * fg;
+            if (n >= g.N) continue;                 // N is a multiple of 4
+            float o[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                if constexpr (KIND == EE_GEMM_I8) {
+                    float v = (float)acc[i][j][r];
+                    v = v * as;
+                    o[r] = v * g.b_scale[n + r];
+                } else if constexpr (KIND == EE_GEMM_F8) {
+                    const float v = acc[i][j][r] * as;
+                    o[r] = v * g.b_scale[n + r];
+                } else {
+                    o[r] = acc[i][j][r];
+                }
+            }
+            *(u32x2*)(cr + n) = u32x2{pack_f16x2(o[0], o[1]), pack_f16x2(o[2], o[3])};
+            if constexpr (KIND == EE_GEMM_I8) {
+                if (g.acc) *(i32x4*)(g.acc + crow * g.ldc + n) = acc[i][j];
+            }
+        }
+    }
+}
+
+#define GPTR(p) ((const void __attribute__((address_space(1)))*)(p))
+#define LPTR(p) ((void __attribute__((address_space(3)))*)(p))
+
+// 16 bytes per lane from global memory straight into LDS at lds_base + 16 * lane
+// (lds_base wave-uniform).  Issued as inline asm so that the compiler's wait
+// model contains only the kernel's ds_reads (an LDS DMA it can see makes it
+// fall back to waiting for every outstanding LDS read); the kernel tracks these
+// loads itself with explicit vmcnt waits before each stage barrier.
+EE_DEV void dma16(const uint8_t* gptr, uint32_t lds_base) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds_base), "v"(gptr) : "memory", "m0");
+}
+EE_DEV uint32_t lds_addr(const uint8_t* p) { return (uint32_t)(uintptr_t)LPTR(p); }
+
+// s_waitcnt with only vmcnt constrained (gfx9 encoding: vmcnt[3:0] | expcnt 7 << 4 |
+// lgkmcnt 15 << 8 | vmcnt[5:4] << 14).
+#define WAITCNT_VM(n) __builtin_amdgcn_s_waitcnt((((n) & 15) | (7 << 4) | (15 << 8) | (((n) >> 4) << 14)))
+// s_waitcnt lgkmcnt(0) with vmcnt and expcnt left unconstrained.
+#define WAITCNT_LGKM0() __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14))
+
+// ---------------------------------------------------------------------------
+// Pipelined kernel: 32x32 MFMA blocks (the full-rate shapes on gfx950:
+// i8 32x32x32 and f16 32x32x16 run at twice the rate of their 16x16 forms),
+// K stages split into slices of one MFMA depth, fragments of slice s+1 read
+// from LDS while the MFMAs of slice s run.
+template <int KIND> struct Pipe;
+template <> struct Pipe<EE_GEMM_I8> {            // 32x32x32 i8: 32 K bytes per slice, 16 B per lane
+    static constexpr int SB = 32, CPF = 1;
+    typedef u32x4 frag_t;
+    typedef i32x16 acc_t;
+    static EE_DEV acc_t mma(const frag_t& b, const frag_t& a, const acc_t& c) {
+        return __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(i32x4, b), __builtin_bit_cast(i32x4, a), c, 0, 0, 0);
+    }
+};
+template <> struct Pipe<EE_GEMM_F16> {           // 32x32x16 f16: 32 K bytes per slice, 16 B per lane
+    static constexpr int SB = 32, CPF = 1;
+    typedef u32x4 frag_t;
+    typedef f32x16 acc_t;
+    static EE_DEV acc_t mma(const frag_t& b, const frag_t& a, const acc_t& c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, b), __builtin_bit_cast(f16x8, a), c, 0, 0, 0);
+    }
+};
+template <> struct Pipe<EE_GEMM_F8> {            // 32x32x64 e4m3: 64 K bytes per slice, 32 B per lane
+    static constexpr int SB = 64, CPF = 2;
+    typedef i32x8 frag_t;
+    typedef f32x16 acc_t;
+    static EE_DEV acc_t mma(const frag_t& b, const frag_t& a, const acc_t& c) {
+        return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(b, a, c, 0, 0, 0, 0, 0, 0);
+    }
+};
+
+template <int KIND>
+struct Frags {
+    typename Pipe<KIND>::frag_t a[2], b[2];
+};
+
+// Fragments of one K slice: lane l reads row (l & 31) of each 32-row block, K
+// chunk(s) slice * SB/16 + (l >> 5) * CPF (+1): lanes 0-31 and 32-63 cover the
+// two K halves of the slice, as the 32x32 MFMA operands expect.
+template <int KIND>
+EE_DEV void read_frags(const uint8_t* s, int slice, int wm, int wn, int lane, Frags<KIND>& f) {
+    typedef Pipe<KIND> P;
+    const int r = lane & 31;
+    const int c0 = slice * (P::SB / 16) + (lane >> 5) * P::CPF;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int ra = wm * 64 + i * 32 + r, rb = BM + wn * 64 + i * 32 + r;
+        if constexpr (P::CPF == 1) {
+            f.a[i] = *(const u32x4*)(s + lds_off(ra, c0));
+            f.b[i] = *(const u32x4*)(s + lds_off(rb, c0));
+        } else {
+            const u32x4 a0 = *(const u32x4*)(s + lds_off(ra, c0)), a1 = *(const u32x4*)(s + lds_off(ra, c0 + 1));
+            const u32x4 b0 = *(const u32x4*)(s + lds_off(rb, c0)), b1 = *(const u32x4*)(s + lds_off(rb, c0 + 1));
+            f.a[i] = i32x8{(int)a0[0], (int)a0[1], (int)a0[2], (int)a0[3], (int)a1[0], (int)a1[1], (int)a1[2], (int)a1[3]};
+            f.b[i] = i32x8{(int)b0[0], (int)b0[1], (int)b0[2], (int)b0[3], (int)b1[0], (int)b1[1], (int)b1[2], (int)b1[3]};
+        }
+    }
+}
+
+template <int KIND>
+EE_DEV void mma_all(const Frags<KIND>& f, typename Pipe<KIND>::acc_t (&acc)[2][2]) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = Pipe<KIND>::mma(f.b[j], f.a[i], acc[i][j]);
+}
+
+// Scheduling groups for one slice: all LDS reads of the next slice first (4
+// ds_read_b128, 8 for the 32-byte e4m3 fragments), then the 4 MFMAs of the
+// current slice, which cover the reads' latency before the next slice waits.
+template <int KIND>
+EE_DEV void interleave() {
+    __builtin_amdgcn_sched_group_barrier(0x100, 4 * Pipe<KIND>::CPF, 0);   // DS read
+    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);                     // MFMA
+}
+
+// 32x32 epilogue: lane l, register r of block (i, j) holds
+// C[m0 + wm*64 + 32i + (l & 31)][n0 + wn*64 + 32j + 8*(r/4) + 4*(l >> 5) + r%4].
+template <int KIND>
+EE_DEV void epilogue32(const EeGemmArgs& g, const typename Pipe<KIND>::acc_t (&acc)[2][2], int m0, int n0, int M,
+                       int64_t off, int wm, int wn, int lane) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int m = m0 + wm * 64 + i * 32 + (lane & 31);
+        if (m >= M) continue;
+        const int64_t crow = g.c_idx ? (int64_t)g.c_idx[off + m] : (int64_t)m;
+        const float as = (KIND == EE_GEMM_F16) ? 0.0f : g.a_scale[off + m];
+        uint16_t* cr = g.c + crow * g.ldc;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int n = n0 + wn * 64 + j * 32 + 8 * q + 4 * (lane >> 5);
+                if (n >= g.N) continue;             // N is a multiple of 4
+                float o[4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    if constexpr (KIND == EE_GEMM_I8) {
+                        float v = (float)acc[i][j][4 * q + r];
+                        v = v * as;
+                        o[r] = v * g.b_scale[n + r];
+                    } else if constexpr (KIND == EE_GEMM_F8) {
+                        const float v = acc[i][j][4 * q + r] * as;
+                        o[r] = v * g.b_scale[n + r];
+                    } else {
+                        o[r] = acc[i][j][4 * q + r];
+                    }
+                }
+                *(u32x2*)(cr + n) = u32x2{pack_f16x2(o[0], o[1]), pack_f16x2(o[2], o[3])};
+                if constexpr (KIND == EE_GEMM_I8) {
+                    if (g.acc)
+                        *(i32x4*)(g.acc + crow * g.ldc + n) =
+                            i32x4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+                }
+            }
+        }
+    }
+}
+
+// Epilogue through LDS: the wave's 64 x 64 fp16 tile is written to a free 8 KB
+// LDS region in the 32x32 MFMA layout, read back as rows, and stored 16 bytes
+// per lane -- each store instruction covers 8 rows x 128 contiguous bytes of C
+// instead of 32 rows x 16 bytes.  (The optional int32 accumulators keep the
+// direct path; they are a debug output.)
+template <int KIND>
+EE_DEV void epilogue32_lds(const EeGemmArgs& g, const typename Pipe<KIND>::acc_t (&acc)[2][2], uint8_t* tile, int m0,
+                           int n0, int M, int64_t off, int wm, int wn, int lane) {
+    // 1. dequantise and write: lane l holds rows i*32 + (l & 31), columns j*32 + 8q + 4(l >> 5) + 0..3.
+    // The lane's 8 groups of 4 column scales and 2 row scales are loaded first, as vectors.
+    f32x4 bs[2][4];
+    float as[2];
+    if constexpr (KIND != EE_GEMM_F16) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int n = n0 + wn * 64 + j * 32 + 8 * q + 4 * (lane >> 5);
+                bs[j][q] = (n < g.N) ? *(const f32x4*)(g.b_scale + n) : f32x4{0.f, 0.f, 0.f, 0.f};
+            }
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int m = m0 + wm * 64 + i * 32 + (lane & 31);
+            as[i] = (m < M) ? g.a_scale[off + m] : 0.0f;
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int rl = i * 32 + (lane & 31);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int cl = j * 32 + 8 * q + 4 * (lane >> 5);
+                float o[4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    if constexpr (KIND == EE_GEMM_I8) {
+                        float v = (float)acc[i][j][4 * q + r];
+                        v = v * as[i];
+                        o[r] = v * bs[j][q][r];
+                    } else if constexpr (KIND == EE_GEMM_F8) {
+                        const float v = acc[i][j][4 * q + r] * as[i];
+                        o[r] = v * bs[j][q][r];
+                    } else {
+                        o[r] = acc[i][j][4 * q + r];
+                    }
+                }
+                // row rl: 128 bytes = 8 chunks of 16; column cl is chunk cl/8, half (cl/4)&1
+                *(u32x2*)(tile + lds_off(rl, cl >> 3) + ((cl >> 2) & 1) * 8) =
+                    u32x2{pack_f16x2(o[0], o[1]), pack_f16x2(o[2], o[3])};
+            }
+        }
+    }
+    // 2. read back row-contiguous and store (each wave reads only its own region)
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const int rl = k * 8 + (lane >> 3), ch = lane & 7;
+        const u32x4 v = *(const u32x4*)(tile + lds_off(rl, ch));
+        const int m = m0 + wm * 64 + rl;
+        const int n = n0 + wn * 64 + ch * 8;
+        if (m >= M || n >= g.N) continue;
+        const int64_t crow = g.c_idx ? (int64_t)g.c_idx[off + m] : (int64_t)m;
+        uint16_t* dst = g.c + crow * g.ldc + n;
+        if (n + 8 <= g.N && ((uintptr_t)dst & 15) == 0) {
+            *(u32x4*)dst = v;
+        } else {                                           // N % 8 == 4 tail, or C only 8-byte aligned
+            *(u32x2*)dst = u32x2{v[0], v[1]};
+            if (n + 4 < g.N) *(u32x2*)(dst + 4) = u32x2{v[2], v[3]};
+        }
+    }
+}
+
+template <int KIND>
+EE_DEV void gemm_pipelined(const EeGemmArgs& g) {
+    typedef Pipe<KIND> P;
+    typedef typename P::acc_t acc_t;
+    constexpr int ESZ = (KIND == EE_GEMM_F16) ? 2 : 1;
+    constexpr int LOADS = 8;                          // direct loads per lane per stage (4 A + 4 B)
+    constexpr int NSL = BKB / P::SB;                  // K slices per stage (4 or 2)
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[NSTAGE * LDS_STAGE];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int M = g.counts ? g.counts[g.tier] : g.M;
+    const int64_t off = g.counts ? tier_offset(g.counts, g.tier) : 0;
+    const int tiles_m = (g.M + BM - 1) / BM;
+    int tm, tn;
+    tile_of((int)blockIdx.x, (int)gridDim.x, tiles_m, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+    if (m0 >= M) return;                              // whole workgroup, before any barrier
+
+    const int nk = (int)((int64_t)g.K * ESZ / BKB);   // K * ESZ is a multiple of BKB here
+
+    // Loader geometry: one global_load_lds_dwordx4 fills 8 LDS rows (1 KB); lane l
+    // lands at row r = 8*grp + l/8, physical chunk l%8, which holds logical chunk
+    // (l%8) ^ swz(r).  Wave w fills row groups 4w..4w+3 of A and of B.
+    const int lrow = lane >> 3;
+    const uint8_t* pa[4];
+    const uint8_t* pb[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int r = (wave * 4 + i) * 8 + lrow;
+        const int lchunk = (lane & 7) ^ swz(r);        // swz(BM + r) == swz(r): BM is a multiple of 16
+        const int m = min(m0 + r, M - 1);
+        const int64_t ar = g.a_idx ? (int64_t)g.a_idx[off + m] : off + m;
+        pa[i] = (const uint8_t*)g.a + ar * g.lda * ESZ + lchunk * 16;
+        const int n = min(n0 + r, g.N - 1);
+        pb[i] = (const uint8_t*)g.b + (int64_t)n * g.ldb * ESZ + lchunk * 16;
+    }
+    const int uwave = __builtin_amdgcn_readfirstlane(wave);
+    auto issue = [&](int kt) {
+        const uint32_t s = lds_addr(smem) + (uint32_t)((kt % NSTAGE) * LDS_STAGE);
+        const int64_t kb = (int64_t)kt * BKB;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int grp = uwave * 4 + i;
+            dma16(pa[i] + kb, s + grp * 8 * BKB);
+            dma16(pb[i] + kb, s + (BM + grp * 8) * BKB);
+        }
+    };
+    // Wait until stage `next` has landed for this wave while the stages issued
+    // after it (up to `last`) stay in flight, then one barrier makes it visible to
+    // the workgroup and frees every buffer read before it.
+    auto sync_stage = [&](int next, int last) {
+        const int after = last - next;
+        if (after >= 4) WAITCNT_VM(4 * LOADS);
+        else if (after == 3) WAITCNT_VM(3 * LOADS);
+        else if (after == 2) WAITCNT_VM(2 * LOADS);
+        else if (after == 1) WAITCNT_VM(LOADS);
+        else WAITCNT_VM(0);
+        WAITCNT_LGKM0();                              // this wave's reads of the freed buffer are done
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+    };
+
+    acc_t acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = acc_t{};
+
+    // All NSTAGE buffers start filling; afterwards stage kt + NSTAGE goes into the
+    // buffer of stage kt as soon as every wave has finished reading it.
+#pragma unroll
+    for (int st = 0; st < NSTAGE; ++st)
+        if (st < nk) issue(st);
+    sync_stage(0, min(NSTAGE, nk) - 1);
+
+    // Fragments alternate between f0 and f1 slice by slice (NSL is even, so slice 0
+    // of every stage is in f0): the reads of the next slice are issued between the
+    // MFMAs of the current one, and the MFMAs wait only for reads a slice old.
+    Frags<KIND> f0, f1;
+    read_frags<KIND>(smem, 0, wm, wn, lane, f0);
+    for (int kt = 0; kt < nk; ++kt) {
+        const uint8_t* s = smem + (kt % NSTAGE) * LDS_STAGE;
+#pragma unroll
+        for (int sl = 0; sl + 1 < NSL; ++sl) {
+            Frags<KIND>& cur = (sl & 1) ? f1 : f0;
+            Frags<KIND>& nxt = (sl & 1) ? f0 : f1;
+            read_frags<KIND>(s, sl + 1, wm, wn, lane, nxt);
+            mma_all<KIND>(cur, acc);
+            interleave<KIND>();
+        }
+        if (kt + 1 < nk) {
+            sync_stage(kt + 1, min(kt + NSTAGE - 1, nk - 1));   // every wave is done with stage kt
+            if (kt + NSTAGE < nk) issue(kt + NSTAGE);
+        }
+        read_frags<KIND>(smem + (min(kt + 1, nk - 1) % NSTAGE) * LDS_STAGE, 0, wm, wn, lane, f0);
+        mma_all<KIND>(f1, acc);
+        interleave<KIND>();
+    }
+    if (g.acc) {
+        epilogue32<KIND>(g, acc, m0, n0, M, off, wm, wn, lane);
+    } else {
+        // The buffer after the last stage's is free: every DMA has landed (vmcnt(0)
+        // at the last stage sync) and every read of it preceded that sync's barrier.
+        uint8_t* tile = smem + (nk % NSTAGE) * LDS_STAGE + wave * (64 * BKB);
+        epilogue32_lds<KIND>(g, acc, tile, m0, n0, M, off, wm, wn, lane);
+    }
+}
+
+template <int KIND>
+EE_DEV void gemm_generic(const EeGemmArgs& g) {
+    typedef typename AccT<KIND>::type acc_t;
+    constexpr int ESZ = (KIND == EE_GEMM_F16) ? 2 : 1;
+    __shared__ __attribute__((aligned(16))) uint8_t smem[2 * LDS_STAGE];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int M = g.counts ? g.counts[g.tier] : g.M;
+    const int64_t off = g.counts ? tier_offset(g.counts, g.tier) : 0;
+    const int tiles_m = (g.M + BM - 1) / BM;
+    int tm, tn;
+    tile_of((int)blockIdx.x, (int)gridDim.x, tiles_m, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+    if (m0 >= M) return;                              // whole workgroup, before any barrier
+
+    const int64_t Kb = (int64_t)g.K * ESZ;
+    const int nk = (int)((Kb + BKB - 1) / BKB);
+    const int ch = tid & 7, rr = tid >> 3;            // loader: chunk, first row
+
+    const uint8_t* pa[4];
+    const uint8_t* pb[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int m = min(m0 + rr + 32 * i, M - 1);
+        const int64_t ar = g.a_idx ? (int64_t)g.a_idx[off + m] : off + m;
+        pa[i] = (const uint8_t*)g.a + ar * g.lda * ESZ + ch * 16;
+        const int n = min(n0 + rr + 32 * i, g.N - 1);
+        pb[i] = (const uint8_t*)g.b + (int64_t)n * g.ldb * ESZ + ch * 16;
+    }
+
+    u32x4 ra[4], rb[4];
+    auto gload = [&](int kt) {
+        const bool kin = (int64_t)kt * BKB + ch * 16 < Kb;   // K is a multiple of 16 bytes
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            ra[i] = kin ? *(const u32x4*)(pa[i] + (int64_t)kt * BKB) : u32x4{0, 0, 0, 0};
+            rb[i] = kin ? *(const u32x4*)(pb[i] + (int64_t)kt * BKB) : u32x4{0, 0, 0, 0};
+        }
+    };
+    auto lstore = [&](int buf) {
+        uint8_t* s = smem + buf * LDS_STAGE;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int r = rr + 32 * i;
+            *(u32x4*)(s + lds_off(r, ch)) = ra[i];
+            *(u32x4*)(s + lds_off(BM + r, ch)) = rb[i];
+        }
+    };
+
+    acc_t acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = acc_t{0, 0, 0, 0};
+
+    gload(0);
+    lstore(0);
+    __syncthreads();
+    for (int kt = 0; kt < nk; ++kt) {
+        const int buf = kt & 1;
+        if (kt + 1 < nk) gload(kt + 1);
+        mfma_stage<KIND>(smem + buf * LDS_STAGE, acc, wm, wn, lane);
+        if (kt + 1 < nk) lstore(buf ^ 1);
+        __syncthreads();
+    }
+    epilogue<KIND>(g, acc, m0, n0, M, off, wm, wn, lane);
+}
+
+extern "C" __global__ void __launch_bounds__(EE_BLOCK) __attribute__((amdgpu_waves_per_eu(1, 1))) eek_gemm_i8(EeGemmArgs g) {
+    gemm_pipelined<EE_GEMM_I8>(g);
+}
+extern "C" __global__ void __launch_bounds__(EE_BLOCK) __attribute__((amdgpu_waves_per_eu(1, 1))) eek_gemm_f8(EeGemmArgs g) {
+    gemm_pipelined<EE_GEMM_F8>(g);
+}
+extern "C" __global__ void __launch_bounds__(EE_BLOCK) __attribute__((amdgpu_waves_per_eu(1, 1))) eek_gemm_f16(EeGemmArgs g) {
+    gemm_pipelined<EE_GEMM_F16>(g);
+}
+
+// Fallback for any K that is a multiple of 16 bytes (zero-filled K tail).
+extern "C" __global__ void __launch_bounds__(EE_BLOCK) eek_gemm_i8_generic(EeGemmArgs g) { gemm_generic<EE_GEMM_I8>(g); }
+extern "C" __global__ void __launch_bounds__(EE_BLOCK) eek_gemm_f8_generic(EeGemmArgs g) { gemm_generic<EE_GEMM_F8>(g); }
+extern "C" __global__ void __launch_bounds__(EE_BLOCK) eek_gemm_f16_generic(EeGemmArgs g) { gemm_generic<EE_GEMM_F16>(g); }

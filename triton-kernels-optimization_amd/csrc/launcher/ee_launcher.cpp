@@ -1,0 +1,675 @@
+// ee_launcher.cpp -- host side of the C ABI in include/entropy_engine.h.
+//
+// Loads the gfx950 code objects named by entropy_engine_meta.json with
+// hipModuleLoadData, resolves every kernel with hipModuleGetFunction, checks
+// the launch geometry the meta declares against the functions' attributes,
+// and launches with hipModuleLaunchKernel on the caller's stream.  Every
+// argument check happens before the first HIP call of an entry point.
+// Role of the reference's CubinEngine (EE/csrc/engine.cpp:23-216); the
+// meta-JSON reader serves the same purpose as its from_metadata
+// (engine.cpp:168-199), on a real JSON parser.
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstring>
+#include <fstream>
+#include <map>
+#include <memory>
+#include <sstream>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "../common/ee_kernel_args.h"
+#include "entropy_engine.h"
+
+#define EE_EXPORT extern "C" __attribute__((visibility("default")))
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const std::string& msg) {
+    g_err = msg;
+    return code;
+}
+
+#define EE_HIP(call, what)                                                                   \
+    do {                                                                                     \
+        hipError_t e_ = (call);                                                              \
+        if (e_ != hipSuccess) return fail(EE_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e_)); \
+    } while (0)
+
+// ---------------------------------------------------------------- JSON reader
+struct Json {
+    enum Kind { NUL, BOOL, NUM, STR, ARR, OBJ } kind = NUL;
+    bool b = false;
+    double num = 0.0;
+    std::string str;
+    std::vector<Json> arr;
+    std::map<std::string, Json> obj;
+    const Json* get(const std::string& k) const {
+        if (kind != OBJ) return nullptr;
+        auto it = obj.find(k);
+        return it == obj.end() ? nullptr : &it->second;
+    }
+};
+
+struct JsonParser {
+    const std::string& s;
+    size_t i = 0;
+    std::string err;
+    explicit JsonParser(const std::string& src) : s(src) {}
+    void ws() {
+        while (i < s.size() && (s[i] == ' ' || s[i] == '\n' || s[i] == '\r' || s[i] == '\t')) ++i;
+    }
+    bool lit(const char* t) {
+        size_t n = std::strlen(t);
+        if (s.compare(i, n, t) != 0) return false;
+        i += n;
+        return true;
+    }
+    bool value(Json& out, int depth) {
+        if (depth > 64) { err = "nesting too deep"; return false; }
+        ws();
+        if (i >= s.size()) { err = "unexpected end"; return false; }
+        char c = s[i];
+        if (c == '{') {
+            ++i;
+            out.kind = Json::OBJ;
+            ws();
+            if (i < s.size() && s[i] == '}') { ++i; return true; }
+            for (;;) {
+                ws();
+                Json key;
+                if (i >= s.size() || s[i] != '"' || !string(key.str)) { if (err.empty()) err = "expected key"; return false; }
+                ws();
+                if (i >= s.size() || s[i] != ':') { err = "expected ':'"; return false; }
+                ++i;
+                Json v;
+                if (!value(v, depth + 1)) return false;
+                out.obj[key.str] = std::move(v);
+                ws();
+                if (i < s.size() && s[i] == ',') { ++i; continue; }
+                if (i < s.size() && s[i] == '}') { ++i; return true; }
+                err = "expected ',' or '}'";
+                return false;
+            }
+        }
+        if (c == '[') {
+            ++i;
+            out.kind = Json::ARR;
+            ws();
+            if (i < s.size() && s[i] == ']') { ++i; return true; }
+            for (;;) {
+                Json v;
+                if (!value(v, depth + 1)) return false;
+                out.arr.push_back(std::move(v));
+                ws();
+                if (i < s.size() && s[i] == ',') { ++i; continue; }
+                if (i < s.size() && s[i] == ']') { ++i; return true; }
+                err = "expected ',' or ']'";
+                return false;
+            }
+        }
+        if (c == '"') { out.kind = Json::STR; return string(out.str); }
+        if (lit("true")) { out.kind = Json::BOOL; out.b = true; return true; }
+        if (lit("false")) { out.kind = Json::BOOL; out.b = false; return true; }
+        if (lit("null")) { out.kind = Json::NUL; return true; }
+        size_t st = i;
+        while (i < s.size() && (std::strchr("+-0123456789.eE", s[i]) != nullptr)) ++i;
+        if (st == i) { err = "unexpected character"; return false; }
+        char* end = nullptr;
+        std::string tok = s.substr(st, i - st);
+        out.num = std::strtod(tok.c_str(), &end);
+        if (end == nullptr || *end != '\0') { err = "bad number"; return false; }
+        out.kind = Json::NUM;
+        return true;
+    }
+    bool string(std::string& out) {
+        ++i;  // opening quote
+        while (i < s.size() && s[i] != '"') {
+            if (s[i] == '\\') {
+                if (++i >= s.size()) break;
+                char e = s[i];
+                out.push_back(e == 'n' ? '\n' : e == 't' ? '\t' : e);
+            } else {
+                out.push_back(s[i]);
+            }
+            ++i;
+        }
+        if (i >= s.size()) { err = "unterminated string"; return false; }
+        ++i;
+        return true;
+    }
+};
+
+int read_file(const std::string& path, std::string& out, const char* what) {
+    std::ifstream f(path, std::ios::binary);
+    if (!f.is_open()) return fail(EE_ERR_IO, std::string("Could not open ") + what + ": " + path);
+    std::stringstream ss;
+    ss << f.rdbuf();
+    if (f.bad()) return fail(EE_ERR_IO, std::string("Failed to read ") + what + ": " + path);
+    out = ss.str();
+    return EE_OK;
+}
+
+int parse_json(const std::string& text, const std::string& path, Json& out) {
+    JsonParser p(text);
+    if (!p.value(out, 0)) return fail(EE_ERR_META, "Malformed meta JSON " + path + ": " + p.err);
+    p.ws();
+    if (p.i != text.size()) return fail(EE_ERR_META, "Malformed meta JSON " + path + ": trailing data");
+    return EE_OK;
+}
+
+int json_int(const Json& o, const char* key, const std::string& path, int64_t& v) {
+    const Json* j = o.get(key);
+    if (j == nullptr) return fail(EE_ERR_META, std::string("Missing key: ") + key + " (" + path + ")");
+    if (j->kind != Json::NUM) return fail(EE_ERR_META, std::string("Key is not a number: ") + key + " (" + path + ")");
+    v = (int64_t)j->num;
+    return EE_OK;
+}
+
+bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
+
+struct Kernel {
+    hipFunction_t fn = nullptr;
+    int block = 0;
+    int lds = 0;
+};
+
+int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+}  // namespace
+
+struct ee_engine {
+    int device = -1;
+    std::vector<hipModule_t> modules;
+    std::unordered_map<std::string, Kernel> kernels;
+    std::unordered_map<std::string, int64_t> options;
+};
+
+struct ee_module_engine {
+    std::string func;
+    int device = -1;
+    hipModule_t module = nullptr;
+    hipFunction_t fn = nullptr;
+    int shared_mem = 0, num_warps = 0, block_m = 0, block_n = 0, static_lds = 0;
+};
+
+namespace {
+
+int check_device(int device) {
+    int cur = -1;
+    EE_HIP(hipGetDevice(&cur), "hipGetDevice");
+    if (cur != device)
+        return fail(EE_ERR_INVALID_ARG, "engine was created on device " + std::to_string(device) +
+                                            " but the current device is " + std::to_string(cur));
+    return EE_OK;
+}
+
+const Kernel* find_kernel(const ee_engine* e, const std::string& name) {
+    auto it = e->kernels.find(name);
+    return it == e->kernels.end() ? nullptr : &it->second;
+}
+
+template <typename Args>
+int launch(ee_engine* e, const std::string& name, int64_t gx, int64_t gy, int block, Args args,
+           ee_stream_t stream) {
+    const Kernel* k = find_kernel(e, name);
+    if (k == nullptr) return fail(EE_ERR_NOT_FOUND, "kernel not in the loaded code objects: " + name);
+    if (gx <= 0 || gy <= 0) return EE_OK;
+    if (gx > 0x7fffffff || gy > 65535) return fail(EE_ERR_UNSUPPORTED, "grid too large for " + name);
+    if (block != k->block)
+        return fail(EE_ERR_META, "launch block " + std::to_string(block) + " != meta block " +
+                                     std::to_string(k->block) + " for " + name);
+    int rc = check_device(e->device);
+    if (rc) return rc;
+    void* params[] = {&args};
+    EE_HIP(hipModuleLaunchKernel(k->fn, (unsigned)gx, (unsigned)gy, 1, (unsigned)block, 1, 1, 0,
+                                 (hipStream_t)stream, params, nullptr),
+           "hipModuleLaunchKernel(" + name + ")");
+    return EE_OK;
+}
+
+// (VPT, WPR) for a register-resident row kernel: VPT 16-byte vectors per lane,
+// WPR wave64s per row, VPT * WPR * 512 >= len.  Prefer ~4 waves per SIMD over
+// the chip (1024 SIMDs) before spreading a row over more waves.
+bool pick_row_cfg(int64_t len, int64_t rows, int64_t forced_wpr, int& vpt, int& wpr) {
+    const int options[3] = {1, 2, 4};
+    int best = -1;
+    for (int w : options) {
+        if (forced_wpr && w != forced_wpr) continue;
+        int v = (int)cdiv(len, 512LL * w);
+        if (v < 1) v = 1;
+        if (v > 8) continue;
+        best = w;
+        if (forced_wpr || rows * w >= 4096) break;
+    }
+    if (best < 0) return false;
+    wpr = best;
+    vpt = (int)cdiv(len, 512LL * best);
+    if (vpt < 1) vpt = 1;
+    return true;
+}
+
+int64_t opt(const ee_engine* e, const char* key) {
+    auto it = e->options.find(key);
+    return it == e->options.end() ? 0 : it->second;
+}
+
+}  // namespace
+
+// ============================================================================ API
+
+EE_EXPORT const char* ee_last_error(void) { return g_err.c_str(); }
+EE_EXPORT int ee_abi_version(void) { return EE_ABI_VERSION; }
+
+EE_EXPORT int ee_engine_create(const char* lib_dir, ee_engine** out) {
+    if (out == nullptr) return fail(EE_ERR_INVALID_ARG, "out must not be NULL");
+    *out = nullptr;
+    if (lib_dir == nullptr) return fail(EE_ERR_INVALID_ARG, "lib_dir must not be NULL");
+    const std::string dir(lib_dir);
+    const std::string meta_path = dir + "/entropy_engine_meta.json";
+    std::string text;
+    int rc = read_file(meta_path, text, "meta JSON");
+    if (rc) return rc;
+    Json meta;
+    if ((rc = parse_json(text, meta_path, meta))) return rc;
+    const Json* fmt = meta.get("format");
+    if (fmt == nullptr || fmt->kind != Json::STR || fmt->str != "entropy-engine-meta/1")
+        return fail(EE_ERR_META, "Missing key: format (expected entropy-engine-meta/1) in " + meta_path);
+    const Json* cos = meta.get("code_objects");
+    const Json* kns = meta.get("kernels");
+    if (cos == nullptr || cos->kind != Json::OBJ) return fail(EE_ERR_META, "Missing key: code_objects (" + meta_path + ")");
+    if (kns == nullptr || kns->kind != Json::OBJ) return fail(EE_ERR_META, "Missing key: kernels (" + meta_path + ")");
+
+    // Validate the whole meta, then read every code object, before touching HIP.
+    struct KSpec { std::string co; int64_t block, lds; };
+    std::map<std::string, KSpec> specs;
+    for (const auto& kv : kns->obj) {
+        const Json* co = kv.second.get("code_object");
+        if (co == nullptr || co->kind != Json::STR)
+            return fail(EE_ERR_META, "Missing key: code_object for kernel " + kv.first + " (" + meta_path + ")");
+        if (cos->get(co->str) == nullptr)
+            return fail(EE_ERR_META, "kernel " + kv.first + " names unknown code object " + co->str);
+        KSpec s{co->str, 0, 0};
+        if ((rc = json_int(kv.second, "block", meta_path, s.block))) return rc;
+        if ((rc = json_int(kv.second, "lds", meta_path, s.lds))) return rc;
+        if (s.block <= 0 || s.block > 1024) return fail(EE_ERR_META, "bad block size for " + kv.first);
+        specs[kv.first] = s;
+    }
+
+    struct Pending { std::string file, bytes; };
+    std::map<std::string, Pending> blobs;
+    for (const auto& kv : cos->obj) {
+        const Json* file = kv.second.get("file");
+        if (file == nullptr || file->kind != Json::STR)
+            return fail(EE_ERR_META, "Missing key: file for code object " + kv.first + " (" + meta_path + ")");
+        Pending p;
+        p.file = dir + "/" + file->str;
+        if ((rc = read_file(p.file, p.bytes, "code object"))) return rc;
+        if (p.bytes.size() < 4 || std::memcmp(p.bytes.data(), "\x7f" "ELF", 4) != 0)
+            return fail(EE_ERR_IO, "Not an ELF code object: " + p.file);
+        blobs[kv.first] = std::move(p);
+    }
+    std::unique_ptr<ee_engine> e(new ee_engine());
+    auto cleanup = [&]() {
+        for (hipModule_t m : e->modules) (void)hipModuleUnload(m);
+        e->modules.clear();
+    };
+    if (hipGetDevice(&e->device) != hipSuccess) return fail(EE_ERR_HIP, "hipGetDevice failed (no GPU?)");
+    std::map<std::string, hipModule_t> loaded;
+    for (auto& kv : blobs) {
+        hipModule_t m = nullptr;
+        hipError_t err = hipModuleLoadData(&m, kv.second.bytes.data());
+        if (err != hipSuccess) {
+            cleanup();
+            return fail(EE_ERR_HIP, "hipModuleLoadData failed for " + kv.second.file + ": " + hipGetErrorString(err));
+        }
+        e->modules.push_back(m);
+        loaded[kv.first] = m;
+    }
+    for (auto& kv : specs) {
+        Kernel k;
+        hipError_t err = hipModuleGetFunction(&k.fn, loaded[kv.second.co], kv.first.c_str());
+        if (err != hipSuccess) {
+            cleanup();
+            return fail(EE_ERR_NOT_FOUND, "hipModuleGetFunction failed for '" + kv.first + "' in " +
+                                              blobs[kv.second.co].file + ": " + hipGetErrorString(err));
+        }
+        int max_threads = 0, lds = 0;
+        if (hipFuncGetAttribute(&max_threads, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, k.fn) != hipSuccess ||
+            hipFuncGetAttribute(&lds, HIP_FUNC_ATTRIBUTE_SHARED_SIZE_BYTES, k.fn) != hipSuccess) {
+            cleanup();
+            return fail(EE_ERR_HIP, "hipFuncGetAttribute failed for " + kv.first);
+        }
+        if (max_threads < kv.second.block || lds != kv.second.lds) {
+            cleanup();
+            return fail(EE_ERR_META, "meta of " + kv.first + " (block " + std::to_string(kv.second.block) +
+                                         ", lds " + std::to_string(kv.second.lds) + ") disagrees with the code object (max threads " +
+                                         std::to_string(max_threads) + ", lds " + std::to_string(lds) + ")");
+        }
+        k.block = (int)kv.second.block;
+        k.lds = lds;
+        e->kernels[kv.first] = k;
+    }
+    *out = e.release();
+    return EE_OK;
+}
+
+EE_EXPORT int ee_engine_destroy(ee_engine* eng) {
+    if (eng == nullptr) return EE_OK;
+    int rc = EE_OK;
+    for (hipModule_t m : eng->modules)
+        if (hipModuleUnload(m) != hipSuccess) rc = fail(EE_ERR_HIP, "hipModuleUnload failed");
+    delete eng;
+    return rc;
+}
+
+EE_EXPORT int ee_engine_set_option(ee_engine* eng, const char* key, int64_t value) {
+    if (eng == nullptr || key == nullptr) return fail(EE_ERR_INVALID_ARG, "engine and key must not be NULL");
+    const std::string k(key);
+    if (k == "se_wpr" || k == "quant_wpr") {
+        if (value != 0 && value != 1 && value != 2 && value != 4)
+            return fail(EE_ERR_INVALID_ARG, k + " must be 0 (auto), 1, 2 or 4");
+    } else {
+        return fail(EE_ERR_INVALID_ARG, "unknown option: " + k);
+    }
+    eng->options[k] = value;
+    return EE_OK;
+}
+
+EE_EXPORT int ee_engine_device(const ee_engine* eng) { return eng ? eng->device : -1; }
+
+EE_EXPORT int ee_softmax_entropy(ee_engine* eng, const void* x, void* p, float* h, int64_t rows, int32_t S,
+                                 int64_t ld_x, int64_t ld_p, int32_t causal, int32_t* tier, double tau_low,
+                                 double tau_high, ee_stream_t stream) {
+    if (eng == nullptr) return fail(EE_ERR_INVALID_ARG, "engine must not be NULL");
+    if (x == nullptr || h == nullptr) return fail(EE_ERR_INVALID_ARG, "x and h must not be NULL");
+    if (rows < 0 || S <= 0) return fail(EE_ERR_INVALID_ARG, "need rows >= 0 and S > 0");
+    if (ld_x < S || (p != nullptr && ld_p < S)) return fail(EE_ERR_INVALID_ARG, "row stride smaller than S");
+    if (causal != 0 && causal != 1) return fail(EE_ERR_INVALID_ARG, "causal must be 0 or 1");
+    if (!aligned(x, 2) || !aligned(p, 2) || !aligned(h, 4) || !aligned(tier, 4))
+        return fail(EE_ERR_INVALID_ARG, "misaligned pointer");
+    if (rows == 0) return EE_OK;
+    EeSoftmaxArgs a{(const uint16_t*)x, (uint16_t*)p, h, tier, rows, ld_x, ld_p, S, causal, tau_low, tau_high};
+    const bool vec_ok = aligned(x, 16) && aligned(p, 16) && ld_x % 8 == 0 && (p == nullptr || ld_p % 8 == 0);
+    int vpt = 0, wpr = 0;
+    if (vec_ok && pick_row_cfg(S, rows, opt(eng, "se_wpr"), vpt, wpr)) {
+        const std::string name = "eek_softmax_entropy_v" + std::to_string(vpt) + "_w" + std::to_string(wpr);
+        return launch(eng, name, cdiv(rows, 4 / wpr), 1, EE_BLOCK, a, stream);
+    }
+    return launch(eng, "eek_softmax_entropy_generic", cdiv(rows, 4), 1, EE_BLOCK, a, stream);
+}
+
+EE_EXPORT int ee_quant_act(ee_engine* eng, const void* x, int64_t M, int64_t K, int64_t ld_x, int32_t mode,
+                           void* codes, int64_t ld_c, float* scale, const int32_t* idx, const int32_t* counts,
+                           int32_t tier, ee_stream_t stream) {
+    if (eng == nullptr) return fail(EE_ERR_INVALID_ARG, "engine must not be NULL");
+    if (x == nullptr || codes == nullptr || scale == nullptr)
+        return fail(EE_ERR_INVALID_ARG, "x, codes and scale must not be NULL");
+    if (M < 0 || K <= 0) return fail(EE_ERR_INVALID_ARG, "need M >= 0 and K > 0");
+    if (ld_x < K || ld_c < K) return fail(EE_ERR_INVALID_ARG, "row stride smaller than K");
+    if (mode < EE_QUANT_I8_DISPATCH || mode > EE_QUANT_F8_ROW) return fail(EE_ERR_INVALID_ARG, "unknown quant mode");
+    if ((idx != nullptr) && counts == nullptr) return fail(EE_ERR_INVALID_ARG, "idx needs counts");
+    if (counts != nullptr && (tier < 0 || tier > 2)) return fail(EE_ERR_INVALID_ARG, "tier must be 0, 1 or 2");
+    if (!aligned(x, 2) || !aligned(scale, 4) || !aligned(idx, 4) || !aligned(counts, 4))
+        return fail(EE_ERR_INVALID_ARG, "misaligned pointer");
+    if (M == 0) return EE_OK;
+    EeQuantArgs a{(const uint16_t*)x, codes, scale, idx, counts, M, K, ld_x, ld_c, mode, counts ? tier : 0};
+    const bool vec_ok = aligned(x, 16) && aligned(codes, 8) && ld_x % 8 == 0 && ld_c % 8 == 0;
+    int vpt = 0, wpr = 0;
+    if (vec_ok && pick_row_cfg(K, M, opt(eng, "quant_wpr"), vpt, wpr)) {
+        const std::string name = "eek_quant_v" + std::to_string(vpt) + "_w" + std::to_string(wpr);
+        return launch(eng, name, cdiv(M, 4 / wpr), 1, EE_BLOCK, a, stream);
+    }
+    return launch(eng, "eek_quant_generic", cdiv(M, 4), 1, EE_BLOCK, a, stream);
+}
+
+EE_EXPORT int ee_quant_weight_i8(ee_engine* eng, const void* w, int64_t N, int64_t K, int64_t ld_w,
+                                 int8_t* codes_nk, int64_t ld_c, float* scale, ee_stream_t stream) {
+    // Per output channel n: the f32-scale, round-half-even, clamp(+-127) quantiser.
+    return ee_quant_act(eng, w, N, K, ld_w, EE_QUANT_I8_ENGINE, codes_nk, ld_c, scale, nullptr, nullptr, 0, stream);
+}
+
+EE_EXPORT int ee_transpose_i8(ee_engine* eng, const int8_t* src, int64_t R, int64_t C, int64_t ld_src,
+                              int8_t* dst, int64_t ld_dst, ee_stream_t stream) {
+    if (eng == nullptr || src == nullptr || dst == nullptr) return fail(EE_ERR_INVALID_ARG, "NULL argument");
+    if (R < 0 || C < 0 || ld_src < C || ld_dst < R) return fail(EE_ERR_INVALID_ARG, "bad shape or stride");
+    if (cdiv(R, 64) > 65535) return fail(EE_ERR_UNSUPPORTED, "too many rows for ee_transpose_i8");
+    EeWeightArgs a{src, dst, nullptr, nullptr, R, C, ld_src, ld_dst};
+    return launch(eng, "eek_transpose_i8", cdiv(C, 64), cdiv(R, 64), EE_BLOCK, a, stream);
+}
+
+EE_EXPORT int ee_pack_b_f8(ee_engine* eng, const int8_t* codes_nk, int64_t N, int64_t K, int64_t ld_src,
+                           uint8_t* dst, int64_t ld_dst, ee_stream_t stream) {
+    if (eng == nullptr || codes_nk == nullptr || dst == nullptr) return fail(EE_ERR_INVALID_ARG, "NULL argument");
+    if (N < 0 || K < 0 || ld_src < K || ld_dst < K) return fail(EE_ERR_INVALID_ARG, "bad shape or stride");
+    EeWeightArgs a{codes_nk, dst, nullptr, nullptr, N, K, ld_src, ld_dst};
+    int64_t g = cdiv(N * K, EE_BLOCK);
+    return launch(eng, "eek_pack_b_f8", g > 16384 ? 16384 : g, 1, EE_BLOCK, a, stream);
+}
+
+EE_EXPORT int ee_pack_b_f16(ee_engine* eng, const int8_t* codes_nk, const float* scale, int64_t N, int64_t K,
+                            int64_t ld_src, void* dst, int64_t ld_dst, ee_stream_t stream) {
+    if (eng == nullptr || codes_nk == nullptr || scale == nullptr || dst == nullptr)
+        return fail(EE_ERR_INVALID_ARG, "NULL argument");
+    if (N < 0 || K < 0 || ld_src < K || ld_dst < K) return fail(EE_ERR_INVALID_ARG, "bad shape or stride");
+    if (!aligned(dst, 2) || !aligned(scale, 4)) return fail(EE_ERR_INVALID_ARG, "misaligned pointer");
+    EeWeightArgs a{codes_nk, dst, nullptr, scale, N, K, ld_src, ld_dst};
+    int64_t g = cdiv(N * K, EE_BLOCK);
+    return launch(eng, "eek_pack_b_f16", g > 16384 ? 16384 : g, 1, EE_BLOCK, a, stream);
+}
+
+EE_EXPORT int ee_gemm(ee_engine* eng, int32_t kind, const void* a, int64_t lda, const void* b_nk, int64_t ldb,
+                      void* c, int64_t ldc, const float* a_scale, const float* b_scale, int32_t M, int32_t N,
+                      int32_t K, const int32_t* a_idx, const int32_t* c_idx, const int32_t* counts, int32_t tier,
+                      int32_t* acc_out, ee_stream_t stream) {
+    if (eng == nullptr) return fail(EE_ERR_INVALID_ARG, "engine must not be NULL");
+    if (kind < EE_GEMM_I8 || kind > EE_GEMM_F16) return fail(EE_ERR_INVALID_ARG, "unknown GEMM kind");
+    if (a == nullptr || b_nk == nullptr || c == nullptr) return fail(EE_ERR_INVALID_ARG, "a, b and c must not be NULL");
+    if (kind != EE_GEMM_F16 && (a_scale == nullptr || b_scale == nullptr))
+        return fail(EE_ERR_INVALID_ARG, "a_scale and b_scale are required for the INT8 and FP8 tiers");
+    if (acc_out != nullptr && kind != EE_GEMM_I8) return fail(EE_ERR_INVALID_ARG, "acc_out is INT8 only");
+    if (M < 0 || N <= 0 || K <= 0) return fail(EE_ERR_INVALID_ARG, "need M >= 0, N > 0, K > 0");
+    const int64_t esz = (kind == EE_GEMM_F16) ? 2 : 1;
+    if (lda < K || ldb < K || ldc < N) return fail(EE_ERR_INVALID_ARG, "leading dimension smaller than the row");
+    if ((K * esz) % 16 != 0) return fail(EE_ERR_UNSUPPORTED, "K * element size must be a multiple of 16 bytes");
+    if ((lda * esz) % 16 != 0 || (ldb * esz) % 16 != 0)
+        return fail(EE_ERR_UNSUPPORTED, "lda and ldb must be multiples of 16 bytes");
+    if (N % 4 != 0 || ldc % 4 != 0) return fail(EE_ERR_UNSUPPORTED, "N and ldc must be multiples of 4");
+    if (!aligned(a, 16) || !aligned(b_nk, 16) || !aligned(c, 8) || !aligned(acc_out, 16) ||
+        !aligned(a_scale, 4) || !aligned(b_scale, 16) || !aligned(a_idx, 4) || !aligned(c_idx, 4) ||
+        !aligned(counts, 4))
+        return fail(EE_ERR_INVALID_ARG,
+                    "misaligned pointer (a, b, b_scale, acc: 16 B; c: 8 B; a_scale, indices: 4 B)");
+    if ((a_idx != nullptr || c_idx != nullptr) && counts == nullptr)
+        return fail(EE_ERR_INVALID_ARG, "a_idx / c_idx need counts");
+    if (counts != nullptr && (tier < 0 || tier > 2)) return fail(EE_ERR_INVALID_ARG, "tier must be 0, 1 or 2");
+    if (M == 0) return EE_OK;
+    EeGemmArgs g{a, b_nk, (uint16_t*)c, acc_out, a_scale, b_scale, a_idx, c_idx, counts, lda, ldb, ldc,
+                 M, N, K, counts ? tier : 0};
+    // The pipelined kernels stream whole 128-byte K stages; other K take the fallback.
+    static const char* names[3] = {"eek_gemm_i8", "eek_gemm_f8", "eek_gemm_f16"};
+    const std::string name = std::string(names[kind]) + (((K * esz) % 128 == 0) ? "" : "_generic");
+    return launch(eng, name, cdiv(M, 128) * cdiv(N, 128), 1, EE_BLOCK, g, stream);
+}
+
+EE_EXPORT int ee_route(ee_engine* eng, const float* h, int64_t rows, double tau_low, double tau_high,
+                       int32_t* tier, int32_t* idx, int32_t* counts, ee_stream_t stream) {
+    if (eng == nullptr || h == nullptr || tier == nullptr || idx == nullptr || counts == nullptr)
+        return fail(EE_ERR_INVALID_ARG, "NULL argument");
+    if (rows < 0 || rows > 0x7fffffff) return fail(EE_ERR_INVALID_ARG, "rows out of range");
+    if (!aligned(h, 4) || !aligned(tier, 4) || !aligned(idx, 4) || !aligned(counts, 4))
+        return fail(EE_ERR_INVALID_ARG, "misaligned pointer");
+    EeRouteArgs a{h, tier, idx, counts, rows, tau_low, tau_high};
+    return launch(eng, "eek_route", 1, 1, 1024, a, stream);
+}
+
+EE_EXPORT int ee_row_copy(ee_engine* eng, const void* src, int64_t ld_src_bytes, void* dst, int64_t ld_dst_bytes,
+                          int64_t rows, int64_t row_bytes, const int32_t* idx, const int32_t* counts, int32_t tier,
+                          int32_t scatter, ee_stream_t stream) {
+    if (eng == nullptr || src == nullptr || dst == nullptr) return fail(EE_ERR_INVALID_ARG, "NULL argument");
+    if (rows < 0 || row_bytes < 0 || ld_src_bytes < row_bytes || ld_dst_bytes < row_bytes)
+        return fail(EE_ERR_INVALID_ARG, "bad shape or stride");
+    if (scatter != 0 && scatter != 1) return fail(EE_ERR_INVALID_ARG, "scatter must be 0 or 1");
+    if (counts != nullptr && (tier < 0 || tier > 2)) return fail(EE_ERR_INVALID_ARG, "tier must be 0, 1 or 2");
+    if (!aligned(idx, 4) || !aligned(counts, 4)) return fail(EE_ERR_INVALID_ARG, "misaligned pointer");
+    if (rows == 0 || row_bytes == 0) return EE_OK;
+    EeRowCopyArgs a{(const uint8_t*)src, (uint8_t*)dst, idx, counts, rows, row_bytes, ld_src_bytes, ld_dst_bytes,
+                    counts ? tier : 0, scatter};
+    return launch(eng, "eek_row_copy", cdiv(rows, 4), 1, EE_BLOCK, a, stream);
+}
+
+EE_EXPORT int ee_routed_linear(ee_engine* eng, const void* x, int64_t ld_x, int32_t M, int32_t K, int32_t N,
+                               const int32_t* idx, const int32_t* counts, const int8_t* b_i8, const uint8_t* b_f8,
+                               const void* b_f16, const float* b_scale, void* c, int64_t ldc, void* ws_codes,
+                               float* ws_scale, ee_stream_t stream) {
+    if (eng == nullptr || x == nullptr || idx == nullptr || counts == nullptr || b_i8 == nullptr ||
+        b_f8 == nullptr || b_f16 == nullptr || b_scale == nullptr || c == nullptr || ws_codes == nullptr ||
+        ws_scale == nullptr)
+        return fail(EE_ERR_INVALID_ARG, "NULL argument");
+    if (M < 0 || K <= 0 || N <= 0 || ld_x < K || ldc < N) return fail(EE_ERR_INVALID_ARG, "bad shape or stride");
+    // The GEMM contracts, checked here so that no launch of the sequence can fail half way.
+    if (K % 16 != 0 || (ld_x * 2) % 16 != 0 || N % 4 != 0 || ldc % 4 != 0)
+        return fail(EE_ERR_UNSUPPORTED, "routed linear needs K % 16 == 0, ld_x % 8 == 0, N % 4 == 0, ldc % 4 == 0");
+    if (!aligned(x, 16) || !aligned(b_i8, 16) || !aligned(b_f8, 16) || !aligned(b_f16, 16) || !aligned(c, 8) ||
+        !aligned(ws_codes, 16) || !aligned(ws_scale, 4) || !aligned(b_scale, 16) || !aligned(idx, 4) ||
+        !aligned(counts, 4))
+        return fail(EE_ERR_INVALID_ARG, "misaligned pointer");
+    if (M == 0) return EE_OK;
+    int rc;
+    // INT8 rows: quantise into partition slots, GEMM, scatter.
+    if ((rc = ee_quant_act(eng, x, M, K, ld_x, EE_QUANT_I8_DISPATCH, ws_codes, K, ws_scale, idx, counts,
+                           EE_TIER_INT8, stream)))
+        return rc;
+    if ((rc = ee_gemm(eng, EE_GEMM_I8, ws_codes, K, b_i8, K, c, ldc, ws_scale, b_scale, M, N, K, nullptr, idx,
+                      counts, EE_TIER_INT8, nullptr, stream)))
+        return rc;
+    // FP8 rows.
+    if ((rc = ee_quant_act(eng, x, M, K, ld_x, EE_QUANT_F8_ROW, ws_codes, K, ws_scale, idx, counts, EE_TIER_FP8,
+                           stream)))
+        return rc;
+    if ((rc = ee_gemm(eng, EE_GEMM_F8, ws_codes, K, b_f8, K, c, ldc, ws_scale, b_scale, M, N, K, nullptr, idx,
+                      counts, EE_TIER_FP8, nullptr, stream)))
+        return rc;
+    // FP16 (W8A16) rows: gather straight from x.
+    return ee_gemm(eng, EE_GEMM_F16, x, ld_x, b_f16, K, c, ldc, nullptr, nullptr, M, N, K, idx, idx, counts,
+                   EE_TIER_FP16, nullptr, stream);
+}
+
+// ------------------------------------------------------------ CubinEngine counterpart
+
+EE_EXPORT int ee_module_engine_create(const char* code_object_path, const char* func_name, int32_t shared_mem,
+                                      int32_t num_warps, int32_t block_m, int32_t block_n, ee_module_engine** out) {
+    if (out == nullptr) return fail(EE_ERR_INVALID_ARG, "out must not be NULL");
+    *out = nullptr;
+    if (code_object_path == nullptr || func_name == nullptr)
+        return fail(EE_ERR_INVALID_ARG, "code_object_path and func_name must not be NULL");
+    if (num_warps <= 0 || num_warps * 64 > 1024) return fail(EE_ERR_INVALID_ARG, "num_warps must be in 1..16 (wave64)");
+    if (block_m <= 0 || block_n <= 0 || shared_mem < 0) return fail(EE_ERR_INVALID_ARG, "bad tile or shared size");
+    std::string bytes;
+    int rc = read_file(code_object_path, bytes, "code object file");
+    if (rc) return rc;
+    if (bytes.size() < 4 || std::memcmp(bytes.data(), "\x7f" "ELF", 4) != 0)
+        return fail(EE_ERR_IO, std::string("Not an ELF code object: ") + code_object_path);
+    std::unique_ptr<ee_module_engine> me(new ee_module_engine());
+    EE_HIP(hipGetDevice(&me->device), "hipGetDevice");
+    EE_HIP(hipModuleLoadData(&me->module, bytes.data()), std::string("hipModuleLoadData failed for ") + code_object_path);
+    hipError_t err = hipModuleGetFunction(&me->fn, me->module, func_name);
+    if (err != hipSuccess) {
+        (void)hipModuleUnload(me->module);
+        return fail(EE_ERR_NOT_FOUND, std::string("hipModuleGetFunction failed for '") + func_name + "' in " +
+                                          code_object_path + ": " + hipGetErrorString(err));
+    }
+    int max_threads = 0, lds = 0;
+    if (hipFuncGetAttribute(&max_threads, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, me->fn) != hipSuccess ||
+        hipFuncGetAttribute(&lds, HIP_FUNC_ATTRIBUTE_SHARED_SIZE_BYTES, me->fn) != hipSuccess) {
+        (void)hipModuleUnload(me->module);
+        return fail(EE_ERR_HIP, "hipFuncGetAttribute failed");
+    }
+    // The GEMM kernels assume exactly their 256-thread workgroup and 128x128 tile.
+    if (num_warps * 64 != max_threads || block_m != 128 || block_n != 128) {
+        (void)hipModuleUnload(me->module);
+        return fail(EE_ERR_META, std::string("launch config (num_warps ") + std::to_string(num_warps) +
+                                     ", BLOCK_M " + std::to_string(block_m) + ", BLOCK_N " + std::to_string(block_n) +
+                                     ") does not match '" + func_name + "' (" + std::to_string(max_threads / 64) +
+                                     " wave64s, 128x128 tile)");
+    }
+    me->func = func_name;
+    me->shared_mem = shared_mem;
+    me->num_warps = num_warps;
+    me->block_m = block_m;
+    me->block_n = block_n;
+    me->static_lds = lds;
+    *out = me.release();
+    return EE_OK;
+}
+
+EE_EXPORT int ee_module_engine_from_metadata(const char* code_object_path, const char* meta_json_path,
+                                             const char* func_name, ee_module_engine** out) {
+    if (out == nullptr) return fail(EE_ERR_INVALID_ARG, "out must not be NULL");
+    *out = nullptr;
+    if (meta_json_path == nullptr) return fail(EE_ERR_INVALID_ARG, "meta_json_path must not be NULL");
+    std::string text;
+    int rc = read_file(meta_json_path, text, "meta JSON");
+    if (rc) return rc;
+    Json meta;
+    if ((rc = parse_json(text, meta_json_path, meta))) return rc;
+    int64_t shared = 0, warps = 0, bm = 0, bn = 0;
+    if ((rc = json_int(meta, "shared", meta_json_path, shared))) return rc;
+    if ((rc = json_int(meta, "num_warps", meta_json_path, warps))) return rc;
+    if ((rc = json_int(meta, "BLOCK_M", meta_json_path, bm))) return rc;
+    if ((rc = json_int(meta, "BLOCK_N", meta_json_path, bn))) return rc;
+    return ee_module_engine_create(code_object_path, func_name, (int32_t)shared, (int32_t)warps, (int32_t)bm,
+                                   (int32_t)bn, out);
+}
+
+EE_EXPORT int ee_module_engine_info(const ee_module_engine* me, int32_t* shared_mem, int32_t* num_warps,
+                                    int32_t* block_m, int32_t* block_n) {
+    if (me == nullptr) return fail(EE_ERR_INVALID_ARG, "engine must not be NULL");
+    if (shared_mem) *shared_mem = me->shared_mem;
+    if (num_warps) *num_warps = me->num_warps;
+    if (block_m) *block_m = me->block_m;
+    if (block_n) *block_n = me->block_n;
+    return EE_OK;
+}
+
+EE_EXPORT int ee_module_engine_forward(ee_module_engine* me, const int8_t* a, int64_t lda, const int8_t* b_nk,
+                                       int64_t ldb, void* c, int64_t ldc, const float* a_scale, const float* b_scale,
+                                       int32_t M, int32_t N, int32_t K, ee_stream_t stream) {
+    if (me == nullptr) return fail(EE_ERR_INVALID_ARG, "engine must not be NULL");
+    if (a == nullptr || b_nk == nullptr || c == nullptr || a_scale == nullptr || b_scale == nullptr)
+        return fail(EE_ERR_INVALID_ARG, "NULL argument");
+    if (M < 0 || N <= 0 || K <= 0 || lda < K || ldb < K || ldc < N)
+        return fail(EE_ERR_INVALID_ARG, "bad shape or stride");
+    if (K % 16 != 0 || lda % 16 != 0 || ldb % 16 != 0 || N % 4 != 0 || ldc % 4 != 0)
+        return fail(EE_ERR_UNSUPPORTED, "need K, lda, ldb multiples of 16 and N, ldc multiples of 4");
+    const bool generic = me->func.size() > 8 && me->func.compare(me->func.size() - 8, 8, "_generic") == 0;
+    if (!generic && K % 128 != 0)
+        return fail(EE_ERR_UNSUPPORTED, "'" + me->func + "' streams 128-byte K stages: K must be a multiple of 128 "
+                                        "(the *_generic kernel takes any multiple of 16)");
+    if (!aligned(a, 16) || !aligned(b_nk, 16) || !aligned(c, 8) || !aligned(a_scale, 4) || !aligned(b_scale, 16))
+        return fail(EE_ERR_INVALID_ARG, "misaligned pointer (a, b, b_scale: 16 B; c: 8 B; a_scale: 4 B)");
+    if (M == 0) return EE_OK;
+    int rc = check_device(me->device);
+    if (rc) return rc;
+    EeGemmArgs g{a, b_nk, (uint16_t*)c, nullptr, a_scale, b_scale, nullptr, nullptr, nullptr, lda, ldb, ldc,
+                 M, N, K, 0};
+    const int64_t grid = cdiv(M, me->block_m) * cdiv(N, me->block_n);
+    const int dyn = me->shared_mem > me->static_lds ? me->shared_mem - me->static_lds : 0;
+    void* params[] = {&g};
+    EE_HIP(hipModuleLaunchKernel(me->fn, (unsigned)grid, 1, 1, (unsigned)(me->num_warps * 64), 1, 1, (unsigned)dyn,
+                                 (hipStream_t)stream, params, nullptr),
+           "hipModuleLaunchKernel");
+    return EE_OK;
+}
+
+EE_EXPORT int ee_module_engine_destroy(ee_module_engine* me) {
+    if (me == nullptr) return EE_OK;
+    int rc = EE_OK;
+    if (me->module != nullptr && hipModuleUnload(me->module) != hipSuccess) rc = fail(EE_ERR_HIP, "hipModuleUnload failed");
+    delete me;
+    return rc;
+}

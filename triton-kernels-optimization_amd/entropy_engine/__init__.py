@@ -1,0 +1,21 @@
+"""entropy_engine -- the entropy-gated precision path on MI355X (gfx950).
+
+Row softmax + Shannon entropy, tau_low/tau_high routing, and INT8 / FP8-e4m3
+/ W8A16 GEMMs as hand-written CDNA4 HIP kernels, loaded from gfx950 code
+objects by a C-ABI launcher (include/entropy_engine.h) and driven from
+PyTorch-ROCm.  The Python API mirrors the reference's kernels.py and
+dispatch.py (IqtedarU/triton-kernels-optimization, entropy-engine/python).
+"""
+from .dispatch import (EntropyDispatchedLinear, PipelinedEntropyDispatcher, PrecisionTier, RowEntropyRouter,
+                       quantize_weights_int8, tier_of)
+from .engine import CubinEngine, HsacoEngine
+from .kernels import (PackedWeight, fused_softmax_entropy, gemm, prepare_weight, quantize_activations, route,
+                      routed_linear, row_copy, softmax_entropy, triton_fp8_gemm, triton_fp16_gemm,
+                      triton_int8_gemm)
+
+__all__ = [
+    "EntropyDispatchedLinear", "PipelinedEntropyDispatcher", "PrecisionTier", "RowEntropyRouter",
+    "quantize_weights_int8", "tier_of", "CubinEngine", "HsacoEngine", "PackedWeight", "fused_softmax_entropy",
+    "gemm", "prepare_weight", "quantize_activations", "route", "routed_linear", "row_copy", "softmax_entropy",
+    "triton_fp8_gemm", "triton_fp16_gemm", "triton_int8_gemm",
+]

@@ -1,0 +1,136 @@
+"""ctypes binding of libentropy_engine.so (include/entropy_engine.h).
+
+The library is loaded after torch so that it binds to the HIP runtime torch
+already has in the process (both carry the soname libamdhip64.so.7): one
+runtime, so torch's streams and device pointers are valid handles here.
+There is no CPU fallback: without the built library or without a GPU every
+entry point raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch
+
+PKG_ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_DIR = os.environ.get("EE_LIB_DIR", os.path.join(PKG_ROOT, "lib"))
+LIB_PATH = os.path.join(LIB_DIR, "libentropy_engine.so")
+
+# status codes (ee_status)
+EE_OK = 0
+EE_ERR_INVALID_ARG = -1
+EE_ERR_IO = -2
+EE_ERR_META = -3
+EE_ERR_HIP = -4
+EE_ERR_UNSUPPORTED = -5
+EE_ERR_NOT_FOUND = -6
+STATUS_NAMES = {0: "EE_OK", -1: "EE_ERR_INVALID_ARG", -2: "EE_ERR_IO", -3: "EE_ERR_META", -4: "EE_ERR_HIP",
+                -5: "EE_ERR_UNSUPPORTED", -6: "EE_ERR_NOT_FOUND"}
+
+# quantiser modes / GEMM kinds / tiers
+EE_QUANT_I8_DISPATCH, EE_QUANT_I8_ENGINE, EE_QUANT_F8_ROW = 0, 1, 2
+EE_GEMM_I8, EE_GEMM_F8, EE_GEMM_F16 = 0, 1, 2
+
+_p = ctypes.c_void_p
+_i32 = ctypes.c_int32
+_i64 = ctypes.c_int64
+_f64 = ctypes.c_double
+
+SIGNATURES = {
+    "ee_last_error": ([], ctypes.c_char_p),
+    "ee_abi_version": ([], ctypes.c_int),
+    "ee_engine_create": ([ctypes.c_char_p, ctypes.POINTER(_p)], ctypes.c_int),
+    "ee_engine_destroy": ([_p], ctypes.c_int),
+    "ee_engine_set_option": ([_p, ctypes.c_char_p, _i64], ctypes.c_int),
+    "ee_engine_device": ([_p], ctypes.c_int),
+    "ee_softmax_entropy": ([_p, _p, _p, _p, _i64, _i32, _i64, _i64, _i32, _p, _f64, _f64, _p], ctypes.c_int),
+    "ee_quant_act": ([_p, _p, _i64, _i64, _i64, _i32, _p, _i64, _p, _p, _p, _i32, _p], ctypes.c_int),
+    "ee_quant_weight_i8": ([_p, _p, _i64, _i64, _i64, _p, _i64, _p, _p], ctypes.c_int),
+    "ee_transpose_i8": ([_p, _p, _i64, _i64, _i64, _p, _i64, _p], ctypes.c_int),
+    "ee_pack_b_f8": ([_p, _p, _i64, _i64, _i64, _p, _i64, _p], ctypes.c_int),
+    "ee_pack_b_f16": ([_p, _p, _p, _i64, _i64, _i64, _p, _i64, _p], ctypes.c_int),
+    "ee_gemm": ([_p, _i32, _p, _i64, _p, _i64, _p, _i64, _p, _p, _i32, _i32, _i32, _p, _p, _p, _i32, _p, _p],
+                ctypes.c_int),
+    "ee_route": ([_p, _p, _i64, _f64, _f64, _p, _p, _p, _p], ctypes.c_int),
+    "ee_row_copy": ([_p, _p, _i64, _p, _i64, _i64, _i64, _p, _p, _i32, _i32, _p], ctypes.c_int),
+    "ee_routed_linear": ([_p, _p, _i64, _i32, _i32, _i32, _p, _p, _p, _p, _p, _p, _p, _i64, _p, _p, _p],
+                         ctypes.c_int),
+    "ee_module_engine_create": ([ctypes.c_char_p, ctypes.c_char_p, _i32, _i32, _i32, _i32, ctypes.POINTER(_p)],
+                                ctypes.c_int),
+    "ee_module_engine_from_metadata": ([ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, ctypes.POINTER(_p)],
+                                       ctypes.c_int),
+    "ee_module_engine_info": ([_p, ctypes.POINTER(_i32), ctypes.POINTER(_i32), ctypes.POINTER(_i32),
+                               ctypes.POINTER(_i32)], ctypes.c_int),
+    "ee_module_engine_forward": ([_p, _p, _i64, _p, _i64, _p, _i64, _p, _p, _i32, _i32, _i32, _p], ctypes.c_int),
+    "ee_module_engine_destroy": ([_p], ctypes.c_int),
+}
+
+_lib = None
+_lock = threading.Lock()
+_engines: dict[int, int] = {}
+
+
+class EngineError(RuntimeError):
+    """A C-ABI call returned a non-zero ee_status."""
+
+    def __init__(self, status: int, message: str):
+        super().__init__(message)
+        self.status = status
+        self.status_name = STATUS_NAMES.get(status, str(status))
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded C-ABI library (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        with _lock:
+            if _lib is None:
+                if not os.path.exists(LIB_PATH):
+                    raise ImportError(
+                        f"entropy_engine: native library missing at {LIB_PATH}; "
+                        "build it with `python triton-kernels-optimization_amd/build.py`")
+                L = ctypes.CDLL(LIB_PATH)
+                for name, (args, res) in SIGNATURES.items():
+                    fn = getattr(L, name)
+                    fn.argtypes = args
+                    fn.restype = res
+                _lib = L
+    return _lib
+
+
+def check(rc: int) -> None:
+    if rc != EE_OK:
+        msg = lib().ee_last_error()
+        raise EngineError(rc, (msg.decode() if msg else "") or STATUS_NAMES.get(rc, str(rc)))
+
+
+def engine(device=None) -> int:
+    """Per-device engine handle (code objects loaded once per device)."""
+    if not torch.cuda.is_available():
+        raise RuntimeError("entropy_engine needs a ROCm GPU (gfx950); none is visible")
+    dev = torch.cuda.current_device() if device is None else torch.device(device).index
+    if dev is None:
+        dev = torch.cuda.current_device()
+    h = _engines.get(dev)
+    if h is None:
+        with _lock:
+            h = _engines.get(dev)
+            if h is None:
+                L = lib()
+                out = _p()
+                with torch.cuda.device(dev):
+                    torch.cuda.init()
+                    check(L.ee_engine_create(LIB_DIR.encode(), ctypes.byref(out)))
+                h = out.value
+                _engines[dev] = h
+    return h
+
+
+def stream_handle(device=None) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def ptr(t) -> int | None:
+    return None if t is None else t.data_ptr()

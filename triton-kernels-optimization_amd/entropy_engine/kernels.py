@@ -1,0 +1,343 @@
+"""Host-side launchers of the entropy-gated path on the gfx950 kernels.
+
+Drop-in counterparts of EE/python/kernels.py (EE = "entropy-engine (1)/
+entropy-engine" in the reference): the same function names, argument order,
+dtypes and return values, running hand-written HIP kernels through the C ABI
+(no Triton).  Every call launches on torch's current stream of the tensors'
+device.
+
+  triton_int8_gemm(a, b_int8, b_scale)   EE/python/kernels.py:330-351
+  triton_fp8_gemm(a, b_int8, b_scale)    EE/python/kernels.py:354-373
+  triton_fp16_gemm(a, b_int8, b_scale)   EE/python/kernels.py:380-409
+  fused_softmax_entropy(logits, causal)  EE/python/kernels.py:416-453
+
+b_int8 is the reference's weight buffer, int8 [K, N] (N contiguous).  The
+MFMA kernels read weights K-contiguous, as [N, K]; the first call with a
+given weight tensor derives the per-tier operands on the GPU (transpose, e4m3
+codes, W8A16 fp16 weights -- all bit-exact functions of the int8 codes) and
+caches them until that tensor is freed or modified in place.
+"""
+from __future__ import annotations
+
+import weakref
+
+import torch
+
+from . import _lib
+from ._lib import check, engine, ptr, stream_handle
+
+__all__ = [
+    "triton_int8_gemm", "triton_fp8_gemm", "triton_fp16_gemm", "fused_softmax_entropy",
+    "softmax_entropy", "quantize_activations", "gemm", "route", "row_copy", "routed_linear",
+    "prepare_weight", "PackedWeight", "quantize_weight_codes",
+]
+
+
+def _require_cuda(*ts):
+    dev = None
+    for t in ts:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise ValueError("entropy_engine kernels take GPU tensors (got a tensor on %s)" % t.device)
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise ValueError(f"tensors on different devices: {dev} and {t.device}")
+    return dev
+
+
+def _rowmajor(t: torch.Tensor, name: str) -> int:
+    """Row stride of a 2-D tensor with unit column stride."""
+    if t.dim() != 2:
+        raise ValueError(f"{name} must be 2-D, got shape {tuple(t.shape)}")
+    if t.stride(1) != 1 and t.size(1) > 1:
+        raise ValueError(f"{name} must be contiguous along its last dimension")
+    return t.stride(0) if t.size(0) > 1 else max(t.stride(0), t.size(1))
+
+
+# ---------------------------------------------------------------- softmax + entropy
+
+def softmax_entropy(x: torch.Tensor, causal: bool = False, probs: bool = True,
+                    thresholds: tuple[float, float] | None = None, out_probs: torch.Tensor | None = None):
+    """Row softmax + Shannon entropy of fp16 rows x [R, S].
+
+    Returns (probs fp16 [R, S] or None, entropy f32 [R], tier int32 [R] or
+    None).  With `thresholds=(tau_low, tau_high)` the per-row precision tier
+    is produced in the same pass.  causal: column c of row r is kept iff
+    c <= r % S (the reference's [B, H, S, S] rows)."""
+    dev = _require_cuda(x, out_probs)
+    if x.dtype != torch.float16:
+        raise TypeError("logits must be float16")
+    ldx = _rowmajor(x, "logits")
+    R, S = x.shape
+    p = None
+    if probs:
+        p = out_probs if out_probs is not None else torch.empty((R, S), dtype=torch.float16, device=dev)
+        if p.shape != (R, S) or p.dtype != torch.float16:
+            raise ValueError("out_probs must be float16 of the logits' shape")
+    ldp = _rowmajor(p, "probs") if p is not None else S
+    h = torch.empty(R, dtype=torch.float32, device=dev)
+    tier = torch.empty(R, dtype=torch.int32, device=dev) if thresholds is not None else None
+    tl, th = thresholds if thresholds is not None else (0.0, 0.0)
+    with torch.cuda.device(dev):
+        check(_lib.lib().ee_softmax_entropy(engine(), ptr(x), ptr(p), ptr(h), R, S, ldx, ldp, int(bool(causal)),
+                                            ptr(tier), float(tl), float(th), stream_handle()))
+    return p, h, tier
+
+
+def fused_softmax_entropy(logits: torch.Tensor, causal: bool = True) -> tuple[torch.Tensor, torch.Tensor]:
+    """EE/python/kernels.py:416-453: logits fp16 [B, H, S, S] -> (probs fp16
+    [B, H, S, S], mean row entropy per batch f32 [B])."""
+    B, H, S, S2 = logits.shape
+    assert S == S2
+    if not logits.is_contiguous():
+        logits = logits.contiguous()
+    probs = torch.empty_like(logits, dtype=torch.float16)
+    _, row_entropies, _ = softmax_entropy(logits.view(B * H * S, S), causal=causal, probs=True,
+                                          out_probs=probs.view(B * H * S, S))
+    per_batch_entropy = row_entropies.reshape(B, H, S).mean(dim=(1, 2))
+    return probs, per_batch_entropy
+
+
+# ---------------------------------------------------------------- quantisers
+
+_MODES = {"dispatcher": _lib.EE_QUANT_I8_DISPATCH, "engine": _lib.EE_QUANT_I8_ENGINE, "fp8": _lib.EE_QUANT_F8_ROW}
+
+
+def quantize_activations(a: torch.Tensor, mode: str = "dispatcher", idx=None, counts=None, tier: int = 0,
+                         out_codes=None, out_scale=None):
+    """Per-row activation codes + f32 scales.
+
+    mode "dispatcher": int8, EE/python/kernels.py:336-338 (fp16 scale, truncation)
+    mode "engine":     int8, EE/test_cubin.py:93-103 (f32 scale, round, clamp)
+    mode "fp8":        e4m3 bytes (uint8), EE/python/kernels.py:361,144,159-160
+    Routed form (idx, counts, tier): rows idx[off + r] of `a` are quantised
+    into slot off + r of the outputs (off = rows of the lower tiers)."""
+    dev = _require_cuda(a, idx, counts, out_codes, out_scale)
+    if a.dtype != torch.float16:
+        raise TypeError("activations must be float16")
+    lda = _rowmajor(a, "a")
+    M, K = a.shape
+    code_dtype = torch.uint8 if mode == "fp8" else torch.int8
+    codes = out_codes if out_codes is not None else torch.empty((M, K), dtype=code_dtype, device=dev)
+    scale = out_scale if out_scale is not None else torch.empty(M, dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        check(_lib.lib().ee_quant_act(engine(), ptr(a), M, K, lda, _MODES[mode], ptr(codes), _rowmajor(codes, "codes"),
+                                      ptr(scale), ptr(idx), ptr(counts), int(tier), stream_handle()))
+    return codes, scale
+
+
+def quantize_weight_codes(weight: torch.Tensor):
+    """nn.Linear weight fp16 [N, K] -> (int8 codes [N, K], f32 scale [N]),
+    the per-channel quantiser of EE/python/dispatch.py:43-48 in operand order."""
+    dev = _require_cuda(weight)
+    w = weight.detach()
+    if w.dtype != torch.float16:
+        w = w.to(torch.float16)
+    w = w.contiguous()
+    N, K = w.shape
+    codes = torch.empty((N, K), dtype=torch.int8, device=dev)
+    scale = torch.empty(N, dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        check(_lib.lib().ee_quant_weight_i8(engine(), ptr(w), N, K, K, ptr(codes), K, ptr(scale), stream_handle()))
+    return codes, scale
+
+
+def transpose_i8(src: torch.Tensor) -> torch.Tensor:
+    dev = _require_cuda(src)
+    if src.dtype not in (torch.int8, torch.uint8):
+        raise TypeError("transpose_i8 takes int8/uint8")
+    R, C = src.shape
+    dst = torch.empty((C, R), dtype=src.dtype, device=dev)
+    with torch.cuda.device(dev):
+        check(_lib.lib().ee_transpose_i8(engine(), ptr(src), R, C, _rowmajor(src, "src"), ptr(dst), R, stream_handle()))
+    return dst
+
+
+# ---------------------------------------------------------------- weights
+
+class PackedWeight:
+    """The three tier operands of one int8 weight, in MFMA operand order [N, K].
+
+    i8:  int8 codes                              (INT8 tier)
+    f8:  e4m3(fp16(code))                        (FP8 tier, EE/python/kernels.py:166)
+    f16: fp16(fp16(code) * fp16(scale[n]))       (W8A16 tier, EE/python/kernels.py:215,233)
+    """
+
+    def __init__(self, codes_nk: torch.Tensor, scale: torch.Tensor):
+        self.i8 = codes_nk.contiguous()
+        self.scale = scale.contiguous()
+        self._f8 = None
+        self._f16 = None
+
+    @property
+    def N(self) -> int:
+        return self.i8.shape[0]
+
+    @property
+    def K(self) -> int:
+        return self.i8.shape[1]
+
+    @property
+    def f8(self) -> torch.Tensor:
+        if self._f8 is None:
+            N, K = self.i8.shape
+            out = torch.empty((N, K), dtype=torch.uint8, device=self.i8.device)
+            with torch.cuda.device(self.i8.device):
+                check(_lib.lib().ee_pack_b_f8(engine(), ptr(self.i8), N, K, K, ptr(out), K, stream_handle()))
+            self._f8 = out
+        return self._f8
+
+    @property
+    def f16(self) -> torch.Tensor:
+        if self._f16 is None:
+            N, K = self.i8.shape
+            out = torch.empty((N, K), dtype=torch.float16, device=self.i8.device)
+            with torch.cuda.device(self.i8.device):
+                check(_lib.lib().ee_pack_b_f16(engine(), ptr(self.i8), ptr(self.scale), N, K, K, ptr(out), K,
+                                               stream_handle()))
+            self._f16 = out
+        return self._f16
+
+    def materialize(self) -> "PackedWeight":
+        _ = self.f8, self.f16
+        return self
+
+
+_weight_cache: dict = {}
+
+
+def prepare_weight(b_int8: torch.Tensor, b_scale: torch.Tensor) -> PackedWeight:
+    """Tier operands of the reference's weight buffer int8 [K, N] + scale [N],
+    cached per (tensor, version) and dropped when either tensor is freed."""
+    _require_cuda(b_int8, b_scale)
+    if b_int8.dtype != torch.int8 or b_int8.dim() != 2:
+        raise TypeError("b_int8 must be a 2-D int8 tensor [K, N]")
+    if b_scale.dtype != torch.float32 or b_scale.numel() != b_int8.shape[1]:
+        raise TypeError("b_scale must be float32 [N]")
+    key = (b_int8.data_ptr(), tuple(b_int8.shape), tuple(b_int8.stride()), b_int8._version,
+           b_scale.data_ptr(), b_scale._version, b_int8.device.index)
+    pw = _weight_cache.get(key)
+    if pw is None:
+        pw = PackedWeight(transpose_i8(b_int8), b_scale.contiguous())
+        _weight_cache[key] = pw
+        weakref.finalize(b_int8, _weight_cache.pop, key, None)
+        weakref.finalize(b_scale, _weight_cache.pop, key, None)
+    return pw
+
+
+# ---------------------------------------------------------------- GEMMs
+
+_KINDS = {"int8": _lib.EE_GEMM_I8, "fp8": _lib.EE_GEMM_F8, "fp16": _lib.EE_GEMM_F16}
+
+
+def gemm(kind: str, a: torch.Tensor, b_nk: torch.Tensor, a_scale=None, b_scale=None, out=None, *,
+         M: int | None = None, a_idx=None, c_idx=None, counts=None, tier: int = 0, acc_out=None) -> torch.Tensor:
+    """C = A @ B^T on the tier's MFMA kernel; A [M, K], B [N, K] (operand order)."""
+    dev = _require_cuda(a, b_nk, a_scale, b_scale, out, a_idx, c_idx, counts, acc_out)
+    lda = _rowmajor(a, "a")
+    ldb = _rowmajor(b_nk, "b")
+    N, K = b_nk.shape
+    if M is None:
+        M = a.shape[0] if a_idx is None else a_idx.numel()
+    if a.shape[1] != K:
+        raise ValueError(f"K mismatch: a is {tuple(a.shape)}, b is [{N}, {K}] in operand order")
+    c = out if out is not None else torch.empty((M, N), dtype=torch.float16, device=dev)
+    with torch.cuda.device(dev):
+        check(_lib.lib().ee_gemm(engine(), _KINDS[kind], ptr(a), lda, ptr(b_nk), ldb, ptr(c), _rowmajor(c, "c"),
+                                 ptr(a_scale), ptr(b_scale), M, N, K, ptr(a_idx), ptr(c_idx), ptr(counts), int(tier),
+                                 ptr(acc_out), stream_handle()))
+    return c
+
+
+def _check_gemm_inputs(a, b_int8, b_scale):
+    if a.dim() != 2 or b_int8.dim() != 2:
+        raise ValueError("a must be [M, K] and b_int8 [K, N]")
+    if a.dtype != torch.float16:
+        raise TypeError("a must be float16")
+    if a.shape[1] != b_int8.shape[0]:
+        raise ValueError(f"K mismatch: a is {tuple(a.shape)}, b is {tuple(b_int8.shape)}")
+
+
+def triton_int8_gemm(a: torch.Tensor, b_int8: torch.Tensor, b_scale: torch.Tensor) -> torch.Tensor:
+    """EE/python/kernels.py:330-351: per-row int8 activation quantisation
+    (fp16 scale, truncation) + INT8 MFMA GEMM + dequant epilogue."""
+    _check_gemm_inputs(a, b_int8, b_scale)
+    pw = prepare_weight(b_int8, b_scale)
+    a_int8, a_scale = quantize_activations(a, "dispatcher")
+    return gemm("int8", a_int8, pw.i8, a_scale, pw.scale)
+
+
+def triton_fp8_gemm(a: torch.Tensor, b_int8: torch.Tensor, b_scale: torch.Tensor) -> torch.Tensor:
+    """EE/python/kernels.py:354-373: per-row e4m3 activation codes + FP8 MFMA GEMM."""
+    _check_gemm_inputs(a, b_int8, b_scale)
+    pw = prepare_weight(b_int8, b_scale)
+    a_f8, a_scale = quantize_activations(a, "fp8")
+    return gemm("fp8", a_f8, pw.f8, a_scale, pw.scale)
+
+
+def triton_fp16_gemm(a: torch.Tensor, b_int8: torch.Tensor, b_scale: torch.Tensor) -> torch.Tensor:
+    """EE/python/kernels.py:380-409: W8A16 GEMM (fp16 activations, int8
+    weights dequantised to fp16 exactly as the reference does in SRAM)."""
+    _check_gemm_inputs(a, b_int8, b_scale)
+    if not a.is_contiguous():
+        a = a.contiguous()
+    pw = prepare_weight(b_int8, b_scale)
+    return gemm("fp16", a, pw.f16)
+
+
+# ---------------------------------------------------------------- routing
+
+def route(h: torch.Tensor, tau_low: float, tau_high: float):
+    """Per-row tiers + stable partition: (tier int32 [R], idx int32 [R], counts int32 [3])."""
+    dev = _require_cuda(h)
+    if h.dtype != torch.float32 or h.dim() != 1 or not h.is_contiguous():
+        raise TypeError("entropy must be a contiguous 1-D float32 tensor")
+    R = h.numel()
+    tier = torch.empty(R, dtype=torch.int32, device=dev)
+    idx = torch.empty(R, dtype=torch.int32, device=dev)
+    counts = torch.empty(3, dtype=torch.int32, device=dev)
+    with torch.cuda.device(dev):
+        check(_lib.lib().ee_route(engine(), ptr(h), R, float(tau_low), float(tau_high), ptr(tier), ptr(idx),
+                                  ptr(counts), stream_handle()))
+    return tier, idx, counts
+
+
+def row_copy(src: torch.Tensor, idx: torch.Tensor, counts=None, tier: int = 0, scatter: bool = False,
+             out: torch.Tensor | None = None) -> torch.Tensor:
+    """Gather (dst[r] = src[idx[off+r]]) or scatter (dst[idx[off+r]] = src[r]) whole rows."""
+    dev = _require_cuda(src, idx, counts, out)
+    if src.dim() != 2:
+        raise ValueError("src must be 2-D")
+    rows = idx.numel()
+    if out is None:
+        out = torch.empty((rows, src.shape[1]) if not scatter else src.shape, dtype=src.dtype, device=dev)
+    es = src.element_size()
+    with torch.cuda.device(dev):
+        check(_lib.lib().ee_row_copy(engine(), ptr(src), _rowmajor(src, "src") * es, ptr(out),
+                                     _rowmajor(out, "out") * es, rows, src.shape[1] * es, ptr(idx), ptr(counts),
+                                     int(tier), int(bool(scatter)), stream_handle()))
+    return out
+
+
+def routed_linear(x: torch.Tensor, pw: PackedWeight, idx: torch.Tensor, counts: torch.Tensor,
+                  out: torch.Tensor | None = None, workspace=None) -> torch.Tensor:
+    """One tier per row: INT8 / FP8 / W8A16 GEMMs over the rows `idx`/`counts`
+    assign them (from `route`), scattered back in place; no host sync."""
+    dev = _require_cuda(x, idx, counts, out)
+    if x.dtype != torch.float16:
+        raise TypeError("x must be float16")
+    M, K = x.shape
+    if K != pw.K:
+        raise ValueError(f"K mismatch: x is {tuple(x.shape)}, weight is [{pw.N}, {pw.K}]")
+    N = pw.N
+    c = out if out is not None else torch.empty((M, N), dtype=torch.float16, device=dev)
+    if workspace is None:
+        workspace = (torch.empty((M, K), dtype=torch.uint8, device=dev), torch.empty(M, dtype=torch.float32, device=dev))
+    ws_codes, ws_scale = workspace
+    with torch.cuda.device(dev):
+        check(_lib.lib().ee_routed_linear(engine(), ptr(x), _rowmajor(x, "x"), M, K, N, ptr(idx), ptr(counts),
+                                          ptr(pw.i8), ptr(pw.f8), ptr(pw.f16), ptr(pw.scale), ptr(c),
+                                          _rowmajor(c, "out"), ptr(ws_codes), ptr(ws_scale), stream_handle()))
+    return c
