@@ -110,9 +110,13 @@ def test_built_meta_lists_every_kernel_the_launcher_selects():
         for w in (1, 2, 4):
             assert f"eek_softmax_entropy_v{v}_w{w}" in ks and f"eek_quant_v{v}_w{w}" in ks
     for k in ("eek_softmax_entropy_generic", "eek_quant_generic", "eek_gemm_i8", "eek_gemm_f8", "eek_gemm_f16",
+              "eek_gemm_i8_generic", "eek_gemm_f8_generic", "eek_gemm_f16_generic",
               "eek_route", "eek_row_copy", "eek_transpose_i8", "eek_pack_b_f8", "eek_pack_b_f16"):
         assert k in ks
-    assert ks["eek_gemm_i8"]["lds"] == 65536 and ks["eek_route"]["block"] == 1024
+    # pipelined GEMMs: 5 LDS stages of (128 + 128) rows x 128 bytes = all of gfx950's 160 KB
+    assert ks["eek_gemm_i8"]["lds"] == 5 * 256 * 128 and ks["eek_gemm_i8_generic"]["lds"] == 2 * 256 * 128
+    assert ks["eek_route"]["block"] == 1024
+    assert all(v["block"] <= v["max_flat_workgroup_size"] for v in ks.values())
     src = open(os.path.join(PKG, "csrc", "launcher", "ee_launcher.cpp")).read()
     for name in re.findall(r'"(eek_[a-z0-9_]+)"', src):
         assert name in ks or name.endswith("_v") or name.endswith("_generic") or name in src, name
