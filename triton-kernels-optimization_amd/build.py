@@ -116,7 +116,7 @@ def build(jobs: int = 8, only_host: bool = False, verbose: bool = True) -> str:
                     raise RuntimeError(f"{k['name']} spills to scratch ({k['private_segment_fixed_size']} B/lane)")
                 meta["kernels"][k["name"]] = {
                     "code_object": stem,
-                    "block": 1024 if k["name"] == "eek_route" else 256,
+                    "block": k["max_flat_workgroup_size"],        # every kernel launches at its bound
                     "lds": k["group_segment_fixed_size"],
                     "max_flat_workgroup_size": k["max_flat_workgroup_size"],
                     "vgpr": k["vgpr_count"], "agpr": k.get("agpr_count", 0), "sgpr": k.get("sgpr_count", 0),

@@ -357,17 +357,26 @@ EE_DEV void epilogue32_lds(const EeGemmArgs& g, const typename Pipe<KIND>::acc_t
     }
 }
 
+// Pipelined kernel, 512 threads: waves 0-3 compute (one 64 x 64 quadrant each:
+// LDS fragment reads + MFMAs only), waves 4-7 load (direct-to-LDS DMA of the
+// stages and their vmcnt waits).  Each SIMD runs one wave of each kind, so the
+// loaders' issue and waits never stall the MFMA stream.  One s_barrier per K
+// stage serves both roles: barrier kt means "stage kt has landed" for the
+// compute waves and "stage kt-1 has been read" for the loaders, which then
+// refill that stage's buffer with stage kt-1+NSTAGE.
+#define GEMM_THREADS 512
+
 template <int KIND>
 EE_DEV void gemm_pipelined(const EeGemmArgs& g) {
     typedef Pipe<KIND> P;
     typedef typename P::acc_t acc_t;
     constexpr int ESZ = (KIND == EE_GEMM_F16) ? 2 : 1;
-    constexpr int LOADS = 8;                          // direct loads per lane per stage (4 A + 4 B)
+    constexpr int LOADS = 8;                          // DMA instructions per loader wave per stage (4 A + 4 B)
     constexpr int NSL = BKB / P::SB;                  // K slices per stage (4 or 2)
     __shared__ __attribute__((aligned(1024))) uint8_t smem[NSTAGE * LDS_STAGE];
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int M = g.counts ? g.counts[g.tier] : g.M;
     const int64_t off = g.counts ? tier_offset(g.counts, g.tier) : 0;
     const int tiles_m = (g.M + BM - 1) / BM;
@@ -375,92 +384,107 @@ EE_DEV void gemm_pipelined(const EeGemmArgs& g) {
     tile_of((int)blockIdx.x, (int)gridDim.x, tiles_m, tm, tn);
     const int m0 = tm * BM, n0 = tn * BN;
     if (m0 >= M) return;                              // whole workgroup, before any barrier
-
     const int nk = (int)((int64_t)g.K * ESZ / BKB);   // K * ESZ is a multiple of BKB here
 
-    // Loader geometry: one global_load_lds_dwordx4 fills 8 LDS rows (1 KB); lane l
-    // lands at row r = 8*grp + l/8, physical chunk l%8, which holds logical chunk
-    // (l%8) ^ swz(r).  Wave w fills row groups 4w..4w+3 of A and of B.
-    const int lrow = lane >> 3;
-    const uint8_t* pa[4];
-    const uint8_t* pb[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int r = (wave * 4 + i) * 8 + lrow;
-        const int lchunk = (lane & 7) ^ swz(r);        // swz(BM + r) == swz(r): BM is a multiple of 16
-        const int m = min(m0 + r, M - 1);
-        const int64_t ar = g.a_idx ? (int64_t)g.a_idx[off + m] : off + m;
-        pa[i] = (const uint8_t*)g.a + ar * g.lda * ESZ + lchunk * 16;
-        const int n = min(n0 + r, g.N - 1);
-        pb[i] = (const uint8_t*)g.b + (int64_t)n * g.ldb * ESZ + lchunk * 16;
-    }
-    const int uwave = __builtin_amdgcn_readfirstlane(wave);
-    auto issue = [&](int kt) {
-        const uint32_t s = lds_addr(smem) + (uint32_t)((kt % NSTAGE) * LDS_STAGE);
-        const int64_t kb = (int64_t)kt * BKB;
+    if (wave >= 4) {
+        // ------------------------------------------------------------ loader waves
+        // One global_load_lds_dwordx4 fills 8 LDS rows (1 KB): lane l lands at row
+        // r = 8*grp + l/8, physical chunk l%8, which holds logical chunk
+        // (l%8) ^ swz(r).  Loader w fills row groups 4w..4w+3 of A and of B.
+        const int lw = wave - 4, lrow = lane >> 3;
+        const uint8_t* pa[4];
+        const uint8_t* pb[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int grp = uwave * 4 + i;
-            dma16(pa[i] + kb, s + grp * 8 * BKB);
-            dma16(pb[i] + kb, s + (BM + grp * 8) * BKB);
+            const int r = (lw * 4 + i) * 8 + lrow;
+            const int lchunk = (lane & 7) ^ swz(r);   // swz(BM + r) == swz(r): BM is a multiple of 16
+            const int m = min(m0 + r, M - 1);
+            const int64_t ar = g.a_idx ? (int64_t)g.a_idx[off + m] : off + m;
+            pa[i] = (const uint8_t*)g.a + ar * g.lda * ESZ + lchunk * 16;
+            const int n = min(n0 + r, g.N - 1);
+            pb[i] = (const uint8_t*)g.b + (int64_t)n * g.ldb * ESZ + lchunk * 16;
         }
-    };
-    // Wait until stage `next` has landed for this wave while the stages issued
-    // after it (up to `last`) stay in flight, then one barrier makes it visible to
-    // the workgroup and frees every buffer read before it.
-    auto sync_stage = [&](int next, int last) {
-        const int after = last - next;
-        if (after >= 4) WAITCNT_VM(4 * LOADS);
-        else if (after == 3) WAITCNT_VM(3 * LOADS);
-        else if (after == 2) WAITCNT_VM(2 * LOADS);
-        else if (after == 1) WAITCNT_VM(LOADS);
-        else WAITCNT_VM(0);
-        WAITCNT_LGKM0();                              // this wave's reads of the freed buffer are done
-        __builtin_amdgcn_s_barrier();
-        asm volatile("" ::: "memory");
-    };
+        auto issue = [&](int kt) {
+            const uint32_t s = lds_addr(smem) + (uint32_t)((kt % NSTAGE) * LDS_STAGE);
+            const int64_t kb = (int64_t)kt * BKB;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int grp = lw * 4 + i;
+                dma16(pa[i] + kb, s + grp * 8 * BKB);
+                dma16(pb[i] + kb, s + (BM + grp * 8) * BKB);
+            }
+        };
+#pragma unroll
+        for (int st = 0; st < NSTAGE; ++st)
+            if (st < nk) issue(st);
+        for (int kt = 0; kt < nk; ++kt) {
+            // This wave's loads of stage kt must be done; the stages issued after it
+            // may stay in flight.  Before barrier kt those are stages kt+1 .. kt+NSTAGE-1
+            // when kt == 0 (prologue) and kt+1 .. kt+NSTAGE-2 after (the refill of stage
+            // kt+NSTAGE-1 was issued after barrier kt-1), capped at the last stage.
+            const int last = kt == 0 ? NSTAGE - 1 : kt + NSTAGE - 2;
+            const int after = min(last, nk - 1) - kt;
+            if (after >= 4) WAITCNT_VM(4 * LOADS);
+            else if (after == 3) WAITCNT_VM(3 * LOADS);
+            else if (after == 2) WAITCNT_VM(2 * LOADS);
+            else if (after == 1) WAITCNT_VM(LOADS);
+            else WAITCNT_VM(0);
+            asm volatile("" ::: "memory");
+            __builtin_amdgcn_s_barrier();             // barrier kt
+            asm volatile("" ::: "memory");
+            if (kt >= 1 && kt - 1 + NSTAGE < nk) issue(kt - 1 + NSTAGE);   // stage kt-1's buffer is free
+        }
+        return;
+    }
 
+    // ---------------------------------------------------------------- compute waves
+    const int wm = wave >> 1, wn = wave & 1;
     acc_t acc[2][2];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j) acc[i][j] = acc_t{};
 
-    // All NSTAGE buffers start filling; afterwards stage kt + NSTAGE goes into the
-    // buffer of stage kt as soon as every wave has finished reading it.
-#pragma unroll
-    for (int st = 0; st < NSTAGE; ++st)
-        if (st < nk) issue(st);
-    sync_stage(0, min(NSTAGE, nk) - 1);
-
-    // Fragments alternate between f0 and f1 slice by slice (NSL is even, so slice 0
-    // of every stage is in f0): the reads of the next slice are issued between the
-    // MFMAs of the current one, and the MFMAs wait only for reads a slice old.
+    // Fragments alternate between f0 and f1 slice by slice (NSL is even): the
+    // reads of slice s+1 are issued before the MFMAs of slice s, and the reads of
+    // the next stage's slice 0 before the MFMAs of this stage's last slice.  The
+    // barrier for stage kt+1 therefore sits before those last MFMAs; by then every
+    // read of stage kt has completed (lgkmcnt 0), which is what the loaders need to
+    // refill its buffer after that barrier.
+    // The last stage is peeled off the loop: were its final slice (whose reads are
+    // still in flight) and the steady-state final slice one block, the waitcnt
+    // pass would make the steady state wait for the next stage's reads as well.
     Frags<KIND> f0, f1;
-    read_frags<KIND>(smem, 0, wm, wn, lane, f0);
-    for (int kt = 0; kt < nk; ++kt) {
+    auto stage = [&](int kt, bool more) {
         const uint8_t* s = smem + (kt % NSTAGE) * LDS_STAGE;
 #pragma unroll
-        for (int sl = 0; sl + 1 < NSL; ++sl) {
+        for (int sl = 0; sl < NSL; ++sl) {
             Frags<KIND>& cur = (sl & 1) ? f1 : f0;
             Frags<KIND>& nxt = (sl & 1) ? f0 : f1;
-            read_frags<KIND>(s, sl + 1, wm, wn, lane, nxt);
+            if (sl + 1 < NSL) {
+                read_frags<KIND>(s, sl + 1, wm, wn, lane, nxt);
+            } else if (more) {
+                WAITCNT_LGKM0();
+                asm volatile("" ::: "memory");
+                __builtin_amdgcn_s_barrier();         // barrier kt+1: stage kt+1 has landed
+                asm volatile("" ::: "memory");
+                read_frags<KIND>(smem + ((kt + 1) % NSTAGE) * LDS_STAGE, 0, wm, wn, lane, nxt);
+            }
             mma_all<KIND>(cur, acc);
             interleave<KIND>();
         }
-        if (kt + 1 < nk) {
-            sync_stage(kt + 1, min(kt + NSTAGE - 1, nk - 1));   // every wave is done with stage kt
-            if (kt + NSTAGE < nk) issue(kt + NSTAGE);
-        }
-        read_frags<KIND>(smem + (min(kt + 1, nk - 1) % NSTAGE) * LDS_STAGE, 0, wm, wn, lane, f0);
-        mma_all<KIND>(f1, acc);
-        interleave<KIND>();
-    }
+    };
+    __builtin_amdgcn_s_barrier();                     // barrier 0: stage 0 has landed
+    asm volatile("" ::: "memory");
+    read_frags<KIND>(smem, 0, wm, wn, lane, f0);
+    for (int kt = 0; kt + 1 < nk; ++kt) stage(kt, true);
+    stage(nk - 1, false);
     if (g.acc) {
         epilogue32<KIND>(g, acc, m0, n0, M, off, wm, wn, lane);
     } else {
-        // The buffer after the last stage's is free: every DMA has landed (vmcnt(0)
-        // at the last stage sync) and every read of it preceded that sync's barrier.
+        // Buffer nk % NSTAGE is free: no DMA is in flight after the last barrier
+        // (the loaders waited for all of theirs before it), and its last stage,
+        // nk - NSTAGE, was read before barrier nk - NSTAGE + 1.
         uint8_t* tile = smem + (nk % NSTAGE) * LDS_STAGE + wave * (64 * BKB);
         epilogue32_lds<KIND>(g, acc, tile, m0, n0, M, off, wm, wn, lane);
     }
@@ -535,13 +559,13 @@ EE_DEV void gemm_generic(const EeGemmArgs& g) {
     epilogue<KIND>(g, acc, m0, n0, M, off, wm, wn, lane);
 }
 
-extern "C" __global__ void __launch_bounds__(EE_BLOCK) __attribute__((amdgpu_waves_per_eu(1, 1))) eek_gemm_i8(EeGemmArgs g) {
+extern "C" __global__ void __launch_bounds__(GEMM_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2))) eek_gemm_i8(EeGemmArgs g) {
     gemm_pipelined<EE_GEMM_I8>(g);
 }
-extern "C" __global__ void __launch_bounds__(EE_BLOCK) __attribute__((amdgpu_waves_per_eu(1, 1))) eek_gemm_f8(EeGemmArgs g) {
+extern "C" __global__ void __launch_bounds__(GEMM_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2))) eek_gemm_f8(EeGemmArgs g) {
     gemm_pipelined<EE_GEMM_F8>(g);
 }
-extern "C" __global__ void __launch_bounds__(EE_BLOCK) __attribute__((amdgpu_waves_per_eu(1, 1))) eek_gemm_f16(EeGemmArgs g) {
+extern "C" __global__ void __launch_bounds__(GEMM_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2))) eek_gemm_f16(EeGemmArgs g) {
     gemm_pipelined<EE_GEMM_F16>(g);
 }
 

@@ -493,7 +493,8 @@ EE_EXPORT int ee_gemm(ee_engine* eng, int32_t kind, const void* a, int64_t lda, 
     // The pipelined kernels stream whole 128-byte K stages; other K take the fallback.
     static const char* names[3] = {"eek_gemm_i8", "eek_gemm_f8", "eek_gemm_f16"};
     const std::string name = std::string(names[kind]) + (((K * esz) % 128 == 0) ? "" : "_generic");
-    return launch(eng, name, cdiv(M, 128) * cdiv(N, 128), 1, EE_BLOCK, g, stream);
+    const Kernel* k = find_kernel(eng, name);
+    return launch(eng, name, cdiv(M, 128) * cdiv(N, 128), 1, k ? k->block : EE_BLOCK, g, stream);
 }
 
 EE_EXPORT int ee_route(ee_engine* eng, const float* h, int64_t rows, double tau_low, double tau_high,
