@@ -15,9 +15,13 @@ GEMM, the entropy kernel, the quantisers and the end-to-end launchers are
 timed the same way and reported under "kernels".
 
 Timing: W untimed warmup steps, then EXACTLY K steps between events recorded
-on the stream the kernels run on, bracketed by torch.cuda.synchronize().  The
-K launches are captured once into a HIP graph and replayed, so host launch
-overhead stays out of the kernel time (eager-launch times are reported too).
+on the stream the kernels run on, bracketed by torch.cuda.synchronize(); the
+median of 5 such timed regions is reported.  Each
+kernel is timed twice: from K eager launches (the reference's own loop) and
+from one HIP graph holding the K launches.  The GEMMs report the eager figure
+(their launches keep the queue full; graph replay adds per-node overhead); the
+6-9 us entropy and quantiser kernels report the graph figure (eager Python
+launches of them are host-bound).  Both figures are in kernels.timings_us.
 GEMM operands stay resident (as in the reference's loop); the HBM-bound
 entropy kernel rotates through enough input/output buffers to exceed the
 256 MB Infinity Cache ("cold", the roofline figure) and also reports the
@@ -45,6 +49,7 @@ PEAK_F16_TFLOPS = 2500.0       # MI355X dense fp16
 PEAK_HBM_GBS = 8000.0          # MI355X HBM3E
 M, K, N = 1024, 4096, 4096
 ER, ES = 1024, 4096            # entropy rows x columns
+COPY_BYTES = 256 << 20         # calibration copy for the FETCH_SIZE / WRITE_SIZE counters
 
 
 def parse():
@@ -58,8 +63,10 @@ def parse():
     return ap.parse_args()
 
 
-def time_steps(fn, steps: int, warmup: int, use_graph: bool, stream):
-    """Average ms per step of `fn` (which launches on `stream`)."""
+def time_steps(fn, steps: int, warmup: int, use_graph: bool, stream, repeats: int = 5):
+    """ms per step of `fn` (which launches on `stream`): the median over
+    `repeats` timed regions, each of exactly `steps` launches between events
+    on `stream`, bracketed by torch.cuda.synchronize()."""
     import torch
     for _ in range(warmup):
         fn()
@@ -77,18 +84,22 @@ def time_steps(fn, steps: int, warmup: int, use_graph: bool, stream):
             print(f"# graph capture failed ({type(e).__name__}: {e}); timing eager launches", file=sys.stderr)
             graph = None
             torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    times = []
     with torch.cuda.stream(stream):
-        torch.cuda.synchronize()
-        start.record(stream)
-        if graph is not None:
-            graph.replay()
-        else:
-            for _ in range(steps):
-                fn()
-        end.record(stream)
-        torch.cuda.synchronize()
-    return start.elapsed_time(end) / steps, graph is not None
+        for _ in range(repeats):
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            start.record(stream)
+            if graph is not None:
+                graph.replay()
+            else:
+                for _ in range(steps):
+                    fn()
+            end.record(stream)
+            torch.cuda.synchronize()
+            times.append(start.elapsed_time(end) / steps)
+    times.sort()
+    return times[len(times) // 2], graph is not None
 
 
 def main():
@@ -133,19 +144,26 @@ def main():
     use_graph = not args.no_graph
     results = {}
 
-    def run(name, fn, steps=args.steps, warmup=args.warmup, graph=use_graph):
+    def run(name, fn, steps=args.steps, warmup=args.warmup, primary="graph"):
+        """Times `fn` from eager launches and, unless --no-graph, from a replayed
+        HIP graph of the K launches; "ms" is the `primary` one of the two."""
         if only and name not in only:
             return None
         with torch.cuda.stream(stream):
-            ms, g = time_steps(fn, steps, warmup, graph, stream)
-        results[name] = {"ms": ms, "graph": g}
-        return ms
+            ms_eager, _ = time_steps(fn, steps, warmup, False, stream)
+            ms_graph, g = time_steps(fn, steps, warmup, True, stream) if use_graph else (None, False)
+        use = "graph" if (primary == "graph" and g) else "eager"
+        results[name] = {"ms": ms_graph if use == "graph" else ms_eager, "timing": use,
+                         "ms_eager": ms_eager, "ms_graph": ms_graph}
+        return results[name]["ms"]
 
     with torch.cuda.stream(stream):
         # headline: INT8 GEMM kernel on pre-quantised activations
-        run("gemm_i8", lambda: ee.gemm("int8", a_i8, pw.i8, s_i8, pw.scale, out=c))
-        run("gemm_f8", lambda: ee.gemm("fp8", a_f8, pw.f8, s_f8, pw.scale, out=c))
-        run("gemm_f16w8", lambda: ee.gemm("fp16", a, w16, out=c))
+        # GEMMs (26-50 us each) keep the queue full from eager launches, as in the
+        # reference's own timing loop; graph replay adds per-node overhead on top.
+        run("gemm_i8", lambda: ee.gemm("int8", a_i8, pw.i8, s_i8, pw.scale, out=c), primary="eager")
+        run("gemm_f8", lambda: ee.gemm("fp8", a_f8, pw.f8, s_f8, pw.scale, out=c), primary="eager")
+        run("gemm_f16w8", lambda: ee.gemm("fp16", a, w16, out=c), primary="eager")
         rot = {"i": 0}
 
         def ent_cold():
@@ -159,16 +177,21 @@ def main():
         run("quant_f8", lambda: ee.quantize_activations(a, "fp8", out_codes=a_f8, out_scale=s_f8))
         run("launcher_int8", lambda: ee.gemm("int8", *ee.quantize_activations(a, "dispatcher", out_codes=a_i8,
                                                                                 out_scale=s_i8)[:1], pw.i8,
-                                             s_i8, pw.scale, out=c), graph=False)
-        run("torch_matmul_fp16", lambda: torch.matmul(a, w16.t()))
+                                             s_i8, pw.scale, out=c), primary="eager")
+        run("torch_matmul_fp16", lambda: torch.matmul(a, w16.t()), primary="eager")
+        try:                                                           # vendor INT8 GEMM (hipBLASLt) comparator
+            b_kn = pw.i8.t().contiguous()
+            torch._int_mm(a_i8, b_kn)
+            run("torch_int_mm", lambda: torch._int_mm(a_i8, b_kn), primary="eager")
+        except RuntimeError as e:
+            print(f"# torch._int_mm unavailable: {e}", file=sys.stderr)
+        if "hbm_copy" in only:                                         # PMC calibration: 256 MiB read + 256 MiB written
+            src = torch.empty(COPY_BYTES // 4, dtype=torch.float32, device=dev).fill_(1.0)
+            dst = torch.empty_like(src)
+            run("hbm_copy", lambda: dst.copy_(src))
     if only:
         print(json.dumps({k: v for k, v in results.items()}))
         return
-
-    # eager-launch cross-check of the headline kernel
-    with torch.cuda.stream(stream):
-        eager_ms, _ = time_steps(lambda: ee.gemm("int8", a_i8, pw.i8, s_i8, pw.scale, out=c), args.steps,
-                                 args.warmup, False, stream)
 
     t_i8 = results["gemm_i8"]["ms"]
     tops = ops / (t_i8 * 1e-3) / 1e12
@@ -194,16 +217,25 @@ def main():
                                 "TOPS": ops / (results["launcher_int8"]["ms"] * 1e-3) / 1e12},
         "torch_matmul_fp16": {"us": results["torch_matmul_fp16"]["ms"] * 1e3,
                               "TFLOPS": ops / (results["torch_matmul_fp16"]["ms"] * 1e-3) / 1e12},
-        "gemm_i8_eager_us": eager_ms * 1e3,
-        "timing": "hip graph of K launches" if results["gemm_i8"]["graph"] else "eager launches",
+        "torch_int_mm_hipblaslt": ({"us": results["torch_int_mm"]["ms"] * 1e3,
+                                    "TOPS": ops / (results["torch_int_mm"]["ms"] * 1e-3) / 1e12}
+                                   if "torch_int_mm" in results else None),
     }
+    for k, r in results.items():                                       # both timings of every kernel, in us
+        kernels.setdefault("timings_us", {})[k] = {
+            "eager": r["ms_eager"] * 1e3, "graph": None if r["ms_graph"] is None else r["ms_graph"] * 1e3,
+            "reported": r["timing"]}
 
-    traffic = None
+    # HBM-side bytes per launch from the committed FETCH_SIZE / WRITE_SIZE passes
+    # (calibrated against a 256 MiB copy); null when that summary is absent.
+    traffic = ent_traffic = None
     pmc = os.path.join(ROOT, "profiles", "gemm_i8_c0_hbm_traffic.txt")
     if os.path.exists(pmc):
         for line in open(pmc):
             if line.startswith("traffic_bytes_per_launch:"):
                 traffic = float(line.split(":", 1)[1])
+            elif line.startswith("traffic_bytes_per_launch.eek_softmax_entropy:"):
+                ent_traffic = float(line.split(":", 1)[1])
 
     cpu = None
     if not args.no_cpu:
@@ -229,7 +261,7 @@ def main():
         "roofline": {"bound": "mfma", "achieved": round(tops, 2), "peak": PEAK_I8_TOPS, "unit": "TFLOP/s",
                      "frac": round(tops / PEAK_I8_TOPS, 4), "traffic": traffic},
         "roofline_entropy": {"bound": "hbm", "achieved": round(ent_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                             "frac": round(ent_gbs / PEAK_HBM_GBS, 4), "traffic": None},
+                             "frac": round(ent_gbs / PEAK_HBM_GBS, 4), "traffic": ent_traffic},
         "kernels": kernels,
         "cpu_baseline": cpu,
     }

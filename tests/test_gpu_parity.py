@@ -425,3 +425,42 @@ def test_cubin_engine_counterpart(ee, orc):
     with pytest.raises(RuntimeError, match="K mismatch"):
         e.forward(cuda(codes[:, :512]), cuda(B), cuda(a_s), cuda(bs))
     assert os.path.exists(eng_mod.DEFAULT_META)
+
+
+# ---------------------------------------------------------------------------- committed fixtures
+
+def test_golden_vectors_through_the_abi(ee):
+    """tests/golden/vectors_small.npz: every stage of the path on the GPU
+    against the committed oracle outputs (hazard rows included: zero row, a
+    row whose FP8 inverse scale overflows, fp16 extremes)."""
+    import os
+    z = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "vectors_small.npz"))
+    a = cuda(z["a"])
+    for mode, key in (("dispatcher", "i8_dispatcher"), ("engine", "i8_engine"), ("fp8", "f8")):
+        c, s = ee.quantize_activations(a, mode)
+        assert np.array_equal(host(c), z["codes_" + key]), mode
+        assert np.array_equal(host(s).view(np.uint32), z["scale_" + key].view(np.uint32)), mode
+    w_codes, w_scale = ee.quantize_weight_codes(cuda(z["w"]))
+    assert np.array_equal(host(w_codes), z["b_kn"].T) and np.array_equal(host(w_scale), z["b_scale"])
+    b_kn, bs = cuda(z["b_kn"]), cuda(z["b_scale"])
+    pw = ee.prepare_weight(b_kn, bs)
+    ci, si = cuda(z["codes_i8_dispatcher"]), cuda(z["scale_i8_dispatcher"])
+    acc = torch.empty((24, 40), dtype=torch.int32, device="cuda")
+    out = ee.gemm("int8", ci, pw.i8, si, pw.scale, acc_out=acc)
+    assert np.array_equal(host(acc), z["acc_i32"])
+    assert np.array_equal(host(out).view(np.uint16), z["out_i8_bits"])
+    assert np.array_equal(host(ee.triton_int8_gemm(a, b_kn, bs)).view(np.uint16), z["out_i8_bits"])
+    out8 = ee.gemm("fp8", cuda(z["codes_f8"]), pw.f8, cuda(z["scale_f8"]), pw.scale)
+    check_close_f64(host(out8), z["out_f8_f64"])
+    check_close_f64(host(ee.triton_fp8_gemm(a, b_kn, bs)), z["out_f8_f64"])
+    check_close_f64(host(ee.triton_fp16_gemm(a, b_kn, bs)), z["out_w8a16_f64"])
+    p, h, _ = ee.softmax_entropy(cuda(z["logits"]))
+    check_entropy(host(h), z["entropy_f64"])
+    check_probs(host(p), z["probs_f16"])
+    p, h, _ = ee.softmax_entropy(cuda(z["logits_causal"].reshape(12, 6)), causal=True)
+    check_entropy(host(h), z["entropy_causal_f64"])
+    check_probs(host(p), z["probs_causal_f16"])
+    for i, (tl, th) in enumerate(z["route_thresholds"]):
+        tier, idx, counts = ee.route(cuda(z["route_h"]), float(tl), float(th))
+        assert np.array_equal(host(tier), z["route_tier"][i]) and np.array_equal(host(idx), z["route_idx"][i])
+        assert np.array_equal(host(counts), z["route_counts"][i])
