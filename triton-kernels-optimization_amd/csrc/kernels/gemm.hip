@@ -289,27 +289,38 @@ EE_DEV void epilogue32(const EeGemmArgs& g, const typename Pipe<KIND>::acc_t (&a
 // per lane -- each store instruction covers 8 rows x 128 contiguous bytes of C
 // instead of 32 rows x 16 bytes.  (The optional int32 accumulators keep the
 // direct path; they are a debug output.)
-template <int KIND>
-EE_DEV void epilogue32_lds(const EeGemmArgs& g, const typename Pipe<KIND>::acc_t (&acc)[2][2], uint8_t* tile, int m0,
-                           int n0, int M, int64_t off, int wm, int wn, int lane) {
-    // 1. dequantise and write: lane l holds rows i*32 + (l & 31), columns j*32 + 8q + 4(l >> 5) + 0..3.
-    // The lane's 8 groups of 4 column scales and 2 row scales are loaded first, as vectors.
+// Per-lane dequantisation scales of a wave's 64 x 64 quadrant: lane l needs the
+// column scales of columns j*32 + 8q + 4(l >> 5) + 0..3 (8 vectors of 4) and the
+// row scales of rows i*32 + (l & 31).  Loaded before the K loop so that their
+// latency is hidden behind it.
+struct TileScales {
     f32x4 bs[2][4];
     float as[2];
+};
+
+template <int KIND>
+EE_DEV void load_scales(const EeGemmArgs& g, int m0, int n0, int M, int64_t off, int wm, int wn, int lane,
+                        TileScales& sc) {
     if constexpr (KIND != EE_GEMM_F16) {
 #pragma unroll
         for (int j = 0; j < 2; ++j)
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const int n = n0 + wn * 64 + j * 32 + 8 * q + 4 * (lane >> 5);
-                bs[j][q] = (n < g.N) ? *(const f32x4*)(g.b_scale + n) : f32x4{0.f, 0.f, 0.f, 0.f};
+                sc.bs[j][q] = (n < g.N) ? *(const f32x4*)(g.b_scale + n) : f32x4{0.f, 0.f, 0.f, 0.f};
             }
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             const int m = m0 + wm * 64 + i * 32 + (lane & 31);
-            as[i] = (m < M) ? g.a_scale[off + m] : 0.0f;
+            sc.as[i] = (m < M) ? g.a_scale[off + m] : 0.0f;
         }
     }
+}
+
+template <int KIND>
+EE_DEV void epilogue32_lds(const EeGemmArgs& g, const typename Pipe<KIND>::acc_t (&acc)[2][2], const TileScales& sc,
+                           uint8_t* tile, int m0, int n0, int M, int64_t off, int wm, int wn, int lane) {
+    // 1. dequantise and write: lane l holds rows i*32 + (l & 31), columns j*32 + 8q + 4(l >> 5) + 0..3.
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
         const int rl = i * 32 + (lane & 31);
@@ -323,11 +334,11 @@ EE_DEV void epilogue32_lds(const EeGemmArgs& g, const typename Pipe<KIND>::acc_t
                 for (int r = 0; r < 4; ++r) {
                     if constexpr (KIND == EE_GEMM_I8) {
                         float v = (float)acc[i][j][4 * q + r];
-                        v = v * as[i];
-                        o[r] = v * bs[j][q][r];
+                        v = v * sc.as[i];
+                        o[r] = v * sc.bs[j][q][r];
                     } else if constexpr (KIND == EE_GEMM_F8) {
-                        const float v = acc[i][j][4 * q + r] * as[i];
-                        o[r] = v * bs[j][q][r];
+                        const float v = acc[i][j][4 * q + r] * sc.as[i];
+                        o[r] = v * sc.bs[j][q][r];
                     } else {
                         o[r] = acc[i][j][4 * q + r];
                     }
@@ -348,11 +359,13 @@ EE_DEV void epilogue32_lds(const EeGemmArgs& g, const typename Pipe<KIND>::acc_t
         if (m >= M || n >= g.N) continue;
         const int64_t crow = g.c_idx ? (int64_t)g.c_idx[off + m] : (int64_t)m;
         uint16_t* dst = g.c + crow * g.ldc + n;
+        // C is written once and read by a later kernel: non-temporal stores keep
+        // it from lingering dirty in L2 (measured ~0.5 us per launch at C0).
         if (n + 8 <= g.N && ((uintptr_t)dst & 15) == 0) {
-            *(u32x4*)dst = v;
+            __builtin_nontemporal_store(v, (u32x4*)dst);
         } else {                                           // N % 8 == 4 tail, or C only 8-byte aligned
-            *(u32x2*)dst = u32x2{v[0], v[1]};
-            if (n + 4 < g.N) *(u32x2*)(dst + 4) = u32x2{v[2], v[3]};
+            __builtin_nontemporal_store(u32x2{v[0], v[1]}, (u32x2*)dst);
+            if (n + 4 < g.N) __builtin_nontemporal_store(u32x2{v[2], v[3]}, (u32x2*)(dst + 4));
         }
     }
 }
@@ -450,10 +463,13 @@ EE_DEV void gemm_pipelined(const EeGemmArgs& g) {
     // the next stage's slice 0 before the MFMAs of this stage's last slice.  The
     // barrier for stage kt+1 therefore sits before those last MFMAs; by then every
     // read of stage kt has completed (lgkmcnt 0), which is what the loaders need to
-    // refill its buffer after that barrier.
+    // refill its buffer after that barrier.  (Reading two slices ahead measured
+    // slower: LDS latency is not what bounds this loop.)
     // The last stage is peeled off the loop: were its final slice (whose reads are
     // still in flight) and the steady-state final slice one block, the waitcnt
     // pass would make the steady state wait for the next stage's reads as well.
+    TileScales sc;
+    if (!g.acc) load_scales<KIND>(g, m0, n0, M, off, wm, wn, lane, sc);
     Frags<KIND> f0, f1;
     auto stage = [&](int kt, bool more) {
         const uint8_t* s = smem + (kt % NSTAGE) * LDS_STAGE;
@@ -464,6 +480,8 @@ EE_DEV void gemm_pipelined(const EeGemmArgs& g) {
             if (sl + 1 < NSL) {
                 read_frags<KIND>(s, sl + 1, wm, wn, lane, nxt);
             } else if (more) {
+                // keep the previous slice's MFMAs ahead of this wait: they cover its latency
+                __builtin_amdgcn_sched_barrier(0);
                 WAITCNT_LGKM0();
                 asm volatile("" ::: "memory");
                 __builtin_amdgcn_s_barrier();         // barrier kt+1: stage kt+1 has landed
@@ -486,7 +504,7 @@ EE_DEV void gemm_pipelined(const EeGemmArgs& g) {
         // (the loaders waited for all of theirs before it), and its last stage,
         // nk - NSTAGE, was read before barrier nk - NSTAGE + 1.
         uint8_t* tile = smem + (nk % NSTAGE) * LDS_STAGE + wave * (64 * BKB);
-        epilogue32_lds<KIND>(g, acc, tile, m0, n0, M, off, wm, wn, lane);
+        epilogue32_lds<KIND>(g, acc, sc, tile, m0, n0, M, off, wm, wn, lane);
     }
 }
 
