@@ -54,7 +54,8 @@ enum { EE_TIER_INT8 = 0, EE_TIER_FP8 = 1, EE_TIER_FP16 = 2 };
 enum {
     EE_QUANT_I8_DISPATCH = 0, /* EE/python/kernels.py:336-338: fp16 scale, truncating cast   */
     EE_QUANT_I8_ENGINE = 1,   /* EE/test_cubin.py:93-103: f32 scale, round + clamp(+-127)    */
-    EE_QUANT_F8_ROW = 2       /* EE/python/kernels.py:361,144,159-160: e4m3 codes per row    */
+    EE_QUANT_F8_ROW = 2,      /* EE/python/kernels.py:361,144,159-160: e4m3 codes per row    */
+    EE_QUANT_F8_TENSOR = 3    /* one e4m3 scale per tensor: ee_quant_tensor_f8 only           */
 };
 
 /* GEMM kinds (the three tiers). */
@@ -108,6 +109,20 @@ int ee_quant_act(ee_engine* eng, const void* x, int64_t M, int64_t K, int64_t ld
  * codes into the reference's [K, N] buffer. */
 int ee_quant_weight_i8(ee_engine* eng, const void* w, int64_t N, int64_t K, int64_t ld_w,
                        int8_t* codes_nk, int64_t ld_c, float* scale, ee_stream_t stream);
+
+/* ---- FP8 e4m3 with one scale per tensor ------------------------------------
+ * No counterpart in the reference, whose FP8 tier scales per row
+ * (EE/python/kernels.py:361); BASELINE config 1 ("FP8 e4m3 with per-tensor
+ * amax scaling") names this scheme.  For x fp16 [M, K] (activations, or an
+ * nn.Linear weight [N, K]):
+ *   amax = max |x|;  s = amax / 448 (f32 division) if 0 < amax < inf, else 1;
+ *   code = e4m3_rne_sat(f32(x) * f32(1 / s)).
+ * Every scale[r] (r < M) receives s, so the FP8 GEMM applies it unchanged.
+ * Two launches: per-block partial maxima into ws (EE_TENSOR_WS_FLOATS floats
+ * of caller workspace), then the quantiser, which reduces them itself. */
+#define EE_TENSOR_WS_FLOATS 1024
+int ee_quant_tensor_f8(ee_engine* eng, const void* x, int64_t M, int64_t K, int64_t ld_x, uint8_t* codes,
+                       int64_t ld_c, float* scale, float* ws, ee_stream_t stream);
 
 /* dst[c, r] = src[r, c] for int8 [R, C]. */
 int ee_transpose_i8(ee_engine* eng, const int8_t* src, int64_t R, int64_t C, int64_t ld_src,

@@ -62,6 +62,7 @@ def lib() -> ctypes.CDLL:
             "eo_quant_act_i8_dispatch": ([_p, _i64, _i64, _i64, _p, _i64, _p], None),
             "eo_quant_act_i8_engine": ([_p, _i64, _i64, _i64, _p, _i64, _p], None),
             "eo_quant_act_f8": ([_p, _i64, _i64, _i64, _p, _i64, _p], None),
+            "eo_quant_tensor_f8": ([_p, _i64, _i64, _i64, _p, _i64, _p], None),
             "eo_quant_weight_i8": ([_p, _i64, _i64, _i64, _p, _i64, _p], None),
             "eo_gemm_i8_acc": ([_p, _i64, _p, _i64, _p, _i64, _i64, _i64, _i64], None),
             "eo_epilogue_i8": ([_p, _i64, _p, _p, _p, _i64, _i64, _i64], None),
@@ -178,6 +179,17 @@ def quant_act_f8(a):
     codes = np.empty((M, K), np.uint8)
     scale = np.empty(M, np.float32)
     lib().eo_quant_act_f8(_ptr(a16), M, K, K, _ptr(codes), K, _ptr(scale))
+    return codes, scale
+
+
+def quant_tensor_f8(a):
+    """Per-tensor FP8 e4m3 codes (uint8) + f32 scale per row (all equal): the
+    build's definition of BASELINE config 1's scheme (no reference counterpart)."""
+    a16 = _f16_2d(a)
+    M, K = a16.shape
+    codes = np.empty((M, K), np.uint8)
+    scale = np.empty(M, np.float32)
+    lib().eo_quant_tensor_f8(_ptr(a16), M, K, K, _ptr(codes), K, _ptr(scale))
     return codes, scale
 
 

@@ -218,6 +218,31 @@ EO_API void eo_quant_act_f8(const uint16_t* A, int64_t M, int64_t K, int64_t lda
     }
 }
 
+/* FP8 e4m3 with one scale per tensor.  No counterpart in the reference (its
+ * FP8 tier scales per row, EE/python/kernels.py:361); BASELINE config 1 names
+ * the scheme and this is the build's definition of it:
+ *   amax = max |x| over the tensor (NaN propagates);
+ *   s = amax / 448 (f32 division) if 0 < amax < inf, else 1;  inv = 1 / s (f32);
+ *   code = e4m3_rne_sat(f32(x) * inv);   scale[r] = s for every row r. */
+EO_API void eo_quant_tensor_f8(const uint16_t* A, int64_t M, int64_t K, int64_t lda,
+                               uint8_t* codes, int64_t ldc, float* scale) {
+    float amax = 0.0f;
+    for (int64_t i = 0; i < M && amax == amax; ++i)
+        for (int64_t k = 0; k < K; ++k) {
+            float v = fabsf(eo_f16_to_f32(A[i * lda + k]));
+            if (v > amax || v != v) amax = v;
+            if (amax != amax) break;
+        }
+    volatile float d448 = 448.0f, one = 1.0f;
+    const float s = (amax > 0.0f && amax < INFINITY) ? amax / d448 : 1.0f;
+    const float inv = one / s;
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < M; ++i) {
+        scale[i] = s;
+        for (int64_t k = 0; k < K; ++k) codes[i * ldc + k] = eo_e4m3_from_f32(eo_f16_to_f32(A[i * lda + k]) * inv);
+    }
+}
+
 /* a7: offline weight quantiser, EE/python/dispatch.py:43-48
  *   w = W.float().t()   [K, N];  scale = (amax_k |w| / 127.0).clamp(min=1e-8)
  *   code = (w / scale).round().clamp(-127, 127).to(int8)       -> [K, N]

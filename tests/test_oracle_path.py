@@ -4,7 +4,8 @@ Quantisers: the reference's PyTorch expressions evaluated by torch on the
 CPU, with one substitution -- the reference ran them on the GPU, where
 `tensor / python_float` multiplies by the binary32 reciprocal (ATen's
 div_true for a CPU-scalar divisor).  That substitution is itself checked on
-the GPU in tests/test_gpu_torch_semantics.py.
+the GPU (tests/test_gpu_parity.py,
+test_torch_gpu_scalar_division_is_reciprocal_multiply).
 GEMMs: torch._int_mm, brute-force Python integers, numpy float64.
 Entropy: closed forms, invariants and the textbook -sum p ln p in float64.
 Routing: the reference's own known answers.
@@ -75,6 +76,40 @@ def test_quant_act_f8(orc, scale_in):
     assert np.array_equal(scale.view(np.uint32), s.numpy().view(np.uint32))
     assert np.array_equal(codes, ref.numpy())
     assert np.all(codes[3] & 0x7F == 0x7F)
+
+
+def _tensor_f8_torch(a):
+    """The per-tensor FP8 definition evaluated by numpy (f32 divisions and
+    product, RNE) and torch's float8_e4m3fn cast (clamped to +-448 first:
+    torch's cast does not saturate)."""
+    amax = np.float32(np.abs(a.astype(np.float32)).max())
+    s = np.float32(amax / np.float32(448)) if 0 < amax < np.inf else np.float32(1)
+    inv = np.float32(1) / s
+    x = a.astype(np.float32) * inv
+    codes = torch.from_numpy(x).clamp(-448, 448).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    return codes, s
+
+
+def test_quant_tensor_f8(orc):
+    """Per-tensor FP8 (BASELINE config 1's scheme; the build's own definition)."""
+    rng = np.random.default_rng(30)
+    for a in (_acts(rng, 64, 512, outliers=0.001),                      # config 1 style: +-20 outliers
+              (rng.standard_normal((33, 100)) * 0.02).astype(np.float16),   # weight-like
+              (rng.standard_normal((5, 64)) * 3e-5).astype(np.float16)):    # subnormal-heavy
+        codes, scale = orc.quant_tensor_f8(a)
+        ref, s = _tensor_f8_torch(a)
+        assert np.all(scale == s) and np.array_equal(codes, ref)
+    # amax = 448 * 2^k: s is a power of two and the max element codes to +-448 exactly
+    a = np.float16([[896.0, -896.0, 1.0, 0.0]])
+    codes, scale = orc.quant_tensor_f8(a)
+    assert scale[0] == 2.0 and codes[0].tolist() == [0x7E, 0xFE, 0x30, 0x00]
+    # all-zero or non-finite amax: s = 1
+    codes, scale = orc.quant_tensor_f8(np.zeros((2, 8), np.float16))
+    assert np.all(scale == 1.0) and not codes.any()
+    a = np.float16([[np.inf, 1.0, -2.0, np.nan]])
+    codes, scale = orc.quant_tensor_f8(a)
+    assert scale[0] == 1.0 and codes[0, 1] == 0x38 and codes[0, 2] == 0xC0 and codes[0, 0] == 0x7E
+    assert codes[0, 3] & 0x7F == 0x7F
 
 
 def test_quantize_weights_int8(orc):

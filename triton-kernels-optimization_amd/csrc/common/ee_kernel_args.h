@@ -41,6 +41,17 @@ struct EeQuantArgs {
     int64_t ld_c;
     int32_t mode;
     int32_t tier;           // which counts[] entry / idx segment (routing)
+    const uint32_t* tmax;   // EE_QUANT_F8_TENSOR: per-block |x| maxima (fp16 bits)
+    int32_t n_tmax;         //   and their count
+};
+
+// Per-block max |x| over fp16 rows (first pass of the per-tensor FP8 scale).
+struct EeAbsmaxArgs {
+    const uint16_t* x;      // fp16 [M, K], row stride ld_x
+    uint32_t* out;          // [gridDim.x] max |x| as fp16 bits (NaN propagates)
+    int64_t M;
+    int64_t K;
+    int64_t ld_x;
 };
 
 // Tiled GEMM on MFMA.  C[m, n] = sum_k A[m, k] * B[n, k]  (B packed K-contiguous).

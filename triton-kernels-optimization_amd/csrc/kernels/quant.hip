@@ -53,11 +53,22 @@ EE_DEV RowScale row_scale(int mode, float amax) {
         if (s < 1e-8f) s = 1e-8f;            // clamp(min=1e-8); NaN stays NaN
         r.s = s;
         r.mul = 0.f;
-    } else {
+    } else if (mode == EE_QUANT_F8_ROW) {
         r.s = f16_round(amax * INV448);
         r.mul = f16_round(1.0f / r.s);
+    } else {                                  // EE_QUANT_F8_TENSOR: amax is the tensor's
+        r.s = (amax > 0.0f && amax < INFINITY) ? amax / 448.0f : 1.0f;
+        r.mul = 1.0f / r.s;
     }
     return r;
+}
+
+// EE_QUANT_F8_TENSOR: max |x| of the whole tensor from the per-block maxima of
+// eek_absmax_partial (fp16 bits; NaN sorts above inf).  Wave-uniform.
+EE_DEV float tensor_amax(const EeQuantArgs& a) {
+    uint32_t m = 0;
+    for (int i = lane_id(); i < a.n_tmax; i += 64) m = max(m, a.tmax[i]);
+    return f16_lo(wave_max_u32(m));
 }
 
 EE_DEV uint32_t quant_one(int mode, float x, const RowScale& rs) {
@@ -71,6 +82,8 @@ EE_DEV uint32_t quant_one(int mode, float x, const RowScale& rs) {
         float r = rintf(x / rs.s);
         r = fminf(fmaxf(r, -127.0f), 127.0f);
         return (r != r) ? 0u : ((uint32_t)(int32_t)r & 0xffu);
+    } else if (mode == EE_QUANT_F8_TENSOR) {
+        return e4m3_rne_sat(x * rs.mul);
     } else {
         // fp16 x fp16 -> fp16 (RNE), as the reference multiplies its fp16 tile by the
         // fp16 inverse scale.  Written as a half-precision product on purpose: the
@@ -128,7 +141,7 @@ EE_DEV void quant_vec(const EeQuantArgs& a) {
         for (int i = 1; i < WPR; ++i) am = max(am, slot[base + i]);
     }
     if (!valid) return;
-    const RowScale rs = row_scale(a.mode, f16_lo(am));
+    const RowScale rs = row_scale(a.mode, a.mode == EE_QUANT_F8_TENSOR ? tensor_amax(a) : f16_lo(am));
     uint8_t* cr = (uint8_t*)a.codes + dst * a.ld_c;
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
@@ -166,7 +179,7 @@ EE_DEV void quant_generic(const EeQuantArgs& a) {
     uint32_t am = 0;
     for (int64_t c = lane; c < a.K; c += 64) am = max(am, (uint32_t)(xr[c] & 0x7fffu));
     am = wave_max_u32(am);
-    const RowScale rs = row_scale(a.mode, f16_lo(am));
+    const RowScale rs = row_scale(a.mode, a.mode == EE_QUANT_F8_TENSOR ? tensor_amax(a) : f16_lo(am));
     uint8_t* cr = (uint8_t*)a.codes + dst * a.ld_c;
     for (int64_t c = lane; c < a.K; c += 64) cr[c] = (uint8_t)quant_one(a.mode, f16_lo(xr[c]), rs);
     if (lane == 0) a.scale[dst] = rs.s;
@@ -187,6 +200,33 @@ EE_Q_VEC_W(7)
 EE_Q_VEC_W(8)
 
 extern "C" __global__ void __launch_bounds__(EE_BLOCK) eek_quant_generic(EeQuantArgs a) { quant_generic(a); }
+
+// First pass of the per-tensor FP8 scale: out[b] = max |x| over the rows
+// b*4 + w, b*4 + w + 4*gridDim.x, ... (w = wave), as fp16 bits.
+extern "C" __global__ void __launch_bounds__(EE_BLOCK) eek_absmax_partial(EeAbsmaxArgs a) {
+    __shared__ uint32_t red[4];
+    const int lane = lane_id(), w = wave_id();
+    uint32_t m = 0;
+    for (int64_t r = (int64_t)blockIdx.x * 4 + w; r < a.M; r += (int64_t)gridDim.x * 4) {
+        const uint16_t* xr = a.x + r * a.ld_x;
+        const bool vec = ((uintptr_t)xr & 15) == 0;
+        for (int64_t c = (int64_t)lane * 8; c < a.K; c += 512) {
+            if (vec && c + 8 <= a.K) {
+                const u32x4 v = *(const u32x4*)(xr + c);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) m = absmax_bits(m, v[i]);
+            } else {
+                for (int i = 0; i < 8; ++i)
+                    if (c + i < a.K) m = absmax_bits(m, (uint32_t)xr[c + i]);
+            }
+        }
+    }
+    m = max(m & 0xffffu, m >> 16);
+    m = wave_max_u32(m);
+    if (lane == 0) red[w] = m;
+    __syncthreads();
+    if (threadIdx.x == 0) a.out[blockIdx.x] = max(max(red[0], red[1]), max(red[2], red[3]));
+}
 
 // ---------------------------------------------------------------------------
 // Weight preparation.  The GEMMs read B as [N, K] (K contiguous, the MFMA

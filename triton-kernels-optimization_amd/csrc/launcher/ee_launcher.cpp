@@ -10,6 +10,7 @@
 // (engine.cpp:168-199), on a real JSON parser.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdio>
 #include <cstring>
 #include <fstream>
@@ -403,6 +404,17 @@ EE_EXPORT int ee_softmax_entropy(ee_engine* eng, const void* x, void* p, float* 
     return launch(eng, "eek_softmax_entropy_generic", cdiv(rows, 4), 1, EE_BLOCK, a, stream);
 }
 
+// The register-resident row kernel when rows are 16-byte aligned and fit, else the generic one.
+static int launch_quant(ee_engine* eng, const EeQuantArgs& a, ee_stream_t stream) {
+    const bool vec_ok = aligned(a.x, 16) && aligned(a.codes, 8) && a.ld_x % 8 == 0 && a.ld_c % 8 == 0;
+    int vpt = 0, wpr = 0;
+    if (vec_ok && pick_row_cfg(a.K, a.M, opt(eng, "quant_wpr"), vpt, wpr)) {
+        const std::string name = "eek_quant_v" + std::to_string(vpt) + "_w" + std::to_string(wpr);
+        return launch(eng, name, cdiv(a.M, 4 / wpr), 1, EE_BLOCK, a, stream);
+    }
+    return launch(eng, "eek_quant_generic", cdiv(a.M, 4), 1, EE_BLOCK, a, stream);
+}
+
 EE_EXPORT int ee_quant_act(ee_engine* eng, const void* x, int64_t M, int64_t K, int64_t ld_x, int32_t mode,
                            void* codes, int64_t ld_c, float* scale, const int32_t* idx, const int32_t* counts,
                            int32_t tier, ee_stream_t stream) {
@@ -411,20 +423,35 @@ EE_EXPORT int ee_quant_act(ee_engine* eng, const void* x, int64_t M, int64_t K, 
         return fail(EE_ERR_INVALID_ARG, "x, codes and scale must not be NULL");
     if (M < 0 || K <= 0) return fail(EE_ERR_INVALID_ARG, "need M >= 0 and K > 0");
     if (ld_x < K || ld_c < K) return fail(EE_ERR_INVALID_ARG, "row stride smaller than K");
+    if (mode == EE_QUANT_F8_TENSOR)
+        return fail(EE_ERR_INVALID_ARG, "EE_QUANT_F8_TENSOR needs a workspace: use ee_quant_tensor_f8");
     if (mode < EE_QUANT_I8_DISPATCH || mode > EE_QUANT_F8_ROW) return fail(EE_ERR_INVALID_ARG, "unknown quant mode");
     if ((idx != nullptr) && counts == nullptr) return fail(EE_ERR_INVALID_ARG, "idx needs counts");
     if (counts != nullptr && (tier < 0 || tier > 2)) return fail(EE_ERR_INVALID_ARG, "tier must be 0, 1 or 2");
     if (!aligned(x, 2) || !aligned(scale, 4) || !aligned(idx, 4) || !aligned(counts, 4))
         return fail(EE_ERR_INVALID_ARG, "misaligned pointer");
     if (M == 0) return EE_OK;
-    EeQuantArgs a{(const uint16_t*)x, codes, scale, idx, counts, M, K, ld_x, ld_c, mode, counts ? tier : 0};
-    const bool vec_ok = aligned(x, 16) && aligned(codes, 8) && ld_x % 8 == 0 && ld_c % 8 == 0;
-    int vpt = 0, wpr = 0;
-    if (vec_ok && pick_row_cfg(K, M, opt(eng, "quant_wpr"), vpt, wpr)) {
-        const std::string name = "eek_quant_v" + std::to_string(vpt) + "_w" + std::to_string(wpr);
-        return launch(eng, name, cdiv(M, 4 / wpr), 1, EE_BLOCK, a, stream);
-    }
-    return launch(eng, "eek_quant_generic", cdiv(M, 4), 1, EE_BLOCK, a, stream);
+    EeQuantArgs a{(const uint16_t*)x, codes, scale, idx, counts, M, K, ld_x, ld_c, mode, counts ? tier : 0,
+                  nullptr, 0};
+    return launch_quant(eng, a, stream);
+}
+
+EE_EXPORT int ee_quant_tensor_f8(ee_engine* eng, const void* x, int64_t M, int64_t K, int64_t ld_x, uint8_t* codes,
+                                 int64_t ld_c, float* scale, float* ws, ee_stream_t stream) {
+    if (eng == nullptr) return fail(EE_ERR_INVALID_ARG, "engine must not be NULL");
+    if (x == nullptr || codes == nullptr || scale == nullptr || ws == nullptr)
+        return fail(EE_ERR_INVALID_ARG, "x, codes, scale and ws must not be NULL");
+    if (M < 0 || K <= 0) return fail(EE_ERR_INVALID_ARG, "need M >= 0 and K > 0");
+    if (ld_x < K || ld_c < K) return fail(EE_ERR_INVALID_ARG, "row stride smaller than K");
+    if (!aligned(x, 2) || !aligned(scale, 4) || !aligned(ws, 4)) return fail(EE_ERR_INVALID_ARG, "misaligned pointer");
+    if (M == 0) return EE_OK;
+    const int64_t nblk = std::min<int64_t>(EE_TENSOR_WS_FLOATS, cdiv(M, 4));
+    EeAbsmaxArgs p{(const uint16_t*)x, (uint32_t*)ws, M, K, ld_x};
+    int rc = launch(eng, "eek_absmax_partial", nblk, 1, EE_BLOCK, p, stream);
+    if (rc) return rc;
+    EeQuantArgs a{(const uint16_t*)x, codes, scale, nullptr, nullptr, M, K, ld_x, ld_c, EE_QUANT_F8_TENSOR, 0,
+                  (const uint32_t*)ws, (int32_t)nblk};
+    return launch_quant(eng, a, stream);
 }
 
 EE_EXPORT int ee_quant_weight_i8(ee_engine* eng, const void* w, int64_t N, int64_t K, int64_t ld_w,

@@ -9,14 +9,15 @@ dispatch.py (IqtedarU/triton-kernels-optimization, entropy-engine/python).
 from .dispatch import (EntropyDispatchedLinear, PipelinedEntropyDispatcher, PrecisionTier, RowEntropyRouter,
                        quantize_weights_int8, tier_of)
 from .engine import CubinEngine, HsacoEngine
-from .kernels import (PackedWeight, fused_softmax_entropy, gemm, prepare_weight, quantize_activations,
-                      quantize_weight_codes, route, routed_linear, row_copy, softmax_entropy, transpose_i8,
-                      triton_fp8_gemm, triton_fp16_gemm, triton_int8_gemm)
+from .kernels import (PackedWeight, fp8_tensor_gemm, fused_softmax_entropy, gemm, prepare_weight,
+                      quantize_activations, quantize_tensor_fp8, quantize_weight_codes, route, routed_linear, row_copy,
+                      softmax_entropy, transpose_i8, triton_fp8_gemm, triton_fp16_gemm, triton_int8_gemm)
 
 __all__ = [
     "EntropyDispatchedLinear", "PipelinedEntropyDispatcher", "PrecisionTier", "RowEntropyRouter",
     "quantize_weights_int8", "tier_of", "CubinEngine", "HsacoEngine", "PackedWeight", "fused_softmax_entropy",
     "gemm", "prepare_weight", "quantize_activations", "quantize_weight_codes", "route", "routed_linear", "row_copy",
+    "fp8_tensor_gemm", "quantize_tensor_fp8",
     "softmax_entropy", "transpose_i8",
     "triton_fp8_gemm", "triton_fp16_gemm", "triton_int8_gemm",
 ]

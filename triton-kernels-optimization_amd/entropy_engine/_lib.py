@@ -30,7 +30,8 @@ STATUS_NAMES = {0: "EE_OK", -1: "EE_ERR_INVALID_ARG", -2: "EE_ERR_IO", -3: "EE_E
                 -5: "EE_ERR_UNSUPPORTED", -6: "EE_ERR_NOT_FOUND"}
 
 # quantiser modes / GEMM kinds / tiers
-EE_QUANT_I8_DISPATCH, EE_QUANT_I8_ENGINE, EE_QUANT_F8_ROW = 0, 1, 2
+EE_QUANT_I8_DISPATCH, EE_QUANT_I8_ENGINE, EE_QUANT_F8_ROW, EE_QUANT_F8_TENSOR = 0, 1, 2, 3
+EE_TENSOR_WS_FLOATS = 1024
 EE_GEMM_I8, EE_GEMM_F8, EE_GEMM_F16 = 0, 1, 2
 
 _p = ctypes.c_void_p
@@ -48,6 +49,7 @@ SIGNATURES = {
     "ee_softmax_entropy": ([_p, _p, _p, _p, _i64, _i32, _i64, _i64, _i32, _p, _f64, _f64, _p], ctypes.c_int),
     "ee_quant_act": ([_p, _p, _i64, _i64, _i64, _i32, _p, _i64, _p, _p, _p, _i32, _p], ctypes.c_int),
     "ee_quant_weight_i8": ([_p, _p, _i64, _i64, _i64, _p, _i64, _p, _p], ctypes.c_int),
+    "ee_quant_tensor_f8": ([_p, _p, _i64, _i64, _i64, _p, _i64, _p, _p, _p], ctypes.c_int),
     "ee_transpose_i8": ([_p, _p, _i64, _i64, _i64, _p, _i64, _p], ctypes.c_int),
     "ee_pack_b_f8": ([_p, _p, _i64, _i64, _i64, _p, _i64, _p], ctypes.c_int),
     "ee_pack_b_f16": ([_p, _p, _p, _i64, _i64, _i64, _p, _i64, _p], ctypes.c_int),

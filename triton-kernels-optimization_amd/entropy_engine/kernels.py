@@ -128,6 +128,27 @@ def quantize_activations(a: torch.Tensor, mode: str = "dispatcher", idx=None, co
     return codes, scale
 
 
+def quantize_tensor_fp8(x: torch.Tensor):
+    """FP8 e4m3 codes with ONE scale for the whole tensor -- BASELINE config 1's
+    "per-tensor amax" scheme, which the reference does not have (its FP8 tier
+    scales per row, EE/python/kernels.py:361):
+        s = amax|x| / 448 (1 if amax is 0 or not finite); code = e4m3(f32(x) * f32(1/s)).
+    x fp16 [R, K] (activations, or an nn.Linear weight [N, K]) -> (codes uint8
+    [R, K], scale f32 [R] holding s in every entry, as the FP8 GEMM expects)."""
+    dev = _require_cuda(x)
+    if x.dtype != torch.float16:
+        raise TypeError("x must be float16")
+    ldx = _rowmajor(x, "x")
+    R, K = x.shape
+    codes = torch.empty((R, K), dtype=torch.uint8, device=dev)
+    scale = torch.empty(R, dtype=torch.float32, device=dev)
+    ws = torch.empty(_lib.EE_TENSOR_WS_FLOATS, dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        check(_lib.lib().ee_quant_tensor_f8(engine(), ptr(x), R, K, ldx, ptr(codes), K, ptr(scale), ptr(ws),
+                                            stream_handle()))
+    return codes, scale
+
+
 def quantize_weight_codes(weight: torch.Tensor):
     """nn.Linear weight fp16 [N, K] -> (int8 codes [N, K], f32 scale [N]),
     the per-channel quantiser of EE/python/dispatch.py:43-48 in operand order."""
@@ -285,6 +306,14 @@ def triton_fp16_gemm(a: torch.Tensor, b_int8: torch.Tensor, b_scale: torch.Tenso
         a = a.contiguous()
     pw = prepare_weight(b_int8, b_scale)
     return gemm("fp16", a, pw.f16)
+
+
+def fp8_tensor_gemm(a: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+    """a fp16 [M, K] @ weight fp16 [N, K]^T with per-tensor e4m3 scaling of both
+    operands (quantize_tensor_fp8) on the FP8 MFMA GEMM: fp16((acc * s_a) * s_w)."""
+    ca, sa = quantize_tensor_fp8(a)
+    cw, sw = quantize_tensor_fp8(weight)
+    return gemm("fp8", ca, cw, sa, sw)
 
 
 # ---------------------------------------------------------------- routing
