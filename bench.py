@@ -52,6 +52,35 @@ ER, ES = 1024, 4096            # entropy rows x columns
 COPY_BYTES = 256 << 20         # calibration copy for the FETCH_SIZE / WRITE_SIZE counters
 
 
+def mixture_logits(rng, M: int, S: int, fractions=(0.2, 0.4, 0.4),
+                   bands=((0.05, 0.36), (0.46, 1.62), (1.75, 7.5))):
+    """Config 3's routing logits: fp16 [M, S] rows whose entropies fall ~20% below
+    0.41, ~40% in [0.41, 1.68) and ~40% above 1.68 nats.  Each row is N(0,1)
+    background plus one spike column; with spike mass p and background entropy
+    H_b the row entropy is H(p) = -p ln p - (1-p) ln(1-p) + (1-p) H_b, which is
+    solved for p by bisection toward a target drawn from the row's band.
+    Returns (logits fp16, class per row)."""
+    import numpy as np
+    x = rng.standard_normal((M, S))
+    m = x.max(axis=1, keepdims=True)
+    e = np.exp(x - m)
+    zb = e.sum(axis=1)
+    pb = e / zb[:, None]
+    hb = -(pb * np.log(pb)).sum(axis=1)
+    cls = rng.choice(3, M, p=fractions)
+    lo = np.array([b[0] for b in bands])[cls]
+    hi = np.array([b[1] for b in bands])[cls]
+    target = lo + (hi - lo) * rng.random(M)
+    a, b = np.full(M, 1e-9), np.full(M, 1 - 1e-12)
+    for _ in range(60):
+        p = 0.5 * (a + b)
+        h = -p * np.log(p) - (1 - p) * np.log1p(-p) + (1 - p) * hb
+        a, b = np.where(h > target, p, a), np.where(h > target, b, p)
+    p = 0.5 * (a + b)
+    x[np.arange(M), rng.integers(0, S, M)] = m[:, 0] + np.log(p * zb / (1 - p))
+    return x.astype(np.float16), cls
+
+
 def parse():
     ap = argparse.ArgumentParser(description="entropy-gated path benchmark (1 GPU)")
     ap.add_argument("--gpus", type=int, default=1)
@@ -189,6 +218,38 @@ def main():
             src = torch.empty(COPY_BYTES // 4, dtype=torch.float32, device=dev).fill_(1.0)
             dst = torch.empty_like(src)
             run("hbm_copy", lambda: dst.copy_(src))
+        # ---- config 3: the dispatcher end to end on a mixed batch (M = K = N = 4096)
+        c3 = None
+        c3_names = ("c3_entropy", "c3_route", "c3_linear", "c3_end_to_end")
+        if not only or any(n in only for n in c3_names):
+            M3 = K3 = N3 = 4096
+            L3, _ = mixture_logits(rng, M3, K3)
+            X3 = torch.from_numpy(rng.standard_normal((M3, K3), dtype=np.float32)).half()
+            W3 = (torch.from_numpy(rng.standard_normal((N3, K3), dtype=np.float32)) * 0.02).half()
+            l3, x3 = torch.from_numpy(L3).to(dev), X3.to(dev)
+            B3, bs3 = ee.quantize_weights_int8(W3.to(dev))
+            pw3 = ee.prepare_weight(B3, bs3).materialize()
+            out3 = torch.empty((M3, N3), dtype=torch.float16, device=dev)
+            ws3 = (torch.empty((M3, K3), dtype=torch.uint8, device=dev),
+                   torch.empty(M3, dtype=torch.float32, device=dev))
+            _, h3, _ = ee.softmax_entropy(l3, probs=False)
+            fr = {}
+            for tl, th in ((0.41, 1.68), (2.34, 6.03)):
+                _, _, cnt = ee.route(h3, tl, th)
+                fr[f"({tl},{th})"] = [round(v / M3, 4) for v in cnt.cpu().tolist()]
+            _, idx3, counts3 = ee.route(h3, 0.41, 1.68)
+
+            def c3_all():
+                _, h, _ = ee.softmax_entropy(l3, probs=False)
+                _, idx, counts = ee.route(h, 0.41, 1.68)
+                ee.routed_linear(x3, pw3, idx, counts, out=out3, workspace=ws3)
+
+            run("c3_entropy", lambda: ee.softmax_entropy(l3, probs=False))
+            run("c3_route", lambda: ee.route(h3, 0.41, 1.68))
+            run("c3_linear", lambda: ee.routed_linear(x3, pw3, idx3, counts3, out=out3, workspace=ws3))
+            run("c3_end_to_end", c3_all)
+            c3 = {"routing_fractions": fr, "thresholds_timed": [0.41, 1.68],
+                  "ops": 2.0 * M3 * N3 * K3}
     if only:
         print(json.dumps({k: v for k, v in results.items()}))
         return
@@ -221,6 +282,16 @@ def main():
                                     "TOPS": ops / (results["torch_int_mm"]["ms"] * 1e-3) / 1e12}
                                    if "torch_int_mm" in results else None),
     }
+    if c3 is not None:
+        kernels["dispatcher_c3"] = {
+            "us_end_to_end": results["c3_end_to_end"]["ms"] * 1e3,
+            "us_entropy": results["c3_entropy"]["ms"] * 1e3,
+            "us_route": results["c3_route"]["ms"] * 1e3,
+            "us_routed_linear": results["c3_linear"]["ms"] * 1e3,
+            "TOPS_routed_linear": c3["ops"] / (results["c3_linear"]["ms"] * 1e-3) / 1e12,
+            "routing_fractions_int8_fp8_fp16": c3["routing_fractions"],
+            "shape": "M=K=N=4096; entropy over fp16 [4096,4096] mixture logits",
+        }
     for k, r in results.items():                                       # both timings of every kernel, in us
         kernels.setdefault("timings_us", {})[k] = {
             "eager": r["ms_eager"] * 1e3, "graph": None if r["ms_graph"] is None else r["ms_graph"] * 1e3,

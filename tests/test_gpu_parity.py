@@ -526,3 +526,49 @@ def test_fp8_per_tensor_edge_cases(ee, orc):
     c, s = ee.quantize_tensor_fp8(view)
     oc, os_ = orc.quant_tensor_f8(big[:, :999])
     assert np.array_equal(host(c), oc) and np.array_equal(host(s), os_)
+
+
+# ---------------------------------------------------------------------------- config 3
+
+def test_config3_dispatcher(ee, orc):
+    """M = K = N = 4096 with row logits a seeded mixture of
+    ~20% low / 40% mid / 40% high-entropy rows (bench.mixture_logits).
+    entropy -> route under (0.41, 1.68) and under (2.34, 6.03) -> per-tier
+    GEMMs on the gathered rows -> scatter.  Entropy within 1e-5 relative of
+    the oracle; routing identical except rows within 1e-5 of a threshold;
+    fractions near 20/40/40 at (0.41, 1.68); sampled output rows of each tier
+    equal that tier's GEMM of the row (INT8 bit-exact, FP8 / FP16 within the
+    1e-2 bar of float64)."""
+    import bench
+    M = K = N = 4096
+    rng = np.random.default_rng(51)
+    L, _ = bench.mixture_logits(rng, M, K)
+    X = rng.standard_normal((M, K)).astype(np.float16)
+    W = (rng.standard_normal((N, K)) * 0.02).astype(np.float16)
+    B, bs = orc.quantize_weights_int8(W)
+    H_ref, _ = orc.softmax_entropy(L, probs=False)
+    _, h, _ = ee.softmax_entropy(cuda(L), probs=False)
+    check_entropy(host(h), H_ref)
+    pw = ee.prepare_weight(cuda(B), cuda(bs)).materialize()
+    x = cuda(X)
+    refs = (lambda r: orc.triton_int8_gemm(X[r], B, bs), lambda r: orc.triton_fp8_gemm_f64(X[r], B, bs),
+            lambda r: orc.triton_fp16_gemm_f64(X[r], B, bs))
+    for (tl, th), want in (((0.41, 1.68), (0.2, 0.4, 0.4)), ((2.34, 6.03), None)):
+        tier, idx, counts = ee.route(h, tl, th)
+        t = host(tier)
+        t_ref, _, _ = orc.route(H_ref.astype(np.float32), tl, th)
+        near = (np.abs(H_ref - tl) <= 1e-5) | (np.abs(H_ref - th) <= 1e-5)
+        assert np.array_equal(t[~near], t_ref[~near])
+        assert host(counts).tolist() == [int((t == k).sum()) for k in range(3)]
+        if want is not None:
+            assert np.allclose(host(counts) / M, want, atol=0.03)
+        out = host(ee.routed_linear(x, pw, idx, counts))
+        for k in range(3):
+            rows = np.flatnonzero(t == k)
+            if rows.size == 0:
+                continue
+            rows = np.sort(rng.choice(rows, min(12, rows.size), replace=False))
+            if k == 0:
+                assert np.array_equal(out[rows].view(np.uint16), refs[0](rows).view(np.uint16))
+            else:
+                check_close_f64(out[rows], refs[k](rows))
