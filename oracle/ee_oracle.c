@@ -443,8 +443,10 @@ EO_API void eo_softmax_entropy(const uint16_t* X, int64_t R, int64_t S, int64_t 
                 else {
                     double v = eo_f16_to_f32(x[c]);
                     p = (v == -INFINITY) ? 0.0 : exp(v - m) / Z;
-                    if (h != h) p = NAN;
                 }
+                /* no finite maximum (all -inf, or a NaN entry): the reference's
+                 * e^(x - m) is NaN for every column, masked ones included */
+                if (h != h) p = NAN;
                 if (P) P[r * S + c] = p;
                 if (P16) P16[r * S + c] = eo_f32_to_f16((float)p);
             }

@@ -38,6 +38,12 @@ def host(t):
     return t.cpu().numpy()
 
 
+def _lib_set(ee, key, value):
+    """Engine option through the C ABI (row-split overrides for coverage)."""
+    from entropy_engine import _lib
+    _lib.check(_lib.lib().ee_engine_set_option(_lib.engine(), key.encode(), value))
+
+
 def logits_rows(rng, R, S, scales=(0.25, 1.0, 4.0, 16.0)):
     s = rng.choice(np.asarray(scales), R)
     return (rng.standard_normal((R, S)) * s[:, None]).astype(np.float16)
@@ -128,6 +134,31 @@ def test_softmax_entropy_closed_forms(ee, orc):
     assert h[4] == 0.0
     H_ref, _ = orc.softmax_entropy(X)
     check_entropy(h, H_ref)
+
+
+@pytest.mark.parametrize("S", [64, 4096, 5000])
+def test_softmax_entropy_rows_without_a_finite_max(ee, orc, S):
+    """All -inf rows and rows holding a NaN are NaN in H and in every probability,
+    as in the reference; other rows are unaffected.  Every row split."""
+    rng = np.random.default_rng(S)
+    X = rng.standard_normal((8, S)).astype(np.float16)
+    X[1] = -np.inf
+    X[3, S // 3] = np.nan
+    X[5, :] = -np.inf
+    X[5, S - 1] = np.nan
+    H_ref, P_ref = orc.softmax_entropy(X)
+    try:
+        for w in (0, 1, 2, 4):
+            _lib_set(ee, "se_wpr", w)
+            p, h, _ = ee.softmax_entropy(cuda(X))
+            h, p = host(h), host(p)
+            assert np.array_equal(np.isnan(h), np.isnan(H_ref)) and np.isnan(h[[1, 3, 5]]).all()
+            assert np.isnan(p[[1, 3, 5]]).all() and not np.isnan(p[[0, 2, 4, 6, 7]]).any()
+            ok = ~np.isnan(H_ref)
+            check_entropy(h[ok], H_ref[ok])
+            check_probs(p[ok], P_ref[ok])
+    finally:
+        _lib_set(ee, "se_wpr", 0)
 
 
 def test_softmax_entropy_causal_4d(ee, orc):

@@ -226,6 +226,19 @@ def test_entropy_closed_forms(orc):
     assert np.all(P[1] == np.float16(1 / S))
 
 
+def test_entropy_rows_without_a_finite_max(orc):
+    """All -inf, or a NaN anywhere: the reference's e^(x - m) / Z is NaN for every
+    column (m = -inf gives -inf - -inf; a NaN poisons Z), so H and p are NaN."""
+    X = np.zeros((3, 64), np.float16)
+    X[0] = -np.inf
+    X[1, 7] = np.nan
+    H, P = orc.softmax_entropy(X)
+    assert np.isnan(H[0]) and np.isnan(H[1]) and np.isnan(P[:2]).all()
+    assert H[2] == pytest.approx(math.log(64), rel=1e-15) and not np.isnan(P[2]).any()
+    H, P = orc.softmax_entropy(np.full((2, 8), -np.inf, np.float16), causal=True)
+    assert np.isnan(H).all() and np.isnan(P).all()
+
+
 def test_entropy_vs_textbook_and_invariants(orc):
     rng = np.random.default_rng(10)
     R, S = 64, 1000

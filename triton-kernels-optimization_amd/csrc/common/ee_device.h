@@ -21,16 +21,60 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 EE_DEV int lane_id() { return (int)(threadIdx.x & 63); }
 EE_DEV int wave_id() { return (int)(threadIdx.x >> 6); }
 
-// Butterfly reductions across the 64 lanes of a wave (every lane gets the result).
+// Reductions across the 64 lanes of a wave, all lanes active; every lane gets
+// the (wave-uniform) result.  Within each 16-lane row, four DPP steps
+// (quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror, row_mirror)
+// leave the row's result in all its lanes; the four rows are then combined
+// from v_readlane.  No LDS traffic, unlike __shfl_xor (ds_bpermute).
+template <int CTRL>
+EE_DEV uint32_t dpp_u32(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, CTRL, 0xF, 0xF, false);
+}
+template <int CTRL>
+EE_DEV float dpp_f32(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+EE_DEV float lane_f32(float v, int l) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l)); }
+
 EE_DEV float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
+    v = fmaxf(v, dpp_f32<0xB1>(v));
+    v = fmaxf(v, dpp_f32<0x4E>(v));
+    v = fmaxf(v, dpp_f32<0x141>(v));
+    v = fmaxf(v, dpp_f32<0x140>(v));
+    return fmaxf(fmaxf(lane_f32(v, 0), lane_f32(v, 16)), fmaxf(lane_f32(v, 32), lane_f32(v, 48)));
+}
+// IEEE 754-2019 maximum (v_maximum_f32 / v_pk_maximum3_f16): a NaN operand gives NaN.
+EE_DEV float fmaximum(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+EE_DEV float wave_maximum(float v) {
+    v = fmaximum(v, dpp_f32<0xB1>(v));
+    v = fmaximum(v, dpp_f32<0x4E>(v));
+    v = fmaximum(v, dpp_f32<0x141>(v));
+    v = fmaximum(v, dpp_f32<0x140>(v));
+    return fmaximum(fmaximum(lane_f32(v, 0), lane_f32(v, 16)), fmaximum(lane_f32(v, 32), lane_f32(v, 48)));
 }
 EE_DEV float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
+    v += dpp_f32<0xB1>(v);
+    v += dpp_f32<0x4E>(v);
+    v += dpp_f32<0x141>(v);
+    v += dpp_f32<0x140>(v);
+    return (lane_f32(v, 0) + lane_f32(v, 16)) + (lane_f32(v, 32) + lane_f32(v, 48));
+}
+EE_DEV int32_t wave_sum_i32(int32_t v) {
+    v += (int32_t)dpp_u32<0xB1>((uint32_t)v);
+    v += (int32_t)dpp_u32<0x4E>((uint32_t)v);
+    v += (int32_t)dpp_u32<0x141>((uint32_t)v);
+    v += (int32_t)dpp_u32<0x140>((uint32_t)v);
+    return (__builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 16)) +
+           (__builtin_amdgcn_readlane(v, 32) + __builtin_amdgcn_readlane(v, 48));
+}
+EE_DEV uint32_t wave_max_u32(uint32_t v) {
+    v = max(v, dpp_u32<0xB1>(v));
+    v = max(v, dpp_u32<0x4E>(v));
+    v = max(v, dpp_u32<0x141>(v));
+    v = max(v, dpp_u32<0x140>(v));
+    const uint32_t a = max((uint32_t)__builtin_amdgcn_readlane((int)v, 0), (uint32_t)__builtin_amdgcn_readlane((int)v, 16));
+    const uint32_t b = max((uint32_t)__builtin_amdgcn_readlane((int)v, 32), (uint32_t)__builtin_amdgcn_readlane((int)v, 48));
+    return max(a, b);
 }
 
 EE_DEV f16x2 f16x2_from_bits(uint32_t u) {

@@ -32,11 +32,6 @@ EE_DEV uint32_t absmax_bits(uint32_t acc, uint32_t u) {
     a.v = __builtin_elementwise_max(a.v, b.v);
     return a.u;
 }
-EE_DEV uint32_t wave_max_u32(uint32_t v) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v = max(v, (uint32_t)__shfl_xor((int)v, o, 64));
-    return v;
-}
 
 struct RowScale {
     float s;     // scale stored per row

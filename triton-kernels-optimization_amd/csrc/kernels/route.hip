@@ -33,9 +33,7 @@ extern "C" __global__ void __launch_bounds__(1024) eek_route(EeRouteArgs a) {
     }
 #pragma unroll
     for (int t = 0; t < 3; ++t) {
-        int32_t v = c[t];
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+        const int32_t v = wave_sum_i32(c[t]);
         if (lane == 0) wsum[w][t] = v;
     }
     __syncthreads();

@@ -28,7 +28,7 @@ EE_DEV float row_reduce_max(float v, float (*slot)[4], int q) {
     const int base = (w / WPR) * WPR;
     float r = slot[base][q];
 #pragma unroll
-    for (int i = 1; i < WPR; ++i) r = fmaxf(r, slot[base + i][q]);
+    for (int i = 1; i < WPR; ++i) r = fmaximum(r, slot[base + i][q]);
     return r;
 }
 template <int WPR>
@@ -85,18 +85,24 @@ EE_DEV void softmax_entropy_vec(const EeSoftmaxArgs& a) {
         }
     }
 
-    // ---- max (packed fp16 max is exact)
+    // ---- max: packed fp16 maximum is exact and propagates NaN, so a NaN
+    // anywhere in the row (or no finite entry) makes the whole row NaN, as the
+    // reference's e^(x - m) / Z does.
     f16x2 mx2 = f16x2_from_bits(0xFC00FC00u);
 #pragma unroll
     for (int j = 0; j < VPT; ++j)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) mx2 = __builtin_elementwise_max(mx2, f16x2_from_bits(v[j][i]));
-    float m = fmaxf((float)mx2.x, (float)mx2.y);
-    m = wave_max(m);
+        for (int i = 0; i < 4; ++i) mx2 = __builtin_elementwise_maximum(mx2, f16x2_from_bits(v[j][i]));
+    float m = fmaximum((float)mx2.x, (float)mx2.y);
+    m = wave_maximum(m);
     m = row_reduce_max<WPR>(m, slot, 0);
+    const bool dead = !(m > -INFINITY);
+    if (dead) m = 0.0f;
 
-    // ---- exact sums: c0 (entries at the max), Z' (the others), T = sum e*s
-    float cz = 0.f, z0 = 0.f, z1 = 0.f, t0 = 0.f, t1 = 0.f;
+    // ---- exact sums: c0 (entries at the max, counted by ballot on the scalar
+    // unit), Z' (e over the others), T = sum e*s
+    int nmax = 0;
+    float z0 = 0.f, z1 = 0.f, t0 = 0.f, t1 = 0.f;
     float ek[KEEP_E ? VPT * 8 : 1];
 #pragma unroll
     for (int j = 0; j < VPT; ++j)
@@ -107,16 +113,16 @@ EE_DEV void softmax_entropy_vec(const EeSoftmaxArgs& a) {
             const float s = fmaxf(xv - m, -256.0f);          // -inf (masked) -> e = 0, e*s = 0
             const float e = __builtin_amdgcn_exp2f(s * LOG2E);
             const bool at_max = (s == 0.0f);
-            cz += at_max ? 1.0f : 0.0f;
+            nmax += __builtin_popcountll(__builtin_amdgcn_ballot_w64(at_max));
             if (i & 1) { z1 += at_max ? 0.0f : e; t1 = fmaf(e, s, t1); }
             else       { z0 += at_max ? 0.0f : e; t0 = fmaf(e, s, t0); }
             if (KEEP_E) ek[j * 8 + i] = e;
         }
     float z = wave_sum(z0 + z1);
     float t = wave_sum(t0 + t1);
-    cz = wave_sum(cz);
+    float cz = (float)nmax;                                  // already the wave's count
     row_reduce_sum3<WPR>(z, t, cz, slot);
-    const float H = entropy_from(cz, z, t);
+    const float H = dead ? NAN : entropy_from(cz, z, t);
     if (valid && wr == 0 && lane == 0) {
         a.h[row] = H;
         if (a.tier) a.tier[row] = tier_of(H, a.tau_low, a.tau_high);
@@ -124,7 +130,7 @@ EE_DEV void softmax_entropy_vec(const EeSoftmaxArgs& a) {
     if (a.p == nullptr || !valid) return;
 
     // ---- one write of the probabilities
-    const float invZ = 1.0f / (cz + z);
+    const float invZ = dead ? NAN : 1.0f / (cz + z);
     uint16_t* pr = a.p + row * a.ld_p;
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
@@ -166,8 +172,10 @@ EE_DEV void softmax_entropy_generic(const EeSoftmaxArgs& a) {
     const int nvalid = a.causal ? min(S, (int)(row % S) + 1) : S;
     const uint16_t* xr = a.x + row * a.ld_x;
     float m = -INFINITY;
-    for (int c = lane; c < nvalid; c += 64) m = fmaxf(m, f16_lo(xr[c]));
-    m = wave_max(m);
+    for (int c = lane; c < nvalid; c += 64) m = fmaximum(m, f16_lo(xr[c]));
+    m = wave_maximum(m);
+    const bool dead = !(m > -INFINITY);                // NaN or no finite entry: NaN row
+    if (dead) m = 0.0f;
     float cz = 0.f, z = 0.f, t = 0.f;
     for (int c = lane; c < nvalid; c += 64) {
         const float s = fmaxf(f16_lo(xr[c]) - m, -256.0f);
@@ -180,13 +188,13 @@ EE_DEV void softmax_entropy_generic(const EeSoftmaxArgs& a) {
     z = wave_sum(z);
     t = wave_sum(t);
     cz = wave_sum(cz);
-    const float H = entropy_from(cz, z, t);
+    const float H = dead ? NAN : entropy_from(cz, z, t);
     if (lane == 0) {
         a.h[row] = H;
         if (a.tier) a.tier[row] = tier_of(H, a.tau_low, a.tau_high);
     }
     if (a.p == nullptr) return;
-    const float invZ = 1.0f / (cz + z);
+    const float invZ = dead ? NAN : 1.0f / (cz + z);
     uint16_t* pr = a.p + row * a.ld_p;
     for (int c = lane; c < S; c += 64) {
         float e = 0.0f;
