@@ -603,3 +603,95 @@ def test_config3_dispatcher(ee, orc):
                 assert np.array_equal(out[rows].view(np.uint16), refs[0](rows).view(np.uint16))
             else:
                 check_close_f64(out[rows], refs[k](rows))
+
+
+# ---------------------------------------------------------------------------- Llama (config 4)
+
+def test_dispatched_linear_after_half(ee, orc):
+    """Module.half() casts weight_scale to fp16, as it does the reference's
+    buffer (whose kernels then read fp16 scales): the tiers use exactly those
+    fp16-rounded scales -- INT8 bit-exact, FP8 within the 1e-2 bar."""
+    rng = np.random.default_rng(61)
+    lin = torch.nn.Linear(512, 384, bias=False)
+    lin.weight.data = torch.from_numpy(rng.standard_normal((384, 512)).astype(np.float32) * 0.02)
+    layer = ee.EntropyDispatchedLinear.from_linear(lin.half().cuda()).half()
+    assert layer.weight_scale.dtype == torch.float16
+    x = rng.standard_normal((100, 512)).astype(np.float16)
+    B, bs16 = host(layer.weight_int8), host(layer.weight_scale).astype(np.float32)
+    y = host(layer(cuda(x), tier=ee.PrecisionTier.INT8))
+    assert np.array_equal(y.view(np.uint16), orc.triton_int8_gemm(x, B, bs16).view(np.uint16))
+    check_close_f64(host(layer(cuda(x), tier=ee.PrecisionTier.FP8)), orc.triton_fp8_gemm_f64(x, B, bs16))
+
+
+def test_dispatched_llama_block_against_hf(ee):
+    """EE/python/dispatch.py:150-247 with the reference harness's tiny config
+    (benchmark.py:220-277: hidden 256, 4 Q / 2 KV heads, eager attention, no
+    mask).  layer_entropy equals -sum p ln(p + 1e-10) over HF's own attention
+    weights (dispatch.py:243-245) within the fp16 rounding of p; the block's
+    output equals HF's attention + an MLP on the FP16 tier's (W8A16) weights;
+    with a dispatcher the tier follows the submitted entropy."""
+    pytest.importorskip("transformers")
+    from transformers import LlamaConfig, LlamaForCausalLM
+    import torch.nn.functional as F
+    torch.manual_seed(0)
+    config = LlamaConfig(hidden_size=256, intermediate_size=512, num_hidden_layers=2, num_attention_heads=4,
+                         num_key_value_heads=2, max_position_embeddings=128, vocab_size=1000,
+                         attn_implementation="eager")
+    model = LlamaForCausalLM(config).cuda().half().eval()
+    layer = model.model.layers[0]
+    block = ee.EntropyDispatchedLlamaBlock(layer, layer_idx=0).cuda().half().eval()
+    B, S = 2, 32
+    hidden = torch.randn(B, S, config.hidden_size, device="cuda", dtype=torch.float16)
+    pos = torch.arange(S, device="cuda").unsqueeze(0).expand(B, -1)
+    pe = model.model.rotary_emb(hidden, pos)
+    with torch.no_grad():
+        attn_ref, w = layer.self_attn(layer.input_layernorm(hidden), position_embeddings=pe, attention_mask=None)
+        h_ref = -(w.float() * torch.log(w.float() + 1e-10)).sum(dim=-1).mean(dim=(1, 2))
+        out = block(hidden, position_ids=pos, position_embeddings=pe)[0]
+        assert torch.allclose(block.layer_entropy, h_ref, rtol=5e-3)
+        h1 = hidden + attn_ref
+        x2 = layer.post_attention_layernorm(h1)
+        wg, wu, wd = block.gate_proj.weight_f16_nk, block.up_proj.weight_f16_nk, block.down_proj.weight_f16_nk
+        ref = h1 + F.linear(F.silu(F.linear(x2, wg)) * F.linear(x2, wu), wd)
+        assert out.shape == (B, S, config.hidden_size)
+        assert (out.float() - ref.float()).abs().max() <= 2e-2 * ref.float().abs().max()
+        d = ee.PipelinedEntropyDispatcher(tau_low=2.0, tau_high=3.5)
+        out2 = block(hidden, dispatcher=d, position_ids=pos, position_embeddings=pe)[0]
+        e = float(block.layer_entropy.max())
+        want = ee.tier_of(e, 2.0, 3.5).name
+        stats = d.get_stats()
+        assert stats[want]["count"] == 1 and torch.isfinite(out2).all()
+        blocks, disp = ee.build_dispatched_llama(model, 2.0, 3.5)
+        assert len(blocks) == 2 and isinstance(disp, ee.PipelinedEntropyDispatcher)
+
+
+SMALL_LLAMA = dict(layers=2, hidden=256, heads=4, kv_heads=2, head_dim=64, ffn=512, vocab=1000,
+                   rope_theta=10000.0, eps=1e-5)
+
+
+def test_entropy_gated_llama_small(ee):
+    """Config 4's model at a small size.  With thresholds below every entropy
+    all rows take the FP16 tier, and the logits equal an fp16 forward on the
+    W8A16-dequantised weights (up to GEMM summation order).  At (2.34, 6.03)
+    the gated logits stay close to the all-FP16 run, the per-tier row counts
+    cover every linear call, and routing mixes tiers per row."""
+    m = ee.EntropyGatedLlama.random_init(SMALL_LLAMA, seed=3)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(4)
+    ids = torch.randint(0, SMALL_LLAMA["vocab"], (2, 64), generator=g, device="cuda")
+    B, S = ids.shape
+    fp16 = m.forward(ids, gated=False).float()
+    out = m.forward(ids).float()
+    fr = m.last_fractions.tolist()
+    L = SMALL_LLAMA["layers"]
+    assert sum(fr) == B * S * (7 * L + 1)
+    assert torch.isfinite(out).all()
+    assert (out - fp16).abs().max() <= 0.1 * fp16.abs().max()
+    low = ee.EntropyGatedLlama(m.p, SMALL_LLAMA, tau_low=-1.0, tau_high=-1.0)
+    deq = dict(m.p)
+    for key, pw in m.packed.items():
+        deq["lm_head" if key == "lm_head" else f"{key[0]}.{key[1]}"] = pw.f16
+    ref = ee.EntropyGatedLlama(deq, SMALL_LLAMA).forward(ids, gated=False).float()
+    got = low.forward(ids).float()
+    assert low.last_fractions.tolist() == [0, 0, B * S * (7 * L + 1)]
+    assert (got - ref).abs().max() <= 1e-2 * ref.abs().max()

@@ -6,7 +6,8 @@ objects by a C-ABI launcher (include/entropy_engine.h) and driven from
 PyTorch-ROCm.  The Python API mirrors the reference's kernels.py and
 dispatch.py (IqtedarU/triton-kernels-optimization, entropy-engine/python).
 """
-from .dispatch import (EntropyDispatchedLinear, PipelinedEntropyDispatcher, PrecisionTier, RowEntropyRouter,
+from .dispatch import (TINYLLAMA_1B, EntropyDispatchedLinear, EntropyDispatchedLlamaBlock, EntropyGatedLlama,
+                       PipelinedEntropyDispatcher, PrecisionTier, RowEntropyRouter, build_dispatched_llama,
                        quantize_weights_int8, tier_of)
 from .engine import CubinEngine, HsacoEngine
 from .kernels import (PackedWeight, fp8_tensor_gemm, fused_softmax_entropy, gemm, prepare_weight,
@@ -15,6 +16,7 @@ from .kernels import (PackedWeight, fp8_tensor_gemm, fused_softmax_entropy, gemm
 
 __all__ = [
     "EntropyDispatchedLinear", "PipelinedEntropyDispatcher", "PrecisionTier", "RowEntropyRouter",
+    "EntropyDispatchedLlamaBlock", "EntropyGatedLlama", "TINYLLAMA_1B", "build_dispatched_llama",
     "quantize_weights_int8", "tier_of", "CubinEngine", "HsacoEngine", "PackedWeight", "fused_softmax_entropy",
     "gemm", "prepare_weight", "quantize_activations", "quantize_weight_codes", "route", "routed_linear", "row_copy",
     "fp8_tensor_gemm", "quantize_tensor_fp8",

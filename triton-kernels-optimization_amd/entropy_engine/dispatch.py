@@ -178,8 +178,22 @@ class EntropyDispatchedLinear(nn.Module):
             layer.bias = linear.bias.detach().to(device=w.device, dtype=torch.float16)
         return layer
 
+    def _scale_f32(self) -> torch.Tensor:
+        """The per-channel scale as f32 for the kernels.  Module.half() casts the
+        buffer to fp16 (as it does the reference's, whose Triton kernels then
+        read fp16 scales, kernels.py:103-104); the f32 copy of those values is
+        exact, so both see the same numbers."""
+        s = self.weight_scale
+        if s.dtype == torch.float32:
+            return s
+        key = (s.data_ptr(), s._version, s.dtype)
+        if getattr(self, "_scale_key", None) != key:
+            self._scale_cache = s.float().contiguous()
+            self._scale_key = key
+        return self._scale_cache
+
     def _packed(self) -> K.PackedWeight:
-        pw = K.PackedWeight(self.weight_i8_nk, self.weight_scale)
+        pw = K.PackedWeight(self.weight_i8_nk, self._scale_f32())
         pw._f8, pw._f16 = self.weight_f8_nk, self.weight_f16_nk
         return pw
 
@@ -216,3 +230,251 @@ class EntropyDispatchedLinear(nn.Module):
 
     def extra_repr(self):
         return f'in={self.in_features}, out={self.out_features}, bias={self.bias is not None}'
+
+
+# ============================================================================ Llama
+
+def _rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """Rotary embedding in the Llama convention: x*cos + rotate_half(x)*sin,
+    cos/sin [B or 1, S, head_dim] broadcast over heads."""
+    h = x.shape[-1] // 2
+    rot = torch.cat((-x[..., h:], x[..., :h]), dim=-1)
+    return x * cos.unsqueeze(1) + rot * sin.unsqueeze(1)
+
+
+def _attention_entropy(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scaling: float,
+                       attention_mask: Optional[torch.Tensor] = None, causal: bool = False):
+    """softmax(q k^T * scaling [+ mask]) v, the probabilities and their per-row
+    Shannon entropy from the fused softmax+entropy kernel (one pass over the
+    scores).  q [B, Hq, S, d], k/v [B, Hkv, Sk, d] fp16 (grouped-query heads
+    are repeated).  Returns (out [B, Hq, S, d] fp16, H [B, Hq, S] f32).
+    causal: key c of query s is kept iff c <= s (needs Sk == S)."""
+    B, Hq, S, d = q.shape
+    Hkv, Sk = k.shape[1], k.shape[2]
+    if Hkv != Hq:
+        k = k.repeat_interleave(Hq // Hkv, dim=1)
+        v = v.repeat_interleave(Hq // Hkv, dim=1)
+    scores = torch.matmul(q.contiguous(), k.transpose(-1, -2).contiguous()) * scaling
+    if attention_mask is not None:
+        scores = scores + attention_mask[..., :Sk].to(scores.dtype)
+    probs, H, _ = K.softmax_entropy(scores.reshape(-1, Sk), causal=causal and attention_mask is None)
+    out = torch.matmul(probs.view(B, Hq, S, Sk), v.contiguous())
+    return out, H.view(B, Hq, S)
+
+
+class EntropyDispatchedLlamaBlock(nn.Module):
+    """EE/python/dispatch.py:150-247 on the gfx950 path.
+
+    Wraps an HF Llama decoder layer: the MLP projections become
+    EntropyDispatchedLinear (one tier per call, from the dispatcher), and the
+    attention probabilities come from the fused softmax+entropy kernel, which
+    yields each probability row's Shannon entropy in the same pass.
+    layer_entropy is the mean row entropy per batch element [B] (f32): the
+    quantity the reference computes as -sum p ln(p + 1e-10) over HF's attention
+    weights (dispatch.py:243-245); the kernel's exact H = ln Z - sum p*s differs
+    from it only by the 1e-10 regulariser and the fp16 rounding of p.
+    attention_mask follows HF eager attention: an additive [B, 1, S, Sk] mask,
+    or None for unmasked attention (as in the reference's own test,
+    benchmark.py:220-277).  KV caches are outside this path."""
+
+    def __init__(self, llama_block, layer_idx: int = 0):
+        super().__init__()
+        self.layer_idx = layer_idx
+        self.self_attn = llama_block.self_attn
+        self.input_layernorm = llama_block.input_layernorm
+        self.post_attention_layernorm = llama_block.post_attention_layernorm
+        self.gate_proj = EntropyDispatchedLinear.from_linear(llama_block.mlp.gate_proj)
+        self.up_proj = EntropyDispatchedLinear.from_linear(llama_block.mlp.up_proj)
+        self.down_proj = EntropyDispatchedLinear.from_linear(llama_block.mlp.down_proj)
+        self.act_fn = nn.SiLU()
+        self.layer_entropy: Optional[torch.Tensor] = None
+        self._rotary = None
+
+    def forward(self, hidden_states: torch.Tensor, dispatcher: Optional[PipelinedEntropyDispatcher] = None,
+                attention_mask: Optional[torch.Tensor] = None, position_ids: Optional[torch.Tensor] = None,
+                past_key_value=None, use_cache: bool = False, **kwargs) -> Tuple[torch.Tensor, ...]:
+        if past_key_value is not None or use_cache:
+            raise NotImplementedError("EntropyDispatchedLlamaBlock: KV caches are not supported")
+        residual = hidden_states
+        hidden_states = self.input_layernorm(hidden_states)
+        attn_output, entropy_batch, _ = self._attention_with_fused_entropy(
+            hidden_states, attention_mask=attention_mask, position_ids=position_ids, **kwargs)
+        self.layer_entropy = entropy_batch
+        if dispatcher is not None:
+            dispatcher.submit_entropy(entropy_batch)
+        hidden_states = residual + attn_output
+        residual = hidden_states
+        hidden_states = self.post_attention_layernorm(hidden_states)
+        tier = dispatcher.get_tier() if dispatcher is not None else PrecisionTier.FP16
+        gate = self.gate_proj(hidden_states, tier=tier)
+        up = self.up_proj(hidden_states, tier=tier)
+        hidden_states = self.down_proj(self.act_fn(gate) * up, tier=tier)
+        hidden_states = residual + hidden_states
+        return (hidden_states,)
+
+    def _attention_with_fused_entropy(self, hidden_states: torch.Tensor, attention_mask=None, position_ids=None,
+                                      **kwargs):
+        attn = self.self_attn
+        B, S, _ = hidden_states.shape
+        hd = attn.head_dim
+        q = attn.q_proj(hidden_states).view(B, S, -1, hd).transpose(1, 2)
+        k = attn.k_proj(hidden_states).view(B, S, -1, hd).transpose(1, 2)
+        v = attn.v_proj(hidden_states).view(B, S, -1, hd).transpose(1, 2)
+        pe = kwargs.get("position_embeddings")
+        if pe is None:                      # isolated block: build the rotary tables from its config
+            if self._rotary is None:
+                from transformers.models.llama.modeling_llama import LlamaRotaryEmbedding
+                self._rotary = LlamaRotaryEmbedding(config=attn.config, device=hidden_states.device)
+            if position_ids is None:
+                position_ids = torch.arange(S, device=hidden_states.device).unsqueeze(0).expand(B, -1)
+            pe = self._rotary(hidden_states, position_ids)
+        cos, sin = pe
+        q, k = _rope(q, cos, sin), _rope(k, cos, sin)
+        out, H = _attention_entropy(q, k, v, attn.scaling, attention_mask)
+        out = attn.o_proj(out.transpose(1, 2).reshape(B, S, -1).contiguous())
+        return out, H.mean(dim=(1, 2)), None
+
+
+def build_dispatched_llama(model, tau_low: float, tau_high: float):
+    """EE/python/dispatch.py:250-260: every decoder layer of an HF Llama model
+    as an EntropyDispatchedLlamaBlock (fp16, eval), plus one dispatcher."""
+    device = next(model.parameters()).device
+    blocks = []
+    for i, layer in enumerate(model.model.layers):
+        block = EntropyDispatchedLlamaBlock(layer, layer_idx=i).to(device).half()
+        block.eval()
+        blocks.append(block)
+    return blocks, PipelinedEntropyDispatcher(tau_low=tau_low, tau_high=tau_high)
+
+
+TINYLLAMA_1B = dict(layers=22, hidden=2048, heads=32, kv_heads=4, head_dim=64, ffn=5632, vocab=32000,
+                    rope_theta=10000.0, eps=1e-5)
+
+_LINEARS = ("q", "k", "v", "o", "gate", "up", "down")
+
+
+class EntropyGatedLlama:
+    """A Llama forward in which EVERY linear layer routes each token row to the
+    INT8, FP8 or FP16 (W8A16) GEMM by entropy -- BASELINE config 4.  This
+    extends EE/python/dispatch.py:150-260, which gates only the MLP and picks
+    one tier per layer.
+
+    A token's routing entropy is the mean over heads of its attention-row
+    entropy (fused softmax+entropy kernel, causal): q/k/v of layer l use layer
+    l-1's (layer 0 runs them on the FP16 tier), o/gate/up/down use layer l's,
+    and the LM head uses the last layer's.  Rows are grouped per tier into one
+    launch per tier and scattered back (routed_linear); nothing syncs with the
+    host inside forward.  forward(..., gated=False) is the all-FP16 run: every
+    linear as a plain fp16 GEMM on the original weights (hipBLASLt).
+
+    Weights: fp16 tensors in `params` (embed [V, D]; per layer ln1, q [Hq*d, D],
+    k/v [Hkv*d, D], o [D, Hq*d], ln2, gate/up [F, D], down [D, F]; norm;
+    lm_head [V, D]).  RMSNorm and RoPE follow the Llama definitions."""
+
+    def __init__(self, params: dict, cfg: dict, tau_low: float = 2.34, tau_high: float = 6.03):
+        self.p = params
+        self.cfg = dict(cfg)
+        self.tau_low, self.tau_high = tau_low, tau_high
+        self.packed = {}
+        for l in range(cfg["layers"]):
+            for n in _LINEARS:
+                self.packed[(l, n)] = self._pack(params[f"{l}.{n}"])
+        self.packed["lm_head"] = self._pack(params["lm_head"])
+        self.last_fractions = None
+        self._rope_cache = {}
+
+    @staticmethod
+    def _pack(w: torch.Tensor) -> K.PackedWeight:
+        codes, scale = K.quantize_weight_codes(w)
+        return K.PackedWeight(codes, scale).materialize()
+
+    @classmethod
+    def random_init(cls, cfg: dict = TINYLLAMA_1B, seed: int = 0, device=None, std: float = 0.02, **kw):
+        """Random-init weights N(0, std) (RMSNorm weights 1), generated on the GPU."""
+        dev = device if device is not None else torch.device("cuda", torch.cuda.current_device())
+        g = torch.Generator(device=dev)
+        g.manual_seed(seed)
+        D, F, V = cfg["hidden"], cfg["ffn"], cfg["vocab"]
+        qd, kvd = cfg["heads"] * cfg["head_dim"], cfg["kv_heads"] * cfg["head_dim"]
+
+        def w(*shape):
+            return (torch.randn(*shape, generator=g, device=dev, dtype=torch.float32) * std).half()
+
+        p = {"embed": w(V, D), "norm": torch.ones(D, device=dev, dtype=torch.float16), "lm_head": w(V, D)}
+        for l in range(cfg["layers"]):
+            p[f"{l}.ln1"] = torch.ones(D, device=dev, dtype=torch.float16)
+            p[f"{l}.ln2"] = torch.ones(D, device=dev, dtype=torch.float16)
+            p[f"{l}.q"], p[f"{l}.k"], p[f"{l}.v"], p[f"{l}.o"] = w(qd, D), w(kvd, D), w(kvd, D), w(D, qd)
+            p[f"{l}.gate"], p[f"{l}.up"], p[f"{l}.down"] = w(F, D), w(F, D), w(D, F)
+        return cls(p, cfg, **kw)
+
+    # ---------------------------------------------------------------- pieces
+    def _rmsnorm(self, x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+        xf = x.float()
+        xf = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.cfg["eps"])
+        return w * xf.to(torch.float16)
+
+    def _rope_tables(self, S: int, dev):
+        key = (S, dev)
+        if key not in self._rope_cache:
+            d = self.cfg["head_dim"]
+            inv = 1.0 / (self.cfg["rope_theta"] ** (torch.arange(0, d, 2, device=dev, dtype=torch.float32) / d))
+            f = torch.outer(torch.arange(S, device=dev, dtype=torch.float32), inv)
+            emb = torch.cat((f, f), dim=-1)
+            self._rope_cache[key] = (emb.cos().half().unsqueeze(0), emb.sin().half().unsqueeze(0))
+        return self._rope_cache[key]
+
+    def _linear(self, x2d: torch.Tensor, key, route, gated: bool) -> torch.Tensor:
+        if not gated:
+            w = self.p["lm_head"] if key == "lm_head" else self.p[f"{key[0]}.{key[1]}"]
+            return torch.matmul(x2d, w.t())
+        pw = self.packed[key]
+        if route is None:                    # no entropy yet: FP16 tier (W8A16), as the reference's default
+            return K.gemm("fp16", x2d, pw.f16)
+        idx, counts = route
+        return K.routed_linear(x2d, pw, idx, counts)
+
+    def _route(self, h_tok: torch.Tensor, counts_log: list):
+        _, idx, counts = K.route(h_tok, self.tau_low, self.tau_high)
+        counts_log.append(counts)
+        return idx, counts
+
+    # ---------------------------------------------------------------- forward
+    @torch.no_grad()
+    def forward(self, input_ids: torch.Tensor, gated: bool = True) -> torch.Tensor:
+        """input_ids int64 [B, S] -> logits fp16 [B, S, V].  With gated=True,
+        last_fractions holds the device tensor (int64 [3]) of rows per tier
+        summed over every linear call (read it after the forward)."""
+        c = self.cfg
+        B, S = input_ids.shape
+        T = B * S
+        Hq, Hkv, d = c["heads"], c["kv_heads"], c["head_dim"]
+        x = self.p["embed"][input_ids]                                   # [B, S, D] fp16
+        cos, sin = self._rope_tables(S, x.device)
+        counts_log = []
+        route_prev = None
+        for l in range(c["layers"]):
+            xn = self._rmsnorm(x, self.p[f"{l}.ln1"]).reshape(T, -1)
+            q = self._linear(xn, (l, "q"), route_prev, gated).view(B, S, Hq, d).transpose(1, 2)
+            k = self._linear(xn, (l, "k"), route_prev, gated).view(B, S, Hkv, d).transpose(1, 2)
+            v = self._linear(xn, (l, "v"), route_prev, gated).view(B, S, Hkv, d).transpose(1, 2)
+            q, k = _rope(q, cos, sin), _rope(k, cos, sin)
+            att, H = _attention_entropy(q, k, v, d ** -0.5, causal=True)
+            att = att.transpose(1, 2).reshape(T, Hq * d)
+            route_cur = self._route(H.mean(dim=1).reshape(T).contiguous(), counts_log) if gated else None
+            x = x + self._linear(att, (l, "o"), route_cur, gated).view(B, S, -1)
+            xn = self._rmsnorm(x, self.p[f"{l}.ln2"]).reshape(T, -1)
+            g = self._linear(xn, (l, "gate"), route_cur, gated)
+            u = self._linear(xn, (l, "up"), route_cur, gated)
+            x = x + self._linear(torch.nn.functional.silu(g) * u, (l, "down"), route_cur, gated).view(B, S, -1)
+            route_prev = route_cur
+        xn = self._rmsnorm(x, self.p["norm"]).reshape(T, -1)
+        logits = self._linear(xn, "lm_head", route_prev, gated)
+        if gated:
+            # rows per tier over every linear call: each route feeds o/gate/up/down (4)
+            # plus the next layer's q/k/v (3) or the LM head (1); layer 0's q/k/v run
+            # on the FP16 tier
+            weights = [4 + (3 if i + 1 < len(counts_log) else 1) for i in range(len(counts_log))]
+            total = sum(cnt.to(torch.int64) * w for cnt, w in zip(counts_log, weights))
+            self.last_fractions = total + torch.tensor([0, 0, 3 * T], device=total.device, dtype=torch.int64)
+        return logits.view(B, S, -1)
