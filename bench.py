@@ -16,7 +16,10 @@ timed the same way and reported under "kernels".
 
 Timing: W untimed warmup steps, then EXACTLY K steps between events recorded
 on the stream the kernels run on, bracketed by torch.cuda.synchronize(); the
-median of 5 such timed regions is reported.  Each
+median of 5 such timed regions is reported (`value`, `ms_per_step`).  The
+roofline figures divide the algorithmic work by the kernel's own per-launch
+duration: each of K launches between its own event pair, median (the
+launch-to-launch gaps of a back-to-back stream are left out).  Each
 kernel is timed twice: from K eager launches (the reference's own loop) and
 from one HIP graph holding the K launches.  The GEMMs report the eager figure
 (their launches keep the queue full; graph replay adds per-node overhead); the
@@ -131,6 +134,26 @@ def time_steps(fn, steps: int, warmup: int, use_graph: bool, stream, repeats: in
     return times[len(times) // 2], graph is not None
 
 
+def time_launches(fn, steps: int, warmup: int, stream) -> float:
+    """Average duration (ms) of one launch of `fn`: every launch bracketed by
+    its own pair of events on `stream`, so the gaps between launches are left
+    out -- the per-launch figure the roofline divides into, comparable with
+    the profiler's per-dispatch durations."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    with torch.cuda.stream(stream):
+        for a, b in ev:
+            a.record(stream)
+            fn()
+            b.record(stream)
+        torch.cuda.synchronize()
+    d = sorted(a.elapsed_time(b) for a, b in ev)
+    return d[len(d) // 2]
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -173,14 +196,14 @@ def main():
     use_graph = not args.no_graph
     results = {}
 
-    def run(name, fn, steps=args.steps, warmup=args.warmup, primary="graph"):
-        """Times `fn` from eager launches and, unless --no-graph, from a replayed
-        HIP graph of the K launches; "ms" is the `primary` one of the two."""
+    def run(name, fn, steps=args.steps, warmup=args.warmup, primary="graph", graph=True):
+        """Times `fn` from eager launches and, unless --no-graph (or graph=False),
+        from a replayed HIP graph of the K launches; "ms" is the `primary` one."""
         if only and name not in only:
             return None
         with torch.cuda.stream(stream):
             ms_eager, _ = time_steps(fn, steps, warmup, False, stream)
-            ms_graph, g = time_steps(fn, steps, warmup, True, stream) if use_graph else (None, False)
+            ms_graph, g = time_steps(fn, steps, warmup, True, stream) if (use_graph and graph) else (None, False)
         use = "graph" if (primary == "graph" and g) else "eager"
         results[name] = {"ms": ms_graph if use == "graph" else ms_eager, "timing": use,
                          "ms_eager": ms_eager, "ms_graph": ms_graph}
@@ -276,6 +299,24 @@ def main():
             run("c3_end_to_end", c3_all)
             c3 = {"routing_fractions": fr, "thresholds_timed": [0.41, 1.68],
                   "ops": 2.0 * M3 * N3 * K3}
+        # ---- config 4: TinyLlama-1.1B architecture, every linear entropy-gated at (2.34, 6.03)
+        c4 = None
+        if not only or any(n in only for n in ("c4_forward", "c4_forward_fp16")):
+            model = ee.EntropyGatedLlama.random_init(ee.TINYLLAMA_1B, seed=0, tau_low=2.34, tau_high=6.03)
+            g4 = torch.Generator(device=dev)
+            g4.manual_seed(1)
+            ids = torch.randint(0, ee.TINYLLAMA_1B["vocab"], (8, 512), generator=g4, device=dev)
+            ref16 = model.forward(ids, gated=False).float()
+            gated = model.forward(ids).float()
+            rows = model.last_fractions.tolist()
+            err = (gated - ref16).abs().max().item()
+            absmax = ref16.abs().max().item()
+            del gated, ref16
+            run("c4_forward", lambda: model.forward(ids), steps=5, warmup=2, primary="eager", graph=False)
+            run("c4_forward_fp16", lambda: model.forward(ids, gated=False), steps=5, warmup=2, primary="eager",
+                graph=False)
+            c4 = {"rows": rows, "err": err, "absmax": absmax}
+            del model
     if only:
         print(json.dumps({k: v for k, v in results.items()}))
         return
@@ -327,10 +368,39 @@ def main():
             "routing_fractions_int8_fp8_fp16": c3["routing_fractions"],
             "shape": "M=K=N=4096; entropy over fp16 [4096,4096] mixture logits",
         }
+    if c4 is not None:
+        tot = sum(c4["rows"])
+        kernels["llama_c4"] = {
+            "ms_forward_gated": results["c4_forward"]["ms"],
+            "ms_forward_all_fp16": results["c4_forward_fp16"]["ms"],
+            "routing_fraction_int8_fp8_fp16": [round(r / tot, 4) for r in c4["rows"]],
+            "max_abs_logit_err_vs_fp16": c4["err"],
+            "logit_absmax_fp16": c4["absmax"],
+            "shape": "TinyLlama-1.1B architecture (22 layers, hidden 2048, 32 Q / 4 KV heads, FFN 5632, vocab "
+                     "32000), random N(0,0.02) weights, batch 8 x seq 512 uniform token ids; every linear "
+                     "routed per token row at (2.34, 6.03); all-FP16 run = hipBLASLt fp16 on the original weights",
+        }
     for k, r in results.items():                                       # both timings of every kernel, in us
         kernels.setdefault("timings_us", {})[k] = {
             "eager": r["ms_eager"] * 1e3, "graph": None if r["ms_graph"] is None else r["ms_graph"] * 1e3,
             "reported": r["timing"]}
+
+    # per-launch durations of the two roofline kernels (median over K launches)
+    with torch.cuda.stream(stream):
+        i8_launch_ms = time_launches(lambda: ee.gemm("int8", a_i8, pw.i8, s_i8, pw.scale, out=c), args.steps,
+                                     args.warmup, stream)
+        rot_l = {"i": 0}
+
+        def ent_one():
+            i = rot_l["i"] % n_rot
+            rot_l["i"] += 1
+            ee.softmax_entropy(logits[i], out_probs=probs[i])
+
+        ent_launch_ms = time_launches(ent_one, n_rot * max(1, args.steps // n_rot), n_rot, stream)
+    i8_launch_tops = ops / (i8_launch_ms * 1e-3) / 1e12
+    ent_launch_gbs = ent_bytes / (ent_launch_ms * 1e-3) / 1e9
+    kernels["gemm_i8"]["us_per_launch"] = i8_launch_ms * 1e3
+    kernels["softmax_entropy"]["us_cold_per_launch"] = ent_launch_ms * 1e3
 
     # HBM-side bytes per launch from the committed FETCH_SIZE / WRITE_SIZE passes
     # (calibrated against a 256 MiB copy); null when that summary is absent.
@@ -364,10 +434,12 @@ def main():
                                "accumulate, fp16 dequant); FP8 e4m3 GEMM and fused softmax+entropy fp16 "
                                "[1024,4096] in 'kernels'",
                    "M": M, "K": K, "N": N, "entropy_rows": ER, "entropy_cols": ES},
-        "roofline": {"bound": "mfma", "achieved": round(tops, 2), "peak": PEAK_I8_TOPS, "unit": "TFLOP/s",
-                     "frac": round(tops / PEAK_I8_TOPS, 4), "traffic": traffic},
-        "roofline_entropy": {"bound": "hbm", "achieved": round(ent_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                             "frac": round(ent_gbs / PEAK_HBM_GBS, 4), "traffic": ent_traffic},
+        "roofline": {"bound": "mfma", "achieved": round(i8_launch_tops, 2), "peak": PEAK_I8_TOPS, "unit": "TFLOP/s",
+                     "frac": round(i8_launch_tops / PEAK_I8_TOPS, 4), "traffic": traffic,
+                     "kernel": "eek_gemm_i8", "us_per_launch": round(i8_launch_ms * 1e3, 3)},
+        "roofline_entropy": {"bound": "hbm", "achieved": round(ent_launch_gbs, 1), "peak": PEAK_HBM_GBS,
+                             "unit": "GB/s", "frac": round(ent_launch_gbs / PEAK_HBM_GBS, 4), "traffic": ent_traffic,
+                             "kernel": "eek_softmax_entropy (cold)", "us_per_launch": round(ent_launch_ms * 1e3, 3)},
         "kernels": kernels,
         "cpu_baseline": cpu,
     }
