@@ -75,7 +75,9 @@ int ee_abi_version(void);
  * (the reference leaks its CUmodule). */
 int ee_engine_create(const char* lib_dir, ee_engine** out);
 int ee_engine_destroy(ee_engine* eng);
-/* Tuning knobs (0 = automatic): "se_wpr" / "quant_wpr" waves per row (1,2,4). */
+/* Tuning knobs (0 = automatic): "se_wpr" / "quant_wpr" waves per row (1,2,4);
+ * "routed_unfused" = 1 makes ee_routed_linear use its five-launch sequence for
+ * every K (for comparisons). */
 int ee_engine_set_option(ee_engine* eng, const char* key, int64_t value);
 int ee_engine_device(const ee_engine* eng);
 
@@ -170,7 +172,11 @@ int ee_row_copy(ee_engine* eng, const void* src, int64_t ld_src_bytes, void* dst
  * I8 GEMM, FP8 rows on the F8 GEMM, FP16 rows on the W8A16 GEMM, outputs
  * scattered back to their rows; no host synchronisation.  idx/counts come
  * from ee_route.  ws_codes: bytes [M, K] (row stride K), ws_scale: f32 [M].
- * b_i8 / b_f8 / b_f16: the three weight operands [N, K] (row stride K). */
+ * b_i8 / b_f8 / b_f16: the three weight operands [N, K] (row stride K).
+ * K % 128 == 0: two launches -- one quantiser for the INT8 and FP8 rows, then
+ * the three tier GEMMs in one grid (an M-tile never mixes tiers).  Other K
+ * (a multiple of 16): five launches, each tier's quantiser and GEMM in turn.
+ * Both produce the same bits. */
 int ee_routed_linear(ee_engine* eng, const void* x, int64_t ld_x, int32_t M, int32_t K, int32_t N,
                      const int32_t* idx, const int32_t* counts, const int8_t* b_i8, const uint8_t* b_f8,
                      const void* b_f16, const float* b_scale, void* c, int64_t ldc, void* ws_codes,

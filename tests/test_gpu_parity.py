@@ -400,6 +400,34 @@ def test_routed_linear_equals_per_tier(ee, orc, M, K, N):
         assert np.array_equal(o[t == k], ref[t == k]), f"tier {k}"
 
 
+@pytest.mark.parametrize("M,K,N,H_hi", [(700, 1024, 384, 3.0), (300, 1008, 136, 3.0), (257, 512, 256, 0.3),
+                                         (129, 256, 128, 10.0)])
+def test_routed_linear_fused_equals_unfused(ee, orc, M, K, N, H_hi):
+    """The two-launch routed linear (K % 128 == 0: one quantiser, one grid for
+    the three tier GEMMs) and the five-launch sequence give the same bits; K =
+    1008 takes the five-launch path.  Entropy ranges make some tiers empty."""
+    rng = np.random.default_rng(M + K)
+    X = rng.standard_normal((M, K)).astype(np.float16)
+    B, bs = weights(orc, rng, N, K)
+    H = (rng.random(M) * H_hi).astype(np.float32)
+    pw = ee.prepare_weight(cuda(B), cuda(bs)).materialize()
+    x = cuda(X)
+    tier, idx, counts = ee.route(cuda(H), 0.41, 1.68)
+    fused = host(ee.routed_linear(x, pw, idx, counts)).view(np.uint16)
+    try:
+        _lib_set(ee, "routed_unfused", 1)
+        unfused = host(ee.routed_linear(x, pw, idx, counts)).view(np.uint16)
+    finally:
+        _lib_set(ee, "routed_unfused", 0)
+    assert np.array_equal(fused, unfused)
+    t = host(tier)
+    full = [host(ee.triton_int8_gemm(x, cuda(B), cuda(bs))).view(np.uint16),
+            host(ee.triton_fp8_gemm(x, cuda(B), cuda(bs))).view(np.uint16),
+            host(ee.triton_fp16_gemm(x, cuda(B), cuda(bs))).view(np.uint16)]
+    for k in range(3):
+        assert np.array_equal(fused[t == k], full[k][t == k]), f"tier {k}"
+
+
 # ---------------------------------------------------------------------------- dispatcher API
 
 def test_dispatcher_reference_answers(ee):
@@ -689,8 +717,17 @@ def test_entropy_gated_llama_small(ee):
     assert (out - fp16).abs().max() <= 0.1 * fp16.abs().max()
     low = ee.EntropyGatedLlama(m.p, SMALL_LLAMA, tau_low=-1.0, tau_high=-1.0)
     deq = dict(m.p)
+    D, F, Hd, KVd = SMALL_LLAMA["hidden"], SMALL_LLAMA["ffn"], 4 * 64, 2 * 64
     for key, pw in m.packed.items():
-        deq["lm_head" if key == "lm_head" else f"{key[0]}.{key[1]}"] = pw.f16
+        w = pw.f16
+        if key == "lm_head":
+            deq["lm_head"] = w
+        elif key[1] == "qkv":
+            deq[f"{key[0]}.q"], deq[f"{key[0]}.k"], deq[f"{key[0]}.v"] = w[:Hd], w[Hd:Hd + KVd], w[Hd + KVd:]
+        elif key[1] == "gu":
+            deq[f"{key[0]}.gate"], deq[f"{key[0]}.up"] = w[:F], w[F:]
+        else:
+            deq[f"{key[0]}.{key[1]}"] = w
     ref = ee.EntropyGatedLlama(deq, SMALL_LLAMA).forward(ids, gated=False).float()
     got = low.forward(ids).float()
     assert low.last_fractions.tolist() == [0, 0, B * S * (7 * L + 1)]

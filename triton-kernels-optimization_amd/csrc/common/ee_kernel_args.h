@@ -76,6 +76,18 @@ struct EeGemmArgs {
     int32_t tier;
 };
 
+// The routed linear's tier GEMMs in one launch (eek_gemm_routed): t[k] is the
+// EE_GEMM_I8 / F8 / F16 argument block of tier k (all with the same counts);
+// mt_max = M-tile slots of the grid.
+struct EeRoutedGemmArgs {
+    EeGemmArgs t[3];
+    int32_t mt_max;
+};
+
+// Internal quantiser mode of the routed linear: partition slots below counts[0]
+// get EE_QUANT_I8_DISPATCH codes, the next counts[1] slots EE_QUANT_F8_ROW codes.
+#define EE_QUANT_ROUTED_I8_F8 16
+
 // Per-row routing: tier + stable partition of row indices.
 struct EeRouteArgs {
     const float* h;

@@ -379,22 +379,20 @@ EE_DEV void epilogue32_lds(const EeGemmArgs& g, const typename Pipe<KIND>::acc_t
 // refill that stage's buffer with stage kt-1+NSTAGE.
 #define GEMM_THREADS 512
 
+// One 128 x 128 C tile (tile coordinates tm, tn) of the pipelined GEMM;
+// smem is the workgroup's NSTAGE * LDS_STAGE bytes of LDS (1 KB aligned).
 template <int KIND>
-EE_DEV void gemm_pipelined(const EeGemmArgs& g) {
+EE_DEV void gemm_tile(const EeGemmArgs& g, int tm, int tn, uint8_t* smem) {
     typedef Pipe<KIND> P;
     typedef typename P::acc_t acc_t;
     constexpr int ESZ = (KIND == EE_GEMM_F16) ? 2 : 1;
     constexpr int LOADS = 8;                          // DMA instructions per loader wave per stage (4 A + 4 B)
     constexpr int NSL = BKB / P::SB;                  // K slices per stage (4 or 2)
-    __shared__ __attribute__((aligned(1024))) uint8_t smem[NSTAGE * LDS_STAGE];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int M = g.counts ? g.counts[g.tier] : g.M;
     const int64_t off = g.counts ? tier_offset(g.counts, g.tier) : 0;
-    const int tiles_m = (g.M + BM - 1) / BM;
-    int tm, tn;
-    tile_of((int)blockIdx.x, (int)gridDim.x, tiles_m, tm, tn);
     const int m0 = tm * BM, n0 = tn * BN;
     if (m0 >= M) return;                              // whole workgroup, before any barrier
     const int nk = (int)((int64_t)g.K * ESZ / BKB);   // K * ESZ is a multiple of BKB here
@@ -509,6 +507,14 @@ EE_DEV void gemm_pipelined(const EeGemmArgs& g) {
 }
 
 template <int KIND>
+EE_DEV void gemm_pipelined(const EeGemmArgs& g) {
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[NSTAGE * LDS_STAGE];
+    int tm, tn;
+    tile_of((int)blockIdx.x, (int)gridDim.x, (g.M + BM - 1) / BM, tm, tn);
+    gemm_tile<KIND>(g, tm, tn, smem);
+}
+
+template <int KIND>
 EE_DEV void gemm_generic(const EeGemmArgs& g) {
     typedef typename AccT<KIND>::type acc_t;
     constexpr int ESZ = (KIND == EE_GEMM_F16) ? 2 : 1;
@@ -585,6 +591,26 @@ extern "C" __global__ void __launch_bounds__(GEMM_THREADS) __attribute__((amdgpu
 }
 extern "C" __global__ void __launch_bounds__(GEMM_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2))) eek_gemm_f16(EeGemmArgs g) {
     gemm_pipelined<EE_GEMM_F16>(g);
+}
+
+// The routed linear's three tier GEMMs in one launch.  Tier t owns partition
+// slots [off_t, off_t + counts[t]) (off_t = counts[0] + ... + counts[t-1]) and
+// the ceil(counts[t] / 128) M-tile indices after those of the lower tiers, so
+// an M-tile never mixes tiers; workgroups past the last tile exit at once.
+// The grid holds r.mt_max = ceil(M / 128) + 2 M-tile slots (the sum of the
+// three ceilings is at most that) times ceil(N / 128) N-tiles.
+extern "C" __global__ void __launch_bounds__(GEMM_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
+eek_gemm_routed(EeRoutedGemmArgs r) {
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[NSTAGE * LDS_STAGE];
+    const int32_t* counts = r.t[0].counts;
+    const int T0 = (counts[0] + BM - 1) / BM;
+    const int T1 = (counts[1] + BM - 1) / BM;
+    const int T2 = (counts[2] + BM - 1) / BM;
+    int tm, tn;
+    tile_of((int)blockIdx.x, (int)gridDim.x, r.mt_max, tm, tn);
+    if (tm < T0) gemm_tile<EE_GEMM_I8>(r.t[0], tm, tn, smem);
+    else if (tm < T0 + T1) gemm_tile<EE_GEMM_F8>(r.t[1], tm - T0, tn, smem);
+    else if (tm < T0 + T1 + T2) gemm_tile<EE_GEMM_F16>(r.t[2], tm - T0 - T1, tn, smem);
 }
 
 // Fallback for any K that is a multiple of 16 bytes (zero-filled K tail).

@@ -22,6 +22,7 @@
 #define INV448 (1.0f / 448.0f)
 
 typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
+typedef short s16x2 __attribute__((ext_vector_type(2)));
 
 // amax of |fp16| on raw bits: for non-negative halves the integer order is the
 // numeric order, and NaN patterns sort above inf, so NaN propagates like amax.
@@ -35,14 +36,14 @@ EE_DEV uint32_t absmax_bits(uint32_t acc, uint32_t u) {
 
 struct RowScale {
     float s;     // scale stored per row
-    float mul;   // F8: fp16(1/s)
+    float mul;   // F8: fp16(1/s); I8 dispatcher: RN(RN(1/s) * (1 + 2^-21))
 };
 
 EE_DEV RowScale row_scale(int mode, float amax) {
     RowScale r;
     if (mode == EE_QUANT_I8_DISPATCH) {
         r.s = f16_round(amax * INV127);
-        r.mul = 0.f;
+        r.mul = (1.0f / r.s) * (1.0f + 0x1p-21f);
     } else if (mode == EE_QUANT_I8_ENGINE) {
         float s = amax * INV127;
         if (s < 1e-8f) s = 1e-8f;            // clamp(min=1e-8); NaN stays NaN
@@ -68,7 +69,13 @@ EE_DEV float tensor_amax(const EeQuantArgs& a) {
 
 EE_DEV uint32_t quant_one(int mode, float x, const RowScale& rs) {
     if (mode == EE_QUANT_I8_DISPATCH) {
-        const float q = x / rs.s;
+        // trunc(x / s) as trunc(x * mul): for fp16 x and s with |x| <= amax a
+        // non-integer quotient lies >= 2^-19 (relative) from the nearest integer,
+        // and mul errs upward by 2^-22 .. 2^-20.7, so no integer is crossed and
+        // exact-integer quotients are not rounded below -- the same code for every
+        // reachable (amax, x) pair (checked exhaustively by tests/rcp_trunc_check.c).
+        // s = 0 gives mul = inf, as x / 0 does.
+        const float q = x * rs.mul;
         int32_t iv;
         if (fabsf(q) < 2147483648.0f) iv = (int32_t)q;                 // truncation
         else iv = (q > 0.0f) ? 0x7fffffff : (int32_t)0x80000000;       // saturate; NaN -> 0 byte
@@ -97,9 +104,12 @@ EE_DEV void quant_vec(const EeQuantArgs& a) {
     const int w = wave_id();
     const int wr = w % WPR;
     const int64_t lr = (int64_t)blockIdx.x * RPB + w / WPR;
-    const int64_t rows = a.counts ? (int64_t)a.counts[a.tier] : a.M;
+    // EE_QUANT_ROUTED_I8_F8: slots [0, counts[0]) take INT8 codes, the next counts[1] FP8
+    const bool dual = a.mode == EE_QUANT_ROUTED_I8_F8;
+    const int64_t rows = dual ? (int64_t)a.counts[0] + a.counts[1] : (a.counts ? (int64_t)a.counts[a.tier] : a.M);
     const bool valid = lr < rows;
-    const int64_t off = a.counts ? tier_offset(a.counts, a.tier) : 0;
+    const int64_t off = (a.counts && !dual) ? tier_offset(a.counts, a.tier) : 0;
+    const int mode = dual ? (lr < a.counts[0] ? EE_QUANT_I8_DISPATCH : EE_QUANT_F8_ROW) : a.mode;
     int64_t src = 0;
     if (valid) src = a.idx ? (int64_t)a.idx[off + lr] : lr;
     const int64_t dst = off + lr;                 // routed: partition slot; else the row itself
@@ -136,20 +146,40 @@ EE_DEV void quant_vec(const EeQuantArgs& a) {
         for (int i = 1; i < WPR; ++i) am = max(am, slot[base + i]);
     }
     if (!valid) return;
-    const RowScale rs = row_scale(a.mode, a.mode == EE_QUANT_F8_TENSOR ? tensor_amax(a) : f16_lo(am));
+    const float amax = mode == EE_QUANT_F8_TENSOR ? tensor_amax(a) : f16_lo(am);
+    const RowScale rs = row_scale(mode, amax);
+    // FP8 rows whose amax and fp16 inverse scale are finite: every product
+    // fp16(x * inv) is finite with |p| < 464, where the hardware e4m3 conversion
+    // (round to nearest even; checked against e4m3_rne_sat on every fp16 value)
+    // gives the same code -- two codes per instruction.  Zero, tiny and
+    // non-finite rows take quant_one.
+    const bool f8fast = mode == EE_QUANT_F8_ROW && fabsf(amax) < INFINITY && fabsf(rs.mul) < INFINITY;
+    const f16x2 mul2 = {(f16)rs.mul, (f16)rs.mul};
     uint8_t* cr = (uint8_t*)a.codes + dst * a.ld_c;
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
         const int c0 = ((j * WPR + wr) * 64 + lane) * 8;
         if (c0 >= K) continue;
         uint32_t q[8];
+        u32x2 o;
+        if (f8fast) {
+            s16x2 r0 = {0, 0}, r1 = {0, 0};
+            r0 = __builtin_amdgcn_cvt_scalef32_pk_fp8_f16(r0, f16x2_from_bits(v[j][0]) * mul2, 1.0f, false);
+            r0 = __builtin_amdgcn_cvt_scalef32_pk_fp8_f16(r0, f16x2_from_bits(v[j][1]) * mul2, 1.0f, true);
+            r1 = __builtin_amdgcn_cvt_scalef32_pk_fp8_f16(r1, f16x2_from_bits(v[j][2]) * mul2, 1.0f, false);
+            r1 = __builtin_amdgcn_cvt_scalef32_pk_fp8_f16(r1, f16x2_from_bits(v[j][3]) * mul2, 1.0f, true);
+            o = u32x2{__builtin_bit_cast(uint32_t, r0), __builtin_bit_cast(uint32_t, r1)};
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const uint32_t u = v[j][i >> 1];
-            q[i] = quant_one(a.mode, (i & 1) ? f16_hi(u) : f16_lo(u), rs);
-        }
-        const u32x2 o{q[0] | (q[1] << 8) | (q[2] << 16) | (q[3] << 24),
+            for (int i = 0; i < 8; ++i) q[i] = (o[i >> 2] >> ((i & 3) * 8)) & 0xffu;
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const uint32_t u = v[j][i >> 1];
+                q[i] = quant_one(mode, (i & 1) ? f16_hi(u) : f16_lo(u), rs);
+            }
+            o = u32x2{q[0] | (q[1] << 8) | (q[2] << 16) | (q[3] << 24),
                       q[4] | (q[5] << 8) | (q[6] << 16) | (q[7] << 24)};
+        }
         if (c0 + 8 <= K) {
             *(u32x2*)(cr + c0) = o;
         } else {
@@ -165,18 +195,20 @@ EE_DEV void quant_vec(const EeQuantArgs& a) {
 EE_DEV void quant_generic(const EeQuantArgs& a) {
     const int lane = lane_id();
     const int64_t lr = (int64_t)blockIdx.x * 4 + wave_id();
-    const int64_t rows = a.counts ? (int64_t)a.counts[a.tier] : a.M;
+    const bool dual = a.mode == EE_QUANT_ROUTED_I8_F8;
+    const int64_t rows = dual ? (int64_t)a.counts[0] + a.counts[1] : (a.counts ? (int64_t)a.counts[a.tier] : a.M);
     if (lr >= rows) return;
-    const int64_t off = a.counts ? tier_offset(a.counts, a.tier) : 0;
+    const int64_t off = (a.counts && !dual) ? tier_offset(a.counts, a.tier) : 0;
+    const int mode = dual ? (lr < a.counts[0] ? EE_QUANT_I8_DISPATCH : EE_QUANT_F8_ROW) : a.mode;
     const int64_t src = a.idx ? (int64_t)a.idx[off + lr] : lr;
     const int64_t dst = off + lr;
     const uint16_t* xr = a.x + src * a.ld_x;
     uint32_t am = 0;
     for (int64_t c = lane; c < a.K; c += 64) am = max(am, (uint32_t)(xr[c] & 0x7fffu));
     am = wave_max_u32(am);
-    const RowScale rs = row_scale(a.mode, a.mode == EE_QUANT_F8_TENSOR ? tensor_amax(a) : f16_lo(am));
+    const RowScale rs = row_scale(mode, mode == EE_QUANT_F8_TENSOR ? tensor_amax(a) : f16_lo(am));
     uint8_t* cr = (uint8_t*)a.codes + dst * a.ld_c;
-    for (int64_t c = lane; c < a.K; c += 64) cr[c] = (uint8_t)quant_one(a.mode, f16_lo(xr[c]), rs);
+    for (int64_t c = lane; c < a.K; c += 64) cr[c] = (uint8_t)quant_one(mode, f16_lo(xr[c]), rs);
     if (lane == 0) a.scale[dst] = rs.s;
 }
 

@@ -234,9 +234,11 @@ int launch(ee_engine* e, const std::string& name, int64_t gx, int64_t gy, int bl
 }
 
 // (VPT, WPR) for a register-resident row kernel: VPT 16-byte vectors per lane,
-// WPR wave64s per row, VPT * WPR * 512 >= len.  Prefer ~4 waves per SIMD over
-// the chip (1024 SIMDs) before spreading a row over more waves.
-bool pick_row_cfg(int64_t len, int64_t rows, int64_t forced_wpr, int& vpt, int& wpr) {
+// WPR wave64s per row, VPT * WPR * 512 >= len: the fewest waves per row that
+// still put min_waves waves on the chip (1024 SIMDs).  The softmax kernel takes
+// 4096 (~4 per SIMD; more did not help, and a row split costs barriers); the
+// quantisers 16384 (measured 10-15% faster at M = 4096, K = 2048 / 5632).
+bool pick_row_cfg(int64_t len, int64_t rows, int64_t forced_wpr, int& vpt, int& wpr, int64_t min_waves = 4096) {
     const int options[3] = {1, 2, 4};
     int best = -1;
     for (int w : options) {
@@ -245,7 +247,7 @@ bool pick_row_cfg(int64_t len, int64_t rows, int64_t forced_wpr, int& vpt, int& 
         if (v < 1) v = 1;
         if (v > 8) continue;
         best = w;
-        if (forced_wpr || rows * w >= 4096) break;
+        if (forced_wpr || rows * w >= min_waves) break;
     }
     if (best < 0) return false;
     wpr = best;
@@ -374,6 +376,8 @@ EE_EXPORT int ee_engine_set_option(ee_engine* eng, const char* key, int64_t valu
     if (k == "se_wpr" || k == "quant_wpr") {
         if (value != 0 && value != 1 && value != 2 && value != 4)
             return fail(EE_ERR_INVALID_ARG, k + " must be 0 (auto), 1, 2 or 4");
+    } else if (k == "routed_unfused") {
+        if (value != 0 && value != 1) return fail(EE_ERR_INVALID_ARG, k + " must be 0 or 1");
     } else {
         return fail(EE_ERR_INVALID_ARG, "unknown option: " + k);
     }
@@ -408,7 +412,7 @@ EE_EXPORT int ee_softmax_entropy(ee_engine* eng, const void* x, void* p, float* 
 static int launch_quant(ee_engine* eng, const EeQuantArgs& a, ee_stream_t stream) {
     const bool vec_ok = aligned(a.x, 16) && aligned(a.codes, 8) && a.ld_x % 8 == 0 && a.ld_c % 8 == 0;
     int vpt = 0, wpr = 0;
-    if (vec_ok && pick_row_cfg(a.K, a.M, opt(eng, "quant_wpr"), vpt, wpr)) {
+    if (vec_ok && pick_row_cfg(a.K, a.M, opt(eng, "quant_wpr"), vpt, wpr, 16384)) {
         const std::string name = "eek_quant_v" + std::to_string(vpt) + "_w" + std::to_string(wpr);
         return launch(eng, name, cdiv(a.M, 4 / wpr), 1, EE_BLOCK, a, stream);
     }
@@ -568,6 +572,25 @@ EE_EXPORT int ee_routed_linear(ee_engine* eng, const void* x, int64_t ld_x, int3
         return fail(EE_ERR_INVALID_ARG, "misaligned pointer");
     if (M == 0) return EE_OK;
     int rc;
+    if (K % 128 == 0 && !opt(eng, "routed_unfused")) {
+        // Two launches: one quantiser for the INT8 and FP8 slots, then the three
+        // tier GEMMs as one grid (eek_gemm_routed), scattering rows through idx.
+        EeQuantArgs qa{(const uint16_t*)x, ws_codes, ws_scale, idx, counts, M, K, ld_x, K, EE_QUANT_ROUTED_I8_F8, 0,
+                       nullptr, 0};
+        if ((rc = launch_quant(eng, qa, stream))) return rc;
+        EeRoutedGemmArgs ra{};
+        ra.t[0] = EeGemmArgs{ws_codes, b_i8, (uint16_t*)c, nullptr, ws_scale, b_scale, nullptr, idx, counts,
+                             K, K, ldc, M, N, K, EE_TIER_INT8};
+        ra.t[1] = EeGemmArgs{ws_codes, b_f8, (uint16_t*)c, nullptr, ws_scale, b_scale, nullptr, idx, counts,
+                             K, K, ldc, M, N, K, EE_TIER_FP8};
+        ra.t[2] = EeGemmArgs{x, b_f16, (uint16_t*)c, nullptr, nullptr, nullptr, idx, idx, counts,
+                             ld_x, K, ldc, M, N, K, EE_TIER_FP16};
+        ra.mt_max = (int32_t)cdiv(M, 128) + 2;
+        const Kernel* k = find_kernel(eng, "eek_gemm_routed");
+        return launch(eng, "eek_gemm_routed", (int64_t)ra.mt_max * cdiv(N, 128), 1, k ? k->block : EE_BLOCK, ra,
+                      stream);
+    }
+    // Any K (a multiple of 16): five launches, each tier's quantiser and GEMM.
     // INT8 rows: quantise into partition slots, GEMM, scatter.
     if ((rc = ee_quant_act(eng, x, M, K, ld_x, EE_QUANT_I8_DISPATCH, ws_codes, K, ws_scale, idx, counts,
                            EE_TIER_INT8, stream)))

@@ -350,9 +350,6 @@ def build_dispatched_llama(model, tau_low: float, tau_high: float):
 TINYLLAMA_1B = dict(layers=22, hidden=2048, heads=32, kv_heads=4, head_dim=64, ffn=5632, vocab=32000,
                     rope_theta=10000.0, eps=1e-5)
 
-_LINEARS = ("q", "k", "v", "o", "gate", "up", "down")
-
-
 class EntropyGatedLlama:
     """A Llama forward in which EVERY linear layer routes each token row to the
     INT8, FP8 or FP16 (W8A16) GEMM by entropy -- BASELINE config 4.  This
@@ -363,8 +360,9 @@ class EntropyGatedLlama:
     entropy (fused softmax+entropy kernel, causal): q/k/v of layer l use layer
     l-1's (layer 0 runs them on the FP16 tier), o/gate/up/down use layer l's,
     and the LM head uses the last layer's.  Rows are grouped per tier into one
-    launch per tier and scattered back (routed_linear); nothing syncs with the
-    host inside forward.  forward(..., gated=False) is the all-FP16 run: every
+    launch per tier and scattered back (routed_linear); q/k/v, and gate/up, run
+    as one GEMM each on their concatenated weights (same input, same routing).
+    Nothing syncs with the host inside forward.  forward(..., gated=False) is the all-FP16 run: every
     linear as a plain fp16 GEMM on the original weights (hipBLASLt).
 
     Weights: fp16 tensors in `params` (embed [V, D]; per layer ln1, q [Hq*d, D],
@@ -375,11 +373,18 @@ class EntropyGatedLlama:
         self.p = params
         self.cfg = dict(cfg)
         self.tau_low, self.tau_high = tau_low, tau_high
+        # q/k/v and gate/up share their input and routing: each pair runs as one
+        # GEMM on the concatenated weights (one quantiser pass, one launch)
+        self.fused = {}
         self.packed = {}
         for l in range(cfg["layers"]):
-            for n in _LINEARS:
-                self.packed[(l, n)] = self._pack(params[f"{l}.{n}"])
-        self.packed["lm_head"] = self._pack(params["lm_head"])
+            self.fused[(l, "qkv")] = torch.cat([params[f"{l}.q"], params[f"{l}.k"], params[f"{l}.v"]], dim=0)
+            self.fused[(l, "gu")] = torch.cat([params[f"{l}.gate"], params[f"{l}.up"]], dim=0)
+            self.fused[(l, "o")] = params[f"{l}.o"]
+            self.fused[(l, "down")] = params[f"{l}.down"]
+        self.fused["lm_head"] = params["lm_head"]
+        for key, w in self.fused.items():
+            self.packed[key] = self._pack(w)
         self.last_fractions = None
         self._rope_cache = {}
 
@@ -426,8 +431,7 @@ class EntropyGatedLlama:
 
     def _linear(self, x2d: torch.Tensor, key, route, gated: bool) -> torch.Tensor:
         if not gated:
-            w = self.p["lm_head"] if key == "lm_head" else self.p[f"{key[0]}.{key[1]}"]
-            return torch.matmul(x2d, w.t())
+            return torch.matmul(x2d, self.fused[key].t())
         pw = self.packed[key]
         if route is None:                    # no entropy yet: FP16 tier (W8A16), as the reference's default
             return K.gemm("fp16", x2d, pw.f16)
@@ -455,23 +459,25 @@ class EntropyGatedLlama:
         route_prev = None
         for l in range(c["layers"]):
             xn = self._rmsnorm(x, self.p[f"{l}.ln1"]).reshape(T, -1)
-            q = self._linear(xn, (l, "q"), route_prev, gated).view(B, S, Hq, d).transpose(1, 2)
-            k = self._linear(xn, (l, "k"), route_prev, gated).view(B, S, Hkv, d).transpose(1, 2)
-            v = self._linear(xn, (l, "v"), route_prev, gated).view(B, S, Hkv, d).transpose(1, 2)
+            qkv = self._linear(xn, (l, "qkv"), route_prev, gated)
+            q = qkv[:, :Hq * d].reshape(B, S, Hq, d).transpose(1, 2)
+            k = qkv[:, Hq * d:(Hq + Hkv) * d].reshape(B, S, Hkv, d).transpose(1, 2)
+            v = qkv[:, (Hq + Hkv) * d:].reshape(B, S, Hkv, d).transpose(1, 2)
             q, k = _rope(q, cos, sin), _rope(k, cos, sin)
             att, H = _attention_entropy(q, k, v, d ** -0.5, causal=True)
             att = att.transpose(1, 2).reshape(T, Hq * d)
             route_cur = self._route(H.mean(dim=1).reshape(T).contiguous(), counts_log) if gated else None
             x = x + self._linear(att, (l, "o"), route_cur, gated).view(B, S, -1)
             xn = self._rmsnorm(x, self.p[f"{l}.ln2"]).reshape(T, -1)
-            g = self._linear(xn, (l, "gate"), route_cur, gated)
-            u = self._linear(xn, (l, "up"), route_cur, gated)
-            x = x + self._linear(torch.nn.functional.silu(g) * u, (l, "down"), route_cur, gated).view(B, S, -1)
+            gu = self._linear(xn, (l, "gu"), route_cur, gated)
+            F = gu.shape[1] // 2
+            act = torch.nn.functional.silu(gu[:, :F]) * gu[:, F:]
+            x = x + self._linear(act, (l, "down"), route_cur, gated).view(B, S, -1)
             route_prev = route_cur
         xn = self._rmsnorm(x, self.p["norm"]).reshape(T, -1)
         logits = self._linear(xn, "lm_head", route_prev, gated)
         if gated:
-            # rows per tier over every linear call: each route feeds o/gate/up/down (4)
+            # rows per tier over every linear layer: each route feeds o/gate/up/down (4)
             # plus the next layer's q/k/v (3) or the LM head (1); layer 0's q/k/v run
             # on the FP16 tier
             weights = [4 + (3 if i + 1 < len(counts_log) else 1) for i in range(len(counts_log))]
