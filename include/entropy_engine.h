@@ -77,7 +77,11 @@ int ee_engine_create(const char* lib_dir, ee_engine** out);
 int ee_engine_destroy(ee_engine* eng);
 /* Tuning knobs (0 = automatic): "se_wpr" / "quant_wpr" waves per row (1,2,4);
  * "routed_unfused" = 1 makes ee_routed_linear use its five-launch sequence for
- * every K (for comparisons). */
+ * every K (for comparisons); "gemm_variant" = 1 runs every GEMM on the
+ * loader-wave pipeline, 2 on the 8-wave pipeline where one exists (INT8 and
+ * W8A16); automatic: 8-wave for W8A16, and for INT8 grids of at most one tile
+ * per CU.  INT8 results are identical either way; the FP16 tier's f32
+ * summation order follows the pipeline (the routed linear follows ee_gemm). */
 int ee_engine_set_option(ee_engine* eng, const char* key, int64_t value);
 int ee_engine_device(const ee_engine* eng);
 

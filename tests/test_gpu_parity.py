@@ -276,8 +276,18 @@ def weights(orc, rng, N, K, scale=0.02):
     return orc.quantize_weights_int8(W)
 
 
-@pytest.mark.parametrize("M,K,N", [(256, 1024, 512), (200, 512, 260), (1, 4096, 128), (130, 4112, 4), (1024, 4096, 4096)])
-def test_int8_gemm_bit_exact(ee, orc, M, K, N):
+@pytest.fixture(params=[0, 1, 2], ids=["auto", "loader-waves", "8-waves"])
+def gemm_variant(request):
+    """Runs a test on each GEMM pipeline (engine option gemm_variant)."""
+    from entropy_engine import _lib
+    _lib.check(_lib.lib().ee_engine_set_option(_lib.engine(), b"gemm_variant", request.param))
+    yield request.param
+    _lib.check(_lib.lib().ee_engine_set_option(_lib.engine(), b"gemm_variant", 0))
+
+
+@pytest.mark.parametrize("M,K,N", [(256, 1024, 512), (200, 512, 260), (1, 4096, 128), (130, 4112, 4), (1024, 4096, 4096),
+                                   (128, 640, 128), (256, 768, 384)])
+def test_int8_gemm_bit_exact(ee, orc, M, K, N, gemm_variant):
     rng = np.random.default_rng(M + K + N)
     A = rng.standard_normal((M, K)).astype(np.float16)
     B, bs = weights(orc, rng, N, K)
@@ -321,8 +331,8 @@ def test_fp8_gemm(ee, orc, M, K, N, sc):
     assert np.array_equal(host(pw.f8), orc.e4m3_from_f32(B.T.astype(np.float32)))
 
 
-@pytest.mark.parametrize("M,K,N", [(256, 1024, 512), (77, 2048, 132), (1024, 4096, 4096)])
-def test_w8a16_gemm(ee, orc, M, K, N):
+@pytest.mark.parametrize("M,K,N", [(256, 1024, 512), (77, 2048, 132), (1024, 4096, 4096), (130, 320, 64)])
+def test_w8a16_gemm(ee, orc, M, K, N, gemm_variant):
     rng = np.random.default_rng(M * 5 + N)
     A = rng.standard_normal((M, K)).astype(np.float16)
     B, bs = weights(orc, rng, N, K)
@@ -380,7 +390,7 @@ def test_row_copy_gather_scatter(ee):
 
 
 @pytest.mark.parametrize("M,K,N", [(300, 1024, 256), (4096, 4096, 4096)])
-def test_routed_linear_equals_per_tier(ee, orc, M, K, N):
+def test_routed_linear_equals_per_tier(ee, orc, M, K, N, gemm_variant):
     """scatter(gemm_t(gather(X)))[r] == gemm_t(X)[r] bit for bit, every tier."""
     rng = np.random.default_rng(M + 1)
     X = rng.standard_normal((M, K)).astype(np.float16)
@@ -402,7 +412,7 @@ def test_routed_linear_equals_per_tier(ee, orc, M, K, N):
 
 @pytest.mark.parametrize("M,K,N,H_hi", [(700, 1024, 384, 3.0), (300, 1008, 136, 3.0), (257, 512, 256, 0.3),
                                          (129, 256, 128, 10.0)])
-def test_routed_linear_fused_equals_unfused(ee, orc, M, K, N, H_hi):
+def test_routed_linear_fused_equals_unfused(ee, orc, M, K, N, H_hi, gemm_variant):
     """The two-launch routed linear (K % 128 == 0: one quantiser, one grid for
     the three tier GEMMs) and the five-launch sequence give the same bits; K =
     1008 takes the five-launch path.  Entropy ranges make some tiers empty."""

@@ -78,10 +78,12 @@ struct EeGemmArgs {
 
 // The routed linear's tier GEMMs in one launch (eek_gemm_routed): t[k] is the
 // EE_GEMM_I8 / F8 / F16 argument block of tier k (all with the same counts);
-// mt_max = M-tile slots of the grid.
+// mt_max = M-tile slots of the grid; f16_w8 picks the FP16 tier's pipeline so
+// that its f32 summation order is the one ee_gemm uses.
 struct EeRoutedGemmArgs {
     EeGemmArgs t[3];
     int32_t mt_max;
+    int32_t f16_w8;         // 1: the FP16 tier runs the 8-wave pipeline (as ee_gemm does)
 };
 
 // Internal quantiser mode of the routed linear: partition slots below counts[0]

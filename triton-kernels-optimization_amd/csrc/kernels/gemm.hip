@@ -506,6 +506,392 @@ EE_DEV void gemm_tile(const EeGemmArgs& g, int tm, int tn, uint8_t* smem) {
     }
 }
 
+// A 32 x 32 accumulator block through LDS: register group q (4 values) of lane l
+// at byte (q * 64 + l) * 16 of a 4 KB slot, so a ds_write_b128 / ds_read_b128
+// covers 1 KB of consecutive banks.  (Elements are converted one scalar at a
+// time: hipcc turns __builtin_bit_cast of a vector element into element 0.)
+EE_DEV uint32_t word_of(int32_t v) { return (uint32_t)v; }
+EE_DEV uint32_t word_of(float v) { return __float_as_uint(v); }
+template <typename acc_t>
+EE_DEV void xchg_put(uint8_t* slot, const acc_t& v, int lane) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        uint32_t w[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) w[r] = word_of(v[4 * q + r]);
+        *(u32x4*)(slot + (q * 64 + lane) * 16) = u32x4{w[0], w[1], w[2], w[3]};
+    }
+}
+template <int KIND, typename acc_t>
+EE_DEV void xchg_add(const uint8_t* slot, acc_t& v, int lane) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const u32x4 x = *(const u32x4*)(slot + (q * 64 + lane) * 16);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const uint32_t w = x[r];
+            if constexpr (KIND == EE_GEMM_I8) v[4 * q + r] += (int32_t)w;
+            else v[4 * q + r] += __uint_as_float(w);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Fused 8-wave pipeline (512 threads).  Wave w = (kq, wm, wn) = (w >> 2,
+// (w >> 1) & 1, w & 1) accumulates the 64 x 64 quadrant (wm, wn) over its half
+// of every stage's K slices, HPS = NSL / 2 slices starting at kq * HPS, and
+// issues one eighth of every stage's DMA (row groups 2w, 2w+1 of A and B: 4
+// instructions) in the shadow of its own MFMAs.  On gfx950 that is what lets
+// the operand stream overlap the MFMAs: a wave that issues only MFMAs holds
+// back the memory traffic of the other wave on its SIMD (separate loader waves
+// measured DMA time + MFMA time), and eight waves rather than four keep the
+// LDS fragment reads at full rate.  At the end the two K halves of each
+// quadrant are summed through LDS (exact for int32; one fixed order for f32):
+// wave kq keeps row block kq of the quadrant and gets its partner's partial
+// of it, then dequantises and stores that 32 x 64 block.
+//
+// Schedule: barrier kt+1 sits before the MFMAs of the wave's last slice of
+// stage kt; the refill of stage kt+4 (into stage kt-1's buffer, free after
+// barrier kt) is spread over the HPS slices that follow barrier kt.
+#define GEMM8_THREADS 512
+
+// Per-lane scales of one 32-row block (row block rb) of quadrant (wm, wn).
+template <int KIND>
+EE_DEV void load_scales_blk(const EeGemmArgs& g, int m0, int n0, int M, int64_t off, int wm, int wn, int rb, int lane,
+                            TileScales& sc) {
+    if constexpr (KIND != EE_GEMM_F16) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int n = n0 + wn * 64 + j * 32 + 8 * q + 4 * (lane >> 5);
+                sc.bs[j][q] = (n < g.N) ? *(const f32x4*)(g.b_scale + n) : f32x4{0.f, 0.f, 0.f, 0.f};
+            }
+        const int m = m0 + wm * 64 + rb * 32 + (lane & 31);
+        sc.as[0] = (m < M) ? g.a_scale[off + m] : 0.0f;
+        sc.as[1] = 0.0f;
+    }
+}
+
+// Epilogue of one 32 x 64 block (row block rb of quadrant (wm, wn)) held as
+// acc[0..1] (column blocks), through a 4 KB LDS tile: dequantise, write in the
+// MFMA layout, read back as rows and store 16 bytes per lane, non-temporal.
+template <int KIND>
+EE_DEV void epilogue_blk_lds(const EeGemmArgs& g, const typename Pipe<KIND>::acc_t (&acc)[2], const TileScales& sc,
+                             uint8_t* tile, int m0, int n0, int M, int64_t off, int wm, int wn, int rb, int lane) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int cl = j * 32 + 8 * q + 4 * (lane >> 5);
+            float o[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                if constexpr (KIND == EE_GEMM_I8) {
+                    float v = (float)acc[j][4 * q + r];
+                    v = v * sc.as[0];
+                    o[r] = v * sc.bs[j][q][r];
+                } else if constexpr (KIND == EE_GEMM_F8) {
+                    const float v = acc[j][4 * q + r] * sc.as[0];
+                    o[r] = v * sc.bs[j][q][r];
+                } else {
+                    o[r] = acc[j][4 * q + r];
+                }
+            }
+            *(u32x2*)(tile + lds_off(lane & 31, cl >> 3) + ((cl >> 2) & 1) * 8) =
+                u32x2{pack_f16x2(o[0], o[1]), pack_f16x2(o[2], o[3])};
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int rl = k * 8 + (lane >> 3), ch = lane & 7;
+        const u32x4 v = *(const u32x4*)(tile + lds_off(rl, ch));
+        const int m = m0 + wm * 64 + rb * 32 + rl;
+        const int n = n0 + wn * 64 + ch * 8;
+        if (m >= M || n >= g.N) continue;
+        const int64_t crow = g.c_idx ? (int64_t)g.c_idx[off + m] : (int64_t)m;
+        uint16_t* dst = g.c + crow * g.ldc + n;
+        // C is written once and read by a later kernel: non-temporal stores keep
+        // it from lingering dirty in L2.
+        if (n + 8 <= g.N && ((uintptr_t)dst & 15) == 0) {
+            __builtin_nontemporal_store(v, (u32x4*)dst);
+        } else {                                           // N % 8 == 4 tail, or C only 8-byte aligned
+            __builtin_nontemporal_store(u32x2{v[0], v[1]}, (u32x2*)dst);
+            if (n + 4 < g.N) __builtin_nontemporal_store(u32x2{v[2], v[3]}, (u32x2*)(dst + 4));
+        }
+    }
+}
+
+// Debug epilogue (int32 accumulators requested): direct stores of the block.
+template <int KIND>
+EE_DEV void epilogue_blk_direct(const EeGemmArgs& g, const typename Pipe<KIND>::acc_t (&acc)[2], int m0, int n0, int M,
+                                int64_t off, int wm, int wn, int rb, int lane) {
+    const int m = m0 + wm * 64 + rb * 32 + (lane & 31);
+    if (m >= M) return;
+    const int64_t crow = g.c_idx ? (int64_t)g.c_idx[off + m] : (int64_t)m;
+    const float as = (KIND == EE_GEMM_F16) ? 0.0f : g.a_scale[off + m];
+    uint16_t* cr = g.c + crow * g.ldc;
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int n = n0 + wn * 64 + j * 32 + 8 * q + 4 * (lane >> 5);
+            if (n >= g.N) continue;                 // N is a multiple of 4
+            float o[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                if constexpr (KIND == EE_GEMM_I8) {
+                    float v = (float)acc[j][4 * q + r];
+                    v = v * as;
+                    o[r] = v * g.b_scale[n + r];
+                } else if constexpr (KIND == EE_GEMM_F8) {
+                    const float v = acc[j][4 * q + r] * as;
+                    o[r] = v * g.b_scale[n + r];
+                } else {
+                    o[r] = acc[j][4 * q + r];
+                }
+            }
+            *(u32x2*)(cr + n) = u32x2{pack_f16x2(o[0], o[1]), pack_f16x2(o[2], o[3])};
+            if constexpr (KIND == EE_GEMM_I8) {
+                if (g.acc)
+                    *(i32x4*)(g.acc + crow * g.ldc + n) =
+                        i32x4{acc[j][4 * q], acc[j][4 * q + 1], acc[j][4 * q + 2], acc[j][4 * q + 3]};
+            }
+        }
+}
+
+template <int KIND>
+struct Gemm8 {
+    typedef Pipe<KIND> P;
+    typedef typename P::acc_t acc_t;
+    static constexpr int ESZ = (KIND == EE_GEMM_F16) ? 2 : 1;
+    static constexpr int LOADS = 4;                    // DMA instructions per wave per stage
+    static constexpr int NSL = BKB / P::SB;            // K slices per stage (4 or 2)
+    static constexpr int HPS = NSL / 2;                // slices per wave per stage
+    static constexpr int PPS = 2 / HPS;                // DMA parts (2 instructions) per slice
+
+    const EeGemmArgs& g;
+    uint8_t* smem;
+    uint32_t lds0;
+    int lane, wave, kq, wm, wn, nk;
+    const uint8_t* pa[2];
+    const uint8_t* pb[2];
+    acc_t acc[2][2];
+    Frags<KIND> fr[2];
+
+    __device__ __forceinline__ Gemm8(const EeGemmArgs& g_, uint8_t* smem_) : g(g_), smem(smem_) {}
+
+    __device__ __forceinline__ void issue_part(int kt, int part) {
+        const uint32_t s = lds0 + (uint32_t)((kt % NSTAGE) * LDS_STAGE);
+        const int64_t kb = (int64_t)kt * BKB;
+        const int grp = wave * 2 + part;
+        dma16(pa[part] + kb, s + grp * 8 * BKB);
+        dma16(pb[part] + kb, s + (BM + grp * 8) * BKB);
+    }
+    // This wave's loads of stage kt done; the stages issued after it may stay in
+    // flight: before barrier kt those are kt+1 .. kt+NSTAGE-1 (kt == 0) or
+    // kt+1 .. kt+NSTAGE-2, capped at the last stage.
+    __device__ __forceinline__ void wait_stage(int kt) const {
+        const int last = kt == 0 ? NSTAGE - 1 : kt + NSTAGE - 2;
+        const int after = min(last, nk - 1) - kt;
+        if (after >= 4) WAITCNT_VM(4 * LOADS);
+        else if (after == 3) WAITCNT_VM(3 * LOADS);
+        else if (after == 2) WAITCNT_VM(2 * LOADS);
+        else if (after == 1) WAITCNT_VM(LOADS);
+        else WAITCNT_VM(0);
+    }
+
+    // One stage kt.  PAR: parity of the fragment buffer of the wave's first slice.
+    // RPRE: the slices before barrier kt+1 refill stage kt+4 (buffer of stage
+    // kt-1, free since barrier kt); RPOST: the slice after barrier kt+1 refills
+    // stage kt+5; WAITN: stages issued after stage kt+1 that may stay in flight at
+    // barrier kt+1 (vmcnt = WAITN * LOADS); MORE: a stage kt+1 exists.  The
+    // runtime form (GENERIC) decides all of these from kt and nk.
+    template <int PAR, bool GENERIC, bool RPRE, bool RPOST, int WAITN, bool MORE>
+    __device__ __forceinline__ void stage(int kt) {
+        const uint8_t* s = smem + (kt % NSTAGE) * LDS_STAGE;
+        const bool more = GENERIC ? (kt + 1 < nk) : MORE;
+#pragma unroll
+        for (int h = 0; h < HPS; ++h) {
+            Frags<KIND>& cur = fr[(PAR + h) & 1];
+            Frags<KIND>& nxt = fr[(PAR + h + 1) & 1];
+            int dkt = -1, dp0 = 0;
+            bool rd = false;
+            const uint8_t* rs = s;
+            int rsl = kq * HPS + h + 1;
+            if (h + 1 < HPS) {
+                rd = true;
+                if (GENERIC ? (kt >= 1 && kt + NSTAGE - 1 < nk) : RPRE) { dkt = kt + NSTAGE - 1; dp0 = (h + 1) * PPS; }
+            } else if (more) {
+                __builtin_amdgcn_sched_barrier(0);
+                if (GENERIC) wait_stage(kt + 1);
+                else WAITCNT_VM(WAITN * LOADS);
+                WAITCNT_LGKM0();
+                asm volatile("" ::: "memory");
+                __builtin_amdgcn_s_barrier();         // barrier kt+1: stage kt+1 landed, stage kt read
+                asm volatile("" ::: "memory");
+                rd = true;
+                rs = smem + ((kt + 1) % NSTAGE) * LDS_STAGE;
+                rsl = kq * HPS;
+                if (GENERIC ? (kt + NSTAGE < nk) : RPOST) { dkt = kt + NSTAGE; dp0 = 0; }
+            }
+            // MFMA (0,0) | reads A0 B0 B1 | MFMA (0,1) | DMA | MFMA (1,0) | read A1 | MFMA (1,1):
+            // every fragment of the next slice lands two or more MFMAs before its use.
+            acc[0][0] = P::mma(cur.b[0], cur.a[0], acc[0][0]);
+            __builtin_amdgcn_sched_barrier(0);
+            if (rd) { read_frag(rs, rsl, nxt.a[0], 0); read_frag(rs, rsl, nxt.b[0], 2); read_frag(rs, rsl, nxt.b[1], 3); }
+            __builtin_amdgcn_sched_barrier(0);
+            acc[0][1] = P::mma(cur.b[1], cur.a[0], acc[0][1]);
+            __builtin_amdgcn_sched_barrier(0);
+            if (dkt >= 0)
+#pragma unroll
+                for (int p = 0; p < PPS; ++p) issue_part(dkt, dp0 + p);
+            __builtin_amdgcn_sched_barrier(0);
+            acc[1][0] = P::mma(cur.b[0], cur.a[1], acc[1][0]);
+            __builtin_amdgcn_sched_barrier(0);
+            if (rd) read_frag(rs, rsl, nxt.a[1], 1);
+            __builtin_amdgcn_sched_barrier(0);
+            acc[1][1] = P::mma(cur.b[1], cur.a[1], acc[1][1]);
+        }
+    }
+    // One fragment of one K slice: which = 0, 1 (A row block), 2, 3 (B row block).
+    __device__ __forceinline__ void read_frag(const uint8_t* s, int slice, typename P::frag_t& f, int which) const {
+        const int r = lane & 31;
+        const int c0 = slice * (P::SB / 16) + (lane >> 5) * P::CPF;
+        const int row = which < 2 ? wm * 64 + which * 32 + r : BM + wn * 64 + (which - 2) * 32 + r;
+        if constexpr (P::CPF == 1) {
+            f = *(const u32x4*)(s + lds_off(row, c0));
+        } else {
+            const u32x4 x0 = *(const u32x4*)(s + lds_off(row, c0)), x1 = *(const u32x4*)(s + lds_off(row, c0 + 1));
+            f = i32x8{(int)x0[0], (int)x0[1], (int)x0[2], (int)x0[3], (int)x1[0], (int)x1[1], (int)x1[2], (int)x1[3]};
+        }
+    }
+    // The last five stages (kt0 = nk - 5 .. nk - 1, nk >= 6), first one of parity P0.
+    template <int P0>
+    __device__ __forceinline__ void tail(int kt0) {
+        constexpr int D = HPS & 1;                     // parity step per stage
+        stage<P0, false, true, false, 3, true>(kt0);
+        stage<(P0 + D) & 1, false, false, false, 2, true>(kt0 + 1);
+        stage<(P0 + 2 * D) & 1, false, false, false, 1, true>(kt0 + 2);
+        stage<(P0 + 3 * D) & 1, false, false, false, 0, true>(kt0 + 3);
+        stage<(P0 + 4 * D) & 1, false, false, false, 0, false>(kt0 + 4);
+    }
+    __device__ __forceinline__ void run(int tm, int tn) {
+        const int tid = threadIdx.x;
+        lane = tid & 63;
+        wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+        kq = wave >> 2;
+        wm = (wave >> 1) & 1;
+        wn = wave & 1;
+        const int M = g.counts ? g.counts[g.tier] : g.M;
+        const int64_t off = g.counts ? tier_offset(g.counts, g.tier) : 0;
+        const int m0 = tm * BM, n0 = tn * BN;
+        if (m0 >= M) return;                          // whole workgroup, before any barrier
+        nk = (int)((int64_t)g.K * ESZ / BKB);         // K * ESZ is a multiple of BKB here
+
+        // Scales of the wave's final block first: they are the oldest loads the
+        // first stage wait covers.
+        TileScales sc;
+        if (!g.acc) load_scales_blk<KIND>(g, m0, n0, M, off, wm, wn, kq, lane, sc);
+        // DMA: one global_load_lds_dwordx4 fills 8 LDS rows (1 KB): lane l lands at
+        // row r = 8*grp + l/8, physical chunk l%8, which holds logical chunk
+        // (l%8) ^ swz(r).  Wave w fills row groups 2w, 2w+1 of A and of B.
+        const int lrow = lane >> 3;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int r = (wave * 2 + i) * 8 + lrow;
+            const int lchunk = (lane & 7) ^ swz(r);   // swz(BM + r) == swz(r): BM is a multiple of 16
+            const int m = min(m0 + r, M - 1);
+            const int64_t ar = g.a_idx ? (int64_t)g.a_idx[off + m] : off + m;
+            pa[i] = (const uint8_t*)g.a + ar * g.lda * ESZ + lchunk * 16;
+            const int n = min(n0 + r, g.N - 1);
+            pb[i] = (const uint8_t*)g.b + (int64_t)n * g.ldb * ESZ + lchunk * 16;
+        }
+        lds0 = lds_addr(smem);
+#pragma unroll
+        for (int st = 0; st < NSTAGE; ++st)
+            if (st < nk) { issue_part(st, 0); issue_part(st, 1); }
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) acc[i][j] = acc_t{};
+
+        wait_stage(0);
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();                 // barrier 0: stage 0 has landed
+        asm volatile("" ::: "memory");
+        read_frag(smem, kq * HPS, fr[0].a[0], 0);
+        read_frag(smem, kq * HPS, fr[0].b[0], 2);
+        read_frag(smem, kq * HPS, fr[0].b[1], 3);
+        read_frag(smem, kq * HPS, fr[0].a[1], 1);
+        constexpr int D = HPS & 1;
+        if (nk >= 6) {
+            // stage 0 (stage 4 came with the prologue), steady state, tail
+            stage<0, false, false, true, 3, true>(0);
+            int kt = 1;
+            if constexpr (D == 0) {
+                for (; kt <= nk - 6; ++kt) stage<0, false, true, true, 3, true>(kt);
+                tail<0>(kt);
+            } else {
+                for (; kt + 1 <= nk - 6; kt += 2) {
+                    stage<1, false, true, true, 3, true>(kt);
+                    stage<0, false, true, true, 3, true>(kt + 1);
+                }
+                if (kt <= nk - 6) { stage<1, false, true, true, 3, true>(kt); ++kt; }
+                if (kt & 1) tail<1>(kt);
+                else tail<0>(kt);
+            }
+        } else if constexpr (D == 0) {
+            for (int kt = 0; kt < nk; ++kt) stage<0, true, false, false, 0, false>(kt);
+        } else {
+            int kt = 0;
+            for (; kt + 1 < nk; kt += 2) {
+                stage<0, true, false, false, 0, false>(kt);
+                stage<1, true, false, false, 0, false>(kt + 1);
+            }
+            if (kt < nk) stage<0, true, false, false, 0, false>(kt);
+        }
+
+        // Pair exchange.  After the last barrier every buffer but stage nk-1's is
+        // free (all DMA landed before it; stage nk-1-i was read before barrier
+        // nk-i), i.e. buffers (nk + i) % NSTAGE, i = 0..3.  Wave w's 8 KB receive
+        // slot is quarter (w & 3) of buffer (nk + 1 + (w >> 2)) % NSTAGE; its
+        // 4 KB epilogue tile is in buffer nk % NSTAGE.
+        acc_t blk[2];
+        {
+            const int partner = wave ^ 4;
+            uint8_t* dst = smem + ((nk + 1 + (partner >> 2)) % NSTAGE) * LDS_STAGE + (partner & 3) * 8192;
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                xchg_put(dst + j * 4096, kq ? acc[0][j] : acc[1][j], lane);
+                blk[j] = kq ? acc[1][j] : acc[0][j];
+            }
+            WAITCNT_LGKM0();                          // this wave's LDS writes are done
+            asm volatile("" ::: "memory");
+            __builtin_amdgcn_s_barrier();             // every partner's half has landed
+            asm volatile("" ::: "memory");
+            const uint8_t* src = smem + ((nk + 1 + (wave >> 2)) % NSTAGE) * LDS_STAGE + (wave & 3) * 8192;
+#pragma unroll
+            for (int j = 0; j < 2; ++j) xchg_add<KIND>(src + j * 4096, blk[j], lane);
+        }
+        if (g.acc) {
+            epilogue_blk_direct<KIND>(g, blk, m0, n0, M, off, wm, wn, kq, lane);
+        } else {
+            uint8_t* tile = smem + (nk % NSTAGE) * LDS_STAGE + wave * 4096;
+            epilogue_blk_lds<KIND>(g, blk, sc, tile, m0, n0, M, off, wm, wn, kq, lane);
+        }
+    }
+};
+
+template <int KIND>
+EE_DEV void gemm_pipelined_8w(const EeGemmArgs& g) {
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[NSTAGE * LDS_STAGE];
+    int tm, tn;
+    tile_of((int)blockIdx.x, (int)gridDim.x, (g.M + BM - 1) / BM, tm, tn);
+    Gemm8<KIND> k(g, smem);
+    k.run(tm, tn);
+}
+
 template <int KIND>
 EE_DEV void gemm_pipelined(const EeGemmArgs& g) {
     __shared__ __attribute__((aligned(1024))) uint8_t smem[NSTAGE * LDS_STAGE];
@@ -592,6 +978,12 @@ extern "C" __global__ void __launch_bounds__(GEMM_THREADS) __attribute__((amdgpu
 extern "C" __global__ void __launch_bounds__(GEMM_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2))) eek_gemm_f16(EeGemmArgs g) {
     gemm_pipelined<EE_GEMM_F16>(g);
 }
+extern "C" __global__ void __launch_bounds__(GEMM8_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2))) eek_gemm_i8_w8(EeGemmArgs g) {
+    gemm_pipelined_8w<EE_GEMM_I8>(g);
+}
+extern "C" __global__ void __launch_bounds__(GEMM8_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2))) eek_gemm_f16_w8(EeGemmArgs g) {
+    gemm_pipelined_8w<EE_GEMM_F16>(g);
+}
 
 // The routed linear's three tier GEMMs in one launch.  Tier t owns partition
 // slots [off_t, off_t + counts[t]) (off_t = counts[0] + ... + counts[t-1]) and
@@ -610,7 +1002,14 @@ eek_gemm_routed(EeRoutedGemmArgs r) {
     tile_of((int)blockIdx.x, (int)gridDim.x, r.mt_max, tm, tn);
     if (tm < T0) gemm_tile<EE_GEMM_I8>(r.t[0], tm, tn, smem);
     else if (tm < T0 + T1) gemm_tile<EE_GEMM_F8>(r.t[1], tm - T0, tn, smem);
-    else if (tm < T0 + T1 + T2) gemm_tile<EE_GEMM_F16>(r.t[2], tm - T0 - T1, tn, smem);
+    else if (tm < T0 + T1 + T2) {
+        if (r.f16_w8) {
+            Gemm8<EE_GEMM_F16> k(r.t[2], smem);
+            k.run(tm - T0 - T1, tn);
+        } else {
+            gemm_tile<EE_GEMM_F16>(r.t[2], tm - T0 - T1, tn, smem);
+        }
+    }
 }
 
 // Fallback for any K that is a multiple of 16 bytes (zero-filled K tail).

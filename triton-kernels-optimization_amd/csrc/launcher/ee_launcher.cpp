@@ -376,6 +376,8 @@ EE_EXPORT int ee_engine_set_option(ee_engine* eng, const char* key, int64_t valu
     if (k == "se_wpr" || k == "quant_wpr") {
         if (value != 0 && value != 1 && value != 2 && value != 4)
             return fail(EE_ERR_INVALID_ARG, k + " must be 0 (auto), 1, 2 or 4");
+    } else if (k == "gemm_variant") {
+        if (value < 0 || value > 2) return fail(EE_ERR_INVALID_ARG, k + " must be 0 (auto), 1 or 2");
     } else if (k == "routed_unfused") {
         if (value != 0 && value != 1) return fail(EE_ERR_INVALID_ARG, k + " must be 0 or 1");
     } else {
@@ -522,10 +524,22 @@ EE_EXPORT int ee_gemm(ee_engine* eng, int32_t kind, const void* a, int64_t lda, 
     EeGemmArgs g{a, b_nk, (uint16_t*)c, acc_out, a_scale, b_scale, a_idx, c_idx, counts, lda, ldb, ldc,
                  M, N, K, counts ? tier : 0};
     // The pipelined kernels stream whole 128-byte K stages; other K take the fallback.
+    // Two pipelines: loader waves + MFMA waves (eek_gemm_*), and eight waves that
+    // each load and compute (eek_gemm_*_w8).  Measured on MI355X (identical data,
+    // interleaved runs): the 8-wave form is faster for W8A16 at every shape and
+    // for INT8 when the grid is at most one tile per CU (1024 x 4096 x 4096:
+    // 22.9 vs 24.9 us); with several tiles per CU the loader-wave form is ~5%
+    // faster for INT8.  FP8 keeps the loader-wave form (its 8-wave form spills).
     static const char* names[3] = {"eek_gemm_i8", "eek_gemm_f8", "eek_gemm_f16"};
-    const std::string name = std::string(names[kind]) + (((K * esz) % 128 == 0) ? "" : "_generic");
+    const int64_t tiles = cdiv(M, 128) * cdiv(N, 128);
+    std::string name = std::string(names[kind]) + (((K * esz) % 128 == 0) ? "" : "_generic");
+    if ((K * esz) % 128 == 0) {
+        const int64_t v = opt(eng, "gemm_variant");
+        const bool w8 = v == 2 || (v == 0 && (kind == EE_GEMM_F16 || (kind == EE_GEMM_I8 && tiles <= 256)));
+        if (w8 && find_kernel(eng, name + "_w8")) name += "_w8";
+    }
     const Kernel* k = find_kernel(eng, name);
-    return launch(eng, name, cdiv(M, 128) * cdiv(N, 128), 1, k ? k->block : EE_BLOCK, g, stream);
+    return launch(eng, name, tiles, 1, k ? k->block : EE_BLOCK, g, stream);
 }
 
 EE_EXPORT int ee_route(ee_engine* eng, const float* h, int64_t rows, double tau_low, double tau_high,
@@ -586,6 +600,7 @@ EE_EXPORT int ee_routed_linear(ee_engine* eng, const void* x, int64_t ld_x, int3
         ra.t[2] = EeGemmArgs{x, b_f16, (uint16_t*)c, nullptr, nullptr, nullptr, idx, idx, counts,
                              ld_x, K, ldc, M, N, K, EE_TIER_FP16};
         ra.mt_max = (int32_t)cdiv(M, 128) + 2;
+        ra.f16_w8 = opt(eng, "gemm_variant") != 1;   // the FP16 pipeline ee_gemm picks (same f32 order)
         const Kernel* k = find_kernel(eng, "eek_gemm_routed");
         return launch(eng, "eek_gemm_routed", (int64_t)ra.mt_max * cdiv(N, 128), 1, k ? k->block : EE_BLOCK, ra,
                       stream);
