@@ -75,7 +75,8 @@ int ee_abi_version(void);
  * (the reference leaks its CUmodule). */
 int ee_engine_create(const char* lib_dir, ee_engine** out);
 int ee_engine_destroy(ee_engine* eng);
-/* Tuning knobs (0 = automatic): "se_wpr" / "quant_wpr" waves per row (1,2,4);
+/* Tuning knobs (0 = automatic): "se_wpr" waves per softmax row (1..8),
+ * "quant_wpr" waves per quantiser row (1,2,4);
  * "routed_unfused" = 1 makes ee_routed_linear use its five-launch sequence for
  * every K (for comparisons); "gemm_variant" = 1 runs every GEMM on the
  * loader-wave pipeline, 2 on the 8-wave pipeline where one exists (INT8 and

@@ -108,8 +108,15 @@ def test_built_meta_lists_every_kernel_the_launcher_selects():
     ks = meta["kernels"]
     for v in range(1, 9):
         for w in (1, 2, 4):
-            assert f"eek_softmax_entropy_v{v}_w{w}" in ks and f"eek_quant_v{v}_w{w}" in ks
+            assert f"eek_quant_v{v}_w{w}" in ks
+    # softmax row kernels: 1..8 waves per row with up to 4 vectors per lane, and
+    # eight waves with 5..8; block = rows per block * waves per row * 64
+    se = [(v, w) for v in range(1, 5) for w in range(1, 9)] + [(v, 8) for v in range(5, 9)]
+    for v, w in se:
+        rpb = 4 if w == 1 else (2 if w == 2 else 1)
+        assert ks[f"eek_softmax_entropy_v{v}_w{w}"]["block"] == rpb * w * 64
     for k in ("eek_softmax_entropy_generic", "eek_quant_generic", "eek_gemm_i8", "eek_gemm_f8", "eek_gemm_f16",
+              "eek_gemm_i8_w8", "eek_gemm_f16_w8",
               "eek_gemm_i8_generic", "eek_gemm_f8_generic", "eek_gemm_f16_generic",
               "eek_route", "eek_row_copy", "eek_transpose_i8", "eek_pack_b_f8", "eek_pack_b_f16"):
         assert k in ks
@@ -117,7 +124,7 @@ def test_built_meta_lists_every_kernel_the_launcher_selects():
     assert ks["eek_gemm_i8"]["lds"] == 5 * 256 * 128 and ks["eek_gemm_i8_generic"]["lds"] == 2 * 256 * 128
     assert ks["eek_route"]["block"] == 1024
     # pipelined GEMMs: 4 compute + 4 loader wave64s; the Triton-style meta says 8 "warps"
-    for k in ("eek_gemm_i8", "eek_gemm_f8", "eek_gemm_f16", "eek_gemm_routed"):
+    for k in ("eek_gemm_i8", "eek_gemm_f8", "eek_gemm_f16", "eek_gemm_routed", "eek_gemm_i8_w8", "eek_gemm_f16_w8"):
         assert ks[k]["block"] == 512 and ks[k]["lds"] == 5 * 256 * 128
     for f in ("gemm_int8_meta.json", "gemm_fp8_meta.json", "gemm_fp16_meta.json"):
         gm = json.load(open(os.path.join(PKG, "lib", f)))

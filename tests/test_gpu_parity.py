@@ -101,11 +101,11 @@ def test_softmax_entropy_rows(ee, orc, R, S):
     check_probs(host(p), P_ref)
 
 
-@pytest.mark.parametrize("wpr", [1, 2, 4])
-def test_softmax_entropy_every_row_split(ee, orc, wpr):
+@pytest.mark.parametrize("wpr,S", [(w, 2048) for w in range(1, 9)] + [(7, 14336), (8, 14336), (8, 30000), (3, 1000)])
+def test_softmax_entropy_every_row_split(ee, orc, wpr, S):
     from entropy_engine import _lib
-    rng = np.random.default_rng(wpr)
-    X = logits_rows(rng, 40, 2048)
+    rng = np.random.default_rng(wpr * 31 + S)
+    X = logits_rows(rng, 40, S)
     H_ref, P_ref = orc.softmax_entropy(X)
     L = _lib.lib()
     _lib.check(L.ee_engine_set_option(_lib.engine(), b"se_wpr", wpr))
@@ -115,6 +115,31 @@ def test_softmax_entropy_every_row_split(ee, orc, wpr):
         check_probs(host(p), P_ref)
     finally:
         _lib.check(L.ee_engine_set_option(_lib.engine(), b"se_wpr", 0))
+
+
+def test_softmax_entropy_max_in_several_waves(ee, orc):
+    """Rows whose maximum (and its ties) sit in different waves of the row, near
+    one-hot rows, and +-0 maxima: the waves holding the max take the counting
+    loop, the others the test-free one; H within 1e-5 relative either way."""
+    S = 14336
+    rng = np.random.default_rng(77)
+    X = (rng.standard_normal((10, S)) * 0.5).astype(np.float16)
+    X[0, [0, 3000, 9000, S - 1]] = 9.0          # four tied maxima in four waves
+    X[1, 5] = 30.0                              # near one-hot
+    X[2, [7, 8]] = 25.0                         # two ties in one lane
+    X[3] = -1.0; X[3, 100] = 0.0                # max +0 ...
+    X[4] = -1.0; X[4, 100] = -0.0; X[4, 2000] = 0.0   # ... and -0 tied with +0
+    X[5] = -np.inf; X[5, 4096] = -3.0; X[5, 12000] = -3.0
+    X[6] = 3.0                                  # constant row: every wave holds the max
+    H_ref, P_ref = orc.softmax_entropy(X)
+    try:
+        for w in (0, 7, 8):
+            _lib_set(ee, "se_wpr", w)
+            p, h, _ = ee.softmax_entropy(cuda(X))
+            check_entropy(host(h), H_ref)
+            check_probs(host(p), P_ref)
+    finally:
+        _lib_set(ee, "se_wpr", 0)
 
 
 def test_softmax_entropy_closed_forms(ee, orc):
@@ -148,7 +173,7 @@ def test_softmax_entropy_rows_without_a_finite_max(ee, orc, S):
     X[5, S - 1] = np.nan
     H_ref, P_ref = orc.softmax_entropy(X)
     try:
-        for w in (0, 1, 2, 4):
+        for w in range(0, 9):
             _lib_set(ee, "se_wpr", w)
             p, h, _ = ee.softmax_entropy(cuda(X))
             h, p = host(h), host(p)

@@ -256,6 +256,33 @@ bool pick_row_cfg(int64_t len, int64_t rows, int64_t forced_wpr, int& vpt, int& 
     return true;
 }
 
+// (VPT, WPR) for the softmax row kernel: WPR = 1..8 waves per row holding
+// VPT <= 4 vectors per lane (the kernel keeps e in registers up to 4), with
+// VPT * WPR * 512 >= len.  Among the layouts that cover the row with the
+// least padding, the fewest waves per row that still put >= 4096 waves on the
+// chip.  Rows longer than 4 * 8 * 512 take eight waves and VPT 5..8.
+bool pick_se_cfg(int64_t len, int64_t rows, int64_t forced_wpr, int& vpt, int& wpr) {
+    int best_w = -1, best_v = 0;
+    int64_t best_pad = 0;
+    for (int w = 1; w <= 8; ++w) {
+        if (forced_wpr && w != forced_wpr) continue;
+        const int v = (int)std::max<int64_t>(1, cdiv(len, 512LL * w));
+        if (v > 4 && !(w == 8 && v <= 8)) continue;
+        const int64_t pad = (int64_t)v * w * 512 - len;
+        const bool fills = rows * w >= 4096;
+        if (best_w < 0) { best_w = w; best_v = v; best_pad = pad; continue; }
+        const bool best_fills = rows * best_w >= 4096;
+        // prefer filling the chip, then least padding, then fewer waves per row
+        if ((fills && !best_fills) || (fills == best_fills && pad < best_pad)) {
+            best_w = w; best_v = v; best_pad = pad;
+        }
+    }
+    if (best_w < 0) return false;
+    wpr = best_w;
+    vpt = best_v;
+    return true;
+}
+
 int64_t opt(const ee_engine* e, const char* key) {
     auto it = e->options.find(key);
     return it == e->options.end() ? 0 : it->second;
@@ -373,7 +400,9 @@ EE_EXPORT int ee_engine_destroy(ee_engine* eng) {
 EE_EXPORT int ee_engine_set_option(ee_engine* eng, const char* key, int64_t value) {
     if (eng == nullptr || key == nullptr) return fail(EE_ERR_INVALID_ARG, "engine and key must not be NULL");
     const std::string k(key);
-    if (k == "se_wpr" || k == "quant_wpr") {
+    if (k == "se_wpr") {
+        if (value < 0 || value > 8) return fail(EE_ERR_INVALID_ARG, k + " must be 0 (auto) or 1..8");
+    } else if (k == "quant_wpr") {
         if (value != 0 && value != 1 && value != 2 && value != 4)
             return fail(EE_ERR_INVALID_ARG, k + " must be 0 (auto), 1, 2 or 4");
     } else if (k == "gemm_variant") {
@@ -403,9 +432,11 @@ EE_EXPORT int ee_softmax_entropy(ee_engine* eng, const void* x, void* p, float* 
     EeSoftmaxArgs a{(const uint16_t*)x, (uint16_t*)p, h, tier, rows, ld_x, ld_p, S, causal, tau_low, tau_high};
     const bool vec_ok = aligned(x, 16) && aligned(p, 16) && ld_x % 8 == 0 && (p == nullptr || ld_p % 8 == 0);
     int vpt = 0, wpr = 0;
-    if (vec_ok && pick_row_cfg(S, rows, opt(eng, "se_wpr"), vpt, wpr)) {
+    if (vec_ok && pick_se_cfg(S, rows, opt(eng, "se_wpr"), vpt, wpr)) {
         const std::string name = "eek_softmax_entropy_v" + std::to_string(vpt) + "_w" + std::to_string(wpr);
-        return launch(eng, name, cdiv(rows, 4 / wpr), 1, EE_BLOCK, a, stream);
+        const int rpb = wpr == 1 ? 4 : (wpr == 2 ? 2 : 1);      // rows per block (kernel's SeGeom)
+        const Kernel* k = find_kernel(eng, name);
+        return launch(eng, name, cdiv(rows, rpb), 1, k ? k->block : rpb * wpr * 64, a, stream);
     }
     return launch(eng, "eek_softmax_entropy_generic", cdiv(rows, 4), 1, EE_BLOCK, a, stream);
 }
