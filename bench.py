@@ -265,9 +265,10 @@ def main():
         except RuntimeError as e:
             print(f"# torch._int_mm unavailable: {e}", file=sys.stderr)
         if "hbm_copy" in only:                                         # PMC calibration: 256 MiB read + 256 MiB written
+            # an elementwise kernel (a device-to-device copy_ of this size goes to the DMA engine)
             src = torch.empty(COPY_BYTES // 4, dtype=torch.float32, device=dev).fill_(1.0)
             dst = torch.empty_like(src)
-            run("hbm_copy", lambda: dst.copy_(src))
+            run("hbm_copy", lambda: torch.neg(src, out=dst))
         # ---- config 3: the dispatcher end to end on a mixed batch (M = K = N = 4096)
         c3 = None
         c3_names = ("c3_entropy", "c3_route", "c3_linear", "c3_end_to_end")
