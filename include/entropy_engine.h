@@ -187,6 +187,52 @@ int ee_routed_linear(ee_engine* eng, const void* x, int64_t ld_x, int32_t M, int
                      const void* b_f16, const float* b_scale, void* c, int64_t ldc, void* ws_codes,
                      float* ws_scale, ee_stream_t stream);
 
+/* ---- fused MLP: the engine EE/test_engine.py:17-26 calls ----------------------
+ * The reference's test constructs entropy_engine_cuda.EntropyMLPEngine(gate_w,
+ * up_w, down_w, tau_low, tau_high) and calls .forward(hidden, entropy), but
+ * EE/csrc/engine.cpp:202-216 never defines it; its baseline is
+ * F.linear(F.silu(F.linear(x, gate_w)) * F.linear(x, up_w), down_w) under the
+ * dispatcher's tier choice (EE/test_engine.py:33-39).  These entry points are
+ * that engine with every linear on the tier GEMMs above, as the Llama block
+ * gates its MLP (EE/python/dispatch.py:199-203).
+ *
+ * ee_silu_mul: act[m, f] = fp16( fp16(silu(g)) * u ) with g = gu[m, f],
+ * u = gu[m, F + f] (gate columns, then up columns, as one [M, 2F] row); the
+ * two roundings of torch's fp16 F.silu(g) * u. */
+int ee_silu_mul(ee_engine* eng, const void* gu, int64_t ld_gu, void* act, int64_t ld_act, int64_t M,
+                int64_t F, ee_stream_t stream);
+
+/* Weight preparation: gate_w, up_w fp16 [F, H] and down_w fp16 [H, F] (the
+ * nn.Linear layout, EE/test_engine.py:12-14) quantised per output channel as
+ * quantize_weights_int8 does (EE/python/dispatch.py:43-48), into the caller's
+ * buffers: gu_* hold the [2F, H] operand (gate rows 0..F-1, up rows F..2F-1)
+ * as int8 codes, e4m3 codes, W8A16 fp16 weights and f32 scales [2F]; dn_* the
+ * [H, F] down operand and scales [H].  All 16-byte aligned, row stride = K. */
+int ee_mlp_prepare(ee_engine* eng, const void* gate_w, const void* up_w, const void* down_w, int64_t H,
+                   int64_t F, int64_t ld_gate, int64_t ld_up, int64_t ld_down, int8_t* gu_i8, uint8_t* gu_f8,
+                   void* gu_f16, float* gu_scale, int8_t* dn_i8, uint8_t* dn_f8, void* dn_f16, float* dn_scale,
+                   ee_stream_t stream);
+
+/* Workspace bytes ee_mlp_forward needs for M rows (routed != 0: per-row
+ * tiers); -1 for a bad shape. */
+int64_t ee_mlp_workspace_bytes(int64_t M, int64_t H, int64_t F, int32_t routed);
+
+/* out[M, H] = down( silu(gate(x)) * up(x) ) for x fp16 [M, H].
+ * h_rows == NULL: one tier for the call from `entropy` by the dispatcher's
+ * strict compares (EE/python/dispatch.py:74-79): INT8 = per-row int8
+ * activations (EE_QUANT_I8_DISPATCH) on the I8 GEMM, FP8 = per-row e4m3 on
+ * the F8 GEMM, FP16 = W8A16; the intermediate is re-quantised by the same
+ * tier before the down GEMM, as a separate dispatched linear would.
+ * h_rows != NULL (f32 [M]): one tier per row (ee_route), both linears on
+ * ee_routed_linear; `entropy` is ignored.  No host synchronisation, no
+ * allocation; workspace 256-byte aligned, ws_bytes >= ee_mlp_workspace_bytes.
+ * Contract: H, F multiples of 16; ld_x multiple of 8; ldo multiple of 4. */
+int ee_mlp_forward(ee_engine* eng, const void* x, int64_t ld_x, int64_t M, int64_t H, int64_t F,
+                   const int8_t* gu_i8, const uint8_t* gu_f8, const void* gu_f16, const float* gu_scale,
+                   const int8_t* dn_i8, const uint8_t* dn_f8, const void* dn_f16, const float* dn_scale,
+                   double entropy, const float* h_rows, double tau_low, double tau_high, void* out, int64_t ldo,
+                   void* workspace, int64_t ws_bytes, ee_stream_t stream);
+
 /* ---- CubinEngine counterpart (EE/csrc/engine.cpp:64-216) --------------------
  * One code object + one GEMM function, launched on the caller's stream (the
  * reference launched on the NULL stream, engine.cpp:160).  create mirrors the

@@ -22,6 +22,11 @@ Pinning (each function's independent checks live in tests/test_oracle_*.py):
                       ln 2), shift invariance, numpy float64 recompute
   route ............. the reference's own tier answers (EE/python/
                       benchmark.py:185-210) and sweep table (NB:555-561)
+  silu_mul .......... numpy restatement of the f32 evaluation with numpy's
+                      casts, torch's CPU and GPU fp16 F.silu, closed forms
+                      (silu(0) = 0, silu(x) - silu(-x) = x, large |x|)
+  mlp_forward ....... composition of the pinned functions above, checked
+                      against an independent numpy float64 MLP
 """
 from __future__ import annotations
 
@@ -76,6 +81,9 @@ def lib() -> ctypes.CDLL:
             "eo_e4m3_from_f32_n": ([_p, _p, _i64], None),
             "eo_e4m3_to_f32_n": ([_p, _p, _i64], None),
             "eo_i8_trunc_n": ([_p, _p, _i64], None),
+            "eo_f64_to_f16": ([ctypes.c_double], ctypes.c_uint16),
+            "eo_f64_to_f16_n": ([_p, _p, _i64], None),
+            "eo_silu_mul": ([_p, _i64, _p, _i64, _i64, _i64, _p], None),
             "eo_num_threads": ([], ctypes.c_int),
         }
         for name, (args, res) in sigs.items():
@@ -328,3 +336,57 @@ def triton_fp8_gemm_f64(a, b_int8, b_scale) -> np.ndarray:
 def triton_fp16_gemm_f64(a, b_int8, b_scale) -> np.ndarray:
     """EE/python/kernels.py:380-409 end to end, float64 before the fp16 store."""
     return gemm_w8a16_f64(a, b_int8, b_scale)
+
+
+# --------------------------------------------------------------------------
+# the Llama MLP (EntropyMLPEngine, EE/test_engine.py:17-39)
+# --------------------------------------------------------------------------
+
+def f64_to_f16(x) -> np.ndarray:
+    """binary64 -> binary16, correctly rounded."""
+    x = _c(x, np.float64)
+    y = np.empty(x.shape, np.uint16)
+    lib().eo_f64_to_f16_n(_ptr(x), _ptr(y), x.size)
+    return y.view(np.float16)
+
+
+def silu_mul(gu, F: int | None = None, with_silu: bool = False):
+    """act fp16 [M, F] = fp16(fp16(silu(gate)) * up) from gu fp16 [M, 2F] (gate | up), silu
+    evaluated in f32 as torch does; with_silu also returns that f32 silu [M, F]."""
+    gu16 = _f16_2d(gu)
+    M, F2 = gu16.shape
+    F = F2 // 2 if F is None else F
+    act = np.empty((M, F), np.uint16)
+    s = np.empty((M, F), np.float32) if with_silu else None
+    lib().eo_silu_mul(_ptr(gu16), F2, _ptr(act), F, M, F, _ptr(s) if with_silu else None)
+    return (act.view(np.float16), s) if with_silu else act.view(np.float16)
+
+
+def mlp_weights(gate_w, up_w, down_w):
+    """Per-channel int8 quantisation of the three projections (EE/python/dispatch.py:43-48):
+    ((B_gu int8 [H, 2F], s_gu [2F]), (B_dn int8 [F, H], s_dn [H])); gate columns, then up."""
+    Bg, sg = quantize_weights_int8(gate_w)
+    Bu, su = quantize_weights_int8(up_w)
+    Bd, sd = quantize_weights_int8(down_w)
+    return (np.concatenate([Bg, Bu], axis=1), np.concatenate([sg, su])), (Bd, sd)
+
+
+def mlp_linear(x, B, s, tier: int):
+    """One dispatched linear of the tier: INT8 fp16 bit-exact; FP8 / FP16 float64 before the store."""
+    if tier == 0:
+        return triton_int8_gemm(x, B, s)
+    if tier == 1:
+        return triton_fp8_gemm_f64(x, B, s)
+    return triton_fp16_gemm_f64(x, B, s)
+
+
+def mlp_forward(x, gate_w, up_w, down_w, tier: int, act=None):
+    """The MLP under one tier: (gu, act, out).  gu and out are fp16 for INT8, float64 (pre-store)
+    otherwise; FP8 / FP16 intermediates are rounded to fp16 before the next op, as the GPU stores
+    them.  `act` (fp16 [M, F]) replaces the computed activation for the down projection, to check
+    the down GEMM on exactly the operand the device used."""
+    (Bgu, sgu), (Bdn, sdn) = mlp_weights(gate_w, up_w, down_w)
+    gu = mlp_linear(x, Bgu, sgu, tier)
+    gu16 = f64_to_f16(gu) if tier != 0 else gu
+    a = silu_mul(gu16) if act is None else np.asarray(act, np.float16)
+    return gu, a, mlp_linear(a, Bdn, sdn, tier)

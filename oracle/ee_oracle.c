@@ -478,6 +478,53 @@ EO_API void eo_route(const float* H, int64_t R, double tau_low, double tau_high,
 }
 
 /* ------------------------------------------------------------------------ */
+/* SiLU * up of the Llama MLP                                                */
+/* ------------------------------------------------------------------------ */
+
+/* binary64 -> binary16, correctly rounded: round to odd into binary32 first
+ * (24 bits >= 11 + 2, so the final RNE step sees the true sticky bit), then
+ * RNE to binary16.  Finite inputs well inside the binary32 range. */
+EO_API uint16_t eo_f64_to_f16(double d) {
+    float f = (float)d;
+    if ((double)f != d) {
+        uint32_t b;
+        memcpy(&b, &f, 4);
+        if ((b & 1u) == 0) {
+            if (fabs((double)f) > fabs(d)) b -= 1u; else b += 1u;
+        }
+        memcpy(&f, &b, 4);
+    }
+    return eo_f32_to_f16(f);
+}
+
+/* act[m, f] = fp16( fp16(silu(g)) * u ), g = gu[m, f], u = gu[m, F + f]:
+ * torch's fp16 F.silu(gate) * up (HF LlamaMLP, the MLP the reference gates in
+ * EE/python/dispatch.py:199-203 and times in EE/test_engine.py:35).  PyTorch
+ * evaluates silu of an fp16 tensor in f32 ("opmath") as x / (1 + exp(-x)) and
+ * rounds the result to fp16; the product of two fp16 values is exact in f32,
+ * so its fp16 store is its only rounding.  Here exp is the correctly rounded
+ * f32 value (binary64 exp rounded once); the add and the divide are single
+ * f32 operations.  A device exp with a last-bit error can move the fp16 silu
+ * by one ulp, rarely.  silu_f32 (optional, row stride F) receives the f32
+ * silu before its fp16 rounding. */
+EO_API void eo_silu_mul(const uint16_t* gu, int64_t ld_gu, uint16_t* act, int64_t ld_act, int64_t M, int64_t F,
+                        float* silu_f32) {
+#pragma omp parallel for schedule(static)
+    for (int64_t m = 0; m < M; ++m) {
+        for (int64_t f = 0; f < F; ++f) {
+            const float g = eo_f16_to_f32(gu[m * ld_gu + f]);
+            const float e = (float)exp(-(double)g);
+            const float den = 1.0f + e;
+            const float s = g / den;
+            if (silu_f32) silu_f32[m * F + f] = s;
+            const float s16 = eo_f16_to_f32(eo_f32_to_f16(s));
+            const float u = eo_f16_to_f32(gu[m * ld_gu + F + f]);
+            act[m * ld_act + f] = eo_f32_to_f16(s16 * u);
+        }
+    }
+}
+
+/* ------------------------------------------------------------------------ */
 /* Array forms of the scalar conversions (used by the Python face)           */
 /* ------------------------------------------------------------------------ */
 
@@ -492,6 +539,9 @@ EO_API void eo_e4m3_from_f32_n(const float* x, uint8_t* y, int64_t n) {
 }
 EO_API void eo_e4m3_to_f32_n(const uint8_t* x, float* y, int64_t n) {
     for (int64_t i = 0; i < n; ++i) y[i] = eo_e4m3_to_f32(x[i]);
+}
+EO_API void eo_f64_to_f16_n(const double* x, uint16_t* y, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) y[i] = eo_f64_to_f16(x[i]);
 }
 EO_API void eo_i8_trunc_n(const float* x, int8_t* y, int64_t n) {
     for (int64_t i = 0; i < n; ++i) y[i] = eo_i8_trunc(x[i]);

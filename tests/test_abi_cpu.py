@@ -100,7 +100,24 @@ def test_null_engine_rejected(L):
     assert L.ee_softmax_entropy(None, None, None, None, 1, 1, 1, 1, 0, None, 0.0, 0.0, None) == _lib.EE_ERR_INVALID_ARG
     assert L.ee_route(None, None, 1, 0.0, 0.0, None, None, None, None) == _lib.EE_ERR_INVALID_ARG
     assert L.ee_engine_set_option(None, b"se_wpr", 1) == _lib.EE_ERR_INVALID_ARG
+    assert L.ee_silu_mul(None, None, 16, None, 8, 1, 8, None) == _lib.EE_ERR_INVALID_ARG
+    assert L.ee_mlp_forward(None, None, 16, 1, 16, 16, *([None] * 8), 1.0, None, 1.5, 2.5, None, 16, None, 0,
+                            None) == _lib.EE_ERR_INVALID_ARG
+    assert L.ee_mlp_prepare(None, None, None, None, 16, 16, 16, 16, 16, *([None] * 8), None) == _lib.EE_ERR_INVALID_ARG
     assert L.ee_engine_destroy(None) == _lib.EE_OK
+
+
+def test_mlp_workspace_layout(L):
+    """Regions of 256-byte-aligned size: int8/e4m3 codes [M, max(H, F)], f32
+    scales [M], fp16 gate|up [M, 2F], fp16 activation [M, F]; routed adds
+    tier [M], idx [M] (int32) and counts [3]."""
+    M, H, F = 1024, 2048, 5632
+    plain = M * F + M * 4 + M * 2 * F * 2 + M * F * 2
+    assert L.ee_mlp_workspace_bytes(M, H, F, 0) == plain
+    assert L.ee_mlp_workspace_bytes(M, H, F, 1) == plain + 2 * M * 4 + 256
+    assert L.ee_mlp_workspace_bytes(3, 16, 16, 0) == 256 * 4
+    assert L.ee_mlp_workspace_bytes(0, 16, 16, 1) == 256
+    assert L.ee_mlp_workspace_bytes(-1, 16, 16, 0) == -1 and L.ee_mlp_workspace_bytes(4, 0, 16, 0) == -1
 
 
 def test_built_meta_lists_every_kernel_the_launcher_selects():
@@ -118,8 +135,9 @@ def test_built_meta_lists_every_kernel_the_launcher_selects():
     for k in ("eek_softmax_entropy_generic", "eek_quant_generic", "eek_gemm_i8", "eek_gemm_f8", "eek_gemm_f16",
               "eek_gemm_i8_w8", "eek_gemm_f16_w8",
               "eek_gemm_i8_generic", "eek_gemm_f8_generic", "eek_gemm_f16_generic",
-              "eek_route", "eek_row_copy", "eek_transpose_i8", "eek_pack_b_f8", "eek_pack_b_f16"):
+              "eek_route", "eek_row_copy", "eek_transpose_i8", "eek_pack_b_f8", "eek_pack_b_f16", "eek_silu_mul"):
         assert k in ks
+    assert ks["eek_silu_mul"]["block"] == 256
     # pipelined GEMMs: 5 LDS stages of (128 + 128) rows x 128 bytes = all of gfx950's 160 KB
     assert ks["eek_gemm_i8"]["lds"] == 5 * 256 * 128 and ks["eek_gemm_i8_generic"]["lds"] == 2 * 256 * 128
     assert ks["eek_route"]["block"] == 1024
@@ -145,6 +163,11 @@ def test_product_has_no_cpu_path():
             fn(a, b, s)
     with pytest.raises(ValueError, match="GPU tensors"):
         ee.softmax_entropy(a)
+    with pytest.raises(ValueError, match="GPU tensors"):
+        ee.silu_mul(a)
+    w = torch.zeros((32, 16), dtype=torch.float16)
+    with pytest.raises(RuntimeError, match="GPU tensor"):
+        ee.EntropyMLPEngine(w, w, w.T.contiguous(), 1.5, 2.5)
     # the product never imports the test oracle
     for dirpath, _, files in os.walk(os.path.join(PKG, "entropy_engine")):
         for f in files:

@@ -1,0 +1,251 @@
+"""GPU parity of the fused entropy-gated MLP (EntropyMLPEngine, ee_mlp_*,
+ee_silu_mul) against the CPU oracle.
+
+The reference's test builds EntropyMLPEngine(gate_w, up_w, down_w, 1.5, 2.5)
+and calls .forward(hidden, entropy) at B, S, H, Inter = 1, 1024, 2048, 5632
+(EE/test_engine.py:10-26).  Bars: SiLU*up equal to the oracle's (torch's f32
+evaluation with a correctly rounded exp) or to the product of an fp16 silu
+one ulp away (a last-bit exp difference), with >= 99.9 % of elements
+bit-exact, and the same against torch's own GPU F.silu(gate) * up; the engine's
+forward bit-exact to the same chain of public kernels; each stage against the
+oracle -- INT8 linears bit-exact, FP8 / W8A16 linears within 1e-2 relative of
+a float64 recompute from the same codes, each fed the device's own input so
+that one-ulp activation differences do not compound; per-token routing
+bit-exact, row for row, to the single-tier forward of the row's tier.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+F_RTOL = 1e-2
+F_ATOL_RMS = 1e-3
+TAUS = (1.5, 2.5)
+TIER_ENTROPY = {0: 1.0, 1: 2.0, 2: 3.0}
+
+
+@pytest.fixture(scope="module")
+def ee():
+    import entropy_engine
+    return entropy_engine
+
+
+def cuda(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def check_act(act16, gu16, orc, ref=None, min_exact=0.999):
+    """act == oracle, or == fp16(s' * u) for s' the fp16 neighbour of the oracle's fp16 silu."""
+    gu16 = np.asarray(gu16, np.float16)
+    F = gu16.shape[1] // 2
+    ref_o, s32 = orc.silu_mul(gu16, with_silu=True)
+    ref = ref_o if ref is None else ref
+    a, r = act16.view(np.uint16), np.asarray(ref, np.float16).view(np.uint16)
+    nan_a, nan_r = np.isnan(act16), np.isnan(ref)
+    assert np.array_equal(nan_a, nan_r), "NaN positions differ"
+    exact = (a == r) | nan_r
+    assert exact.mean() >= min_exact, f"only {exact.mean():.5f} bit-exact"
+    bad = np.nonzero(~exact)
+    if bad[0].size:
+        s16 = s32[bad].astype(np.float16)
+        u = gu16[:, F:][bad].astype(np.float32)
+        with np.errstate(over="ignore"):
+            alts = [(np.nextafter(s16, np.float16(d)).astype(np.float32) * u).astype(np.float16).view(np.uint16)
+                    for d in (np.inf, -np.inf)] + [(s16.astype(np.float32) * u).astype(np.float16).view(np.uint16)]
+        ok = np.zeros(bad[0].size, bool)
+        for alt in alts:
+            ok |= alt == a[bad]
+        assert ok.all(), f"{(~ok).sum()} elements beyond a one-ulp silu"
+
+
+def check_close_f64(out16, ref64):
+    out = out16.astype(np.float64)
+    fin = np.isfinite(ref64)
+    rms = math.sqrt(np.mean(ref64[fin] ** 2)) if fin.any() else 0.0
+    err = np.abs(out[fin] - ref64[fin])
+    tol = F_RTOL * np.abs(ref64[fin]) + F_ATOL_RMS * rms
+    assert (err <= tol).all(), f"max err {err.max():.3e}; worst excess {(err - tol).max():.3e}"
+
+
+def mlp_weights(rng, H, F):
+    g = (rng.standard_normal((F, H)) / np.sqrt(H)).astype(np.float16)
+    u = (rng.standard_normal((F, H)) / np.sqrt(H)).astype(np.float16)
+    d = (rng.standard_normal((H, F)) / np.sqrt(F)).astype(np.float16)
+    return g, u, d
+
+
+def chain(ee, eng, x, tier):
+    """The same MLP through the public per-op entry points: (gu, act, out)."""
+    if tier == 2:
+        gu = ee.gemm("fp16", x, eng.gu_f16)
+        act = ee.silu_mul(gu)
+        return gu, act, ee.gemm("fp16", act, eng.dn_f16)
+    mode, kind = ("dispatcher", "int8") if tier == 0 else ("fp8", "fp8")
+    b_gu, b_dn = (eng.gu_i8, eng.dn_i8) if tier == 0 else (eng.gu_f8, eng.dn_f8)
+    c, s = ee.quantize_activations(x, mode)
+    gu = ee.gemm(kind, c, b_gu, s, eng.gu_scale)
+    act = ee.silu_mul(gu)
+    c2, s2 = ee.quantize_activations(act, mode)
+    return gu, act, ee.gemm(kind, c2, b_dn, s2, eng.dn_scale)
+
+
+# ---------------------------------------------------------------------------- SiLU * up
+
+SPECIAL = np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 65504.0, -65504.0, 6e-8, -6e-8, 1e-4, -1e-4,
+                    20.0, -20.0, 11.0, -11.0, 0.5, -0.5, -17.3, 8.0, -1.278], np.float16)
+
+
+@pytest.mark.parametrize("M,F,pad", [(7, 24, 0), (5, 20, 0), (256, 5632, 0), (33, 64, 8), (3, 40, 3), (1, 8, 0)])
+def test_silu_mul(ee, orc, M, F, pad):
+    rng = np.random.default_rng(M * 1000 + F + pad)
+    gu = (rng.standard_normal((M, 2 * F + pad)) * rng.choice([0.1, 1.0, 4.0, 30.0], (M, 1))).astype(np.float16)
+    n = min(SPECIAL.size, F)
+    gu[0, :n] = SPECIAL[:n]
+    gu[0, F:F + n] = SPECIAL[::-1][:n]
+    dev = cuda(gu)[:, :2 * F]
+    act = host(ee.silu_mul(dev))
+    check_act(act, gu[:, :2 * F], orc)
+
+
+@pytest.mark.parametrize("up", [1.0, -3.0, 0.001, 20.0])
+def test_silu_mul_every_fp16_gate(ee, orc, up):
+    """All 65,536 fp16 gate values; against the oracle and against torch's own
+    GPU fp16 F.silu(gate) * up (the reference baseline's op, EE/test_engine.py:35)."""
+    g = np.arange(65536, dtype=np.uint32).astype(np.uint16).view(np.float16).reshape(256, 256)
+    gu = np.concatenate([g, np.full_like(g, up)], axis=1)
+    gd = cuda(gu)
+    act = host(ee.silu_mul(gd))
+    check_act(act, gu, orc)
+    ref_torch = host(torch.nn.functional.silu(gd[:, :256]) * gd[:, 256:])
+    check_act(act, gu, orc, ref=ref_torch)
+
+
+def test_silu_mul_rejects_bad_input(ee):
+    with pytest.raises(ValueError):
+        ee.silu_mul(torch.zeros((4, 7), dtype=torch.float16, device="cuda"))
+    with pytest.raises(TypeError):
+        ee.silu_mul(torch.zeros((4, 8), dtype=torch.float32, device="cuda"))
+
+
+# ---------------------------------------------------------------------------- engine
+
+def test_mlp_prepare_matches_oracle(ee, orc):
+    rng = np.random.default_rng(7)
+    H, F = 128, 96
+    g, u, d = mlp_weights(rng, H, F)
+    eng = ee.EntropyMLPEngine(cuda(g), cuda(u), cuda(d), *TAUS)
+    (Bgu, sgu), (Bdn, sdn) = orc.mlp_weights(g, u, d)
+    assert np.array_equal(host(eng.gu_i8), Bgu.T)
+    assert np.array_equal(host(eng.gu_scale).view(np.uint32), sgu.view(np.uint32))
+    assert np.array_equal(host(eng.dn_i8), Bdn.T)
+    assert np.array_equal(host(eng.dn_scale).view(np.uint32), sdn.view(np.uint32))
+    assert np.array_equal(host(eng.gu_f8), orc.e4m3_from_f32(Bgu.T.astype(np.float32)))
+    assert np.array_equal(host(eng.dn_f8), orc.e4m3_from_f32(Bdn.T.astype(np.float32)))
+    assert np.array_equal(host(eng.gu_f16).view(np.uint16), orc.dequant_w8a16(Bgu, sgu).T.copy().view(np.uint16))
+    assert np.array_equal(host(eng.dn_f16).view(np.uint16), orc.dequant_w8a16(Bdn, sdn).T.copy().view(np.uint16))
+
+
+@pytest.mark.parametrize("tier", [0, 1, 2], ids=["int8", "fp8", "fp16"])
+@pytest.mark.parametrize("M,H,F", [(96, 256, 352), (1, 128, 64), (130, 512, 1024)])
+def test_mlp_forward_tier(ee, orc, tier, M, H, F):
+    rng = np.random.default_rng(M + H + F + tier)
+    g, u, d = mlp_weights(rng, H, F)
+    x = rng.standard_normal((M, H)).astype(np.float16)
+    eng = ee.EntropyMLPEngine(cuda(g), cuda(u), cuda(d), *TAUS)
+    assert int(eng.tier(TIER_ENTROPY[tier])) == tier
+    xd = cuda(x)
+    out = host(eng.forward(xd, TIER_ENTROPY[tier]))
+    gu_d, act_d, out_c = chain(ee, eng, xd, tier)
+    assert np.array_equal(out.view(np.uint16), host(out_c).view(np.uint16)), "engine != chain of public kernels"
+    gu, act = host(gu_d), host(act_d)
+    gu_ref, _, out_ref = orc.mlp_forward(x, g, u, d, tier, act=act)
+    check_act(act, gu, orc)
+    if tier == 0:
+        assert np.array_equal(gu.view(np.uint16), gu_ref.view(np.uint16))
+        assert np.array_equal(out.view(np.uint16), out_ref.view(np.uint16))
+    else:
+        check_close_f64(gu, gu_ref)
+        check_close_f64(out, out_ref)
+
+
+def test_mlp_tier_thresholds_are_strict(ee):
+    """Ties go up a tier (EE/python/dispatch.py:74-79): entropy == tau_low runs
+    FP8, == tau_high runs FP16."""
+    rng = np.random.default_rng(3)
+    H, F, M = 128, 64, 16
+    g, u, d = mlp_weights(rng, H, F)
+    eng = ee.EntropyMLPEngine(cuda(g), cuda(u), cuda(d), *TAUS)
+    x = cuda(rng.standard_normal((M, H)).astype(np.float16))
+    outs = {t: host(eng.forward(x, TIER_ENTROPY[t])).view(np.uint16) for t in range(3)}
+    assert not np.array_equal(outs[0], outs[1]) and not np.array_equal(outs[1], outs[2])
+    assert np.array_equal(host(eng.forward(x, TAUS[0])).view(np.uint16), outs[1])
+    assert np.array_equal(host(eng.forward(x, TAUS[1])).view(np.uint16), outs[2])
+    assert np.array_equal(host(eng.forward(x, np.nextafter(TAUS[0], 0))).view(np.uint16), outs[0])
+
+
+@pytest.mark.parametrize("M,H,F", [(200, 256, 352), (300, 512, 1024), (5, 128, 64)])
+def test_mlp_routed_rows_equal_single_tier(ee, orc, M, H, F):
+    """Per-token tiers: each row equals that row's single-tier forward, bit for bit."""
+    rng = np.random.default_rng(M * 7 + F)
+    g, u, d = mlp_weights(rng, H, F)
+    eng = ee.EntropyMLPEngine(cuda(g), cuda(u), cuda(d), *TAUS)
+    x = rng.standard_normal((M, H)).astype(np.float16)
+    h = rng.choice(np.array([0.3, 1.0, 1.5, 2.0, 2.5, 3.0, 7.0], np.float32), M)
+    out = host(eng.forward(cuda(x), cuda(h))).view(np.uint16)
+    tier, _, _ = orc.route(h, *TAUS)
+    for t in range(3):
+        rows = np.nonzero(tier == t)[0]
+        if rows.size == 0:
+            continue
+        ref = host(eng.forward(cuda(x[rows]), TIER_ENTROPY[t])).view(np.uint16)
+        assert np.array_equal(out[rows], ref), f"tier {t} rows differ"
+
+
+def test_mlp_reference_shape(ee, orc):
+    """EE/test_engine.py:10-26's shape, B, S, H, Inter = 1, 1024, 2048, 5632.
+    Weights are scaled by 1/sqrt(fan_in): the reference's unit-variance weights
+    overflow fp16 in the down projection.  Checks: shape, the chain identity,
+    sampled rows against the oracle, the per-token routed invariant, and the
+    quantisation error against an unquantised float32 MLP."""
+    B, S, H, F = 1, 1024, 2048, 5632
+    torch.manual_seed(0)
+    dev = torch.device("cuda")
+    hidden = torch.randn(B, S, H, device=dev, dtype=torch.float16)
+    gate_w = (torch.randn(F, H, device=dev) / math.sqrt(H)).half()
+    up_w = (torch.randn(F, H, device=dev) / math.sqrt(H)).half()
+    down_w = (torch.randn(H, F, device=dev) / math.sqrt(F)).half()
+    eng = ee.EntropyMLPEngine(gate_w, up_w, down_w, *TAUS)
+    x32 = hidden.float().reshape(S, H)
+    ref = torch.nn.functional.linear(
+        torch.nn.functional.silu(x32 @ gate_w.float().T) * (x32 @ up_w.float().T), down_w.float())
+    rows = np.array([0, 1, 511, 1023])
+    g, u, d = (host(w) for w in (gate_w, up_w, down_w))
+    outs = {}
+    for tier, bound in ((0, 0.1), (1, 0.1), (2, 0.03)):
+        out = eng.forward(hidden, TIER_ENTROPY[tier])
+        assert out.shape == (B, S, H) and out.dtype == torch.float16
+        _, act_d, out_c = chain(ee, eng, hidden.reshape(S, H), tier)
+        assert torch.equal(out.reshape(S, H), out_c)
+        rel = (torch.linalg.norm(out.reshape(S, H).float() - ref) / torch.linalg.norm(ref)).item()
+        assert rel < bound, f"tier {tier}: relative error {rel:.4f}"
+        xs, acts = host(hidden.reshape(S, H)[rows]), host(act_d[rows])
+        _, _, out_ref = orc.mlp_forward(xs, g, u, d, tier, act=acts)
+        got = host(out.reshape(S, H)[rows])
+        if tier == 0:
+            assert np.array_equal(got.view(np.uint16), out_ref.view(np.uint16))
+        else:
+            check_close_f64(got, out_ref)
+        outs[tier] = out.reshape(S, H)
+    h = torch.tensor(np.random.default_rng(5).choice(np.array([1.0, 2.0, 3.0], np.float32), S), device=dev)
+    routed = eng.forward(hidden, h).reshape(S, H)
+    for tier in range(3):
+        sel = h == TIER_ENTROPY[tier]
+        assert torch.equal(routed[sel], outs[tier][sel])

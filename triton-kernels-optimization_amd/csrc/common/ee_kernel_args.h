@@ -126,3 +126,14 @@ struct EeRowCopyArgs {
     int32_t tier;
     int32_t scatter;        // 0: dst[r] = src[idx[r]]; 1: dst[idx[r]] = src[r]
 };
+
+// MLP activation (eek_silu_mul): act[m, j] = silu(gu[m, j]) * gu[m, F + j], fp16.
+struct EeSiluMulArgs {
+    const uint16_t* gu;     // fp16 [M, 2F] (gate | up), row stride ld_gu
+    uint16_t* act;          // fp16 [M, F], row stride ld_act
+    int64_t M;
+    int64_t F;
+    int64_t ld_gu;
+    int64_t ld_act;
+    int32_t vec;            // 1: F, strides and pointers allow 16-byte accesses
+};

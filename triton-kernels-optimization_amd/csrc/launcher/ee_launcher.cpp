@@ -658,6 +658,128 @@ EE_EXPORT int ee_routed_linear(ee_engine* eng, const void* x, int64_t ld_x, int3
 
 // ------------------------------------------------------------ CubinEngine counterpart
 
+// ============================================================================ fused MLP
+
+EE_EXPORT int ee_silu_mul(ee_engine* eng, const void* gu, int64_t ld_gu, void* act, int64_t ld_act, int64_t M,
+                          int64_t F, ee_stream_t stream) {
+    if (eng == nullptr || gu == nullptr || act == nullptr) return fail(EE_ERR_INVALID_ARG, "NULL argument");
+    if (M < 0 || F <= 0 || ld_gu < 2 * F || ld_act < F) return fail(EE_ERR_INVALID_ARG, "bad shape or stride");
+    if (!aligned(gu, 2) || !aligned(act, 2)) return fail(EE_ERR_INVALID_ARG, "misaligned pointer");
+    if (M == 0) return EE_OK;
+    const int32_t vec = F % 8 == 0 && ld_gu % 8 == 0 && ld_act % 8 == 0 && aligned(gu, 16) && aligned(act, 16);
+    EeSiluMulArgs a{(const uint16_t*)gu, (uint16_t*)act, M, F, ld_gu, ld_act, vec};
+    const int64_t work = vec ? M * (F / 8) : M * F;
+    const int64_t g = std::min<int64_t>(cdiv(work, EE_BLOCK), 16384);
+    return launch(eng, "eek_silu_mul", g, 1, EE_BLOCK, a, stream);
+}
+
+EE_EXPORT int ee_mlp_prepare(ee_engine* eng, const void* gate_w, const void* up_w, const void* down_w, int64_t H,
+                             int64_t F, int64_t ld_gate, int64_t ld_up, int64_t ld_down, int8_t* gu_i8,
+                             uint8_t* gu_f8, void* gu_f16, float* gu_scale, int8_t* dn_i8, uint8_t* dn_f8,
+                             void* dn_f16, float* dn_scale, ee_stream_t stream) {
+    if (eng == nullptr || gate_w == nullptr || up_w == nullptr || down_w == nullptr || gu_i8 == nullptr ||
+        gu_f8 == nullptr || gu_f16 == nullptr || gu_scale == nullptr || dn_i8 == nullptr || dn_f8 == nullptr ||
+        dn_f16 == nullptr || dn_scale == nullptr)
+        return fail(EE_ERR_INVALID_ARG, "NULL argument");
+    if (H <= 0 || F <= 0 || ld_gate < H || ld_up < H || ld_down < F)
+        return fail(EE_ERR_INVALID_ARG, "bad shape or stride");
+    int rc;
+    // gate|up: one [2F, H] operand (gate rows, then up rows); per-row scales are per output channel,
+    // so quantising the halves separately equals quantising the concatenation.
+    if ((rc = ee_quant_weight_i8(eng, gate_w, F, H, ld_gate, gu_i8, H, gu_scale, stream))) return rc;
+    if ((rc = ee_quant_weight_i8(eng, up_w, F, H, ld_up, gu_i8 + F * H, H, gu_scale + F, stream))) return rc;
+    if ((rc = ee_pack_b_f8(eng, gu_i8, 2 * F, H, H, gu_f8, H, stream))) return rc;
+    if ((rc = ee_pack_b_f16(eng, gu_i8, gu_scale, 2 * F, H, H, gu_f16, H, stream))) return rc;
+    if ((rc = ee_quant_weight_i8(eng, down_w, H, F, ld_down, dn_i8, F, dn_scale, stream))) return rc;
+    if ((rc = ee_pack_b_f8(eng, dn_i8, H, F, F, dn_f8, F, stream))) return rc;
+    return ee_pack_b_f16(eng, dn_i8, dn_scale, H, F, F, dn_f16, F, stream);
+}
+
+namespace {
+// Workspace carve-up of ee_mlp_forward: each region 256-byte aligned.
+struct MlpWs {
+    uint8_t* codes; float* scale; uint16_t* gu; uint16_t* act; int32_t* tier; int32_t* idx; int32_t* counts;
+    int64_t bytes;
+};
+MlpWs mlp_ws(void* base, int64_t M, int64_t H, int64_t F, bool routed) {
+    auto up = [](int64_t v) { return (v + 255) & ~int64_t(255); };
+    MlpWs w{};
+    int64_t o = 0;
+    uint8_t* b = (uint8_t*)base;
+    w.codes = b + o; o = up(o + M * std::max(H, F));
+    w.scale = (float*)(b + o); o = up(o + M * 4);
+    w.gu = (uint16_t*)(b + o); o = up(o + M * 2 * F * 2);
+    w.act = (uint16_t*)(b + o); o = up(o + M * F * 2);
+    if (routed) {
+        w.tier = (int32_t*)(b + o); o = up(o + M * 4);
+        w.idx = (int32_t*)(b + o); o = up(o + M * 4);
+        w.counts = (int32_t*)(b + o); o = up(o + 16);
+    }
+    w.bytes = o;
+    return w;
+}
+}  // namespace
+
+EE_EXPORT int64_t ee_mlp_workspace_bytes(int64_t M, int64_t H, int64_t F, int32_t routed) {
+    if (M < 0 || H <= 0 || F <= 0) return -1;
+    return mlp_ws(nullptr, M, H, F, routed != 0).bytes;
+}
+
+EE_EXPORT int ee_mlp_forward(ee_engine* eng, const void* x, int64_t ld_x, int64_t M, int64_t H, int64_t F,
+                             const int8_t* gu_i8, const uint8_t* gu_f8, const void* gu_f16, const float* gu_scale,
+                             const int8_t* dn_i8, const uint8_t* dn_f8, const void* dn_f16, const float* dn_scale,
+                             double entropy, const float* h_rows, double tau_low, double tau_high, void* out,
+                             int64_t ldo, void* workspace, int64_t ws_bytes, ee_stream_t stream) {
+    if (eng == nullptr || x == nullptr || out == nullptr || workspace == nullptr || gu_i8 == nullptr ||
+        gu_f8 == nullptr || gu_f16 == nullptr || gu_scale == nullptr || dn_i8 == nullptr || dn_f8 == nullptr ||
+        dn_f16 == nullptr || dn_scale == nullptr)
+        return fail(EE_ERR_INVALID_ARG, "NULL argument");
+    if (M < 0 || M > 0x7fffffff || H <= 0 || F <= 0 || ld_x < H || ldo < H)
+        return fail(EE_ERR_INVALID_ARG, "bad shape or stride");
+    if (H % 16 != 0 || F % 16 != 0 || ld_x % 8 != 0 || ldo % 4 != 0)
+        return fail(EE_ERR_UNSUPPORTED, "fused MLP needs H % 16 == 0, F % 16 == 0, ld_x % 8 == 0, ldo % 4 == 0");
+    if (!aligned(x, 16) || !aligned(out, 8) || !aligned(workspace, 256))
+        return fail(EE_ERR_INVALID_ARG, "misaligned pointer (x 16 B, out 8 B, workspace 256 B)");
+    const MlpWs w = mlp_ws(workspace, M, H, F, h_rows != nullptr);
+    if (ws_bytes < w.bytes)
+        return fail(EE_ERR_INVALID_ARG, "workspace too small: need " + std::to_string(w.bytes) + " bytes");
+    if (M == 0) return EE_OK;
+    const int32_t m = (int32_t)M, h = (int32_t)H, f = (int32_t)F;
+    int rc;
+    if (h_rows != nullptr) {
+        // one tier per row: route, gate|up routed linear, activation, down routed linear
+        if ((rc = ee_route(eng, h_rows, M, tau_low, tau_high, w.tier, w.idx, w.counts, stream))) return rc;
+        if ((rc = ee_routed_linear(eng, x, ld_x, m, h, 2 * f, w.idx, w.counts, gu_i8, gu_f8, gu_f16, gu_scale, w.gu,
+                                   2 * F, w.codes, w.scale, stream)))
+            return rc;
+        if ((rc = ee_silu_mul(eng, w.gu, 2 * F, w.act, F, M, F, stream))) return rc;
+        return ee_routed_linear(eng, w.act, F, m, f, h, w.idx, w.counts, dn_i8, dn_f8, dn_f16, dn_scale, out, ldo,
+                                w.codes, w.scale, stream);
+    }
+    // one tier for the call, by the dispatcher's strict comparisons (EE/python/dispatch.py:74-79)
+    const int tier = entropy < tau_low ? EE_TIER_INT8 : (entropy < tau_high ? EE_TIER_FP8 : EE_TIER_FP16);
+    if (tier == EE_TIER_FP16) {
+        if ((rc = ee_gemm(eng, EE_GEMM_F16, x, ld_x, gu_f16, H, w.gu, 2 * F, nullptr, nullptr, m, 2 * f, h, nullptr,
+                          nullptr, nullptr, 0, nullptr, stream)))
+            return rc;
+        if ((rc = ee_silu_mul(eng, w.gu, 2 * F, w.act, F, M, F, stream))) return rc;
+        return ee_gemm(eng, EE_GEMM_F16, w.act, F, dn_f16, F, out, ldo, nullptr, nullptr, m, h, f, nullptr, nullptr,
+                       nullptr, 0, nullptr, stream);
+    }
+    const int32_t qmode = tier == EE_TIER_INT8 ? EE_QUANT_I8_DISPATCH : EE_QUANT_F8_ROW;
+    const int32_t kind = tier == EE_TIER_INT8 ? EE_GEMM_I8 : EE_GEMM_F8;
+    const void* bgu = tier == EE_TIER_INT8 ? (const void*)gu_i8 : (const void*)gu_f8;
+    const void* bdn = tier == EE_TIER_INT8 ? (const void*)dn_i8 : (const void*)dn_f8;
+    if ((rc = ee_quant_act(eng, x, M, H, ld_x, qmode, w.codes, H, w.scale, nullptr, nullptr, 0, stream))) return rc;
+    if ((rc = ee_gemm(eng, kind, w.codes, H, bgu, H, w.gu, 2 * F, w.scale, gu_scale, m, 2 * f, h, nullptr, nullptr,
+                      nullptr, 0, nullptr, stream)))
+        return rc;
+    if ((rc = ee_silu_mul(eng, w.gu, 2 * F, w.act, F, M, F, stream))) return rc;
+    if ((rc = ee_quant_act(eng, w.act, M, F, F, qmode, w.codes, F, w.scale, nullptr, nullptr, 0, stream))) return rc;
+    return ee_gemm(eng, kind, w.codes, F, bdn, F, out, ldo, w.scale, dn_scale, m, h, f, nullptr, nullptr, nullptr, 0,
+                   nullptr, stream);
+}
+
 EE_EXPORT int ee_module_engine_create(const char* code_object_path, const char* func_name, int32_t shared_mem,
                                       int32_t num_warps, int32_t block_m, int32_t block_n, ee_module_engine** out) {
     if (out == nullptr) return fail(EE_ERR_INVALID_ARG, "out must not be NULL");

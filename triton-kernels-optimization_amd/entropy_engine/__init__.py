@@ -9,17 +9,17 @@ dispatch.py (IqtedarU/triton-kernels-optimization, entropy-engine/python).
 from .dispatch import (TINYLLAMA_1B, EntropyDispatchedLinear, EntropyDispatchedLlamaBlock, EntropyGatedLlama,
                        PipelinedEntropyDispatcher, PrecisionTier, RowEntropyRouter, build_dispatched_llama,
                        quantize_weights_int8, tier_of)
-from .engine import CubinEngine, HsacoEngine
+from .engine import CubinEngine, EntropyMLPEngine, HsacoEngine
 from .kernels import (PackedWeight, fp8_tensor_gemm, fused_softmax_entropy, gemm, prepare_weight,
                       quantize_activations, quantize_tensor_fp8, quantize_weight_codes, route, routed_linear, row_copy,
-                      softmax_entropy, transpose_i8, triton_fp8_gemm, triton_fp16_gemm, triton_int8_gemm)
+                      silu_mul, softmax_entropy, transpose_i8, triton_fp8_gemm, triton_fp16_gemm, triton_int8_gemm)
 
 __all__ = [
     "EntropyDispatchedLinear", "PipelinedEntropyDispatcher", "PrecisionTier", "RowEntropyRouter",
     "EntropyDispatchedLlamaBlock", "EntropyGatedLlama", "TINYLLAMA_1B", "build_dispatched_llama",
-    "quantize_weights_int8", "tier_of", "CubinEngine", "HsacoEngine", "PackedWeight", "fused_softmax_entropy",
+    "quantize_weights_int8", "tier_of", "CubinEngine", "EntropyMLPEngine", "HsacoEngine", "PackedWeight", "fused_softmax_entropy",
     "gemm", "prepare_weight", "quantize_activations", "quantize_weight_codes", "route", "routed_linear", "row_copy",
     "fp8_tensor_gemm", "quantize_tensor_fp8",
-    "softmax_entropy", "transpose_i8",
+    "silu_mul", "softmax_entropy", "transpose_i8",
     "triton_fp8_gemm", "triton_fp16_gemm", "triton_int8_gemm",
 ]

@@ -59,6 +59,12 @@ SIGNATURES = {
     "ee_row_copy": ([_p, _p, _i64, _p, _i64, _i64, _i64, _p, _p, _i32, _i32, _p], ctypes.c_int),
     "ee_routed_linear": ([_p, _p, _i64, _i32, _i32, _i32, _p, _p, _p, _p, _p, _p, _p, _i64, _p, _p, _p],
                          ctypes.c_int),
+    "ee_silu_mul": ([_p, _p, _i64, _p, _i64, _i64, _i64, _p], ctypes.c_int),
+    "ee_mlp_prepare": ([_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _p],
+                       ctypes.c_int),
+    "ee_mlp_workspace_bytes": ([_i64, _i64, _i64, _i32], _i64),
+    "ee_mlp_forward": ([_p, _p, _i64, _i64, _i64, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _f64, _p, _f64, _f64, _p,
+                        _i64, _p, _i64, _p], ctypes.c_int),
     "ee_module_engine_create": ([ctypes.c_char_p, ctypes.c_char_p, _i32, _i32, _i32, _i32, ctypes.POINTER(_p)],
                                 ctypes.c_int),
     "ee_module_engine_from_metadata": ([ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, ctypes.POINTER(_p)],

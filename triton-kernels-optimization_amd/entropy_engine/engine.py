@@ -108,3 +108,94 @@ class CubinEngine:
 
 
 HsacoEngine = CubinEngine
+
+
+class EntropyMLPEngine:
+    """The fused MLP engine EE/test_engine.py:17-26 constructs and calls:
+
+        eng = EntropyMLPEngine(gate_w, up_w, down_w, tau_low, tau_high)
+        out = eng.forward(hidden, entropy)
+
+    gate_w, up_w fp16 [Inter, H] and down_w fp16 [H, Inter] (nn.Linear
+    layout).  The reference's extension never defines the class
+    (EE/csrc/engine.cpp:202-216); its test times it against
+    F.linear(F.silu(F.linear(x, gate_w)) * F.linear(x, up_w), down_w) under
+    the dispatcher's tier choice (EE/test_engine.py:33-39).  Here the weights
+    are quantised per output channel once (EE/python/dispatch.py:43-48) and
+    each forward runs the tier's GEMMs, SiLU*up and the tier's re-quantisation
+    of the intermediate in one C call (ee_mlp_forward), with gate and up as one
+    [2*Inter, H] operand.
+
+    entropy: a float picks one tier for the call by the dispatcher's strict
+    compares (EE/python/dispatch.py:74-79; no host sync); a float32 tensor with
+    one value per token routes each token to its own tier (no host sync).
+    """
+
+    def __init__(self, gate_w: torch.Tensor, up_w: torch.Tensor, down_w: torch.Tensor, tau_low: float = 2.0,
+                 tau_high: float = 3.5):
+        for name, w in (("gate_w", gate_w), ("up_w", up_w), ("down_w", down_w)):
+            if not w.is_cuda:
+                raise RuntimeError(f"{name} must be a GPU tensor")
+            if w.dtype != torch.float16 or w.dim() != 2:
+                raise RuntimeError(f"{name} must be a 2-D float16 tensor")
+        F, H = gate_w.shape
+        if tuple(up_w.shape) != (F, H) or tuple(down_w.shape) != (H, F):
+            raise RuntimeError(f"shape mismatch: gate {tuple(gate_w.shape)}, up {tuple(up_w.shape)}, "
+                               f"down {tuple(down_w.shape)}; expected [I, H], [I, H], [H, I]")
+        if H % 16 or F % 16:
+            raise RuntimeError("hidden and intermediate sizes must be multiples of 16")
+        self.device = gate_w.device
+        self.H, self.F = H, F
+        self.tau_low, self.tau_high = float(tau_low), float(tau_high)
+        dev = self.device
+        g, u, d = (w.contiguous() for w in (gate_w, up_w, down_w))
+        e = lambda shape, dt: torch.empty(shape, dtype=dt, device=dev)
+        self.gu_i8, self.gu_f8, self.gu_f16, self.gu_scale = (e((2 * F, H), torch.int8), e((2 * F, H), torch.uint8),
+                                                              e((2 * F, H), torch.float16), e(2 * F, torch.float32))
+        self.dn_i8, self.dn_f8, self.dn_f16, self.dn_scale = (e((H, F), torch.int8), e((H, F), torch.uint8),
+                                                              e((H, F), torch.float16), e(H, torch.float32))
+        with torch.cuda.device(dev):
+            _lib.check(_lib.lib().ee_mlp_prepare(
+                _lib.engine(), g.data_ptr(), u.data_ptr(), d.data_ptr(), H, F, H, H, F,
+                self.gu_i8.data_ptr(), self.gu_f8.data_ptr(), self.gu_f16.data_ptr(), self.gu_scale.data_ptr(),
+                self.dn_i8.data_ptr(), self.dn_f8.data_ptr(), self.dn_f16.data_ptr(), self.dn_scale.data_ptr(),
+                _lib.stream_handle()))
+
+    def tier(self, entropy: float):
+        """The tier a scalar entropy selects (EE/python/dispatch.py:74-79)."""
+        from .dispatch import tier_of
+        return tier_of(float(entropy), self.tau_low, self.tau_high)
+
+    def forward(self, hidden: torch.Tensor, entropy) -> torch.Tensor:
+        if not hidden.is_cuda or hidden.device != self.device:
+            raise RuntimeError(f"hidden must be on {self.device}")
+        if hidden.dtype != torch.float16:
+            raise RuntimeError("hidden must be float16")
+        if hidden.shape[-1] != self.H:
+            raise RuntimeError(f"hidden size mismatch: got {hidden.shape[-1]}, engine has {self.H}")
+        x = hidden.reshape(-1, self.H)
+        if x.stride(-1) != 1 or (x.shape[0] > 1 and x.stride(0) != self.H) or x.data_ptr() % 16:
+            x = x.contiguous()
+        M = x.shape[0]
+        h_rows = None
+        if isinstance(entropy, torch.Tensor) and entropy.numel() > 1:
+            if entropy.numel() != M:
+                raise RuntimeError(f"per-token entropy needs {M} values, got {entropy.numel()}")
+            h_rows = entropy.reshape(M).to(device=self.device, dtype=torch.float32).contiguous()
+            e = 0.0
+        else:
+            e = float(entropy)
+        out = torch.empty((M, self.H), dtype=torch.float16, device=self.device)
+        L = _lib.lib()
+        nbytes = L.ee_mlp_workspace_bytes(M, self.H, self.F, int(h_rows is not None))
+        ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=self.device)
+        with torch.cuda.device(self.device):
+            _lib.check(L.ee_mlp_forward(
+                _lib.engine(), x.data_ptr(), self.H, M, self.H, self.F,
+                self.gu_i8.data_ptr(), self.gu_f8.data_ptr(), self.gu_f16.data_ptr(), self.gu_scale.data_ptr(),
+                self.dn_i8.data_ptr(), self.dn_f8.data_ptr(), self.dn_f16.data_ptr(), self.dn_scale.data_ptr(),
+                e, h_rows.data_ptr() if h_rows is not None else None, self.tau_low, self.tau_high,
+                out.data_ptr(), self.H, ws.data_ptr(), nbytes, _lib.stream_handle()))
+        return out.reshape(*hidden.shape[:-1], self.H)
+
+    __call__ = forward

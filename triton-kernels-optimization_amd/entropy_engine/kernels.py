@@ -29,7 +29,7 @@ from ._lib import check, engine, ptr, stream_handle
 __all__ = [
     "triton_int8_gemm", "triton_fp8_gemm", "triton_fp16_gemm", "fused_softmax_entropy",
     "softmax_entropy", "quantize_activations", "gemm", "route", "row_copy", "routed_linear",
-    "prepare_weight", "PackedWeight", "quantize_weight_codes",
+    "prepare_weight", "PackedWeight", "quantize_weight_codes", "silu_mul",
 ]
 
 
@@ -370,3 +370,23 @@ def routed_linear(x: torch.Tensor, pw: PackedWeight, idx: torch.Tensor, counts: 
                                           ptr(pw.i8), ptr(pw.f8), ptr(pw.f16), ptr(pw.scale), ptr(c),
                                           _rowmajor(c, "out"), ptr(ws_codes), ptr(ws_scale), stream_handle()))
     return c
+
+
+# ---------------------------------------------------------------- MLP activation
+
+def silu_mul(gu: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """act [M, F] = fp16(fp16(silu(gate)) * up) for gu fp16 [M, 2F] = [gate | up]:
+    torch's fp16 F.silu(gate) * up, the activation of the Llama MLP the reference
+    gates (EE/python/dispatch.py:199-203, EE/test_engine.py:35)."""
+    dev = _require_cuda(gu, out)
+    if gu.dtype != torch.float16:
+        raise TypeError("gu must be float16")
+    M, F2 = gu.shape
+    if F2 % 2:
+        raise ValueError("gu must hold [gate | up]: an even number of columns")
+    F = F2 // 2
+    act = out if out is not None else torch.empty((M, F), dtype=torch.float16, device=dev)
+    with torch.cuda.device(dev):
+        check(_lib.lib().ee_silu_mul(engine(), ptr(gu), _rowmajor(gu, "gu"), ptr(act), _rowmajor(act, "out"), M, F,
+                                     stream_handle()))
+    return act
