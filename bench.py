@@ -301,6 +301,31 @@ def main():
             run("c3_end_to_end", c3_all)
             c3 = {"routing_fractions": fr, "thresholds_timed": [0.41, 1.68],
                   "ops": 2.0 * M3 * N3 * K3}
+        # ---- the fused MLP engine at EE/test_engine.py:10's shape (B, S, H, Inter = 1, 1024, 2048, 5632)
+        mlp = None
+        mlp_names = ("mlp_int8", "mlp_fp8", "mlp_fp16", "mlp_routed", "mlp_torch_fp16")
+        if not only or any(n in only for n in mlp_names):
+            Sm, Hm, Fm = 1024, 2048, 5632
+            gm = torch.Generator().manual_seed(3)
+            hid = torch.randn(1, Sm, Hm, generator=gm).half().to(dev)
+            # 1/sqrt(fan_in) weights: EE/test_engine.py:12-14's unit-variance ones overflow fp16 in down_proj
+            wg, wu = ((torch.randn(Fm, Hm, generator=gm) / Hm ** 0.5).half().to(dev) for _ in range(2))
+            wd = (torch.randn(Hm, Fm, generator=gm) / Fm ** 0.5).half().to(dev)
+            eng_m = ee.EntropyMLPEngine(wg, wu, wd, 1.5, 2.5)
+            h_tok = torch.from_numpy(rng.choice(np.float32([1.0, 2.0, 3.0]), Sm, p=[0.2, 0.4, 0.4])).to(dev)
+            torch.cuda.synchronize()
+            run("mlp_int8", lambda: eng_m.forward(hid, 1.0), primary="eager")
+            run("mlp_fp8", lambda: eng_m.forward(hid, 2.0), primary="eager")
+            run("mlp_fp16", lambda: eng_m.forward(hid, 3.0), primary="eager")
+            run("mlp_routed", lambda: eng_m.forward(hid, h_tok), primary="eager")
+
+            def mlp_torch():                                           # EE/test_engine.py:33-39, one tier
+                F_ = torch.nn.functional
+                return F_.linear(F_.silu(F_.linear(hid, wg)) * F_.linear(hid, wu), wd)
+
+            run("mlp_torch_fp16", mlp_torch, primary="eager")
+            mlp = {"ops": 2.0 * Sm * Hm * Fm * 3}
+            del eng_m
         # ---- config 4: TinyLlama-1.1B architecture, every linear entropy-gated at (2.34, 6.03)
         c4 = None
         if not only or any(n in only for n in ("c4_forward", "c4_forward_fp16")):
@@ -370,6 +395,15 @@ def main():
             "routing_fractions_int8_fp8_fp16": c3["routing_fractions"],
             "shape": "M=K=N=4096; entropy over fp16 [4096,4096] mixture logits",
         }
+    if mlp is not None:
+        kernels["mlp_engine"] = {
+            f"us_{k}": results[f"mlp_{k}"]["ms"] * 1e3 for k in ("int8", "fp8", "fp16", "routed", "torch_fp16")}
+        kernels["mlp_engine"].update({
+            f"TOPS_{k}": mlp["ops"] / (results[f"mlp_{k}"]["ms"] * 1e-3) / 1e12
+            for k in ("int8", "fp8", "fp16", "routed", "torch_fp16")})
+        kernels["mlp_engine"]["shape"] = ("EntropyMLPEngine.forward, B, S, H, Inter = 1, 1024, 2048, 5632 "
+                                          "(EE/test_engine.py:10); routed = per-token tiers 20/40/40 %; "
+                                          "torch_fp16 = the test's F.linear chain on the fp16 weights (hipBLASLt)")
     if c4 is not None:
         tot = sum(c4["rows"])
         kernels["llama_c4"] = {
