@@ -142,7 +142,8 @@ def test_built_meta_lists_every_kernel_the_launcher_selects():
     assert ks["eek_gemm_i8"]["lds"] == 5 * 256 * 128 and ks["eek_gemm_i8_generic"]["lds"] == 2 * 256 * 128
     assert ks["eek_route"]["block"] == 1024
     # pipelined GEMMs: 4 compute + 4 loader wave64s; the Triton-style meta says 8 "warps"
-    for k in ("eek_gemm_i8", "eek_gemm_f8", "eek_gemm_f16", "eek_gemm_routed", "eek_gemm_i8_w8", "eek_gemm_f16_w8"):
+    for k in ("eek_gemm_i8", "eek_gemm_f8", "eek_gemm_f16", "eek_gemm_routed", "eek_gemm_i8_w8", "eek_gemm_f16_w8",
+              "eek_gemm_i8_persist", "eek_gemm_f8_persist", "eek_gemm_routed_persist"):
         assert ks[k]["block"] == 512 and ks[k]["lds"] == 5 * 256 * 128
     for f in ("gemm_int8_meta.json", "gemm_fp8_meta.json", "gemm_fp16_meta.json"):
         gm = json.load(open(os.path.join(PKG, "lib", f)))

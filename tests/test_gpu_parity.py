@@ -310,6 +310,53 @@ def gemm_variant(request):
     _lib.check(_lib.lib().ee_engine_set_option(_lib.engine(), b"gemm_variant", 0))
 
 
+@pytest.fixture(params=[0, 1, 8, 13], ids=["persist-auto", "persist-off", "persist-grid8", "persist-grid13"])
+def gemm_persist(request):
+    """Runs a test with the persistent GEMM grids off, automatic, or forced to a
+    few workgroups (8: XCD-contiguous tile ranges; 13: round robin) so that
+    small shapes put many tiles on each workgroup."""
+    from entropy_engine import _lib
+    _lib.check(_lib.lib().ee_engine_set_option(_lib.engine(), b"gemm_persist", request.param))
+    yield request.param
+    _lib.check(_lib.lib().ee_engine_set_option(_lib.engine(), b"gemm_persist", 0))
+
+
+@pytest.mark.parametrize("M,K,N", [(300, 512, 520), (1024, 2048, 1536), (129, 128, 4), (4096, 2048, 11264)])
+def test_persistent_gemm(ee, orc, M, K, N, gemm_persist):
+    """The persistent INT8 / FP8 kernels (one workgroup walking many tiles, the
+    stage ring running across tile boundaries) against the oracle and, bit for
+    bit, against the one-tile-per-workgroup kernels."""
+    from entropy_engine import _lib
+    rng = np.random.default_rng(M * 3 + K + N)
+    A = rng.standard_normal((M, K)).astype(np.float16)
+    B, bs = weights(orc, rng, N, K)
+    pw = ee.prepare_weight(cuda(B), cuda(bs)).materialize()
+    codes, a_s = orc.quant_act_i8(A, "dispatcher")
+    c8, s8 = orc.quant_act_f8(A)
+    big = M * N > 4096 * 4096 // 2
+    acc = torch.empty((M, N), dtype=torch.int32, device="cuda")
+    out_i8 = host(ee.gemm("int8", cuda(codes), pw.i8, cuda(a_s), cuda(bs), acc_out=None if big else acc))
+    out_f8 = host(ee.gemm("fp8", cuda(c8), pw.f8, cuda(s8), cuda(bs)))
+    if not big:
+        acc_ref = orc.gemm_i8_acc(codes, B)
+        assert np.array_equal(host(acc), acc_ref)
+        assert np.array_equal(out_i8.view(np.uint16), orc.epilogue_i8(acc_ref, a_s, bs).view(np.uint16))
+        check_close_f64(out_f8, orc.gemm_f8_f64(c8, B, s8, bs))
+    else:                                              # sampled rows against the oracle
+        rows = np.array([0, 1, 127, 128, M // 2, M - 1])
+        ref = orc.epilogue_i8(orc.gemm_i8_acc(codes[rows], B), a_s[rows], bs)
+        assert np.array_equal(out_i8[rows].view(np.uint16), ref.view(np.uint16))
+        check_close_f64(out_f8[rows], orc.gemm_f8_f64(c8[rows], B, s8[rows], bs))
+    _lib.check(_lib.lib().ee_engine_set_option(_lib.engine(), b"gemm_persist", 1))
+    try:
+        one_i8 = host(ee.gemm("int8", cuda(codes), pw.i8, cuda(a_s), cuda(bs)))
+        one_f8 = host(ee.gemm("fp8", cuda(c8), pw.f8, cuda(s8), cuda(bs)))
+    finally:
+        _lib.check(_lib.lib().ee_engine_set_option(_lib.engine(), b"gemm_persist", gemm_persist))
+    assert np.array_equal(out_i8.view(np.uint16), one_i8.view(np.uint16))
+    assert np.array_equal(out_f8.view(np.uint16), one_f8.view(np.uint16))
+
+
 @pytest.mark.parametrize("M,K,N", [(256, 1024, 512), (200, 512, 260), (1, 4096, 128), (130, 4112, 4), (1024, 4096, 4096),
                                    (128, 640, 128), (256, 768, 384)])
 def test_int8_gemm_bit_exact(ee, orc, M, K, N, gemm_variant):
@@ -415,7 +462,7 @@ def test_row_copy_gather_scatter(ee):
 
 
 @pytest.mark.parametrize("M,K,N", [(300, 1024, 256), (4096, 4096, 4096)])
-def test_routed_linear_equals_per_tier(ee, orc, M, K, N, gemm_variant):
+def test_routed_linear_equals_per_tier(ee, orc, M, K, N, gemm_variant, gemm_persist):
     """scatter(gemm_t(gather(X)))[r] == gemm_t(X)[r] bit for bit, every tier."""
     rng = np.random.default_rng(M + 1)
     X = rng.standard_normal((M, K)).astype(np.float16)
@@ -437,7 +484,7 @@ def test_routed_linear_equals_per_tier(ee, orc, M, K, N, gemm_variant):
 
 @pytest.mark.parametrize("M,K,N,H_hi", [(700, 1024, 384, 3.0), (300, 1008, 136, 3.0), (257, 512, 256, 0.3),
                                          (129, 256, 128, 10.0)])
-def test_routed_linear_fused_equals_unfused(ee, orc, M, K, N, H_hi, gemm_variant):
+def test_routed_linear_fused_equals_unfused(ee, orc, M, K, N, H_hi, gemm_variant, gemm_persist):
     """The two-launch routed linear (K % 128 == 0: one quantiser, one grid for
     the three tier GEMMs) and the five-launch sequence give the same bits; K =
     1008 takes the five-launch path.  Entropy ranges make some tiers empty."""

@@ -969,6 +969,224 @@ EE_DEV void gemm_generic(const EeGemmArgs& g) {
     epilogue<KIND>(g, acc, m0, n0, M, off, wm, wn, lane);
 }
 
+// ---------------------------------------------------------------- persistent loader-wave GEMM
+// One workgroup per CU walks a list of tiles.  The stage ring runs on across
+// tile boundaries: the loader waves keep streaming the next tile's first
+// stages while the compute waves finish the current tile's MFMAs and
+// epilogue, so the pipeline fills once per workgroup instead of once per
+// tile.  Four DMA stages (128 KB) plus a 32 KB epilogue buffer the DMA never
+// touches.  Global stage s lives in buffer s % NSTAGE_P; barrier s means
+// "stage s has landed" for the compute waves and "stage s-1 has been read"
+// for the loaders, exactly as in gemm_tile.  The compute code and the K order
+// are gemm_tile's, so outputs are bit-identical to it.  1-byte operands only
+// (INT8 and FP8): every tile of one launch then has the same stage count.
+#define NSTAGE_P 4
+#define EPI_BUF (NSTAGE_P * LDS_STAGE)
+
+// The work of one tile: its GEMM, tile coordinates, row count and slot offset.
+struct PTile {
+    const EeGemmArgs* g;
+    int tier, tm, tn, M;
+    int64_t off;
+};
+
+// Tile order and the deal of tiles to workgroups (shared by the plain and the
+// routed persistent kernels).  Logical tiles a = 0 .. nA-1 (the 1-byte-operand
+// tiles) are ordered in bands of 8 M-tiles walked along N, so 32 consecutive
+// tiles form an 8 x 4 block.  They are dealt in rounds: in a round every
+// taking workgroup gets one tile, and with G a multiple of 8 workgroup
+// b = 8j + x (on XCD x) takes position x * G/8 + j, so each XCD gets 32
+// consecutive tiles -- one 8 x 4 block, whose A and B panels its CUs share in
+// that XCD's L2.  W8A16 tiles of a routed launch (nF of them, twice the work
+// of a 1-byte tile at the same K) are dealt first, round robin: workgroups
+// b < rF get qF + 1, the others qF.  The first two rounds of 1-byte tiles then
+// go only to workgroups b >= rF, which levels the load (a static version of
+// what the hardware dispatcher does for one-tile grids).
+struct TileDeal {
+    int tiles_m, tiles_n, nA, b, G, per, rF, P, first_round;
+    __device__ __forceinline__ TileDeal(int tm_count, int tn_count, int nF, int bb, int GG)
+        : tiles_m(tm_count), tiles_n(tn_count), nA(tm_count * tn_count), b(bb), G(GG) {
+        per = (G & 7) == 0 ? G >> 3 : 0;
+        rF = nF % G;
+        P = G - rF;                                   // workgroups in rounds 0 and 1
+        first_round = (rF != 0 && b < rF) ? 2 : 0;    // heavier workgroups skip rounds 0 and 1
+    }
+    // position of this workgroup in a round in which all G take part
+    __device__ __forceinline__ int pos_all() const { return per ? (b & 7) * per + (b >> 3) : b; }
+    __device__ __forceinline__ int tile_index(int round) const {
+        if (rF == 0) return round * G + pos_all();
+        if (round < 2) return round * P + (b - rF);
+        return 2 * P + (round - 2) * G + pos_all();
+    }
+    __device__ __forceinline__ int count() const {
+        // rounds first_round, first_round+1, ... while tile_index(round) < nA
+        if (rF == 0) {
+            const int p = pos_all();
+            return p < nA ? (nA - p + G - 1) / G : 0;
+        }
+        int n = 0;
+        if (first_round == 0) {
+            for (int r = 0; r < 2; ++r) n += tile_index(r) < nA;
+            if (n < 2) return n;
+        }
+        const int p = 2 * P + pos_all();
+        return n + (p < nA ? (nA - p + G - 1) / G : 0);
+    }
+    // logical tile a -> (tm, tn): bands of 8 M-tiles, M fastest within a band
+    __device__ __forceinline__ void coords(int a, int& tm, int& tn) const {
+        const int band = a / (8 * tiles_n);
+        const int m_first = band * 8;
+        const int gsz = min(tiles_m - m_first, 8);
+        const int r = a - band * 8 * tiles_n;
+        tm = m_first + r % gsz;
+        tn = r / gsz;
+    }
+};
+
+// Tiles of a plain GEMM for workgroup b of G.
+struct SeqPlain {
+    const EeGemmArgs* g;
+    TileDeal d;
+    __device__ __forceinline__ SeqPlain(const EeGemmArgs& ga, int b, int G)
+        : g(&ga), d((ga.M + BM - 1) / BM, (ga.N + BN - 1) / BN, 0, b, G) {}
+    __device__ __forceinline__ int count() const { return d.count(); }
+    __device__ __forceinline__ PTile tile(int i) const {
+        int tm, tn;
+        d.coords(d.tile_index(d.first_round + i), tm, tn);
+        return PTile{g, g->tier, tm, tn, g->M, 0};
+    }
+};
+
+// The INT8 and FP8 tiles of a routed launch: M-tiles 0 .. T0-1 are INT8
+// (slots 0 .. c0-1), T0 .. T0+T1-1 FP8 (slots c0 ..).
+struct SeqRouted {
+    const EeRoutedGemmArgs* r;
+    int T0, c0, c1;
+    TileDeal d;
+    __device__ __forceinline__ SeqRouted(const EeRoutedGemmArgs& ra, int t0, int t01, int k0, int k1, int nN, int nF,
+                                         int b, int G)
+        : r(&ra), T0(t0), c0(k0), c1(k1), d(t01, nN, nF, b, G) {}
+    __device__ __forceinline__ int count() const { return d.count(); }
+    __device__ __forceinline__ PTile tile(int i) const {
+        int tmg, tn;
+        d.coords(d.tile_index(d.first_round + i), tmg, tn);
+        return tmg < T0 ? PTile{&r->t[0], 0, tmg, tn, c0, 0} : PTile{&r->t[1], 1, tmg - T0, tn, c1, c0};
+    }
+};
+
+template <class Seq>
+EE_DEV void persist_loader(const Seq& seq, int ntiles, int nk, uint8_t* smem, int lw, int lane) {
+    constexpr int LOADS = 8;                          // DMA instructions per loader wave per stage
+    const int lrow = lane >> 3;
+    const uint8_t* pa[4];
+    const uint8_t* pb[4];
+    const int total = ntiles * nk;
+    int issued = 0, cur = -1;
+    auto issue = [&]() {
+        const int i = issued / nk, kt = issued - i * nk;
+        if (i != cur) {                               // the issue cursor enters tile i
+            cur = i;
+            const PTile t = seq.tile(i);
+            const int m0 = t.tm * BM, n0 = t.tn * BN;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int r = (lw * 4 + q) * 8 + lrow;
+                const int lchunk = (lane & 7) ^ swz(r);
+                const int m = min(m0 + r, t.M - 1);
+                const int64_t ar = t.g->a_idx ? (int64_t)t.g->a_idx[t.off + m] : t.off + m;
+                pa[q] = (const uint8_t*)t.g->a + ar * t.g->lda + lchunk * 16;
+                const int n = min(n0 + r, t.g->N - 1);
+                pb[q] = (const uint8_t*)t.g->b + (int64_t)n * t.g->ldb + lchunk * 16;
+            }
+        }
+        const uint32_t s = lds_addr(smem) + (uint32_t)((issued % NSTAGE_P) * LDS_STAGE);
+        const int64_t kb = (int64_t)kt * BKB;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int grp = lw * 4 + q;
+            dma16(pa[q] + kb, s + grp * 8 * BKB);
+            dma16(pb[q] + kb, s + (BM + grp * 8) * BKB);
+        }
+        ++issued;
+    };
+    while (issued < NSTAGE_P && issued < total) issue();
+    for (int s = 0; s < total; ++s) {
+        // this wave's loads of stage s are done; the (issued - 1 - s) stages issued after it may still fly
+        const int after = issued - 1 - s;
+        if (after >= 3) WAITCNT_VM(3 * LOADS);
+        else if (after == 2) WAITCNT_VM(2 * LOADS);
+        else if (after == 1) WAITCNT_VM(LOADS);
+        else WAITCNT_VM(0);
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();                 // barrier s
+        asm volatile("" ::: "memory");
+        if (s >= 1 && issued < total) issue();        // stage s-1's buffer is free: it gets stage s-1+NSTAGE_P
+    }
+}
+
+// Compute waves (0-3) on one tile whose first stage is global stage s0.
+template <int KIND>
+EE_DEV void persist_compute(const PTile& t, int nk, int s0, uint8_t* smem, int wave, int lane) {
+    typedef Pipe<KIND> P;
+    typedef typename P::acc_t acc_t;
+    constexpr int NSL = BKB / P::SB;
+    const EeGemmArgs& g = *t.g;
+    const int m0 = t.tm * BM, n0 = t.tn * BN;
+    const int wm = wave >> 1, wn = wave & 1;
+    acc_t acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = acc_t{};
+    TileScales sc;
+    if (!g.acc) load_scales<KIND>(g, m0, n0, t.M, t.off, wm, wn, lane, sc);
+    Frags<KIND> f0, f1;
+    auto stage = [&](int kt, bool more) {
+        const uint8_t* s = smem + ((s0 + kt) % NSTAGE_P) * LDS_STAGE;
+#pragma unroll
+        for (int sl = 0; sl < NSL; ++sl) {
+            Frags<KIND>& cur = (sl & 1) ? f1 : f0;
+            Frags<KIND>& nxt = (sl & 1) ? f0 : f1;
+            if (sl + 1 < NSL) {
+                read_frags<KIND>(s, sl + 1, wm, wn, lane, nxt);
+            } else if (more) {
+                __builtin_amdgcn_sched_barrier(0);
+                WAITCNT_LGKM0();
+                asm volatile("" ::: "memory");
+                __builtin_amdgcn_s_barrier();         // barrier s0+kt+1
+                asm volatile("" ::: "memory");
+                read_frags<KIND>(smem + ((s0 + kt + 1) % NSTAGE_P) * LDS_STAGE, 0, wm, wn, lane, nxt);
+            }
+            mma_all<KIND>(cur, acc);
+            interleave<KIND>();
+        }
+    };
+    WAITCNT_LGKM0();                                  // the previous tile's LDS reads are complete
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();                     // barrier s0: the tile's first stage has landed
+    asm volatile("" ::: "memory");
+    read_frags<KIND>(smem + (s0 % NSTAGE_P) * LDS_STAGE, 0, wm, wn, lane, f0);
+    for (int kt = 0; kt + 1 < nk; ++kt) stage(kt, true);
+    stage(nk - 1, false);
+    if (g.acc) epilogue32<KIND>(g, acc, m0, n0, t.M, t.off, wm, wn, lane);
+    else epilogue32_lds<KIND>(g, acc, sc, smem + EPI_BUF + wave * (64 * BKB), m0, n0, t.M, t.off, wm, wn, lane);
+}
+
+template <int KIND>
+EE_DEV void gemm_persistent(const EeGemmArgs& g) {
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[(NSTAGE_P + 1) * LDS_STAGE];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const SeqPlain seq(g, (int)blockIdx.x, (int)gridDim.x);
+    const int nt = seq.count();
+    const int nk = g.K / BKB;
+    if (wave >= 4) {
+        persist_loader(seq, nt, nk, smem, wave - 4, lane);
+        return;
+    }
+    for (int i = 0; i < nt; ++i) persist_compute<KIND>(seq.tile(i), nk, i * nk, smem, wave, lane);
+}
+
 extern "C" __global__ void __launch_bounds__(GEMM_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2))) eek_gemm_i8(EeGemmArgs g) {
     gemm_pipelined<EE_GEMM_I8>(g);
 }
@@ -1009,6 +1227,53 @@ eek_gemm_routed(EeRoutedGemmArgs r) {
         } else {
             gemm_tile<EE_GEMM_F16>(r.t[2], tm - T0 - T1, tn, smem);
         }
+    }
+}
+
+extern "C" __global__ void __launch_bounds__(GEMM_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
+eek_gemm_i8_persist(EeGemmArgs g) {
+    gemm_persistent<EE_GEMM_I8>(g);
+}
+extern "C" __global__ void __launch_bounds__(GEMM_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
+eek_gemm_f8_persist(EeGemmArgs g) {
+    gemm_persistent<EE_GEMM_F8>(g);
+}
+
+// eek_gemm_routed as a persistent grid (at most one workgroup per CU): each
+// workgroup runs its INT8 and FP8 tiles through the cross-tile pipeline, then
+// its W8A16 tiles, one Gemm8 run each (the pipeline ee_gemm uses for that
+// tier, so routed and per-tier outputs stay bit-identical).  TileDeal levels
+// the work: W8A16 tiles first, round robin, then the 1-byte tiles.
+extern "C" __global__ void __launch_bounds__(GEMM_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
+eek_gemm_routed_persist(EeRoutedGemmArgs r) {
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[(NSTAGE_P + 1) * LDS_STAGE];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int32_t* counts = r.t[0].counts;
+    const int c0 = counts[0], c1 = counts[1], c2 = counts[2];
+    const int T0 = (c0 + BM - 1) / BM, T1 = (c1 + BM - 1) / BM, T2 = (c2 + BM - 1) / BM;
+    const int nN = (r.t[0].N + BN - 1) / BN;
+    const int b = (int)blockIdx.x, G = (int)gridDim.x;
+    const int nF = T2 * nN;
+    const SeqRouted seq(r, T0, T0 + T1, c0, c1, nN, nF, b, G);
+    const int nt = seq.count();
+    const int nk = r.t[0].K / BKB;
+    if (nt > 0) {
+        if (wave >= 4) {
+            persist_loader(seq, nt, nk, smem, wave - 4, lane);
+        } else {
+            for (int i = 0; i < nt; ++i) {
+                const PTile t = seq.tile(i);
+                if (t.tier == 0) persist_compute<EE_GEMM_I8>(t, nk, i * nk, smem, wave, lane);
+                else persist_compute<EE_GEMM_F8>(t, nk, i * nk, smem, wave, lane);
+            }
+        }
+    }
+    // W8A16 tiles f = b, b + G, ...: M-tile f % T2, N-tile f / T2
+    for (int f = b; f < nF; f += G) {
+        __syncthreads();                              // the LDS is free: earlier tiles' reads and DMA are done
+        Gemm8<EE_GEMM_F16> k(r.t[2], smem);
+        k.run(f % T2, f / T2);
     }
 }
 

@@ -185,6 +185,7 @@ int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 struct ee_engine {
     int device = -1;
+    int cus = 0;                              // compute units: the persistent GEMM grids
     std::vector<hipModule_t> modules;
     std::unordered_map<std::string, Kernel> kernels;
     std::unordered_map<std::string, int64_t> options;
@@ -288,6 +289,18 @@ int64_t opt(const ee_engine* e, const char* key) {
     return it == e->options.end() ? 0 : it->second;
 }
 
+// Workgroups of a persistent GEMM over `tiles` tiles, or 0 for the one-tile-per-
+// workgroup kernels.  Auto: one workgroup per CU (a multiple of 8, so each XCD
+// gets the same share) once there are more tiles than CUs.  Option
+// "gemm_persist": 1 = never, n >= 2 = always, with min(n, tiles) workgroups.
+int64_t persist_grid(const ee_engine* e, int64_t tiles) {
+    const int64_t v = opt(e, "gemm_persist");
+    if (v == 1) return 0;
+    if (v >= 2) return std::min(v, tiles);
+    const int64_t g = e->cus >= 8 ? (e->cus & ~7) : e->cus;
+    return tiles > e->cus ? g : 0;
+}
+
 }  // namespace
 
 // ============================================================================ API
@@ -349,6 +362,9 @@ EE_EXPORT int ee_engine_create(const char* lib_dir, ee_engine** out) {
         e->modules.clear();
     };
     if (hipGetDevice(&e->device) != hipSuccess) return fail(EE_ERR_HIP, "hipGetDevice failed (no GPU?)");
+    if (hipDeviceGetAttribute(&e->cus, hipDeviceAttributeMultiprocessorCount, e->device) != hipSuccess ||
+        e->cus <= 0)
+        return fail(EE_ERR_HIP, "hipDeviceGetAttribute(MultiprocessorCount) failed");
     std::map<std::string, hipModule_t> loaded;
     for (auto& kv : blobs) {
         hipModule_t m = nullptr;
@@ -409,6 +425,8 @@ EE_EXPORT int ee_engine_set_option(ee_engine* eng, const char* key, int64_t valu
         if (value < 0 || value > 2) return fail(EE_ERR_INVALID_ARG, k + " must be 0 (auto), 1 or 2");
     } else if (k == "routed_unfused") {
         if (value != 0 && value != 1) return fail(EE_ERR_INVALID_ARG, k + " must be 0 or 1");
+    } else if (k == "gemm_persist") {
+        if (value < 0 || value > 65535) return fail(EE_ERR_INVALID_ARG, k + " must be 0 (auto), 1 (off) or a grid >= 2");
     } else {
         return fail(EE_ERR_INVALID_ARG, "unknown option: " + k);
     }
@@ -564,13 +582,23 @@ EE_EXPORT int ee_gemm(ee_engine* eng, int32_t kind, const void* a, int64_t lda, 
     static const char* names[3] = {"eek_gemm_i8", "eek_gemm_f8", "eek_gemm_f16"};
     const int64_t tiles = cdiv(M, 128) * cdiv(N, 128);
     std::string name = std::string(names[kind]) + (((K * esz) % 128 == 0) ? "" : "_generic");
+    int64_t grid = tiles;
     if ((K * esz) % 128 == 0) {
         const int64_t v = opt(eng, "gemm_variant");
         const bool w8 = v == 2 || (v == 0 && (kind == EE_GEMM_F16 || (kind == EE_GEMM_I8 && tiles <= 256)));
-        if (w8 && find_kernel(eng, name + "_w8")) name += "_w8";
+        if (w8 && find_kernel(eng, name + "_w8")) {
+            name += "_w8";
+        } else if (kind != EE_GEMM_F16 && counts == nullptr) {
+            // several tiles per CU: the persistent loader-wave kernel (same K order, same bits)
+            const int64_t pg = persist_grid(eng, tiles);
+            if (pg > 0 && find_kernel(eng, name + "_persist")) {
+                name += "_persist";
+                grid = pg;
+            }
+        }
     }
     const Kernel* k = find_kernel(eng, name);
-    return launch(eng, name, tiles, 1, k ? k->block : EE_BLOCK, g, stream);
+    return launch(eng, name, grid, 1, k ? k->block : EE_BLOCK, g, stream);
 }
 
 EE_EXPORT int ee_route(ee_engine* eng, const float* h, int64_t rows, double tau_low, double tau_high,
@@ -632,9 +660,11 @@ EE_EXPORT int ee_routed_linear(ee_engine* eng, const void* x, int64_t ld_x, int3
                              ld_x, K, ldc, M, N, K, EE_TIER_FP16};
         ra.mt_max = (int32_t)cdiv(M, 128) + 2;
         ra.f16_w8 = opt(eng, "gemm_variant") != 1;   // the FP16 pipeline ee_gemm picks (same f32 order)
-        const Kernel* k = find_kernel(eng, "eek_gemm_routed");
-        return launch(eng, "eek_gemm_routed", (int64_t)ra.mt_max * cdiv(N, 128), 1, k ? k->block : EE_BLOCK, ra,
-                      stream);
+        const int64_t slots = (int64_t)ra.mt_max * cdiv(N, 128);
+        const int64_t pg = ra.f16_w8 ? persist_grid(eng, slots) : 0;   // its W8A16 tiles run on Gemm8
+        const char* rname = pg > 0 ? "eek_gemm_routed_persist" : "eek_gemm_routed";
+        const Kernel* k = find_kernel(eng, rname);
+        return launch(eng, rname, pg > 0 ? pg : slots, 1, k ? k->block : EE_BLOCK, ra, stream);
     }
     // Any K (a multiple of 16): five launches, each tier's quantiser and GEMM.
     // INT8 rows: quantise into partition slots, GEMM, scatter.
