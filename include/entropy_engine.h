@@ -76,13 +76,18 @@ int ee_abi_version(void);
 int ee_engine_create(const char* lib_dir, ee_engine** out);
 int ee_engine_destroy(ee_engine* eng);
 /* Tuning knobs (0 = automatic): "se_wpr" waves per softmax row (1..8),
+ * "se_rpw" softmax rows per wave for short rows (1, 2, 4),
  * "quant_wpr" waves per quantiser row (1,2,4);
  * "routed_unfused" = 1 makes ee_routed_linear use its five-launch sequence for
  * every K (for comparisons); "gemm_variant" = 1 runs every GEMM on the
  * loader-wave pipeline, 2 on the 8-wave pipeline where one exists (INT8 and
  * W8A16); automatic: 8-wave for W8A16, and for INT8 grids of at most one tile
  * per CU.  INT8 results are identical either way; the FP16 tier's f32
- * summation order follows the pipeline (the routed linear follows ee_gemm). */
+ * summation order follows the pipeline (the routed linear follows ee_gemm).
+ * "gemm_persist": INT8 / FP8 GEMMs with more tiles than CUs (and the routed
+ * linear's tier grid) run as persistent grids, one workgroup per CU walking
+ * its tiles with the stage ring running across tile boundaries; 1 turns that
+ * off, n >= 2 forces it with min(n, tiles) workgroups.  Same bits either way. */
 int ee_engine_set_option(ee_engine* eng, const char* key, int64_t value);
 int ee_engine_device(const ee_engine* eng);
 
@@ -201,6 +206,26 @@ int ee_routed_linear(ee_engine* eng, const void* x, int64_t ld_x, int32_t M, int
  * two roundings of torch's fp16 F.silu(g) * u. */
 int ee_silu_mul(ee_engine* eng, const void* gu, int64_t ld_gu, void* act, int64_t ld_act, int64_t M,
                 int64_t F, ee_stream_t stream);
+
+/* ---- the Llama block's elementwise work around the gated linears -----------
+ * ee_add_rmsnorm replaces the residual add + LlamaRMSNorm pair of the block
+ * the reference wraps (EE/python/dispatch.py:150-247 calls the HF layer's
+ * norms around its dispatched MLP): s = fp16(x + y) (y may be NULL: s = x; when
+ * given, s is also written to x_out), then n = fp16(w * fp16(f32(s) *
+ * rsqrt(mean(f32(s)^2) + eps))).  One row per wave; D % 8 == 0, D <= 4096.
+ * The mean sums in another order than torch's reduction (last-bit effects). */
+int ee_add_rmsnorm(ee_engine* eng, const void* x, int64_t ld_x, const void* y, int64_t ld_y, const void* w,
+                   void* x_out, int64_t ld_xo, void* n_out, int64_t ld_n, int64_t T, int64_t D, float eps,
+                   ee_stream_t stream);
+
+/* Rotary embedding of the q and k heads of a fused q|k|v projection output
+ * ([B*S, (Hq + 2*Hkv)*d], row stride ld) into head-major q [B, Hq, S, d],
+ * k and v [B, Hkv, S, d]: x*cos + rotate_half(x)*sin with each op rounded to
+ * fp16, as the HF Llama attention the reference wraps computes it; cos/sin
+ * fp16 [S, d].  q is stored scaled by q_scale (1: unscaled).  d % 16 == 0. */
+int ee_qkv_rope(ee_engine* eng, const void* qkv, int64_t ld, const void* cos_t, const void* sin_t, void* q, void* k,
+                void* v, int32_t B, int32_t S, int32_t Hq, int32_t Hkv, int32_t d, float q_scale,
+                ee_stream_t stream);
 
 /* Weight preparation: gate_w, up_w fp16 [F, H] and down_w fp16 [H, F] (the
  * nn.Linear layout, EE/test_engine.py:12-14) quantised per output channel as

@@ -132,6 +132,10 @@ def test_built_meta_lists_every_kernel_the_launcher_selects():
     for v, w in se:
         rpb = 4 if w == 1 else (2 if w == 2 else 1)
         assert ks[f"eek_softmax_entropy_v{v}_w{w}"]["block"] == rpb * w * 64
+    for k in ("eek_softmax_entropy_v1_r2", "eek_softmax_entropy_v1_r4", "eek_softmax_entropy_v2_r2"):
+        assert ks[k]["block"] == 256
+    for c in (1, 2, 4, 8):
+        assert ks[f"eek_add_rmsnorm_c{c}"]["block"] == 256
     for k in ("eek_softmax_entropy_generic", "eek_quant_generic", "eek_gemm_i8", "eek_gemm_f8", "eek_gemm_f16",
               "eek_gemm_i8_w8", "eek_gemm_f16_w8",
               "eek_gemm_i8_generic", "eek_gemm_f8_generic", "eek_gemm_f16_generic",

@@ -117,6 +117,29 @@ def test_softmax_entropy_every_row_split(ee, orc, wpr, S):
         _lib.check(L.ee_engine_set_option(_lib.engine(), b"se_wpr", 0))
 
 
+@pytest.mark.parametrize("rpw", [1, 2, 4])
+@pytest.mark.parametrize("R,S,causal", [(1027, 512, True), (1029, 512, False), (515, 1000, False), (7, 300, True),
+                                        (2050, 1024, True)])
+def test_softmax_entropy_rows_per_wave(ee, orc, R, S, causal, rpw):
+    """Short rows with several rows per wave (all their loads issued first):
+    ragged row counts (the last wave's rows past the end), causal rows, and the
+    two-vector rows (S <= 1024) that only have a 2-rows variant."""
+    from entropy_engine import _lib
+    rng = np.random.default_rng(R + S + rpw)
+    X = logits_rows(rng, R, S)
+    H_ref, P_ref = orc.softmax_entropy(X, causal=causal)
+    L = _lib.lib()
+    _lib.check(L.ee_engine_set_option(_lib.engine(), b"se_rpw", rpw))
+    try:
+        p, h, _ = ee.softmax_entropy(cuda(X), causal=causal)
+        check_entropy(host(h), H_ref)
+        check_probs(host(p), P_ref)
+        _, h2, _ = ee.softmax_entropy(cuda(X), causal=causal, probs=False)
+        assert np.array_equal(host(h2), host(h))
+    finally:
+        _lib.check(L.ee_engine_set_option(_lib.engine(), b"se_rpw", 0))
+
+
 def test_softmax_entropy_max_in_several_waves(ee, orc):
     """Rows whose maximum (and its ties) sit in different waves of the row, near
     one-hot rows, and +-0 maxima: the waves holding the max take the counting

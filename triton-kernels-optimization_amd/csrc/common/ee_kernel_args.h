@@ -137,3 +137,30 @@ struct EeSiluMulArgs {
     int64_t ld_act;
     int32_t vec;            // 1: F, strides and pointers allow 16-byte accesses
 };
+
+// eek_add_rmsnorm: one wave per row of D fp16 values (D % 8 == 0, D <= 4096).
+struct EeRmsNormArgs {
+    const uint16_t* x;      // fp16 [T, D], row stride ld_x
+    const uint16_t* y;      // optional fp16 [T, D] added to x first (NULL: none), row stride ld_y
+    const uint16_t* w;      // fp16 [D] weight
+    uint16_t* x_out;        // fp16 [T, D]: x + y (only written when y != NULL), row stride ld_xo
+    uint16_t* n_out;        // fp16 [T, D]: the normalised rows, row stride ld_n
+    int64_t T;
+    int64_t D;
+    int64_t ld_x, ld_y, ld_xo, ld_n;
+    float eps;
+    float inv_d;            // f32(1 / D)
+};
+
+// eek_qkv_rope: rotary embedding of q and k and the head-major layouts.
+struct EeQkvRopeArgs {
+    const uint16_t* qkv;    // fp16 [B*S, (Hq + 2*Hkv) * d]: q heads, k heads, v heads; row stride ld
+    const uint16_t* cos_t;  // fp16 [S, d]
+    const uint16_t* sin_t;  // fp16 [S, d]
+    uint16_t* q;            // fp16 [B, Hq, S, d]
+    uint16_t* k;            // fp16 [B, Hkv, S, d]
+    uint16_t* v;            // fp16 [B, Hkv, S, d]
+    int64_t ld;
+    int32_t B, S, Hq, Hkv, d;
+    float q_scale;          // q is stored as fp16(rope(q) * q_scale); 1 stores rope(q)
+};

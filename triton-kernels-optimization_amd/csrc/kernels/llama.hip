@@ -1,0 +1,140 @@
+// llama.hip -- the Llama block's elementwise work around the entropy-gated
+// linears for gfx950: RMSNorm fused with the residual add, and rotary
+// embedding fused with the q/k/v head-major layout.  Each follows the torch
+// op sequence it replaces, op by op and in the same precision.
+#include "../common/ee_device.h"
+
+// Every multiply and add below stands for one torch op, rounded on its own:
+// no contraction into FMAs (which would skip the fp16 rounding of a product
+// before the add that follows it).
+#pragma clang fp contract(off)
+
+// eek_add_rmsnorm: s = x + y (fp16, as torch adds fp16 tensors: f32 sum
+// rounded once to fp16), then RMSNorm as LlamaRMSNorm computes it in f32:
+//   xf = f32(s); r = rsqrt(mean(xf * xf) + eps); n = fp16(xf * r);
+//   out = fp16(f32(w) * f32(n)).
+// One wave per row; lane l holds 16-byte chunks l, l + 64, ... (NC of them:
+// the launcher picks the smallest of 1, 2, 4, 8 that covers the row, which
+// keeps the register count, and so the occupancy, to what the row needs).
+// The mean's f32 sum runs in a different order than torch's reduction, so a
+// row can differ from torch in the last bit of its mean.
+template <int NC>
+EE_DEV void add_rmsnorm(const EeRmsNormArgs& a) {
+    const int lane = lane_id();
+    const int64_t row = (int64_t)blockIdx.x * (EE_BLOCK / 64) + wave_id();
+    if (row >= a.T) return;
+    const int nc = (int)(a.D >> 3);                   // 16-byte chunks per row
+    const uint16_t* xr = a.x + row * a.ld_x;
+    u32x4 s[NC];
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NC; ++i) {
+        const int c = lane + 64 * i;
+        if (c < nc) {
+            u32x4 v = *(const u32x4*)(xr + 8 * c);
+            if (a.y) {
+                const u32x4 yv = *(const u32x4*)(a.y + row * a.ld_y + 8 * c);
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    v[j] = pack_f16x2(f16_lo(v[j]) + f16_lo(yv[j]), f16_hi(v[j]) + f16_hi(yv[j]));
+                *(u32x4*)(a.x_out + row * a.ld_xo + 8 * c) = v;
+            }
+            s[i] = v;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float lo = f16_lo(v[j]), hi = f16_hi(v[j]);
+                ss += lo * lo;
+                ss += hi * hi;
+            }
+        }
+    }
+    const float r = rsqrtf(wave_sum(ss) * a.inv_d + a.eps);
+#pragma unroll
+    for (int i = 0; i < NC; ++i) {
+        const int c = lane + 64 * i;
+        if (c < nc) {
+            const u32x4 w = *(const u32x4*)(a.w + 8 * c);
+            u32x4 o;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float n0 = f16_round(f16_lo(s[i][j]) * r), n1 = f16_round(f16_hi(s[i][j]) * r);
+                o[j] = pack_f16x2(f16_lo(w[j]) * n0, f16_hi(w[j]) * n1);
+            }
+            *(u32x4*)(a.n_out + row * a.ld_n + 8 * c) = o;
+        }
+    }
+}
+#define EE_RMSNORM(NC) \
+    extern "C" __global__ void __launch_bounds__(EE_BLOCK) eek_add_rmsnorm_c##NC(EeRmsNormArgs a) { add_rmsnorm<NC>(a); }
+EE_RMSNORM(1)
+EE_RMSNORM(2)
+EE_RMSNORM(4)
+EE_RMSNORM(8)
+
+// Rotary embedding of 8 + 8 elements: x1 = elements j .. j+7 of the first
+// half, x2 = the same positions of the second half (h = d/2):
+//   out[j]   = fp16( fp16(x[j] * cos[j])     + fp16(-x[j+h] * sin[j]) )
+//   out[j+h] = fp16( fp16(x[j+h] * cos[j+h]) + fp16( x[j]   * sin[j+h]) )
+// which is torch's x * cos + rotate_half(x) * sin, each op rounded to fp16
+// (products of two fp16 values are exact in f32; the sum is rounded from f32,
+// as torch's fp16 add).  q_scale != 1 then stores fp16(out * q_scale).
+EE_DEV uint32_t rope2(uint32_t xa, uint32_t xb, uint32_t c, uint32_t s, bool first, float scale) {
+    float o[2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+        const float a = e ? f16_hi(xa) : f16_lo(xa);  // this element
+        const float b = e ? f16_hi(xb) : f16_lo(xb);  // its partner in the other half
+        const float cc = e ? f16_hi(c) : f16_lo(c), sn = e ? f16_hi(s) : f16_lo(s);
+        const float t1 = f16_round(a * cc);
+        const float t2 = f16_round((first ? -b : b) * sn);
+        float v = f16_round(t1 + t2);
+        if (scale != 1.0f) v = v * scale;
+        o[e] = v;
+    }
+    return pack_f16x2(o[0], o[1]);
+}
+
+extern "C" __global__ void __launch_bounds__(EE_BLOCK) eek_qkv_rope(EeQkvRopeArgs a) {
+    const int d = a.d, h = d >> 1;
+    const int cpr = d >> 4;                           // 8-element chunk pairs per head row
+    const int64_t T = (int64_t)a.B * a.S;
+    const int64_t n_qk = T * (a.Hq + a.Hkv) * cpr;
+    const int64_t n_v = T * a.Hkv * (d >> 3);
+    const int64_t stride = (int64_t)gridDim.x * EE_BLOCK;
+    for (int64_t i = (int64_t)blockIdx.x * EE_BLOCK + threadIdx.x; i < n_qk + n_v; i += stride) {
+        if (i < n_qk) {
+            const int c = (int)(i % cpr);
+            const int64_t th = i / cpr;
+            const int head = (int)(th % (a.Hq + a.Hkv));
+            const int64_t t = th / (a.Hq + a.Hkv);
+            const int b = (int)(t / a.S), s = (int)(t % a.S);
+            const uint16_t* src = a.qkv + t * a.ld + (int64_t)head * d + 8 * c;
+            const u32x4 x1 = *(const u32x4*)src, x2 = *(const u32x4*)(src + h);
+            const uint16_t* cr = a.cos_t + (int64_t)s * d + 8 * c;
+            const uint16_t* sr = a.sin_t + (int64_t)s * d + 8 * c;
+            const u32x4 c1 = *(const u32x4*)cr, c2 = *(const u32x4*)(cr + h);
+            const u32x4 s1 = *(const u32x4*)sr, s2 = *(const u32x4*)(sr + h);
+            const bool isq = head < a.Hq;
+            const float scale = isq ? a.q_scale : 1.0f;
+            u32x4 o1, o2;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                o1[j] = rope2(x1[j], x2[j], c1[j], s1[j], true, scale);
+                o2[j] = rope2(x2[j], x1[j], c2[j], s2[j], false, scale);
+            }
+            uint16_t* dst = isq ? a.q + (((int64_t)b * a.Hq + head) * a.S + s) * d
+                                : a.k + (((int64_t)b * a.Hkv + (head - a.Hq)) * a.S + s) * d;
+            *(u32x4*)(dst + 8 * c) = o1;
+            *(u32x4*)(dst + h + 8 * c) = o2;
+        } else {
+            const int64_t iv = i - n_qk;
+            const int c = (int)(iv % (d >> 3));
+            const int64_t th = iv / (d >> 3);
+            const int head = (int)(th % a.Hkv);
+            const int64_t t = th / a.Hkv;
+            const int b = (int)(t / a.S), s = (int)(t % a.S);
+            const u32x4 v = *(const u32x4*)(a.qkv + t * a.ld + (int64_t)(a.Hq + a.Hkv + head) * d + 8 * c);
+            *(u32x4*)(a.v + (((int64_t)b * a.Hkv + head) * a.S + s) * d + 8 * c) = v;
+        }
+    }
+}

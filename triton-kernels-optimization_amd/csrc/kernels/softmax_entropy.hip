@@ -60,24 +60,14 @@ EE_DEV float sub_hi(uint32_t u, float negm) {
 //     the per-element test that keeps those entries out of Z' and counts them
 //     (c0); the others take the test-free loop;
 //  4. probabilities p = fp16(e / Z) from the kept e (VPT <= 4) or recomputed e.
+// The row's registers: lane l of wave wr of the row holds 16-byte vectors
+// j = 0 .. VPT-1 at column ((j * WPR + wr) * 64 + l) * 8; entries past the row
+// (or past the causal limit) read as -inf and are not loaded.
 template <int VPT, int WPR>
-EE_DEV void softmax_entropy_vec(const EeSoftmaxArgs& a) {
-    typedef SeGeom<WPR> G;
-    constexpr bool KEEP_E = VPT <= 4;
-    __shared__ float red[G::RPB * WPR][4];
-
-    const int lane = lane_id();
-    const int w = wave_id();
-    const int wr = w % WPR;
-    const int64_t row = (int64_t)blockIdx.x * G::RPB + w / WPR;
-    const bool valid = row < a.rows;
-    const int64_t r = valid ? row : a.rows - 1;    // keep every wave in the barriers
+EE_DEV void se_load(const EeSoftmaxArgs& a, int64_t r, int wr, int lane, u32x4 (&v)[VPT]) {
     const int S = a.S;
     const int nvalid = a.causal ? min(S, (int)(r % S) + 1) : S;
     const uint16_t* xr = a.x + r * a.ld_x;
-
-    // ---- one read of the row: VPT x 16 B per lane, lanes adjacent in memory
-    u32x4 v[VPT];
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
         const int c0 = ((j * WPR + wr) * 64 + lane) * 8;
@@ -91,6 +81,14 @@ EE_DEV void softmax_entropy_vec(const EeSoftmaxArgs& a) {
                          e[4] | ((uint32_t)e[5] << 16), e[6] | ((uint32_t)e[7] << 16)};
         }
     }
+}
+
+// Steps 1-4 for one row held in v (red: the block's cross-wave partials when WPR > 1).
+template <int VPT, int WPR>
+EE_DEV void se_process(const EeSoftmaxArgs& a, u32x4 (&v)[VPT], int64_t row, bool valid, int w, int wr, int lane,
+                       float (*red)[4]) {
+    constexpr bool KEEP_E = VPT <= 4;
+    const int S = a.S;
 
     // ---- 1. max
     f16x2 mx2 = f16x2_from_bits(0xFC00FC00u);
@@ -100,7 +98,7 @@ EE_DEV void softmax_entropy_vec(const EeSoftmaxArgs& a) {
         for (int i = 0; i < 4; ++i) mx2 = __builtin_elementwise_maximum(mx2, f16x2_from_bits(v[j][i]));
     const float m_lane = fmaximum((float)mx2.x, (float)mx2.y);
     float m = wave_maximum(m_lane);
-    if (WPR > 1) {
+    if constexpr (WPR > 1) {
         if (lane == 0) red[w][0] = m;
         __syncthreads();
         const int base = (w / WPR) * WPR;
@@ -154,7 +152,7 @@ EE_DEV void softmax_entropy_vec(const EeSoftmaxArgs& a) {
     float z = wave_sum(z0 + z1);
     float t = wave_sum(t0 + t1);
     float cz = (float)wave_sum_i32(cnt);
-    if (WPR > 1) {
+    if constexpr (WPR > 1) {
         if (lane == 0) { red[w][1] = z; red[w][2] = t; red[w][3] = cz; }
         __syncthreads();
         const int base = (w / WPR) * WPR;
@@ -199,6 +197,39 @@ EE_DEV void softmax_entropy_vec(const EeSoftmaxArgs& a) {
             for (int i = 0; i < 8; ++i)
                 if (c0 + i < S) pr[c0 + i] = (uint16_t)(o[i >> 1] >> ((i & 1) * 16));
         }
+    }
+}
+
+template <int VPT, int WPR>
+EE_DEV void softmax_entropy_vec(const EeSoftmaxArgs& a) {
+    typedef SeGeom<WPR> G;
+    __shared__ float red[G::RPB * WPR][4];
+    const int lane = lane_id();
+    const int w = wave_id();
+    const int wr = w % WPR;
+    const int64_t row = (int64_t)blockIdx.x * G::RPB + w / WPR;
+    const bool valid = row < a.rows;
+    const int64_t r = valid ? row : a.rows - 1;    // keep every wave in the barriers
+    u32x4 v[VPT];
+    se_load<VPT, WPR>(a, r, wr, lane, v);
+    se_process<VPT, WPR>(a, v, row, valid, w, wr, lane, red);
+}
+
+// Short rows (one wave per row): each wave takes RPW consecutive rows and
+// issues all their loads before working on the first, so a wave keeps
+// RPW x VPT x 1 KB of the input in flight instead of VPT x 1 KB.
+template <int VPT, int RPW>
+EE_DEV void softmax_entropy_rows(const EeSoftmaxArgs& a) {
+    const int lane = lane_id();
+    const int w = wave_id();
+    const int64_t row0 = ((int64_t)blockIdx.x * (EE_BLOCK / 64) + w) * RPW;
+    u32x4 v[RPW][VPT];
+#pragma unroll
+    for (int q = 0; q < RPW; ++q) se_load<VPT, 1>(a, min(row0 + q, a.rows - 1), 0, lane, v[q]);
+#pragma unroll
+    for (int q = 0; q < RPW; ++q) {
+        if (row0 + q >= a.rows) break;                // wave-uniform; no barriers in se_process<., 1>
+        se_process<VPT, 1>(a, v[q], row0 + q, true, w, 0, lane, nullptr);
     }
 }
 
@@ -255,6 +286,14 @@ EE_SE_VEC_W(1)
 EE_SE_VEC_W(2)
 EE_SE_VEC_W(3)
 EE_SE_VEC_W(4)
+// short rows, several per wave
+#define EE_SE_ROWS(V, R) \
+    extern "C" __global__ void __launch_bounds__(EE_BLOCK) eek_softmax_entropy_v##V##_r##R(EeSoftmaxArgs a) { \
+        softmax_entropy_rows<V, R>(a);                                                                  \
+    }
+EE_SE_ROWS(1, 2)
+EE_SE_ROWS(1, 4)
+EE_SE_ROWS(2, 2)
 // rows longer than 4 * 8 * 512: eight waves, probabilities from recomputed e
 EE_SE_VEC(5, 8)
 EE_SE_VEC(6, 8)

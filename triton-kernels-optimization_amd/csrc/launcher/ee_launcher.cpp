@@ -418,6 +418,9 @@ EE_EXPORT int ee_engine_set_option(ee_engine* eng, const char* key, int64_t valu
     const std::string k(key);
     if (k == "se_wpr") {
         if (value < 0 || value > 8) return fail(EE_ERR_INVALID_ARG, k + " must be 0 (auto) or 1..8");
+    } else if (k == "se_rpw") {
+        if (value != 0 && value != 1 && value != 2 && value != 4)
+            return fail(EE_ERR_INVALID_ARG, k + " must be 0 (auto), 1, 2 or 4");
     } else if (k == "quant_wpr") {
         if (value != 0 && value != 1 && value != 2 && value != 4)
             return fail(EE_ERR_INVALID_ARG, k + " must be 0 (auto), 1, 2 or 4");
@@ -451,6 +454,17 @@ EE_EXPORT int ee_softmax_entropy(ee_engine* eng, const void* x, void* p, float* 
     const bool vec_ok = aligned(x, 16) && aligned(p, 16) && ld_x % 8 == 0 && (p == nullptr || ld_p % 8 == 0);
     int vpt = 0, wpr = 0;
     if (vec_ok && pick_se_cfg(S, rows, opt(eng, "se_wpr"), vpt, wpr)) {
+        // Short single-wave rows: several rows per wave (their loads issued together)
+        // once there are rows enough to keep every CU busy.  Option "se_rpw": 1 = one
+        // row per wave, 2 or 4 = that many where the variant exists.
+        if (wpr == 1 && vpt <= 2) {
+            const int64_t f = opt(eng, "se_rpw");
+            // measured at [131072, 512]: 2 rows per wave -8% (causal) to -11%; 4 no better than 2
+            const int rpw = f ? (int)f : (rows >= 32768 ? 2 : 1);
+            const std::string rname = "eek_softmax_entropy_v" + std::to_string(vpt) + "_r" + std::to_string(rpw);
+            if (rpw > 1 && find_kernel(eng, rname))
+                return launch(eng, rname, cdiv(rows, 4LL * rpw), 1, EE_BLOCK, a, stream);
+        }
         const std::string name = "eek_softmax_entropy_v" + std::to_string(vpt) + "_w" + std::to_string(wpr);
         const int rpb = wpr == 1 ? 4 : (wpr == 2 ? 2 : 1);      // rows per block (kernel's SeGeom)
         const Kernel* k = find_kernel(eng, name);
@@ -701,6 +715,46 @@ EE_EXPORT int ee_silu_mul(ee_engine* eng, const void* gu, int64_t ld_gu, void* a
     const int64_t work = vec ? M * (F / 8) : M * F;
     const int64_t g = std::min<int64_t>(cdiv(work, EE_BLOCK), 16384);
     return launch(eng, "eek_silu_mul", g, 1, EE_BLOCK, a, stream);
+}
+
+EE_EXPORT int ee_add_rmsnorm(ee_engine* eng, const void* x, int64_t ld_x, const void* y, int64_t ld_y,
+                             const void* w, void* x_out, int64_t ld_xo, void* n_out, int64_t ld_n, int64_t T,
+                             int64_t D, float eps, ee_stream_t stream) {
+    if (eng == nullptr || x == nullptr || w == nullptr || n_out == nullptr || (y != nullptr && x_out == nullptr))
+        return fail(EE_ERR_INVALID_ARG, "NULL argument");
+    if (T < 0 || D <= 0 || ld_x < D || ld_n < D || (y != nullptr && (ld_y < D || ld_xo < D)))
+        return fail(EE_ERR_INVALID_ARG, "bad shape or stride");
+    if (D % 8 != 0 || D > 4096 || ld_x % 8 != 0 || ld_n % 8 != 0 || (y != nullptr && (ld_y % 8 != 0 || ld_xo % 8 != 0)))
+        return fail(EE_ERR_UNSUPPORTED, "add_rmsnorm needs D % 8 == 0, D <= 4096 and strides that are multiples of 8");
+    if (!aligned(x, 16) || !aligned(y, 16) || !aligned(w, 16) || !aligned(x_out, 16) || !aligned(n_out, 16))
+        return fail(EE_ERR_INVALID_ARG, "misaligned pointer (16 B)");
+    if (T == 0) return EE_OK;
+    EeRmsNormArgs a{(const uint16_t*)x, (const uint16_t*)y, (const uint16_t*)w, (uint16_t*)x_out, (uint16_t*)n_out,
+                    T, D, ld_x, ld_y, ld_xo, ld_n, eps, 1.0f / (float)D};
+    const int64_t nc = cdiv(D / 8, 64);                // 16-byte chunks per lane
+    const char* name = nc <= 1 ? "eek_add_rmsnorm_c1" : nc <= 2 ? "eek_add_rmsnorm_c2"
+                                                      : nc <= 4 ? "eek_add_rmsnorm_c4" : "eek_add_rmsnorm_c8";
+    return launch(eng, name, cdiv(T, EE_BLOCK / 64), 1, EE_BLOCK, a, stream);
+}
+
+EE_EXPORT int ee_qkv_rope(ee_engine* eng, const void* qkv, int64_t ld, const void* cos_t, const void* sin_t,
+                          void* q, void* k, void* v, int32_t B, int32_t S, int32_t Hq, int32_t Hkv, int32_t d,
+                          float q_scale, ee_stream_t stream) {
+    if (eng == nullptr || qkv == nullptr || cos_t == nullptr || sin_t == nullptr || q == nullptr || k == nullptr ||
+        v == nullptr)
+        return fail(EE_ERR_INVALID_ARG, "NULL argument");
+    if (B < 0 || S < 0 || Hq <= 0 || Hkv <= 0 || d <= 0 || ld < (int64_t)(Hq + 2 * Hkv) * d)
+        return fail(EE_ERR_INVALID_ARG, "bad shape or stride");
+    if (d % 16 != 0 || ld % 8 != 0) return fail(EE_ERR_UNSUPPORTED, "qkv_rope needs d % 16 == 0 and ld % 8 == 0");
+    if (!aligned(qkv, 16) || !aligned(cos_t, 16) || !aligned(sin_t, 16) || !aligned(q, 16) || !aligned(k, 16) ||
+        !aligned(v, 16))
+        return fail(EE_ERR_INVALID_ARG, "misaligned pointer (16 B)");
+    const int64_t T = (int64_t)B * S;
+    if (T == 0) return EE_OK;
+    EeQkvRopeArgs a{(const uint16_t*)qkv, (const uint16_t*)cos_t, (const uint16_t*)sin_t, (uint16_t*)q, (uint16_t*)k,
+                    (uint16_t*)v, ld, B, S, Hq, Hkv, d, q_scale};
+    const int64_t work = T * (Hq + Hkv) * (d / 16) + T * Hkv * (d / 8);
+    return launch(eng, "eek_qkv_rope", std::min<int64_t>(cdiv(work, EE_BLOCK), 16384), 1, EE_BLOCK, a, stream);
 }
 
 EE_EXPORT int ee_mlp_prepare(ee_engine* eng, const void* gate_w, const void* up_w, const void* down_w, int64_t H,

@@ -60,6 +60,9 @@ SIGNATURES = {
     "ee_routed_linear": ([_p, _p, _i64, _i32, _i32, _i32, _p, _p, _p, _p, _p, _p, _p, _i64, _p, _p, _p],
                          ctypes.c_int),
     "ee_silu_mul": ([_p, _p, _i64, _p, _i64, _i64, _i64, _p], ctypes.c_int),
+    "ee_add_rmsnorm": ([_p, _p, _i64, _p, _i64, _p, _p, _i64, _p, _i64, _i64, _i64, ctypes.c_float, _p], ctypes.c_int),
+    "ee_qkv_rope": ([_p, _p, _i64, _p, _p, _p, _p, _p, _i32, _i32, _i32, _i32, _i32, ctypes.c_float, _p],
+                    ctypes.c_int),
     "ee_mlp_prepare": ([_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _p],
                        ctypes.c_int),
     "ee_mlp_workspace_bytes": ([_i64, _i64, _i64, _i32], _i64),

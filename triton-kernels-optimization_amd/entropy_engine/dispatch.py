@@ -246,20 +246,25 @@ def _attention_entropy(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scalin
                        attention_mask: Optional[torch.Tensor] = None, causal: bool = False):
     """softmax(q k^T * scaling [+ mask]) v, the probabilities and their per-row
     Shannon entropy from the fused softmax+entropy kernel (one pass over the
-    scores).  q [B, Hq, S, d], k/v [B, Hkv, Sk, d] fp16 (grouped-query heads
-    are repeated).  Returns (out [B, Hq, S, d] fp16, H [B, Hq, S] f32).
-    causal: key c of query s is kept iff c <= s (needs Sk == S)."""
+    scores).  q [B, Hq, S, d], k/v [B, Hkv, Sk, d] fp16.  Grouped-query heads
+    (Hq = G * Hkv, query head h reading kv head h // G) need no copies of k and
+    v: the G query heads of a kv head are consecutive, so q viewed as
+    [B, Hkv, G * S, d] multiplies k and v of [B, Hkv, Sk, d] directly.
+    Returns (out [B, Hq, S, d] fp16, H [B, Hq, S] f32).  scaling == 1 skips the
+    multiply (for q already scaled).  causal: key c of query s is kept iff
+    c <= s (needs Sk == S)."""
     B, Hq, S, d = q.shape
     Hkv, Sk = k.shape[1], k.shape[2]
-    if Hkv != Hq:
-        k = k.repeat_interleave(Hq // Hkv, dim=1)
-        v = v.repeat_interleave(Hq // Hkv, dim=1)
-    scores = torch.matmul(q.contiguous(), k.transpose(-1, -2).contiguous()) * scaling
+    G = Hq // Hkv
+    qg = q.contiguous().view(B, Hkv, G * S, d)
+    scores = torch.matmul(qg, k.transpose(-1, -2).contiguous())          # [B, Hkv, G*S, Sk]
+    if scaling != 1.0:
+        scores = scores * scaling
     if attention_mask is not None:
-        scores = scores + attention_mask[..., :Sk].to(scores.dtype)
+        scores = scores.view(B, Hq, S, Sk) + attention_mask[..., :Sk].to(scores.dtype)
     probs, H, _ = K.softmax_entropy(scores.reshape(-1, Sk), causal=causal and attention_mask is None)
-    out = torch.matmul(probs.view(B, Hq, S, Sk), v.contiguous())
-    return out, H.view(B, Hq, S)
+    out = torch.matmul(probs.view(B, Hkv, G * S, Sk), v.contiguous())   # [B, Hkv, G*S, d]
+    return out.view(B, Hq, S, d), H.view(B, Hq, S)
 
 
 class EntropyDispatchedLlamaBlock(nn.Module):
@@ -367,7 +372,10 @@ class EntropyGatedLlama:
 
     Weights: fp16 tensors in `params` (embed [V, D]; per layer ln1, q [Hq*d, D],
     k/v [Hkv*d, D], o [D, Hq*d], ln2, gate/up [F, D], down [D, F]; norm;
-    lm_head [V, D]).  RMSNorm and RoPE follow the Llama definitions."""
+    lm_head [V, D]).  RMSNorm and RoPE follow the Llama definitions, as fused
+    kernels (add_rmsnorm: residual add + norm; qkv_rope: RoPE + head-major q/k/v,
+    q pre-scaled by 1/sqrt(d)); SwiGLU is silu_mul; grouped-query attention
+    reads the shared k/v heads without copies."""
 
     def __init__(self, params: dict, cfg: dict, tau_low: float = 2.34, tau_high: float = 6.03):
         self.p = params
@@ -414,11 +422,6 @@ class EntropyGatedLlama:
         return cls(p, cfg, **kw)
 
     # ---------------------------------------------------------------- pieces
-    def _rmsnorm(self, x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
-        xf = x.float()
-        xf = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.cfg["eps"])
-        return w * xf.to(torch.float16)
-
     def _rope_tables(self, S: int, dev):
         key = (S, dev)
         if key not in self._rope_cache:
@@ -453,28 +456,27 @@ class EntropyGatedLlama:
         B, S = input_ids.shape
         T = B * S
         Hq, Hkv, d = c["heads"], c["kv_heads"], c["head_dim"]
-        x = self.p["embed"][input_ids]                                   # [B, S, D] fp16
+        x = self.p["embed"][input_ids].reshape(T, -1)                    # [T, D] fp16
         cos, sin = self._rope_tables(S, x.device)
+        eps = c["eps"]
         counts_log = []
         route_prev = None
+        res = None                                    # the pending residual branch, added by the next norm
         for l in range(c["layers"]):
-            xn = self._rmsnorm(x, self.p[f"{l}.ln1"]).reshape(T, -1)
+            x, xn = K.add_rmsnorm(x, self.p[f"{l}.ln1"], eps, res)
             qkv = self._linear(xn, (l, "qkv"), route_prev, gated)
-            q = qkv[:, :Hq * d].reshape(B, S, Hq, d).transpose(1, 2)
-            k = qkv[:, Hq * d:(Hq + Hkv) * d].reshape(B, S, Hkv, d).transpose(1, 2)
-            v = qkv[:, (Hq + Hkv) * d:].reshape(B, S, Hkv, d).transpose(1, 2)
-            q, k = _rope(q, cos, sin), _rope(k, cos, sin)
-            att, H = _attention_entropy(q, k, v, d ** -0.5, causal=True)
+            # RoPE and the head-major layouts in one pass; q carries the 1/sqrt(d) scaling
+            q, k, v = K.qkv_rope(qkv, cos, sin, B, S, Hq, Hkv, d, d ** -0.5)
+            att, H = _attention_entropy(q, k, v, 1.0, causal=True)
             att = att.transpose(1, 2).reshape(T, Hq * d)
             route_cur = self._route(H.mean(dim=1).reshape(T).contiguous(), counts_log) if gated else None
-            x = x + self._linear(att, (l, "o"), route_cur, gated).view(B, S, -1)
-            xn = self._rmsnorm(x, self.p[f"{l}.ln2"]).reshape(T, -1)
+            o = self._linear(att, (l, "o"), route_cur, gated)
+            x, xn = K.add_rmsnorm(x, self.p[f"{l}.ln2"], eps, o)
             gu = self._linear(xn, (l, "gu"), route_cur, gated)
-            F = gu.shape[1] // 2
-            act = torch.nn.functional.silu(gu[:, :F]) * gu[:, F:]
-            x = x + self._linear(act, (l, "down"), route_cur, gated).view(B, S, -1)
+            act = K.silu_mul(gu)
+            res = self._linear(act, (l, "down"), route_cur, gated)
             route_prev = route_cur
-        xn = self._rmsnorm(x, self.p["norm"]).reshape(T, -1)
+        x, xn = K.add_rmsnorm(x, self.p["norm"], eps, res)
         logits = self._linear(xn, "lm_head", route_prev, gated)
         if gated:
             # rows per tier over every linear layer: each route feeds o/gate/up/down (4)

@@ -29,7 +29,7 @@ from ._lib import check, engine, ptr, stream_handle
 __all__ = [
     "triton_int8_gemm", "triton_fp8_gemm", "triton_fp16_gemm", "fused_softmax_entropy",
     "softmax_entropy", "quantize_activations", "gemm", "route", "row_copy", "routed_linear",
-    "prepare_weight", "PackedWeight", "quantize_weight_codes", "silu_mul",
+    "prepare_weight", "PackedWeight", "quantize_weight_codes", "silu_mul", "add_rmsnorm", "qkv_rope",
 ]
 
 
@@ -390,3 +390,47 @@ def silu_mul(gu: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
         check(_lib.lib().ee_silu_mul(engine(), ptr(gu), _rowmajor(gu, "gu"), ptr(act), _rowmajor(act, "out"), M, F,
                                      stream_handle()))
     return act
+
+
+# ---------------------------------------------------------------- Llama block elementwise work
+
+def add_rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float, y: torch.Tensor | None = None):
+    """(s, n): s = x + y (x itself when y is None), n = LlamaRMSNorm(s) with weight w,
+    each op in torch's precision; rows of the last dimension D (D % 8 == 0, D <= 4096)."""
+    dev = _require_cuda(x, w, y)
+    D = x.shape[-1]
+    x2 = x.reshape(-1, D)
+    if x2.stride(-1) != 1 or x2.data_ptr() % 16 or (x2.shape[0] > 1 and x2.stride(0) % 8):
+        x2 = x2.contiguous()
+    y2 = None
+    if y is not None:
+        y2 = y.reshape(-1, D)
+        if y2.stride(-1) != 1 or y2.data_ptr() % 16 or (y2.shape[0] > 1 and y2.stride(0) % 8):
+            y2 = y2.contiguous()
+    T = x2.shape[0]
+    n = torch.empty((T, D), dtype=torch.float16, device=dev)
+    s = torch.empty((T, D), dtype=torch.float16, device=dev) if y is not None else x2
+    w = w.contiguous()
+    with torch.cuda.device(dev):
+        check(_lib.lib().ee_add_rmsnorm(engine(), ptr(x2), _rowmajor(x2, "x"), ptr(y2),
+                                        _rowmajor(y2, "y") if y2 is not None else D, ptr(w),
+                                        ptr(s) if y is not None else None, D, ptr(n), D, T, D, float(eps),
+                                        stream_handle()))
+    return s.view(x.shape), n.view(x.shape)
+
+
+def qkv_rope(qkv: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, B: int, S: int, Hq: int, Hkv: int, d: int,
+             q_scale: float = 1.0):
+    """q [B, Hq, S, d], k, v [B, Hkv, S, d] from a fused projection output [B*S, (Hq+2Hkv)*d],
+    rotary-embedded (x*cos + rotate_half(x)*sin per fp16 op; cos/sin [S, d]); q scaled by q_scale."""
+    dev = _require_cuda(qkv, cos, sin)
+    ld = _rowmajor(qkv, "qkv")
+    cos = cos.reshape(S, d).contiguous()
+    sin = sin.reshape(S, d).contiguous()
+    q = torch.empty((B, Hq, S, d), dtype=torch.float16, device=dev)
+    k = torch.empty((B, Hkv, S, d), dtype=torch.float16, device=dev)
+    v = torch.empty((B, Hkv, S, d), dtype=torch.float16, device=dev)
+    with torch.cuda.device(dev):
+        check(_lib.lib().ee_qkv_rope(engine(), ptr(qkv), ld, ptr(cos), ptr(sin), ptr(q), ptr(k), ptr(v), B, S, Hq,
+                                     Hkv, d, float(q_scale), stream_handle()))
+    return q, k, v
