@@ -231,8 +231,10 @@ int ee_qkv_rope(ee_engine* eng, const void* qkv, int64_t ld, const void* cos_t, 
  * nn.Linear layout, EE/test_engine.py:12-14) quantised per output channel as
  * quantize_weights_int8 does (EE/python/dispatch.py:43-48), into the caller's
  * buffers: gu_* hold the [2F, H] operand (gate rows 0..F-1, up rows F..2F-1)
- * as int8 codes, e4m3 codes, W8A16 fp16 weights and f32 scales [2F]; dn_* the
- * [H, F] down operand and scales [H].  All 16-byte aligned, row stride = K. */
+ * as int8 codes, e4m3 codes, W8A16 fp16 weights and f32 scales [2F], with gate
+ * and up rows interleaved in blocks of 32 (the SwiGLU layout below); dn_* the
+ * [H, F] down operand and scales [H].  All 16-byte aligned, row stride = K.
+ * F % 32 == 0. */
 int ee_mlp_prepare(ee_engine* eng, const void* gate_w, const void* up_w, const void* down_w, int64_t H,
                    int64_t F, int64_t ld_gate, int64_t ld_up, int64_t ld_down, int8_t* gu_i8, uint8_t* gu_f8,
                    void* gu_f16, float* gu_scale, int8_t* dn_i8, uint8_t* dn_f8, void* dn_f16, float* dn_scale,
@@ -251,12 +253,39 @@ int64_t ee_mlp_workspace_bytes(int64_t M, int64_t H, int64_t F, int32_t routed);
  * h_rows != NULL (f32 [M]): one tier per row (ee_route), both linears on
  * ee_routed_linear; `entropy` is ignored.  No host synchronisation, no
  * allocation; workspace 256-byte aligned, ws_bytes >= ee_mlp_workspace_bytes.
- * Contract: H, F multiples of 16; ld_x multiple of 8; ldo multiple of 4. */
+ * The gate|up GEMM writes silu(gate) * up directly (SwiGLU epilogue) when H
+ * allows the pipelined kernels (H % 128 == 0); otherwise it stores gate|up and
+ * a separate pass applies the activation -- the same bits either way.
+ * Contract: H % 16 == 0; F % 32 == 0; ld_x multiple of 8; ldo multiple of 4. */
 int ee_mlp_forward(ee_engine* eng, const void* x, int64_t ld_x, int64_t M, int64_t H, int64_t F,
                    const int8_t* gu_i8, const uint8_t* gu_f8, const void* gu_f16, const float* gu_scale,
                    const int8_t* dn_i8, const uint8_t* dn_f8, const void* dn_f16, const float* dn_scale,
                    double entropy, const float* h_rows, double tau_low, double tau_high, void* out, int64_t ldo,
                    void* workspace, int64_t ws_bytes, ee_stream_t stream);
+
+/* ---- SwiGLU forms: the gate|up projection of a Llama MLP with its activation -
+ * The block the reference gates computes down(silu(gate(x)) * up(x))
+ * (EE/python/dispatch.py:199-203, EE/test_engine.py:35).  With gate and up
+ * as one operand whose rows are interleaved in blocks of 32 (rows 64k..64k+31
+ * = gate rows 32k.., rows 64k+32..64k+63 = up rows 32k..; ee_interleave_gate_up
+ * builds it from gate rows followed by up rows), the GEMM epilogue pairs each
+ * gate output with its up output and writes act [M, N/2] =
+ * fp16(fp16(silu(gate)) * up) -- the same bits as the plain GEMM followed by
+ * ee_silu_mul, without the [M, N] intermediate.  N % 64 == 0; K * element
+ * size % 128 == 0 (the pipelined kernels); act 16-byte aligned, ld_act % 8 == 0. */
+int ee_gemm_swiglu(ee_engine* eng, int32_t kind, const void* a, int64_t lda, const void* b_nk, int64_t ldb, void* act,
+                   int64_t ld_act, const float* a_scale, const float* b_scale, int32_t M, int32_t N, int32_t K,
+                   const int32_t* a_idx, const int32_t* c_idx, const int32_t* counts, int32_t tier,
+                   ee_stream_t stream);
+int ee_routed_linear_swiglu(ee_engine* eng, const void* x, int64_t ld_x, int32_t M, int32_t K, int32_t N,
+                            const int32_t* idx, const int32_t* counts, const int8_t* b_i8, const uint8_t* b_f8,
+                            const void* b_f16, const float* b_scale, void* act, int64_t ld_act, void* ws_codes,
+                            float* ws_scale, ee_stream_t stream);
+/* Rows 0..F-1 (gate) and F..2F-1 (up) of src into the interleaved order above
+ * (any row payload: int8 codes, e4m3 codes, fp16 weights, or 4-byte scales with
+ * row_bytes = 4).  F % 32 == 0; not in place. */
+int ee_interleave_gate_up(ee_engine* eng, const void* src, int64_t ld_src_bytes, void* dst, int64_t ld_dst_bytes,
+                          int64_t F, int64_t row_bytes, ee_stream_t stream);
 
 /* ---- CubinEngine counterpart (EE/csrc/engine.cpp:64-216) --------------------
  * One code object + one GEMM function, launched on the caller's stream (the

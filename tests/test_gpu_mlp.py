@@ -75,6 +75,22 @@ def check_close_f64(out16, ref64):
     assert (err <= tol).all(), f"max err {err.max():.3e}; worst excess {(err - tol).max():.3e}"
 
 
+def interleave_rows(a):
+    """Gate rows then up rows [2F, ...] -> blocks of 32 alternating (the SwiGLU operand layout)."""
+    F = a.shape[0] // 2
+    g, u = a[:F].reshape(F // 32, 32, *a.shape[1:]), a[F:].reshape(F // 32, 32, *a.shape[1:])
+    st = np.stack if isinstance(a, np.ndarray) else torch.stack
+    return st([g, u], 1).reshape(a.shape)
+
+
+def deinterleave_cols(gu):
+    """[M, 2F] columns in blocks of 32 alternating -> [gate | up] halves."""
+    M, F2 = gu.shape
+    v = gu.reshape(M, F2 // 64, 2, 32)
+    cat = np.concatenate if isinstance(gu, np.ndarray) else torch.cat
+    return cat([v[:, :, 0, :].reshape(M, F2 // 2), v[:, :, 1, :].reshape(M, F2 // 2)], 1)
+
+
 def mlp_weights(rng, H, F):
     g = (rng.standard_normal((F, H)) / np.sqrt(H)).astype(np.float16)
     u = (rng.standard_normal((F, H)) / np.sqrt(H)).astype(np.float16)
@@ -83,15 +99,16 @@ def mlp_weights(rng, H, F):
 
 
 def chain(ee, eng, x, tier):
-    """The same MLP through the public per-op entry points: (gu, act, out)."""
+    """The same MLP through the public per-op entry points, with no SwiGLU
+    epilogue: (gu [gate | up], act, out)."""
     if tier == 2:
-        gu = ee.gemm("fp16", x, eng.gu_f16)
+        gu = deinterleave_cols(ee.gemm("fp16", x, eng.gu_f16)).contiguous()
         act = ee.silu_mul(gu)
         return gu, act, ee.gemm("fp16", act, eng.dn_f16)
     mode, kind = ("dispatcher", "int8") if tier == 0 else ("fp8", "fp8")
     b_gu, b_dn = (eng.gu_i8, eng.dn_i8) if tier == 0 else (eng.gu_f8, eng.dn_f8)
     c, s = ee.quantize_activations(x, mode)
-    gu = ee.gemm(kind, c, b_gu, s, eng.gu_scale)
+    gu = deinterleave_cols(ee.gemm(kind, c, b_gu, s, eng.gu_scale)).contiguous()
     act = ee.silu_mul(gu)
     c2, s2 = ee.quantize_activations(act, mode)
     return gu, act, ee.gemm(kind, c2, b_dn, s2, eng.dn_scale)
@@ -143,6 +160,7 @@ def test_mlp_prepare_matches_oracle(ee, orc):
     g, u, d = mlp_weights(rng, H, F)
     eng = ee.EntropyMLPEngine(cuda(g), cuda(u), cuda(d), *TAUS)
     (Bgu, sgu), (Bdn, sdn) = orc.mlp_weights(g, u, d)
+    Bgu, sgu = interleave_rows(Bgu.T).T.copy(), interleave_rows(sgu)   # the SwiGLU row order
     assert np.array_equal(host(eng.gu_i8), Bgu.T)
     assert np.array_equal(host(eng.gu_scale).view(np.uint32), sgu.view(np.uint32))
     assert np.array_equal(host(eng.dn_i8), Bdn.T)
@@ -154,7 +172,7 @@ def test_mlp_prepare_matches_oracle(ee, orc):
 
 
 @pytest.mark.parametrize("tier", [0, 1, 2], ids=["int8", "fp8", "fp16"])
-@pytest.mark.parametrize("M,H,F", [(96, 256, 352), (1, 128, 64), (130, 512, 1024)])
+@pytest.mark.parametrize("M,H,F", [(96, 256, 352), (1, 128, 64), (130, 512, 1024), (40, 96, 64)])
 def test_mlp_forward_tier(ee, orc, tier, M, H, F):
     rng = np.random.default_rng(M + H + F + tier)
     g, u, d = mlp_weights(rng, H, F)
@@ -249,3 +267,59 @@ def test_mlp_reference_shape(ee, orc):
     for tier in range(3):
         sel = h == TIER_ENTROPY[tier]
         assert torch.equal(routed[sel], outs[tier][sel])
+
+
+# ---------------------------------------------------------------------------- SwiGLU epilogue
+
+@pytest.fixture(params=[(0, 0), (1, 0), (2, 0), (0, 8), (0, 1)],
+                ids=["auto", "loader-waves", "8-waves", "persist-grid8", "persist-off"])
+def pipeline(request):
+    from entropy_engine import _lib
+    L, e = _lib.lib(), _lib.engine()
+    _lib.check(L.ee_engine_set_option(e, b"gemm_variant", request.param[0]))
+    _lib.check(L.ee_engine_set_option(e, b"gemm_persist", request.param[1]))
+    yield request.param
+    _lib.check(L.ee_engine_set_option(e, b"gemm_variant", 0))
+    _lib.check(L.ee_engine_set_option(e, b"gemm_persist", 0))
+
+
+@pytest.mark.parametrize("M,K,F", [(300, 512, 320), (1024, 2048, 1408), (1, 128, 32)])
+def test_swiglu_gemm_equals_gemm_then_silu(ee, orc, M, K, F, pipeline):
+    """The SwiGLU epilogue (every tier, every pipeline) gives the bits of the plain
+    GEMM on the same interleaved operand followed by silu_mul."""
+    rng = np.random.default_rng(M + K + F)
+    W = (rng.standard_normal((2 * F, K)) / np.sqrt(K)).astype(np.float16)
+    codes, scale = ee.quantize_weight_codes(cuda(W))
+    pw = ee.PackedWeight(ee.interleave_gate_up(codes), ee.interleave_gate_up(scale)).materialize()
+    x = cuda(rng.standard_normal((M, K)).astype(np.float16))
+    ci, si = ee.quantize_activations(x, "dispatcher")
+    cf, sf = ee.quantize_activations(x, "fp8")
+    for kind, a, b, sa, sb in (("int8", ci, pw.i8, si, pw.scale), ("fp8", cf, pw.f8, sf, pw.scale),
+                               ("fp16", x, pw.f16, None, None)):
+        fused = ee.gemm(kind, a, b, sa, sb, swiglu=True)
+        ref = ee.silu_mul(deinterleave_cols(ee.gemm(kind, a, b, sa, sb)).contiguous())
+        assert fused.shape == (M, F)
+        assert torch.equal(fused.view(torch.int16), ref.view(torch.int16)), kind
+
+
+@pytest.mark.parametrize("M,K,F", [(700, 1024, 384), (4096, 2048, 1408), (257, 256, 64)])
+def test_swiglu_routed_equals_routed_then_silu(ee, orc, M, K, F, pipeline):
+    rng = np.random.default_rng(M * 5 + F)
+    W = (rng.standard_normal((2 * F, K)) / np.sqrt(K)).astype(np.float16)
+    codes, scale = ee.quantize_weight_codes(cuda(W))
+    pw = ee.PackedWeight(ee.interleave_gate_up(codes), ee.interleave_gate_up(scale)).materialize()
+    x = cuda(rng.standard_normal((M, K)).astype(np.float16))
+    h = cuda((rng.random(M) * 3).astype(np.float32))
+    _, idx, counts = ee.route(h, 0.41, 1.68)
+    fused = ee.routed_linear(x, pw, idx, counts, swiglu=True)
+    ref = ee.silu_mul(deinterleave_cols(ee.routed_linear(x, pw, idx, counts)).contiguous())
+    assert torch.equal(fused.view(torch.int16), ref.view(torch.int16))
+
+
+def test_interleave_gate_up_layout(ee):
+    t = torch.arange(2 * 96 * 8, device="cuda", dtype=torch.int32).reshape(2 * 96, 8).to(torch.int8)
+    assert torch.equal(ee.interleave_gate_up(t), interleave_rows(t))
+    s = torch.randn(2 * 96, device="cuda")
+    assert torch.equal(ee.interleave_gate_up(s), interleave_rows(s))
+    with pytest.raises(ValueError):
+        ee.interleave_gate_up(torch.zeros(2 * 48, 4, device="cuda"))

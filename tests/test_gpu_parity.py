@@ -829,8 +829,9 @@ def test_entropy_gated_llama_small(ee):
             deq["lm_head"] = w
         elif key[1] == "qkv":
             deq[f"{key[0]}.q"], deq[f"{key[0]}.k"], deq[f"{key[0]}.v"] = w[:Hd], w[Hd:Hd + KVd], w[Hd + KVd:]
-        elif key[1] == "gu":
-            deq[f"{key[0]}.gate"], deq[f"{key[0]}.up"] = w[:F], w[F:]
+        elif key[1] == "gu":                             # gate|up rows interleaved in blocks of 32
+            v = w.view(F // 32, 2, 32, -1)
+            deq[f"{key[0]}.gate"], deq[f"{key[0]}.up"] = v[:, 0].reshape(F, -1), v[:, 1].reshape(F, -1)
         else:
             deq[f"{key[0]}.{key[1]}"] = w
     ref = ee.EntropyGatedLlama(deq, SMALL_LLAMA).forward(ids, gated=False).float()

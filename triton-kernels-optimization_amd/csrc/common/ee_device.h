@@ -89,13 +89,37 @@ EE_DEV uint32_t bits_of(f16x2 h) {
 }
 EE_DEV float f16_lo(uint32_t u) { return (float)f16x2_from_bits(u).x; }
 EE_DEV float f16_hi(uint32_t u) { return (float)f16x2_from_bits(u).y; }
+// x as an f32 register value.  hipcc folds an f32 multiply whose only use is an
+// f32 -> fp16 conversion into v_fma_mix{lo,hi}_f16(a, b, 0): one rounding,
+// straight to fp16, even under -ffp-contract=off.  Every fp16 result here is
+// the reference's f32 value rounded to fp16 (f32 op, then .to(float16)), so
+// conversions take their operand through this barrier, which costs no
+// instruction.
+EE_DEV float f32_rn(float x) {
+    asm("" : "+v"(x));
+    return x;
+}
 EE_DEV uint32_t pack_f16x2(float lo, float hi) {
     f16x2 h;
-    h.x = (f16)lo;   // v_cvt_f16_f32: round to nearest even
-    h.y = (f16)hi;
+    h.x = (f16)f32_rn(lo);   // v_cvt_f16_f32: round to nearest even
+    h.y = (f16)f32_rn(hi);
     return bits_of(h);
 }
-EE_DEV float f16_round(float x) { return (float)(f16)x; }
+EE_DEV float f16_round(float x) { return (float)(f16)f32_rn(x); }
+
+// SiLU * up of two fp16 pairs: fp16( f32(fp16(silu(g))) * f32(u) ) per half,
+// silu(g) = g / (1 + e^-g) in f32 -- torch's fp16 F.silu(gate) * up, op by op.
+// No contraction: 1 + e^-g is one rounded add, as in torch.
+EE_DEV float silu_f32(float g) {
+#pragma clang fp contract(off)
+    return g / (1.0f + expf(-g));
+}
+EE_DEV uint32_t silu_mul2(uint32_t g2, uint32_t u2) {
+#pragma clang fp contract(off)
+    const float a0 = f16_round(silu_f32(f16_lo(g2)));
+    const float a1 = f16_round(silu_f32(f16_hi(g2)));
+    return pack_f16x2(a0 * f16_lo(u2), a1 * f16_hi(u2));
+}
 
 // Routing partition bookkeeping: rows of tier t start at counts[0] + ... + counts[t-1].
 EE_DEV int64_t tier_offset(const int32_t* counts, int tier) {

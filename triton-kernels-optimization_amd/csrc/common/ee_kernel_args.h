@@ -74,6 +74,9 @@ struct EeGemmArgs {
     int32_t N;
     int32_t K;
     int32_t tier;
+    int32_t swiglu;         // 1: B is gate|up interleaved in blocks of 32 rows (rows 64k .. 64k+31 =
+                            // gate 32k .., rows 64k+32 .. 64k+63 = up 32k ..); C receives
+                            // act [*, N/2] = fp16(fp16(silu(gate)) * up) instead of [*, N]
 };
 
 // The routed linear's tier GEMMs in one launch (eek_gemm_routed): t[k] is the
@@ -129,13 +132,24 @@ struct EeRowCopyArgs {
 
 // MLP activation (eek_silu_mul): act[m, j] = silu(gu[m, j]) * gu[m, F + j], fp16.
 struct EeSiluMulArgs {
-    const uint16_t* gu;     // fp16 [M, 2F] (gate | up), row stride ld_gu
+    const uint16_t* gu;     // fp16 [M, 2F]: gate | up halves, or (interleave) blocks of 32 alternating; row stride ld_gu
     uint16_t* act;          // fp16 [M, F], row stride ld_act
     int64_t M;
     int64_t F;
     int64_t ld_gu;
     int64_t ld_act;
     int32_t vec;            // 1: F, strides and pointers allow 16-byte accesses
+    int32_t interleave;     // 1: gate of column j at 64*(j/32) + j%32, up 32 columns later
+};
+
+// eek_interleave_rows: dst row 64k + r = src row 32k + r, dst row 64k + 32 + r =
+// src row F + 32k + r (r < 32) -- gate rows then up rows into blocks of 32.
+struct EeInterleaveArgs {
+    const uint8_t* src;
+    uint8_t* dst;
+    int64_t F;              // rows per half (a multiple of 32)
+    int64_t row_bytes;      // a multiple of 4
+    int64_t ld_src_bytes, ld_dst_bytes;
 };
 
 // eek_add_rmsnorm: one wave per row of D fp16 values (D % 8 == 0, D <= 4096).

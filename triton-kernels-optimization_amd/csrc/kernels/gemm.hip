@@ -35,6 +35,12 @@
 // upper bound M and surplus workgroups exit at once.
 #include "../common/ee_device.h"
 
+// Every epilogue / quantiser multiply and add is its own rounded f32
+// operation, as in the reference: no contraction into FMAs.  (Conversions to
+// fp16 take their operand through f32_rn, which keeps a product from being
+// folded into the conversion.)
+#pragma clang fp contract(off)
+
 #define BM 128
 #define BN 128
 #define BKB 128                         // K bytes per LDS stage
@@ -317,9 +323,79 @@ EE_DEV void load_scales(const EeGemmArgs& g, int m0, int n0, int M, int64_t off,
     }
 }
 
+// Dequantised value of one accumulator, as the fp16 epilogues compute it
+// (left-to-right f32 multiplies; W8A16 accumulators are the value).
+template <int KIND, typename E>
+EE_DEV float deq(E acc, float as, float bs) {
+    if constexpr (KIND == EE_GEMM_I8) {
+        float v = (float)acc;
+        v = v * as;
+        return v * bs;
+    } else if constexpr (KIND == EE_GEMM_F8) {
+        const float v = acc * as;
+        return v * bs;
+    } else {
+        return acc;
+    }
+}
+
+// One 16-byte store of C or of the SwiGLU output: non-temporal (written once,
+// read by a later kernel), 8-byte halves when the row is only 8-byte aligned.
+EE_DEV void store_row16(uint16_t* dst, const u32x4& v, bool full) {
+    if (full && ((uintptr_t)dst & 15) == 0) {
+        __builtin_nontemporal_store(v, (u32x4*)dst);
+    } else {
+        __builtin_nontemporal_store(u32x2{v[0], v[1]}, (u32x2*)dst);
+        if (full) __builtin_nontemporal_store(u32x2{v[2], v[3]}, (u32x2*)(dst + 4));
+    }
+}
+
+// SwiGLU epilogue of a wave's 64 x 64 quadrant (swiglu weights: column block
+// j = 0 holds gate values, j = 1 the up values of the same 32 outputs):
+// act = fp16(fp16(silu(fp16(gate))) * fp16(up)), the fp16 gate and up being
+// exactly what the plain epilogue would store.  The 64 x 32 act block goes
+// through the wave's LDS region to act columns (n0 + 64 wn) / 2 ...
 template <int KIND>
+EE_DEV void epilogue32_lds_swiglu(const EeGemmArgs& g, const typename Pipe<KIND>::acc_t (&acc)[2][2],
+                                  const TileScales& sc, uint8_t* tile, int m0, int n0, int M, int64_t off, int wm,
+                                  int wn, int lane) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int rl = i * 32 + (lane & 31);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            float gv[4], uv[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                gv[r] = deq<KIND>(acc[i][0][4 * q + r], sc.as[i], sc.bs[0][q][r]);
+                uv[r] = deq<KIND>(acc[i][1][4 * q + r], sc.as[i], sc.bs[1][q][r]);
+            }
+            // act column 8q + 4(l >> 5) + 0..3 of the block: chunk q, half l >> 5
+            *(u32x2*)(tile + lds_off(rl, q) + (lane >> 5) * 8) =
+                u32x2{silu_mul2(pack_f16x2(gv[0], gv[1]), pack_f16x2(uv[0], uv[1])),
+                      silu_mul2(pack_f16x2(gv[2], gv[3]), pack_f16x2(uv[2], uv[3]))};
+        }
+    }
+    const int na = g.N >> 1;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int rl = k * 16 + (lane >> 2), ch = lane & 3;
+        const u32x4 v = *(const u32x4*)(tile + lds_off(rl, ch));
+        const int m = m0 + wm * 64 + rl;
+        const int n = ((n0 + wn * 64) >> 1) + ch * 8;
+        if (m >= M || n >= na) continue;
+        const int64_t crow = g.c_idx ? (int64_t)g.c_idx[off + m] : (int64_t)m;
+        store_row16(g.c + crow * g.ldc + n, v, true);
+    }
+}
+
+template <int KIND, int SW>
 EE_DEV void epilogue32_lds(const EeGemmArgs& g, const typename Pipe<KIND>::acc_t (&acc)[2][2], const TileScales& sc,
                            uint8_t* tile, int m0, int n0, int M, int64_t off, int wm, int wn, int lane) {
+    if constexpr (SW) {
+        epilogue32_lds_swiglu<KIND>(g, acc, sc, tile, m0, n0, M, off, wm, wn, lane);
+        return;
+    }
     // 1. dequantise and write: lane l holds rows i*32 + (l & 31), columns j*32 + 8q + 4(l >> 5) + 0..3.
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
@@ -381,7 +457,7 @@ EE_DEV void epilogue32_lds(const EeGemmArgs& g, const typename Pipe<KIND>::acc_t
 
 // One 128 x 128 C tile (tile coordinates tm, tn) of the pipelined GEMM;
 // smem is the workgroup's NSTAGE * LDS_STAGE bytes of LDS (1 KB aligned).
-template <int KIND>
+template <int KIND, int SW = 0>
 EE_DEV void gemm_tile(const EeGemmArgs& g, int tm, int tn, uint8_t* smem) {
     typedef Pipe<KIND> P;
     typedef typename P::acc_t acc_t;
@@ -502,7 +578,7 @@ EE_DEV void gemm_tile(const EeGemmArgs& g, int tm, int tn, uint8_t* smem) {
         // (the loaders waited for all of theirs before it), and its last stage,
         // nk - NSTAGE, was read before barrier nk - NSTAGE + 1.
         uint8_t* tile = smem + (nk % NSTAGE) * LDS_STAGE + wave * (64 * BKB);
-        epilogue32_lds<KIND>(g, acc, sc, tile, m0, n0, M, off, wm, wn, lane);
+        epilogue32_lds<KIND, SW>(g, acc, sc, tile, m0, n0, M, off, wm, wn, lane);
     }
 }
 
@@ -573,12 +649,48 @@ EE_DEV void load_scales_blk(const EeGemmArgs& g, int m0, int n0, int M, int64_t 
     }
 }
 
+// SwiGLU form of epilogue_blk_lds: the 32 x 64 block's gate (j = 0) and up
+// (j = 1) halves become a 32 x 32 act block at act columns (n0 + 64 wn) / 2 ...
+template <int KIND>
+EE_DEV void epilogue_blk_lds_swiglu(const EeGemmArgs& g, const typename Pipe<KIND>::acc_t (&acc)[2],
+                                    const TileScales& sc, uint8_t* tile, int m0, int n0, int M, int64_t off, int wm,
+                                    int wn, int rb, int lane) {
+    const int rl0 = lane & 31;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        float gv[4], uv[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            gv[r] = deq<KIND>(acc[0][4 * q + r], sc.as[0], sc.bs[0][q][r]);
+            uv[r] = deq<KIND>(acc[1][4 * q + r], sc.as[0], sc.bs[1][q][r]);
+        }
+        *(u32x2*)(tile + lds_off(rl0, q) + (lane >> 5) * 8) =
+            u32x2{silu_mul2(pack_f16x2(gv[0], gv[1]), pack_f16x2(uv[0], uv[1])),
+                  silu_mul2(pack_f16x2(gv[2], gv[3]), pack_f16x2(uv[2], uv[3]))};
+    }
+    const int na = g.N >> 1;
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const int rl = k * 16 + (lane >> 2), ch = lane & 3;
+        const u32x4 v = *(const u32x4*)(tile + lds_off(rl, ch));
+        const int m = m0 + wm * 64 + rb * 32 + rl;
+        const int n = ((n0 + wn * 64) >> 1) + ch * 8;
+        if (m >= M || n >= na) continue;
+        const int64_t crow = g.c_idx ? (int64_t)g.c_idx[off + m] : (int64_t)m;
+        store_row16(g.c + crow * g.ldc + n, v, true);
+    }
+}
+
 // Epilogue of one 32 x 64 block (row block rb of quadrant (wm, wn)) held as
 // acc[0..1] (column blocks), through a 4 KB LDS tile: dequantise, write in the
 // MFMA layout, read back as rows and store 16 bytes per lane, non-temporal.
-template <int KIND>
+template <int KIND, int SW>
 EE_DEV void epilogue_blk_lds(const EeGemmArgs& g, const typename Pipe<KIND>::acc_t (&acc)[2], const TileScales& sc,
                              uint8_t* tile, int m0, int n0, int M, int64_t off, int wm, int wn, int rb, int lane) {
+    if constexpr (SW) {
+        epilogue_blk_lds_swiglu<KIND>(g, acc, sc, tile, m0, n0, M, off, wm, wn, rb, lane);
+        return;
+    }
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
 #pragma unroll
@@ -660,7 +772,7 @@ EE_DEV void epilogue_blk_direct(const EeGemmArgs& g, const typename Pipe<KIND>::
         }
 }
 
-template <int KIND>
+template <int KIND, int SW = 0>
 struct Gemm8 {
     typedef Pipe<KIND> P;
     typedef typename P::acc_t acc_t;
@@ -878,26 +990,26 @@ struct Gemm8 {
             epilogue_blk_direct<KIND>(g, blk, m0, n0, M, off, wm, wn, kq, lane);
         } else {
             uint8_t* tile = smem + (nk % NSTAGE) * LDS_STAGE + wave * 4096;
-            epilogue_blk_lds<KIND>(g, blk, sc, tile, m0, n0, M, off, wm, wn, kq, lane);
+            epilogue_blk_lds<KIND, SW>(g, blk, sc, tile, m0, n0, M, off, wm, wn, kq, lane);
         }
     }
 };
 
-template <int KIND>
+template <int KIND, int SW = 0>
 EE_DEV void gemm_pipelined_8w(const EeGemmArgs& g) {
     __shared__ __attribute__((aligned(1024))) uint8_t smem[NSTAGE * LDS_STAGE];
     int tm, tn;
     tile_of((int)blockIdx.x, (int)gridDim.x, (g.M + BM - 1) / BM, tm, tn);
-    Gemm8<KIND> k(g, smem);
+    Gemm8<KIND, SW> k(g, smem);
     k.run(tm, tn);
 }
 
-template <int KIND>
+template <int KIND, int SW = 0>
 EE_DEV void gemm_pipelined(const EeGemmArgs& g) {
     __shared__ __attribute__((aligned(1024))) uint8_t smem[NSTAGE * LDS_STAGE];
     int tm, tn;
     tile_of((int)blockIdx.x, (int)gridDim.x, (g.M + BM - 1) / BM, tm, tn);
-    gemm_tile<KIND>(g, tm, tn, smem);
+    gemm_tile<KIND, SW>(g, tm, tn, smem);
 }
 
 template <int KIND>
@@ -1125,7 +1237,7 @@ EE_DEV void persist_loader(const Seq& seq, int ntiles, int nk, uint8_t* smem, in
 }
 
 // Compute waves (0-3) on one tile whose first stage is global stage s0.
-template <int KIND>
+template <int KIND, int SW = 0>
 EE_DEV void persist_compute(const PTile& t, int nk, int s0, uint8_t* smem, int wave, int lane) {
     typedef Pipe<KIND> P;
     typedef typename P::acc_t acc_t;
@@ -1169,10 +1281,10 @@ EE_DEV void persist_compute(const PTile& t, int nk, int s0, uint8_t* smem, int w
     for (int kt = 0; kt + 1 < nk; ++kt) stage(kt, true);
     stage(nk - 1, false);
     if (g.acc) epilogue32<KIND>(g, acc, m0, n0, t.M, t.off, wm, wn, lane);
-    else epilogue32_lds<KIND>(g, acc, sc, smem + EPI_BUF + wave * (64 * BKB), m0, n0, t.M, t.off, wm, wn, lane);
+    else epilogue32_lds<KIND, SW>(g, acc, sc, smem + EPI_BUF + wave * (64 * BKB), m0, n0, t.M, t.off, wm, wn, lane);
 }
 
-template <int KIND>
+template <int KIND, int SW = 0>
 EE_DEV void gemm_persistent(const EeGemmArgs& g) {
     __shared__ __attribute__((aligned(1024))) uint8_t smem[(NSTAGE_P + 1) * LDS_STAGE];
     const int tid = threadIdx.x, lane = tid & 63;
@@ -1184,24 +1296,27 @@ EE_DEV void gemm_persistent(const EeGemmArgs& g) {
         persist_loader(seq, nt, nk, smem, wave - 4, lane);
         return;
     }
-    for (int i = 0; i < nt; ++i) persist_compute<KIND>(seq.tile(i), nk, i * nk, smem, wave, lane);
+    for (int i = 0; i < nt; ++i) persist_compute<KIND, SW>(seq.tile(i), nk, i * nk, smem, wave, lane);
 }
 
-extern "C" __global__ void __launch_bounds__(GEMM_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2))) eek_gemm_i8(EeGemmArgs g) {
-    gemm_pipelined<EE_GEMM_I8>(g);
-}
-extern "C" __global__ void __launch_bounds__(GEMM_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2))) eek_gemm_f8(EeGemmArgs g) {
-    gemm_pipelined<EE_GEMM_F8>(g);
-}
-extern "C" __global__ void __launch_bounds__(GEMM_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2))) eek_gemm_f16(EeGemmArgs g) {
-    gemm_pipelined<EE_GEMM_F16>(g);
-}
-extern "C" __global__ void __launch_bounds__(GEMM8_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2))) eek_gemm_i8_w8(EeGemmArgs g) {
-    gemm_pipelined_8w<EE_GEMM_I8>(g);
-}
-extern "C" __global__ void __launch_bounds__(GEMM8_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2))) eek_gemm_f16_w8(EeGemmArgs g) {
-    gemm_pipelined_8w<EE_GEMM_F16>(g);
-}
+// Kernel entries; each GEMM also has a _swiglu twin whose epilogue writes
+// fp16(fp16(silu(gate)) * up) of gate|up-interleaved weights instead of C (one
+// epilogue per kernel keeps the register budget of each).
+#define EE_GEMM_ENTRY(NAME, BODY)                                                                         \
+    extern "C" __global__ void __launch_bounds__(GEMM_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2))) \
+    NAME(EeGemmArgs g) { BODY<0>(g); }                                                                  \
+    extern "C" __global__ void __launch_bounds__(GEMM_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2))) \
+    NAME##_swiglu(EeGemmArgs g) { BODY<1>(g); }
+template <int SW> EE_DEV void body_i8(const EeGemmArgs& g) { gemm_pipelined<EE_GEMM_I8, SW>(g); }
+template <int SW> EE_DEV void body_f8(const EeGemmArgs& g) { gemm_pipelined<EE_GEMM_F8, SW>(g); }
+template <int SW> EE_DEV void body_f16(const EeGemmArgs& g) { gemm_pipelined<EE_GEMM_F16, SW>(g); }
+template <int SW> EE_DEV void body_i8_w8(const EeGemmArgs& g) { gemm_pipelined_8w<EE_GEMM_I8, SW>(g); }
+template <int SW> EE_DEV void body_f16_w8(const EeGemmArgs& g) { gemm_pipelined_8w<EE_GEMM_F16, SW>(g); }
+EE_GEMM_ENTRY(eek_gemm_i8, body_i8)
+EE_GEMM_ENTRY(eek_gemm_f8, body_f8)
+EE_GEMM_ENTRY(eek_gemm_f16, body_f16)
+EE_GEMM_ENTRY(eek_gemm_i8_w8, body_i8_w8)
+EE_GEMM_ENTRY(eek_gemm_f16_w8, body_f16_w8)
 
 // The routed linear's three tier GEMMs in one launch.  Tier t owns partition
 // slots [off_t, off_t + counts[t]) (off_t = counts[0] + ... + counts[t-1]) and
@@ -1209,8 +1324,8 @@ extern "C" __global__ void __launch_bounds__(GEMM8_THREADS) __attribute__((amdgp
 // an M-tile never mixes tiers; workgroups past the last tile exit at once.
 // The grid holds r.mt_max = ceil(M / 128) + 2 M-tile slots (the sum of the
 // three ceilings is at most that) times ceil(N / 128) N-tiles.
-extern "C" __global__ void __launch_bounds__(GEMM_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
-eek_gemm_routed(EeRoutedGemmArgs r) {
+template <int SW>
+EE_DEV void gemm_routed(const EeRoutedGemmArgs& r) {
     __shared__ __attribute__((aligned(1024))) uint8_t smem[NSTAGE * LDS_STAGE];
     const int32_t* counts = r.t[0].counts;
     const int T0 = (counts[0] + BM - 1) / BM;
@@ -1218,34 +1333,38 @@ eek_gemm_routed(EeRoutedGemmArgs r) {
     const int T2 = (counts[2] + BM - 1) / BM;
     int tm, tn;
     tile_of((int)blockIdx.x, (int)gridDim.x, r.mt_max, tm, tn);
-    if (tm < T0) gemm_tile<EE_GEMM_I8>(r.t[0], tm, tn, smem);
-    else if (tm < T0 + T1) gemm_tile<EE_GEMM_F8>(r.t[1], tm - T0, tn, smem);
+    if (tm < T0) gemm_tile<EE_GEMM_I8, SW>(r.t[0], tm, tn, smem);
+    else if (tm < T0 + T1) gemm_tile<EE_GEMM_F8, SW>(r.t[1], tm - T0, tn, smem);
     else if (tm < T0 + T1 + T2) {
         if (r.f16_w8) {
-            Gemm8<EE_GEMM_F16> k(r.t[2], smem);
+            Gemm8<EE_GEMM_F16, SW> k(r.t[2], smem);
             k.run(tm - T0 - T1, tn);
         } else {
-            gemm_tile<EE_GEMM_F16>(r.t[2], tm - T0 - T1, tn, smem);
+            gemm_tile<EE_GEMM_F16, SW>(r.t[2], tm - T0 - T1, tn, smem);
         }
     }
 }
+extern "C" __global__ void __launch_bounds__(GEMM_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
+eek_gemm_routed(EeRoutedGemmArgs r) {
+    gemm_routed<0>(r);
+}
+extern "C" __global__ void __launch_bounds__(GEMM_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
+eek_gemm_routed_swiglu(EeRoutedGemmArgs r) {
+    gemm_routed<1>(r);
+}
 
-extern "C" __global__ void __launch_bounds__(GEMM_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
-eek_gemm_i8_persist(EeGemmArgs g) {
-    gemm_persistent<EE_GEMM_I8>(g);
-}
-extern "C" __global__ void __launch_bounds__(GEMM_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
-eek_gemm_f8_persist(EeGemmArgs g) {
-    gemm_persistent<EE_GEMM_F8>(g);
-}
+template <int SW> EE_DEV void body_i8_persist(const EeGemmArgs& g) { gemm_persistent<EE_GEMM_I8, SW>(g); }
+template <int SW> EE_DEV void body_f8_persist(const EeGemmArgs& g) { gemm_persistent<EE_GEMM_F8, SW>(g); }
+EE_GEMM_ENTRY(eek_gemm_i8_persist, body_i8_persist)
+EE_GEMM_ENTRY(eek_gemm_f8_persist, body_f8_persist)
 
 // eek_gemm_routed as a persistent grid (at most one workgroup per CU): each
 // workgroup runs its INT8 and FP8 tiles through the cross-tile pipeline, then
 // its W8A16 tiles, one Gemm8 run each (the pipeline ee_gemm uses for that
 // tier, so routed and per-tier outputs stay bit-identical).  TileDeal levels
 // the work: W8A16 tiles first, round robin, then the 1-byte tiles.
-extern "C" __global__ void __launch_bounds__(GEMM_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
-eek_gemm_routed_persist(EeRoutedGemmArgs r) {
+template <int SW>
+EE_DEV void gemm_routed_persist(const EeRoutedGemmArgs& r) {
     __shared__ __attribute__((aligned(1024))) uint8_t smem[(NSTAGE_P + 1) * LDS_STAGE];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1264,17 +1383,25 @@ eek_gemm_routed_persist(EeRoutedGemmArgs r) {
         } else {
             for (int i = 0; i < nt; ++i) {
                 const PTile t = seq.tile(i);
-                if (t.tier == 0) persist_compute<EE_GEMM_I8>(t, nk, i * nk, smem, wave, lane);
-                else persist_compute<EE_GEMM_F8>(t, nk, i * nk, smem, wave, lane);
+                if (t.tier == 0) persist_compute<EE_GEMM_I8, SW>(t, nk, i * nk, smem, wave, lane);
+                else persist_compute<EE_GEMM_F8, SW>(t, nk, i * nk, smem, wave, lane);
             }
         }
     }
     // W8A16 tiles f = b, b + G, ...: M-tile f % T2, N-tile f / T2
     for (int f = b; f < nF; f += G) {
         __syncthreads();                              // the LDS is free: earlier tiles' reads and DMA are done
-        Gemm8<EE_GEMM_F16> k(r.t[2], smem);
+        Gemm8<EE_GEMM_F16, SW> k(r.t[2], smem);
         k.run(f % T2, f / T2);
     }
+}
+extern "C" __global__ void __launch_bounds__(GEMM_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
+eek_gemm_routed_persist(EeRoutedGemmArgs r) {
+    gemm_routed_persist<0>(r);
+}
+extern "C" __global__ void __launch_bounds__(GEMM_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
+eek_gemm_routed_persist_swiglu(EeRoutedGemmArgs r) {
+    gemm_routed_persist<1>(r);
 }
 
 // Fallback for any K that is a multiple of 16 bytes (zero-filled K tail).

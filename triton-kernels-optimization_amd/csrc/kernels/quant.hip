@@ -18,6 +18,12 @@
 // buffer without host-side offsets.
 #include "../common/ee_device.h"
 
+// Every epilogue / quantiser multiply and add is its own rounded f32
+// operation, as in the reference: no contraction into FMAs.  (Conversions to
+// fp16 take their operand through f32_rn, which keeps a product from being
+// folded into the conversion.)
+#pragma clang fp contract(off)
+
 #define INV127 (1.0f / 127.0f)
 #define INV448 (1.0f / 448.0f)
 

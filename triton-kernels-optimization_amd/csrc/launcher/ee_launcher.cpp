@@ -558,10 +558,11 @@ EE_EXPORT int ee_pack_b_f16(ee_engine* eng, const int8_t* codes_nk, const float*
     return launch(eng, "eek_pack_b_f16", g > 16384 ? 16384 : g, 1, EE_BLOCK, a, stream);
 }
 
-EE_EXPORT int ee_gemm(ee_engine* eng, int32_t kind, const void* a, int64_t lda, const void* b_nk, int64_t ldb,
-                      void* c, int64_t ldc, const float* a_scale, const float* b_scale, int32_t M, int32_t N,
-                      int32_t K, const int32_t* a_idx, const int32_t* c_idx, const int32_t* counts, int32_t tier,
-                      int32_t* acc_out, ee_stream_t stream) {
+// sw = 1: SwiGLU epilogue (b_nk gate|up interleaved in blocks of 32 rows; c is act [M, N/2]).
+static int gemm_impl(ee_engine* eng, int32_t kind, const void* a, int64_t lda, const void* b_nk, int64_t ldb,
+                     void* c, int64_t ldc, const float* a_scale, const float* b_scale, int32_t M, int32_t N,
+                     int32_t K, const int32_t* a_idx, const int32_t* c_idx, const int32_t* counts, int32_t tier,
+                     int32_t* acc_out, int sw, ee_stream_t stream) {
     if (eng == nullptr) return fail(EE_ERR_INVALID_ARG, "engine must not be NULL");
     if (kind < EE_GEMM_I8 || kind > EE_GEMM_F16) return fail(EE_ERR_INVALID_ARG, "unknown GEMM kind");
     if (a == nullptr || b_nk == nullptr || c == nullptr) return fail(EE_ERR_INVALID_ARG, "a, b and c must not be NULL");
@@ -570,7 +571,12 @@ EE_EXPORT int ee_gemm(ee_engine* eng, int32_t kind, const void* a, int64_t lda, 
     if (acc_out != nullptr && kind != EE_GEMM_I8) return fail(EE_ERR_INVALID_ARG, "acc_out is INT8 only");
     if (M < 0 || N <= 0 || K <= 0) return fail(EE_ERR_INVALID_ARG, "need M >= 0, N > 0, K > 0");
     const int64_t esz = (kind == EE_GEMM_F16) ? 2 : 1;
-    if (lda < K || ldb < K || ldc < N) return fail(EE_ERR_INVALID_ARG, "leading dimension smaller than the row");
+    if (lda < K || ldb < K || ldc < (sw ? N / 2 : N))
+        return fail(EE_ERR_INVALID_ARG, "leading dimension smaller than the row");
+    if (sw && (N % 64 != 0 || ldc % 8 != 0 || !aligned(c, 16) || (K * esz) % 128 != 0 || acc_out != nullptr))
+        return fail(EE_ERR_UNSUPPORTED, "SwiGLU GEMM needs N % 64 == 0 (gate|up interleaved in blocks of 32), "
+                                        "ld_act % 8 == 0, a 16-byte aligned act, K * element size % 128 == 0 "
+                                        "and no acc_out");
     if ((K * esz) % 16 != 0) return fail(EE_ERR_UNSUPPORTED, "K * element size must be a multiple of 16 bytes");
     if ((lda * esz) % 16 != 0 || (ldb * esz) % 16 != 0)
         return fail(EE_ERR_UNSUPPORTED, "lda and ldb must be multiples of 16 bytes");
@@ -585,7 +591,7 @@ EE_EXPORT int ee_gemm(ee_engine* eng, int32_t kind, const void* a, int64_t lda, 
     if (counts != nullptr && (tier < 0 || tier > 2)) return fail(EE_ERR_INVALID_ARG, "tier must be 0, 1 or 2");
     if (M == 0) return EE_OK;
     EeGemmArgs g{a, b_nk, (uint16_t*)c, acc_out, a_scale, b_scale, a_idx, c_idx, counts, lda, ldb, ldc,
-                 M, N, K, counts ? tier : 0};
+                 M, N, K, counts ? tier : 0, sw};
     // The pipelined kernels stream whole 128-byte K stages; other K take the fallback.
     // Two pipelines: loader waves + MFMA waves (eek_gemm_*), and eight waves that
     // each load and compute (eek_gemm_*_w8).  Measured on MI355X (identical data,
@@ -611,8 +617,25 @@ EE_EXPORT int ee_gemm(ee_engine* eng, int32_t kind, const void* a, int64_t lda, 
             }
         }
     }
+    if (sw) name += "_swiglu";
     const Kernel* k = find_kernel(eng, name);
     return launch(eng, name, grid, 1, k ? k->block : EE_BLOCK, g, stream);
+}
+
+EE_EXPORT int ee_gemm(ee_engine* eng, int32_t kind, const void* a, int64_t lda, const void* b_nk, int64_t ldb,
+                      void* c, int64_t ldc, const float* a_scale, const float* b_scale, int32_t M, int32_t N,
+                      int32_t K, const int32_t* a_idx, const int32_t* c_idx, const int32_t* counts, int32_t tier,
+                      int32_t* acc_out, ee_stream_t stream) {
+    return gemm_impl(eng, kind, a, lda, b_nk, ldb, c, ldc, a_scale, b_scale, M, N, K, a_idx, c_idx, counts, tier,
+                     acc_out, 0, stream);
+}
+
+EE_EXPORT int ee_gemm_swiglu(ee_engine* eng, int32_t kind, const void* a, int64_t lda, const void* b_nk,
+                             int64_t ldb, void* act, int64_t ld_act, const float* a_scale, const float* b_scale,
+                             int32_t M, int32_t N, int32_t K, const int32_t* a_idx, const int32_t* c_idx,
+                             const int32_t* counts, int32_t tier, ee_stream_t stream) {
+    return gemm_impl(eng, kind, a, lda, b_nk, ldb, act, ld_act, a_scale, b_scale, M, N, K, a_idx, c_idx, counts,
+                     tier, nullptr, 1, stream);
 }
 
 EE_EXPORT int ee_route(ee_engine* eng, const float* h, int64_t rows, double tau_low, double tau_high,
@@ -641,15 +664,19 @@ EE_EXPORT int ee_row_copy(ee_engine* eng, const void* src, int64_t ld_src_bytes,
     return launch(eng, "eek_row_copy", cdiv(rows, 4), 1, EE_BLOCK, a, stream);
 }
 
-EE_EXPORT int ee_routed_linear(ee_engine* eng, const void* x, int64_t ld_x, int32_t M, int32_t K, int32_t N,
-                               const int32_t* idx, const int32_t* counts, const int8_t* b_i8, const uint8_t* b_f8,
-                               const void* b_f16, const float* b_scale, void* c, int64_t ldc, void* ws_codes,
-                               float* ws_scale, ee_stream_t stream) {
+static int routed_impl(ee_engine* eng, const void* x, int64_t ld_x, int32_t M, int32_t K, int32_t N,
+                       const int32_t* idx, const int32_t* counts, const int8_t* b_i8, const uint8_t* b_f8,
+                       const void* b_f16, const float* b_scale, void* c, int64_t ldc, void* ws_codes,
+                       float* ws_scale, int sw, ee_stream_t stream) {
     if (eng == nullptr || x == nullptr || idx == nullptr || counts == nullptr || b_i8 == nullptr ||
         b_f8 == nullptr || b_f16 == nullptr || b_scale == nullptr || c == nullptr || ws_codes == nullptr ||
         ws_scale == nullptr)
         return fail(EE_ERR_INVALID_ARG, "NULL argument");
-    if (M < 0 || K <= 0 || N <= 0 || ld_x < K || ldc < N) return fail(EE_ERR_INVALID_ARG, "bad shape or stride");
+    if (M < 0 || K <= 0 || N <= 0 || ld_x < K || ldc < (sw ? N / 2 : N))
+        return fail(EE_ERR_INVALID_ARG, "bad shape or stride");
+    if (sw && (K % 128 != 0 || N % 64 != 0 || ldc % 8 != 0 || !aligned(c, 16)))
+        return fail(EE_ERR_UNSUPPORTED, "SwiGLU routed linear needs K % 128 == 0, N % 64 == 0, ld_act % 8 == 0 "
+                                        "and a 16-byte aligned act");
     // The GEMM contracts, checked here so that no launch of the sequence can fail half way.
     if (K % 16 != 0 || (ld_x * 2) % 16 != 0 || N % 4 != 0 || ldc % 4 != 0)
         return fail(EE_ERR_UNSUPPORTED, "routed linear needs K % 16 == 0, ld_x % 8 == 0, N % 4 == 0, ldc % 4 == 0");
@@ -667,16 +694,17 @@ EE_EXPORT int ee_routed_linear(ee_engine* eng, const void* x, int64_t ld_x, int3
         if ((rc = launch_quant(eng, qa, stream))) return rc;
         EeRoutedGemmArgs ra{};
         ra.t[0] = EeGemmArgs{ws_codes, b_i8, (uint16_t*)c, nullptr, ws_scale, b_scale, nullptr, idx, counts,
-                             K, K, ldc, M, N, K, EE_TIER_INT8};
+                             K, K, ldc, M, N, K, EE_TIER_INT8, sw};
         ra.t[1] = EeGemmArgs{ws_codes, b_f8, (uint16_t*)c, nullptr, ws_scale, b_scale, nullptr, idx, counts,
-                             K, K, ldc, M, N, K, EE_TIER_FP8};
+                             K, K, ldc, M, N, K, EE_TIER_FP8, sw};
         ra.t[2] = EeGemmArgs{x, b_f16, (uint16_t*)c, nullptr, nullptr, nullptr, idx, idx, counts,
-                             ld_x, K, ldc, M, N, K, EE_TIER_FP16};
+                             ld_x, K, ldc, M, N, K, EE_TIER_FP16, sw};
         ra.mt_max = (int32_t)cdiv(M, 128) + 2;
         ra.f16_w8 = opt(eng, "gemm_variant") != 1;   // the FP16 pipeline ee_gemm picks (same f32 order)
         const int64_t slots = (int64_t)ra.mt_max * cdiv(N, 128);
         const int64_t pg = ra.f16_w8 ? persist_grid(eng, slots) : 0;   // its W8A16 tiles run on Gemm8
-        const char* rname = pg > 0 ? "eek_gemm_routed_persist" : "eek_gemm_routed";
+        std::string rname = pg > 0 ? "eek_gemm_routed_persist" : "eek_gemm_routed";
+        if (sw) rname += "_swiglu";
         const Kernel* k = find_kernel(eng, rname);
         return launch(eng, rname, pg > 0 ? pg : slots, 1, k ? k->block : EE_BLOCK, ra, stream);
     }
@@ -685,36 +713,74 @@ EE_EXPORT int ee_routed_linear(ee_engine* eng, const void* x, int64_t ld_x, int3
     if ((rc = ee_quant_act(eng, x, M, K, ld_x, EE_QUANT_I8_DISPATCH, ws_codes, K, ws_scale, idx, counts,
                            EE_TIER_INT8, stream)))
         return rc;
-    if ((rc = ee_gemm(eng, EE_GEMM_I8, ws_codes, K, b_i8, K, c, ldc, ws_scale, b_scale, M, N, K, nullptr, idx,
-                      counts, EE_TIER_INT8, nullptr, stream)))
+    if ((rc = gemm_impl(eng, EE_GEMM_I8, ws_codes, K, b_i8, K, c, ldc, ws_scale, b_scale, M, N, K, nullptr, idx,
+                        counts, EE_TIER_INT8, nullptr, sw, stream)))
         return rc;
     // FP8 rows.
     if ((rc = ee_quant_act(eng, x, M, K, ld_x, EE_QUANT_F8_ROW, ws_codes, K, ws_scale, idx, counts, EE_TIER_FP8,
                            stream)))
         return rc;
-    if ((rc = ee_gemm(eng, EE_GEMM_F8, ws_codes, K, b_f8, K, c, ldc, ws_scale, b_scale, M, N, K, nullptr, idx,
-                      counts, EE_TIER_FP8, nullptr, stream)))
+    if ((rc = gemm_impl(eng, EE_GEMM_F8, ws_codes, K, b_f8, K, c, ldc, ws_scale, b_scale, M, N, K, nullptr, idx,
+                        counts, EE_TIER_FP8, nullptr, sw, stream)))
         return rc;
     // FP16 (W8A16) rows: gather straight from x.
-    return ee_gemm(eng, EE_GEMM_F16, x, ld_x, b_f16, K, c, ldc, nullptr, nullptr, M, N, K, idx, idx, counts,
-                   EE_TIER_FP16, nullptr, stream);
+    return gemm_impl(eng, EE_GEMM_F16, x, ld_x, b_f16, K, c, ldc, nullptr, nullptr, M, N, K, idx, idx, counts,
+                     EE_TIER_FP16, nullptr, sw, stream);
+}
+
+EE_EXPORT int ee_routed_linear(ee_engine* eng, const void* x, int64_t ld_x, int32_t M, int32_t K, int32_t N,
+                               const int32_t* idx, const int32_t* counts, const int8_t* b_i8, const uint8_t* b_f8,
+                               const void* b_f16, const float* b_scale, void* c, int64_t ldc, void* ws_codes,
+                               float* ws_scale, ee_stream_t stream) {
+    return routed_impl(eng, x, ld_x, M, K, N, idx, counts, b_i8, b_f8, b_f16, b_scale, c, ldc, ws_codes, ws_scale, 0,
+                       stream);
+}
+
+EE_EXPORT int ee_routed_linear_swiglu(ee_engine* eng, const void* x, int64_t ld_x, int32_t M, int32_t K, int32_t N,
+                                      const int32_t* idx, const int32_t* counts, const int8_t* b_i8,
+                                      const uint8_t* b_f8, const void* b_f16, const float* b_scale, void* act,
+                                      int64_t ld_act, void* ws_codes, float* ws_scale, ee_stream_t stream) {
+    return routed_impl(eng, x, ld_x, M, K, N, idx, counts, b_i8, b_f8, b_f16, b_scale, act, ld_act, ws_codes,
+                       ws_scale, 1, stream);
+}
+
+EE_EXPORT int ee_interleave_gate_up(ee_engine* eng, const void* src, int64_t ld_src_bytes, void* dst,
+                                    int64_t ld_dst_bytes, int64_t F, int64_t row_bytes, ee_stream_t stream) {
+    if (eng == nullptr || src == nullptr || dst == nullptr) return fail(EE_ERR_INVALID_ARG, "NULL argument");
+    if (F < 0 || row_bytes < 0 || ld_src_bytes < row_bytes || ld_dst_bytes < row_bytes)
+        return fail(EE_ERR_INVALID_ARG, "bad shape or stride");
+    if (F % 32 != 0 || row_bytes % 4 != 0 || ld_src_bytes % 4 != 0 || ld_dst_bytes % 4 != 0 || !aligned(src, 4) ||
+        !aligned(dst, 4))
+        return fail(EE_ERR_UNSUPPORTED, "interleave needs F % 32 == 0 and 4-byte aligned rows");
+    if (src == dst) return fail(EE_ERR_INVALID_ARG, "interleave cannot run in place");
+    if (F == 0 || row_bytes == 0) return EE_OK;
+    EeInterleaveArgs a{(const uint8_t*)src, (uint8_t*)dst, F, row_bytes, ld_src_bytes, ld_dst_bytes};
+    const int64_t g = std::min<int64_t>(cdiv(2 * F * (row_bytes / 4), EE_BLOCK), 16384);
+    return launch(eng, "eek_interleave_rows", g, 1, EE_BLOCK, a, stream);
 }
 
 // ------------------------------------------------------------ CubinEngine counterpart
 
 // ============================================================================ fused MLP
 
-EE_EXPORT int ee_silu_mul(ee_engine* eng, const void* gu, int64_t ld_gu, void* act, int64_t ld_act, int64_t M,
-                          int64_t F, ee_stream_t stream) {
+// interleave = 1: gu holds gate and up in alternating blocks of 32 columns (the SwiGLU weight layout).
+static int silu_mul_impl(ee_engine* eng, const void* gu, int64_t ld_gu, void* act, int64_t ld_act, int64_t M,
+                         int64_t F, int32_t interleave, ee_stream_t stream) {
     if (eng == nullptr || gu == nullptr || act == nullptr) return fail(EE_ERR_INVALID_ARG, "NULL argument");
+    if (interleave && F % 32 != 0) return fail(EE_ERR_UNSUPPORTED, "interleaved gate|up needs F % 32 == 0");
     if (M < 0 || F <= 0 || ld_gu < 2 * F || ld_act < F) return fail(EE_ERR_INVALID_ARG, "bad shape or stride");
     if (!aligned(gu, 2) || !aligned(act, 2)) return fail(EE_ERR_INVALID_ARG, "misaligned pointer");
     if (M == 0) return EE_OK;
     const int32_t vec = F % 8 == 0 && ld_gu % 8 == 0 && ld_act % 8 == 0 && aligned(gu, 16) && aligned(act, 16);
-    EeSiluMulArgs a{(const uint16_t*)gu, (uint16_t*)act, M, F, ld_gu, ld_act, vec};
+    EeSiluMulArgs a{(const uint16_t*)gu, (uint16_t*)act, M, F, ld_gu, ld_act, vec, interleave};
     const int64_t work = vec ? M * (F / 8) : M * F;
     const int64_t g = std::min<int64_t>(cdiv(work, EE_BLOCK), 16384);
     return launch(eng, "eek_silu_mul", g, 1, EE_BLOCK, a, stream);
+}
+
+EE_EXPORT int ee_silu_mul(ee_engine* eng, const void* gu, int64_t ld_gu, void* act, int64_t ld_act, int64_t M,
+                          int64_t F, ee_stream_t stream) {
+    return silu_mul_impl(eng, gu, ld_gu, act, ld_act, M, F, 0, stream);
 }
 
 EE_EXPORT int ee_add_rmsnorm(ee_engine* eng, const void* x, int64_t ld_x, const void* y, int64_t ld_y,
@@ -767,11 +833,19 @@ EE_EXPORT int ee_mlp_prepare(ee_engine* eng, const void* gate_w, const void* up_
         return fail(EE_ERR_INVALID_ARG, "NULL argument");
     if (H <= 0 || F <= 0 || ld_gate < H || ld_up < H || ld_down < F)
         return fail(EE_ERR_INVALID_ARG, "bad shape or stride");
+    if (F % 32 != 0 || H % 4 != 0) return fail(EE_ERR_UNSUPPORTED, "the MLP engine needs F % 32 == 0, H % 4 == 0");
     int rc;
-    // gate|up: one [2F, H] operand (gate rows, then up rows); per-row scales are per output channel,
-    // so quantising the halves separately equals quantising the concatenation.
-    if ((rc = ee_quant_weight_i8(eng, gate_w, F, H, ld_gate, gu_i8, H, gu_scale, stream))) return rc;
-    if ((rc = ee_quant_weight_i8(eng, up_w, F, H, ld_up, gu_i8 + F * H, H, gu_scale + F, stream))) return rc;
+    // gate|up: one [2F, H] operand, gate and up rows interleaved in blocks of 32 (the SwiGLU
+    // epilogue's pairing).  Per-row scales are per output channel, so quantising the halves
+    // separately and permuting rows equals quantising the permuted operand.  The FP8 and
+    // W8A16 buffers hold the unpermuted codes and scales until they are packed.
+    uint8_t* codes_tmp = gu_f8;
+    float* scale_tmp = (float*)gu_f16;
+    if ((rc = ee_quant_weight_i8(eng, gate_w, F, H, ld_gate, (int8_t*)codes_tmp, H, scale_tmp, stream))) return rc;
+    if ((rc = ee_quant_weight_i8(eng, up_w, F, H, ld_up, (int8_t*)codes_tmp + F * H, H, scale_tmp + F, stream)))
+        return rc;
+    if ((rc = ee_interleave_gate_up(eng, codes_tmp, H, gu_i8, H, F, H, stream))) return rc;
+    if ((rc = ee_interleave_gate_up(eng, scale_tmp, 4, gu_scale, 4, F, 4, stream))) return rc;
     if ((rc = ee_pack_b_f8(eng, gu_i8, 2 * F, H, H, gu_f8, H, stream))) return rc;
     if ((rc = ee_pack_b_f16(eng, gu_i8, gu_scale, 2 * F, H, H, gu_f16, H, stream))) return rc;
     if ((rc = ee_quant_weight_i8(eng, down_w, H, F, ld_down, dn_i8, F, dn_scale, stream))) return rc;
@@ -820,8 +894,8 @@ EE_EXPORT int ee_mlp_forward(ee_engine* eng, const void* x, int64_t ld_x, int64_
         return fail(EE_ERR_INVALID_ARG, "NULL argument");
     if (M < 0 || M > 0x7fffffff || H <= 0 || F <= 0 || ld_x < H || ldo < H)
         return fail(EE_ERR_INVALID_ARG, "bad shape or stride");
-    if (H % 16 != 0 || F % 16 != 0 || ld_x % 8 != 0 || ldo % 4 != 0)
-        return fail(EE_ERR_UNSUPPORTED, "fused MLP needs H % 16 == 0, F % 16 == 0, ld_x % 8 == 0, ldo % 4 == 0");
+    if (H % 16 != 0 || F % 32 != 0 || ld_x % 8 != 0 || ldo % 4 != 0)
+        return fail(EE_ERR_UNSUPPORTED, "fused MLP needs H % 16 == 0, F % 32 == 0, ld_x % 8 == 0, ldo % 4 == 0");
     if (!aligned(x, 16) || !aligned(out, 8) || !aligned(workspace, 256))
         return fail(EE_ERR_INVALID_ARG, "misaligned pointer (x 16 B, out 8 B, workspace 256 B)");
     const MlpWs w = mlp_ws(workspace, M, H, F, h_rows != nullptr);
@@ -833,20 +907,27 @@ EE_EXPORT int ee_mlp_forward(ee_engine* eng, const void* x, int64_t ld_x, int64_
     if (h_rows != nullptr) {
         // one tier per row: route, gate|up routed linear, activation, down routed linear
         if ((rc = ee_route(eng, h_rows, M, tau_low, tau_high, w.tier, w.idx, w.counts, stream))) return rc;
-        if ((rc = ee_routed_linear(eng, x, ld_x, m, h, 2 * f, w.idx, w.counts, gu_i8, gu_f8, gu_f16, gu_scale, w.gu,
-                                   2 * F, w.codes, w.scale, stream)))
-            return rc;
-        if ((rc = ee_silu_mul(eng, w.gu, 2 * F, w.act, F, M, F, stream))) return rc;
+        if (H % 128 == 0) {                           // gate|up GEMMs write silu(gate) * up directly
+            if ((rc = routed_impl(eng, x, ld_x, m, h, 2 * f, w.idx, w.counts, gu_i8, gu_f8, gu_f16, gu_scale, w.act,
+                                  F, w.codes, w.scale, 1, stream)))
+                return rc;
+        } else {
+            if ((rc = ee_routed_linear(eng, x, ld_x, m, h, 2 * f, w.idx, w.counts, gu_i8, gu_f8, gu_f16, gu_scale,
+                                       w.gu, 2 * F, w.codes, w.scale, stream)))
+                return rc;
+            if ((rc = silu_mul_impl(eng, w.gu, 2 * F, w.act, F, M, F, 1, stream))) return rc;
+        }
         return ee_routed_linear(eng, w.act, F, m, f, h, w.idx, w.counts, dn_i8, dn_f8, dn_f16, dn_scale, out, ldo,
                                 w.codes, w.scale, stream);
     }
     // one tier for the call, by the dispatcher's strict comparisons (EE/python/dispatch.py:74-79)
     const int tier = entropy < tau_low ? EE_TIER_INT8 : (entropy < tau_high ? EE_TIER_FP8 : EE_TIER_FP16);
     if (tier == EE_TIER_FP16) {
-        if ((rc = ee_gemm(eng, EE_GEMM_F16, x, ld_x, gu_f16, H, w.gu, 2 * F, nullptr, nullptr, m, 2 * f, h, nullptr,
-                          nullptr, nullptr, 0, nullptr, stream)))
+        const int sw = H % 64 == 0;                   // the pipelined W8A16 kernels: K * 2 % 128 == 0
+        if ((rc = gemm_impl(eng, EE_GEMM_F16, x, ld_x, gu_f16, H, sw ? (void*)w.act : (void*)w.gu, sw ? F : 2 * F,
+                            nullptr, nullptr, m, 2 * f, h, nullptr, nullptr, nullptr, 0, nullptr, sw, stream)))
             return rc;
-        if ((rc = ee_silu_mul(eng, w.gu, 2 * F, w.act, F, M, F, stream))) return rc;
+        if (!sw && (rc = silu_mul_impl(eng, w.gu, 2 * F, w.act, F, M, F, 1, stream))) return rc;
         return ee_gemm(eng, EE_GEMM_F16, w.act, F, dn_f16, F, out, ldo, nullptr, nullptr, m, h, f, nullptr, nullptr,
                        nullptr, 0, nullptr, stream);
     }
@@ -855,10 +936,11 @@ EE_EXPORT int ee_mlp_forward(ee_engine* eng, const void* x, int64_t ld_x, int64_
     const void* bgu = tier == EE_TIER_INT8 ? (const void*)gu_i8 : (const void*)gu_f8;
     const void* bdn = tier == EE_TIER_INT8 ? (const void*)dn_i8 : (const void*)dn_f8;
     if ((rc = ee_quant_act(eng, x, M, H, ld_x, qmode, w.codes, H, w.scale, nullptr, nullptr, 0, stream))) return rc;
-    if ((rc = ee_gemm(eng, kind, w.codes, H, bgu, H, w.gu, 2 * F, w.scale, gu_scale, m, 2 * f, h, nullptr, nullptr,
-                      nullptr, 0, nullptr, stream)))
+    const int sw = H % 128 == 0;                      // the pipelined 1-byte kernels: K % 128 == 0
+    if ((rc = gemm_impl(eng, kind, w.codes, H, bgu, H, sw ? (void*)w.act : (void*)w.gu, sw ? F : 2 * F, w.scale,
+                        gu_scale, m, 2 * f, h, nullptr, nullptr, nullptr, 0, nullptr, sw, stream)))
         return rc;
-    if ((rc = ee_silu_mul(eng, w.gu, 2 * F, w.act, F, M, F, stream))) return rc;
+    if (!sw && (rc = silu_mul_impl(eng, w.gu, 2 * F, w.act, F, M, F, 1, stream))) return rc;
     if ((rc = ee_quant_act(eng, w.act, M, F, F, qmode, w.codes, F, w.scale, nullptr, nullptr, 0, stream))) return rc;
     return ee_gemm(eng, kind, w.codes, F, bdn, F, out, ldo, w.scale, dn_scale, m, h, f, nullptr, nullptr, nullptr, 0,
                    nullptr, stream);

@@ -392,13 +392,17 @@ class EntropyGatedLlama:
             self.fused[(l, "down")] = params[f"{l}.down"]
         self.fused["lm_head"] = params["lm_head"]
         for key, w in self.fused.items():
-            self.packed[key] = self._pack(w)
+            self.packed[key] = self._pack(w, swiglu=isinstance(key, tuple) and key[1] == "gu")
         self.last_fractions = None
         self._rope_cache = {}
 
     @staticmethod
-    def _pack(w: torch.Tensor) -> K.PackedWeight:
+    def _pack(w: torch.Tensor, swiglu: bool = False) -> K.PackedWeight:
+        """Tier operands of w [N, K]; swiglu: w is gate rows then up rows, packed
+        interleaved in blocks of 32 for the SwiGLU epilogue (act = silu(gate) * up)."""
         codes, scale = K.quantize_weight_codes(w)
+        if swiglu:
+            codes, scale = K.interleave_gate_up(codes), K.interleave_gate_up(scale)
         return K.PackedWeight(codes, scale).materialize()
 
     @classmethod
@@ -432,14 +436,17 @@ class EntropyGatedLlama:
             self._rope_cache[key] = (emb.cos().half().unsqueeze(0), emb.sin().half().unsqueeze(0))
         return self._rope_cache[key]
 
-    def _linear(self, x2d: torch.Tensor, key, route, gated: bool) -> torch.Tensor:
+    def _linear(self, x2d: torch.Tensor, key, route, gated: bool, swiglu: bool = False) -> torch.Tensor:
+        """x2d @ W^T; swiglu: W is gate|up and the result is silu(gate) * up (fused
+        into the GEMM epilogue on the gated path; a separate pass on the fp16 run)."""
         if not gated:
-            return torch.matmul(x2d, self.fused[key].t())
+            y = torch.matmul(x2d, self.fused[key].t())
+            return K.silu_mul(y) if swiglu else y
         pw = self.packed[key]
         if route is None:                    # no entropy yet: FP16 tier (W8A16), as the reference's default
-            return K.gemm("fp16", x2d, pw.f16)
+            return K.gemm("fp16", x2d, pw.f16, swiglu=swiglu)
         idx, counts = route
-        return K.routed_linear(x2d, pw, idx, counts)
+        return K.routed_linear(x2d, pw, idx, counts, swiglu=swiglu)
 
     def _route(self, h_tok: torch.Tensor, counts_log: list):
         _, idx, counts = K.route(h_tok, self.tau_low, self.tau_high)
@@ -472,8 +479,7 @@ class EntropyGatedLlama:
             route_cur = self._route(H.mean(dim=1).reshape(T).contiguous(), counts_log) if gated else None
             o = self._linear(att, (l, "o"), route_cur, gated)
             x, xn = K.add_rmsnorm(x, self.p[f"{l}.ln2"], eps, o)
-            gu = self._linear(xn, (l, "gu"), route_cur, gated)
-            act = K.silu_mul(gu)
+            act = self._linear(xn, (l, "gu"), route_cur, gated, swiglu=True)
             res = self._linear(act, (l, "down"), route_cur, gated)
             route_prev = route_cur
         x, xn = K.add_rmsnorm(x, self.p["norm"], eps, res)

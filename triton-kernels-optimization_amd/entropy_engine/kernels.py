@@ -30,6 +30,7 @@ __all__ = [
     "triton_int8_gemm", "triton_fp8_gemm", "triton_fp16_gemm", "fused_softmax_entropy",
     "softmax_entropy", "quantize_activations", "gemm", "route", "row_copy", "routed_linear",
     "prepare_weight", "PackedWeight", "quantize_weight_codes", "silu_mul", "add_rmsnorm", "qkv_rope",
+    "interleave_gate_up",
 ]
 
 
@@ -254,8 +255,11 @@ _KINDS = {"int8": _lib.EE_GEMM_I8, "fp8": _lib.EE_GEMM_F8, "fp16": _lib.EE_GEMM_
 
 
 def gemm(kind: str, a: torch.Tensor, b_nk: torch.Tensor, a_scale=None, b_scale=None, out=None, *,
-         M: int | None = None, a_idx=None, c_idx=None, counts=None, tier: int = 0, acc_out=None) -> torch.Tensor:
-    """C = A @ B^T on the tier's MFMA kernel; A [M, K], B [N, K] (operand order)."""
+         M: int | None = None, a_idx=None, c_idx=None, counts=None, tier: int = 0, acc_out=None,
+         swiglu: bool = False) -> torch.Tensor:
+    """C = A @ B^T on the tier's MFMA kernel; A [M, K], B [N, K] (operand order).
+    swiglu: B is a gate|up operand interleaved in blocks of 32 rows (interleave_gate_up)
+    and the result is act [M, N/2] = fp16(fp16(silu(gate)) * up)."""
     dev = _require_cuda(a, b_nk, a_scale, b_scale, out, a_idx, c_idx, counts, acc_out)
     lda = _rowmajor(a, "a")
     ldb = _rowmajor(b_nk, "b")
@@ -264,11 +268,18 @@ def gemm(kind: str, a: torch.Tensor, b_nk: torch.Tensor, a_scale=None, b_scale=N
         M = a.shape[0] if a_idx is None else a_idx.numel()
     if a.shape[1] != K:
         raise ValueError(f"K mismatch: a is {tuple(a.shape)}, b is [{N}, {K}] in operand order")
-    c = out if out is not None else torch.empty((M, N), dtype=torch.float16, device=dev)
+    c = out if out is not None else torch.empty((M, N // 2 if swiglu else N), dtype=torch.float16, device=dev)
     with torch.cuda.device(dev):
-        check(_lib.lib().ee_gemm(engine(), _KINDS[kind], ptr(a), lda, ptr(b_nk), ldb, ptr(c), _rowmajor(c, "c"),
-                                 ptr(a_scale), ptr(b_scale), M, N, K, ptr(a_idx), ptr(c_idx), ptr(counts), int(tier),
-                                 ptr(acc_out), stream_handle()))
+        if swiglu:
+            if acc_out is not None:
+                raise ValueError("acc_out is not available with swiglu")
+            check(_lib.lib().ee_gemm_swiglu(engine(), _KINDS[kind], ptr(a), lda, ptr(b_nk), ldb, ptr(c),
+                                            _rowmajor(c, "act"), ptr(a_scale), ptr(b_scale), M, N, K, ptr(a_idx),
+                                            ptr(c_idx), ptr(counts), int(tier), stream_handle()))
+        else:
+            check(_lib.lib().ee_gemm(engine(), _KINDS[kind], ptr(a), lda, ptr(b_nk), ldb, ptr(c), _rowmajor(c, "c"),
+                                     ptr(a_scale), ptr(b_scale), M, N, K, ptr(a_idx), ptr(c_idx), ptr(counts),
+                                     int(tier), ptr(acc_out), stream_handle()))
     return c
 
 
@@ -351,9 +362,10 @@ def row_copy(src: torch.Tensor, idx: torch.Tensor, counts=None, tier: int = 0, s
 
 
 def routed_linear(x: torch.Tensor, pw: PackedWeight, idx: torch.Tensor, counts: torch.Tensor,
-                  out: torch.Tensor | None = None, workspace=None) -> torch.Tensor:
+                  out: torch.Tensor | None = None, workspace=None, swiglu: bool = False) -> torch.Tensor:
     """One tier per row: INT8 / FP8 / W8A16 GEMMs over the rows `idx`/`counts`
-    assign them (from `route`), scattered back in place; no host sync."""
+    assign them (from `route`), scattered back in place; no host sync.
+    swiglu: pw is an interleaved gate|up weight; the result is act [M, N/2]."""
     dev = _require_cuda(x, idx, counts, out)
     if x.dtype != torch.float16:
         raise TypeError("x must be float16")
@@ -361,15 +373,31 @@ def routed_linear(x: torch.Tensor, pw: PackedWeight, idx: torch.Tensor, counts: 
     if K != pw.K:
         raise ValueError(f"K mismatch: x is {tuple(x.shape)}, weight is [{pw.N}, {pw.K}]")
     N = pw.N
-    c = out if out is not None else torch.empty((M, N), dtype=torch.float16, device=dev)
+    c = out if out is not None else torch.empty((M, N // 2 if swiglu else N), dtype=torch.float16, device=dev)
     if workspace is None:
         workspace = (torch.empty((M, K), dtype=torch.uint8, device=dev), torch.empty(M, dtype=torch.float32, device=dev))
     ws_codes, ws_scale = workspace
+    fn = _lib.lib().ee_routed_linear_swiglu if swiglu else _lib.lib().ee_routed_linear
     with torch.cuda.device(dev):
-        check(_lib.lib().ee_routed_linear(engine(), ptr(x), _rowmajor(x, "x"), M, K, N, ptr(idx), ptr(counts),
-                                          ptr(pw.i8), ptr(pw.f8), ptr(pw.f16), ptr(pw.scale), ptr(c),
-                                          _rowmajor(c, "out"), ptr(ws_codes), ptr(ws_scale), stream_handle()))
+        check(fn(engine(), ptr(x), _rowmajor(x, "x"), M, K, N, ptr(idx), ptr(counts), ptr(pw.i8), ptr(pw.f8),
+                 ptr(pw.f16), ptr(pw.scale), ptr(c), _rowmajor(c, "out"), ptr(ws_codes), ptr(ws_scale),
+                 stream_handle()))
     return c
+
+
+def interleave_gate_up(t: torch.Tensor) -> torch.Tensor:
+    """Rows 0..F-1 (gate) and F..2F-1 (up) of t [2F, ...] interleaved in blocks of 32
+    rows (the SwiGLU operand layout): rows 64k..64k+31 = gate 32k.., 64k+32.. = up 32k..."""
+    dev = _require_cuda(t)
+    t = t.contiguous()
+    if t.shape[0] % 64:
+        raise ValueError("gate|up needs 2F rows with F % 32 == 0")
+    rb = t[0].numel() * t.element_size() if t.dim() > 1 else t.element_size()
+    out = torch.empty_like(t)
+    with torch.cuda.device(dev):
+        check(_lib.lib().ee_interleave_gate_up(engine(), ptr(t), rb, ptr(out), rb, t.shape[0] // 2, rb,
+                                               stream_handle()))
+    return out
 
 
 # ---------------------------------------------------------------- MLP activation
