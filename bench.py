@@ -269,6 +269,37 @@ def main():
             src = torch.empty(COPY_BYTES // 4, dtype=torch.float32, device=dev).fill_(1.0)
             dst = torch.empty_like(src)
             run("hbm_copy", lambda: torch.neg(src, out=dst))
+        # ---- configs 1 and 2: the tier GEMMs at M = 4096 (several tiles per CU: the persistent
+        # kernels) -- config 1 [4096, 4096, 4096] with FP8 per-tensor scaling and 0.1% outliers of
+        # magnitude 20 in A; config 2 [4096, 4096, 14336]; the FP16 baseline is torch.matmul (hipBLASLt)
+        big = {}
+        big_names = ("c1_int8", "c1_fp8_tensor", "c1_fp16_torch", "c2_int8", "c2_fp8", "c2_fp16_torch")
+        if not only or any(n in only for n in big_names):
+            for cfg, (Mb, Kb, Nb) in (("c1", (4096, 4096, 4096)), ("c2", (4096, 4096, 14336))):
+                if only and not any(n.startswith(cfg) for n in only):
+                    continue
+                gb = torch.Generator().manual_seed(11 if cfg == "c1" else 12)
+                Ab = torch.randn(Mb, Kb, generator=gb)
+                if cfg == "c1":
+                    hit = torch.rand(Mb, Kb, generator=gb) < 1e-3
+                    Ab = torch.where(hit, 20.0 * torch.sign(torch.randn(Mb, Kb, generator=gb)), Ab)
+                ab = Ab.half().to(dev)
+                Wb = (torch.randn(Nb, Kb, generator=gb) * 0.02).half().to(dev)
+                Bb, bsb = ee.quantize_weights_int8(Wb)
+                pwb = ee.prepare_weight(Bb, bsb).materialize()
+                ai_b, si_b = ee.quantize_activations(ab, "dispatcher")
+                cb = torch.empty((Mb, Nb), dtype=torch.float16, device=dev)
+                run(f"{cfg}_int8", lambda: ee.gemm("int8", ai_b, pwb.i8, si_b, pwb.scale, out=cb), primary="eager")
+                if cfg == "c1":
+                    ca, sa = ee.quantize_tensor_fp8(ab)
+                    cw, sw = ee.quantize_tensor_fp8(Wb)
+                    run("c1_fp8_tensor", lambda: ee.gemm("fp8", ca, cw, sa, sw, out=cb), primary="eager")
+                else:
+                    af_b, sf_b = ee.quantize_activations(ab, "fp8")
+                    run("c2_fp8", lambda: ee.gemm("fp8", af_b, pwb.f8, sf_b, pwb.scale, out=cb), primary="eager")
+                run(f"{cfg}_fp16_torch", lambda: torch.matmul(ab, Wb.t(), out=cb), primary="eager")
+                big[cfg] = 2.0 * Mb * Nb * Kb
+                del ab, Wb, Bb, pwb, ai_b, cb
         # ---- config 3: the dispatcher end to end on a mixed batch (M = K = N = 4096)
         c3 = None
         c3_names = ("c3_entropy", "c3_route", "c3_linear", "c3_end_to_end")
@@ -395,6 +426,16 @@ def main():
             "routing_fractions_int8_fp8_fp16": c3["routing_fractions"],
             "shape": "M=K=N=4096; entropy over fp16 [4096,4096] mixture logits",
         }
+    for cfg, ops_b in big.items():
+        legs = ("int8", "fp8_tensor", "fp16_torch") if cfg == "c1" else ("int8", "fp8", "fp16_torch")
+        peak = {"int8": PEAK_I8_TOPS, "fp8_tensor": PEAK_F8_TFLOPS, "fp8": PEAK_F8_TFLOPS, "fp16_torch": PEAK_F16_TFLOPS}
+        kernels[f"gemm_{cfg}"] = {
+            leg: {"us": results[f"{cfg}_{leg}"]["ms"] * 1e3,
+                  "TOPS": ops_b / (results[f"{cfg}_{leg}"]["ms"] * 1e-3) / 1e12,
+                  "frac_of_peak": ops_b / (results[f"{cfg}_{leg}"]["ms"] * 1e-3) / 1e12 / peak[leg]}
+            for leg in legs}
+        kernels[f"gemm_{cfg}"]["shape"] = ("M, K, N = 4096, 4096, 4096; A with 0.1% outliers of 20; FP8 per-tensor scales"
+                                           if cfg == "c1" else "M, K, N = 4096, 4096, 14336")
     if mlp is not None:
         kernels["mlp_engine"] = {
             f"us_{k}": results[f"mlp_{k}"]["ms"] * 1e3 for k in ("int8", "fp8", "fp16", "routed", "torch_fp16")}
