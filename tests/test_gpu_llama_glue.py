@@ -112,3 +112,50 @@ def test_gqa_attention_without_head_copies(ee):
     assert (out.float() - ref).abs().max().item() <= 2e-2 * ref.abs().max().item()
     h_ref = -(p * torch.log(p.clamp_min(1e-30))).sum(-1)
     assert torch.allclose(H, h_ref, rtol=2e-3, atol=2e-3)
+
+
+def test_gated_llama_forward_replays_as_a_hip_graph(ee):
+    """The gated forward (routing on the device, no host syncs) captured once as a
+    HIP graph: every replay, with eager work and synchronisations between the
+    replays, gives the eager forward's logits bit for bit; so does the MLP engine."""
+    SMALL = dict(layers=2, hidden=256, heads=4, kv_heads=2, head_dim=64, ffn=512, vocab=1000,
+                 rope_theta=10000.0, eps=1e-5)
+    m = ee.EntropyGatedLlama.random_init(SMALL, seed=5, tau_low=2.34, tau_high=6.03)
+    g = torch.Generator(device="cuda").manual_seed(6)
+    ids = torch.randint(0, SMALL["vocab"], (2, 64), generator=g, device="cuda")
+    for gated in (True, False):
+        eager = m.forward(ids, gated=gated).clone()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            m.forward(ids, gated=gated)               # warm the caches outside the capture
+        torch.cuda.current_stream().wait_stream(s)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            out = m.forward(ids, gated=gated)
+        for _ in range(3):
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(out, eager)
+            m.forward(ids, gated=not gated)           # eager work between the replays
+            torch.cuda.synchronize()
+    rng = np.random.default_rng(8)
+    H, F, M = 256, 320, 96
+    w = [cuda((rng.standard_normal(sh) / np.sqrt(sh[1])).astype(np.float16)) for sh in ((F, H), (F, H), (H, F))]
+    eng = ee.EntropyMLPEngine(*w, 1.5, 2.5)
+    x = cuda(rng.standard_normal((M, H)).astype(np.float16))
+    h = cuda(rng.choice(np.float32([1.0, 2.0, 3.0]), M))
+    ref = [eng.forward(x, 1.0).clone(), eng.forward(x, h).clone()]
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        outs = [eng.forward(x, 1.0), eng.forward(x, h)]
+    for _ in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert all(torch.equal(a, b) for a, b in zip(outs, ref))
+        eng.forward(x, 3.0)
+        torch.cuda.synchronize()
+
+
+def cuda(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()

@@ -490,5 +490,6 @@ class EntropyGatedLlama:
             # on the FP16 tier
             weights = [4 + (3 if i + 1 < len(counts_log) else 1) for i in range(len(counts_log))]
             total = sum(cnt.to(torch.int64) * w for cnt, w in zip(counts_log, weights))
-            self.last_fractions = total + torch.tensor([0, 0, 3 * T], device=total.device, dtype=torch.int64)
+            total[2] += 3 * T                         # a device op: the forward stays capturable as a HIP graph
+            self.last_fractions = total
         return logits.view(B, S, -1)
