@@ -323,3 +323,62 @@ def test_interleave_gate_up_layout(ee):
     assert torch.equal(ee.interleave_gate_up(s), interleave_rows(s))
     with pytest.raises(ValueError):
         ee.interleave_gate_up(torch.zeros(2 * 48, 4, device="cuda"))
+
+
+def test_new_entry_points_reject_bad_arguments(ee):
+    """Argument contracts of the SwiGLU, interleave, RMSNorm, RoPE and MLP entry
+    points: rejected on the host with a status, nothing launched; empty inputs
+    are no-ops."""
+    from entropy_engine import _lib
+    L, e = _lib.lib(), _lib.engine()
+    dev = torch.device("cuda")
+    z16 = lambda *sh: torch.zeros(*sh, dtype=torch.float16, device=dev)
+    a = torch.zeros(128, 256, dtype=torch.int8, device=dev)
+    b = torch.zeros(96, 256, dtype=torch.int8, device=dev)          # N = 96: not a multiple of 64
+    s = torch.ones(128, device=dev)
+    bs = torch.ones(96, device=dev)
+    act = z16(128, 48)
+    rc = L.ee_gemm_swiglu(e, 0, a.data_ptr(), 256, b.data_ptr(), 256, act.data_ptr(), 48, s.data_ptr(),
+                          bs.data_ptr(), 128, 96, 256, None, None, None, 0, None)
+    assert rc == _lib.EE_ERR_UNSUPPORTED and "N % 64" in L.ee_last_error().decode()
+    b2 = torch.zeros(128, 200, dtype=torch.int8, device=dev)        # K = 200: not a pipelined K
+    rc = L.ee_gemm_swiglu(e, 0, a.data_ptr(), 256, b2.data_ptr(), 200, act.data_ptr(), 64, s.data_ptr(),
+                          bs.data_ptr(), 128, 128, 200, None, None, None, 0, None)
+    assert rc == _lib.EE_ERR_UNSUPPORTED
+    with pytest.raises(ValueError):
+        ee.gemm("int8", a, torch.zeros(128, 256, dtype=torch.int8, device=dev), s, torch.ones(128, device=dev),
+                swiglu=True, acc_out=torch.zeros(128, 128, dtype=torch.int32, device=dev))
+    # M = 0: nothing to do
+    assert L.ee_gemm_swiglu(e, 0, a.data_ptr(), 256, a.data_ptr(), 256, act.data_ptr(), 64, s.data_ptr(),
+                            s.data_ptr(), 0, 128, 256, None, None, None, 0, None) == 0
+    # interleave: F % 32, in place
+    t = torch.zeros(2 * 48, 16, dtype=torch.int8, device=dev)
+    assert L.ee_interleave_gate_up(e, t.data_ptr(), 16, t.clone().data_ptr(), 16, 48, 16, None) == _lib.EE_ERR_UNSUPPORTED
+    t = torch.zeros(2 * 64, 16, dtype=torch.int8, device=dev)
+    assert L.ee_interleave_gate_up(e, t.data_ptr(), 16, t.data_ptr(), 16, 64, 16, None) == _lib.EE_ERR_INVALID_ARG
+    # routed SwiGLU needs K % 128 == 0
+    x = z16(8, 96)
+    idx = torch.arange(8, dtype=torch.int32, device=dev)
+    cnt = torch.tensor([8, 0, 0], dtype=torch.int32, device=dev)
+    w8 = torch.zeros(128, 96, dtype=torch.int8, device=dev)
+    rc = L.ee_routed_linear_swiglu(e, x.data_ptr(), 96, 8, 96, 128, idx.data_ptr(), cnt.data_ptr(), w8.data_ptr(),
+                                   w8.data_ptr(), z16(128, 96).data_ptr(), torch.ones(128, device=dev).data_ptr(),
+                                   z16(8, 64).data_ptr(), 64, torch.zeros(8, 96, dtype=torch.uint8, device=dev).data_ptr(),
+                                   torch.zeros(8, device=dev).data_ptr(), None)
+    assert rc == _lib.EE_ERR_UNSUPPORTED
+    # RMSNorm: D % 8, D <= 4096; T = 0 is a no-op
+    w = torch.ones(4104, dtype=torch.float16, device=dev)
+    xx = z16(2, 4104)
+    assert L.ee_add_rmsnorm(e, xx.data_ptr(), 4104, None, 4104, w.data_ptr(), None, 4104, xx.clone().data_ptr(),
+                            4104, 2, 4104, 1e-5, None) == _lib.EE_ERR_UNSUPPORTED
+    assert L.ee_add_rmsnorm(e, xx.data_ptr(), 4104, None, 4104, w.data_ptr(), None, 4104, xx.clone().data_ptr(),
+                            4104, 0, 4096, 1e-5, None) == 0
+    # RoPE: d % 16
+    q = z16(4, 8 * 24)
+    assert L.ee_qkv_rope(e, q.data_ptr(), 8 * 24 // 1, q.data_ptr(), q.data_ptr(), q.data_ptr(), q.data_ptr(),
+                         q.data_ptr(), 1, 4, 4, 2, 24, 1.0, None) == _lib.EE_ERR_UNSUPPORTED
+    # the MLP engine: intermediate size a multiple of 32
+    with pytest.raises(RuntimeError):
+        ee.EntropyMLPEngine(z16(48, 128), z16(48, 128), z16(128, 48), 1.5, 2.5)
+    eng = ee.EntropyMLPEngine(z16(64, 128), z16(64, 128), z16(128, 64), 1.5, 2.5)
+    assert eng.forward(z16(0, 128), 1.0).shape == (0, 128)

@@ -142,8 +142,9 @@ class EntropyMLPEngine:
         if tuple(up_w.shape) != (F, H) or tuple(down_w.shape) != (H, F):
             raise RuntimeError(f"shape mismatch: gate {tuple(gate_w.shape)}, up {tuple(up_w.shape)}, "
                                f"down {tuple(down_w.shape)}; expected [I, H], [I, H], [H, I]")
-        if H % 16 or F % 16:
-            raise RuntimeError("hidden and intermediate sizes must be multiples of 16")
+        if H % 16 or F % 32:
+            raise RuntimeError("the hidden size must be a multiple of 16 and the intermediate size of 32 "
+                               "(gate|up rows are interleaved in blocks of 32)")
         self.device = gate_w.device
         self.H, self.F = H, F
         self.tau_low, self.tau_high = float(tau_low), float(tau_high)
@@ -177,6 +178,8 @@ class EntropyMLPEngine:
         if x.stride(-1) != 1 or (x.shape[0] > 1 and x.stride(0) != self.H) or x.data_ptr() % 16:
             x = x.contiguous()
         M = x.shape[0]
+        if M == 0:
+            return torch.empty((*hidden.shape[:-1], self.H), dtype=torch.float16, device=self.device)
         h_rows = None
         if isinstance(entropy, torch.Tensor) and entropy.numel() > 1:
             if entropy.numel() != M:
