@@ -523,10 +523,10 @@ def main():
                    "M": M, "K": K, "N": N, "entropy_rows": ER, "entropy_cols": ES},
         "roofline": {"bound": "mfma", "achieved": round(i8_launch_tops, 2), "peak": PEAK_I8_TOPS, "unit": "TFLOP/s",
                      "frac": round(i8_launch_tops / PEAK_I8_TOPS, 4), "traffic": traffic,
-                     "kernel": "eek_gemm_i8 (1024x4096x4096)", "us_per_launch": round(i8_roof_ms * 1e3, 3)},
+                     "kernel": "eek_gemm_i8_w8 (8-wave INT8 pipeline, 1024x4096x4096)", "us_per_launch": round(i8_roof_ms * 1e3, 3)},
         "roofline_entropy": {"bound": "hbm", "achieved": round(ent_launch_gbs, 1), "peak": PEAK_HBM_GBS,
                              "unit": "GB/s", "frac": round(ent_launch_gbs / PEAK_HBM_GBS, 4), "traffic": ent_traffic,
-                             "kernel": "eek_softmax_entropy (cold, [1024,4096])", "us_per_launch": round(ent_roof_ms * 1e3, 3)},
+                             "kernel": "eek_softmax_entropy_v4_w2 (cold, [1024,4096])", "us_per_launch": round(ent_roof_ms * 1e3, 3)},
         "kernels": kernels,
         "cpu_baseline": cpu,
     }

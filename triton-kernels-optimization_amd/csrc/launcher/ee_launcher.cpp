@@ -270,9 +270,11 @@ bool pick_se_cfg(int64_t len, int64_t rows, int64_t forced_wpr, int& vpt, int& w
         const int v = (int)std::max<int64_t>(1, cdiv(len, 512LL * w));
         if (v > 4 && !(w == 8 && v <= 8)) continue;
         const int64_t pad = (int64_t)v * w * 512 - len;
-        const bool fills = rows * w >= 4096;
+        // 2048 waves (8 per CU) keep HBM busy; fewer, fuller waves shorten each row's
+        // reduction chain: at [1024, 4096], 2 waves x 4 vectors beat 4 x 2 by 5% (cold)
+        const bool fills = rows * w >= 2048;
         if (best_w < 0) { best_w = w; best_v = v; best_pad = pad; continue; }
-        const bool best_fills = rows * best_w >= 4096;
+        const bool best_fills = rows * best_w >= 2048;
         // prefer filling the chip, then least padding, then fewer waves per row
         if ((fills && !best_fills) || (fills == best_fills && pad < best_pad)) {
             best_w = w; best_v = v; best_pad = pad;
