@@ -62,7 +62,9 @@ enum {
 enum {
     EE_GEMM_I8 = 0,  /* EE/python/kernels.py:50-110  int8 x int8 -> int32 -> fp16 */
     EE_GEMM_F8 = 1,  /* EE/python/kernels.py:118-180 e4m3 x e4m3 -> f32 -> fp16   */
-    EE_GEMM_F16 = 2  /* EE/python/kernels.py:192-246 fp16 x fp16 (W8A16) -> fp16  */
+    EE_GEMM_F16 = 2, /* EE/python/kernels.py:192-246 fp16 x fp16 (W8A16 weights pre-dequantised) -> fp16 */
+    EE_GEMM_W8A16 = 3 /* the same tier from int8 codes + f32 scales, dequantised in the kernel as
+                         kernels.py:215,233 do in SRAM: w = fp16(fp16(b) * fp16(scale[n])) */
 };
 
 const char* ee_last_error(void);

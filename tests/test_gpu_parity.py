@@ -437,6 +437,23 @@ def test_w8a16_gemm(ee, orc, M, K, N, gemm_variant):
     check_close_f64(host(out), orc.gemm_w8a16_f64(A, B, bs))
 
 
+@pytest.mark.parametrize("M,K,N", [(256, 1024, 512), (77, 2048, 132), (1024, 4096, 4096), (130, 320, 64), (1, 64, 4),
+                                   (300, 5632, 2048)])
+def test_w8a16_int8_weights(ee, orc, M, K, N):
+    """The W8A16 tier from int8 codes + scales, dequantised in the kernel
+    (fp16(fp16(b) * fp16(s)), EE/python/kernels.py:215,233): within 1e-2 of the
+    float64 recompute, and within fp16 rounding of the pre-dequantised fp16 kernel
+    (same weights, another f32 summation order)."""
+    rng = np.random.default_rng(M + 3 * K + N)
+    A = rng.standard_normal((M, K)).astype(np.float16)
+    B, bs = weights(orc, rng, N, K)
+    pw = ee.prepare_weight(cuda(B), cuda(bs)).materialize()
+    out = ee.gemm("w8a16", cuda(A), pw.i8, None, pw.scale)
+    check_close_f64(host(out), orc.triton_fp16_gemm_f64(A, B, bs))
+    ref16 = host(ee.gemm("fp16", cuda(A), pw.f16)).astype(np.float64)
+    assert np.abs(host(out).astype(np.float64) - ref16).max() <= 4e-3 * np.abs(ref16).max() + 1e-6
+
+
 def test_gemm_full_size_sampled_rows(ee, orc):
     """BASELINE configs 1-2 at full size (M=4096, K=4096, N=14336): INT8 int32
     accumulators bit-exact on 48 sampled rows (rows are independent)."""

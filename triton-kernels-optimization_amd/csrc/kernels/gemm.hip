@@ -582,6 +582,176 @@ EE_DEV void gemm_tile(const EeGemmArgs& g, int tm, int tn, uint8_t* smem) {
     }
 }
 
+// ---------------------------------------------------------------- W8A16 on int8 weights
+// The reference's FP16 tier (EE/python/kernels.py:192-246) keeps int8 weights
+// and dequantises them in SRAM: w = fp16(fp16(b) * fp16(b_scale[n])) (:215,
+// :233), then an fp16 dot with f32 accumulation.  This kernel does the same
+// from int8 codes in HBM, so B costs 1 byte per element instead of the 2 of
+// pre-dequantised fp16 weights.  Loader-wave pipeline as gemm_tile, with:
+//  * stages of 64 K elements: A fp16 128 rows x 128 B (the usual swizzle) and
+//    B int8 128 rows x 64 B, 16-byte chunk c of row r stored at chunk
+//    c ^ ((r >> 2) & 3) -- conflict-free ds_read_b128 over 16 rows;
+//  * K order: in each 32-element block, lanes 0-31 take elements 0-7 (first
+//    MFMA) and 8-15 (second), lanes 32-63 take 16-23 and 24-31, so one 16-byte
+//    B read per lane feeds two MFMAs; A uses the same mapping (each MFMA sums a
+//    consistent set of products);
+//  * dequantisation in registers: byte b -> fp16 bits 0x6400 | (b ^ 0x80) is
+//    1024 + (b + 128) exactly, minus 1152 gives fp16(b); times fp16(scale) in
+//    one RNE fp16 multiply, the reference's w exactly.
+#define W8_KE 64                                  // K elements per stage
+#define W8_STAGE (BM * 128 + BN * 64)             // 24 KB
+#define W8_NSTAGE 5
+#define W8_EPI (W8_NSTAGE * W8_STAGE)             // 120 KB: the epilogue tiles, 4 x 8 KB
+#define W8_LDS (W8_EPI + 4 * 64 * BKB)            // 152 KB
+
+EE_DEV uint32_t w8_boff(int r, int c) { return (uint32_t)(BM * 128 + r * 64 + ((c ^ ((r >> 2) & 3)) << 4)); }
+
+// 4 int8 codes (one dword) -> 4 fp16 w = fp16(fp16(b) * s), as two f16x2 words
+EE_DEV void dq4(uint32_t w, f16x2 s2, uint32_t& lo, uint32_t& hi) {
+    const uint32_t x = w ^ 0x80808080u;
+    const f16x2 bias = {(f16)1152.0f, (f16)1152.0f};
+    const f16x2 a = f16x2_from_bits(__builtin_amdgcn_perm(0x64646464u, x, 0x04010400u)) - bias;
+    const f16x2 b = f16x2_from_bits(__builtin_amdgcn_perm(0x64646464u, x, 0x04030402u)) - bias;
+    lo = bits_of(a * s2);
+    hi = bits_of(b * s2);
+}
+
+template <int SW>
+EE_DEV void gemm_tile_w8a16(const EeGemmArgs& g, int tm, int tn, uint8_t* smem) {
+    typedef f32x16 acc_t;
+    constexpr int LOADS = 6;                          // per loader wave per stage: 4 A + 2 B
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int M = g.counts ? g.counts[g.tier] : g.M;
+    const int64_t off = g.counts ? tier_offset(g.counts, g.tier) : 0;
+    const int m0 = tm * BM, n0 = tn * BN;
+    if (m0 >= M) return;                              // whole workgroup, before any barrier
+    const int nk = g.K / W8_KE;                       // K is a multiple of 64 here
+
+    if (wave >= 4) {
+        const int lw = wave - 4;
+        const uint8_t* pa[4];
+        const uint8_t* pb[2];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {                 // A: row groups of 8 rows x 128 B
+            const int r = (lw * 4 + i) * 8 + (lane >> 3);
+            const int lchunk = (lane & 7) ^ swz(r);
+            const int m = min(m0 + r, M - 1);
+            const int64_t ar = g.a_idx ? (int64_t)g.a_idx[off + m] : off + m;
+            pa[i] = (const uint8_t*)g.a + ar * g.lda * 2 + lchunk * 16;
+        }
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {                 // B: row groups of 16 rows x 64 B
+            const int r = (lw * 2 + q) * 16 + (lane >> 2);
+            const int lchunk = (lane & 3) ^ ((r >> 2) & 3);
+            const int n = min(n0 + r, g.N - 1);
+            pb[q] = (const uint8_t*)g.b + (int64_t)n * g.ldb + lchunk * 16;
+        }
+        auto issue = [&](int kt) {
+            const uint32_t s = lds_addr(smem) + (uint32_t)((kt % W8_NSTAGE) * W8_STAGE);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) dma16(pa[i] + (int64_t)kt * 128, s + (lw * 4 + i) * 8 * 128);
+#pragma unroll
+            for (int q = 0; q < 2; ++q) dma16(pb[q] + (int64_t)kt * 64, s + BM * 128 + (lw * 2 + q) * 16 * 64);
+        };
+#pragma unroll
+        for (int st = 0; st < W8_NSTAGE; ++st)
+            if (st < nk) issue(st);
+        for (int kt = 0; kt < nk; ++kt) {
+            const int last = kt == 0 ? W8_NSTAGE - 1 : kt + W8_NSTAGE - 2;
+            const int after = min(last, nk - 1) - kt;
+            if (after >= 4) WAITCNT_VM(4 * LOADS);
+            else if (after == 3) WAITCNT_VM(3 * LOADS);
+            else if (after == 2) WAITCNT_VM(2 * LOADS);
+            else if (after == 1) WAITCNT_VM(LOADS);
+            else WAITCNT_VM(0);
+            asm volatile("" ::: "memory");
+            __builtin_amdgcn_s_barrier();             // barrier kt
+            asm volatile("" ::: "memory");
+            if (kt >= 1 && kt - 1 + W8_NSTAGE < nk) issue(kt - 1 + W8_NSTAGE);
+        }
+        return;
+    }
+
+    // ---------------------------------------------------------------- compute waves
+    const int wm = wave >> 1, wn = wave & 1, h = lane >> 5;
+    acc_t acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = acc_t{};
+    f16x2 s2[2];                                      // fp16(b_scale[n]) of this lane's B row in block j
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int n = n0 + wn * 64 + j * 32 + (lane & 31);
+        const f16 sv = (f16)f32_rn(n < g.N ? g.b_scale[n] : 0.0f);
+        s2[j] = f16x2{sv, sv};
+    }
+    // fragments of one 32-element K block t of a stage: A rows (i), B rows (j)
+    struct Fr { u32x4 a[2][2]; u32x4 b[2]; };        // a[i][u]: u = first / second MFMA
+    auto read = [&](const uint8_t* s, int t, Fr& f) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int ra = wm * 64 + i * 32 + (lane & 31);
+#pragma unroll
+            for (int u = 0; u < 2; ++u) f.a[i][u] = *(const u32x4*)(s + lds_off(ra, 4 * t + 2 * h + u));
+        }
+#pragma unroll
+        for (int j = 0; j < 2; ++j) f.b[j] = *(const u32x4*)(s + w8_boff(wn * 64 + j * 32 + (lane & 31), 2 * t + h));
+    };
+    auto mma = [&](const Fr& f) {
+        u32x4 w[2][2];                                // w[j][u]: 8 fp16 weights for MFMA u
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            uint32_t d[8];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) dq4(f.b[j][q], s2[j], d[2 * q], d[2 * q + 1]);
+            w[j][0] = u32x4{d[0], d[1], d[2], d[3]};
+            w[j][1] = u32x4{d[4], d[5], d[6], d[7]};
+        }
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, w[j][u]),
+                                                                       __builtin_bit_cast(f16x8, f.a[i][u]),
+                                                                       acc[i][j], 0, 0, 0);
+    };
+    TileScales sc;                                    // unused by the fp16 epilogue
+    Fr f0, f1;
+    auto stage = [&](int kt, bool more) {
+        const uint8_t* s = smem + (kt % W8_NSTAGE) * W8_STAGE;
+        read(s, 1, f1);                               // block 1 of this stage
+        mma(f0);
+        if (more) {
+            __builtin_amdgcn_sched_barrier(0);
+            WAITCNT_LGKM0();
+            asm volatile("" ::: "memory");
+            __builtin_amdgcn_s_barrier();             // barrier kt+1: stage kt+1 has landed
+            asm volatile("" ::: "memory");
+            read(smem + ((kt + 1) % W8_NSTAGE) * W8_STAGE, 0, f0);
+        }
+        mma(f1);
+    };
+    __builtin_amdgcn_s_barrier();                     // barrier 0: stage 0 has landed
+    asm volatile("" ::: "memory");
+    read(smem, 0, f0);
+    for (int kt = 0; kt + 1 < nk; ++kt) stage(kt, true);
+    stage(nk - 1, false);
+    uint8_t* tile = smem + W8_EPI + wave * (64 * BKB);
+    epilogue32_lds<EE_GEMM_F16, SW>(g, acc, sc, tile, m0, n0, M, off, wm, wn, lane);
+}
+
+template <int SW>
+EE_DEV void gemm_w8a16(const EeGemmArgs& g) {
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[W8_LDS];
+    int tm, tn;
+    tile_of((int)blockIdx.x, (int)gridDim.x, (g.M + BM - 1) / BM, tm, tn);
+    gemm_tile_w8a16<SW>(g, tm, tn, smem);
+}
+
 // A 32 x 32 accumulator block through LDS: register group q (4 values) of lane l
 // at byte (q * 64 + l) * 16 of a 4 KB slot, so a ds_write_b128 / ds_read_b128
 // covers 1 KB of consecutive banks.  (Elements are converted one scalar at a
@@ -1317,6 +1487,8 @@ EE_GEMM_ENTRY(eek_gemm_f8, body_f8)
 EE_GEMM_ENTRY(eek_gemm_f16, body_f16)
 EE_GEMM_ENTRY(eek_gemm_i8_w8, body_i8_w8)
 EE_GEMM_ENTRY(eek_gemm_f16_w8, body_f16_w8)
+template <int SW> EE_DEV void body_w8a16(const EeGemmArgs& g) { gemm_w8a16<SW>(g); }
+EE_GEMM_ENTRY(eek_gemm_w8a16, body_w8a16)
 
 // The routed linear's three tier GEMMs in one launch.  Tier t owns partition
 // slots [off_t, off_t + counts[t]) (off_t = counts[0] + ... + counts[t-1]) and

@@ -566,10 +566,35 @@ static int gemm_impl(ee_engine* eng, int32_t kind, const void* a, int64_t lda, c
                      int32_t K, const int32_t* a_idx, const int32_t* c_idx, const int32_t* counts, int32_t tier,
                      int32_t* acc_out, int sw, ee_stream_t stream) {
     if (eng == nullptr) return fail(EE_ERR_INVALID_ARG, "engine must not be NULL");
-    if (kind < EE_GEMM_I8 || kind > EE_GEMM_F16) return fail(EE_ERR_INVALID_ARG, "unknown GEMM kind");
+    if (kind < EE_GEMM_I8 || kind > EE_GEMM_W8A16) return fail(EE_ERR_INVALID_ARG, "unknown GEMM kind");
     if (a == nullptr || b_nk == nullptr || c == nullptr) return fail(EE_ERR_INVALID_ARG, "a, b and c must not be NULL");
-    if (kind != EE_GEMM_F16 && (a_scale == nullptr || b_scale == nullptr))
+    if (kind != EE_GEMM_F16 && kind != EE_GEMM_W8A16 && (a_scale == nullptr || b_scale == nullptr))
         return fail(EE_ERR_INVALID_ARG, "a_scale and b_scale are required for the INT8 and FP8 tiers");
+    if (kind == EE_GEMM_W8A16) {
+        // fp16 A, int8 B codes + f32 scales, dequantised in the kernel: one pipeline (K % 64 == 0)
+        if (b_scale == nullptr) return fail(EE_ERR_INVALID_ARG, "b_scale is required for W8A16");
+        if (acc_out != nullptr) return fail(EE_ERR_INVALID_ARG, "acc_out is INT8 only");
+        if (M < 0 || N <= 0 || K <= 0) return fail(EE_ERR_INVALID_ARG, "need M >= 0, N > 0, K > 0");
+        if (lda < K || ldb < K || ldc < (sw ? N / 2 : N))
+            return fail(EE_ERR_INVALID_ARG, "leading dimension smaller than the row");
+        if (K % 64 != 0 || lda % 8 != 0 || ldb % 16 != 0 || N % 4 != 0 || ldc % 4 != 0)
+            return fail(EE_ERR_UNSUPPORTED, "W8A16 needs K % 64 == 0, lda % 8 == 0, ldb % 16 == 0, N % 4 == 0, "
+                                            "ldc % 4 == 0");
+        if (sw && (N % 64 != 0 || ldc % 8 != 0 || !aligned(c, 16)))
+            return fail(EE_ERR_UNSUPPORTED, "SwiGLU GEMM needs N % 64 == 0, ld_act % 8 == 0, a 16-byte aligned act");
+        if (!aligned(a, 16) || !aligned(b_nk, 16) || !aligned(c, 8) || !aligned(b_scale, 4) || !aligned(a_idx, 4) ||
+            !aligned(c_idx, 4) || !aligned(counts, 4))
+            return fail(EE_ERR_INVALID_ARG, "misaligned pointer (a, b: 16 B; c: 8 B; b_scale, indices: 4 B)");
+        if ((a_idx != nullptr || c_idx != nullptr) && counts == nullptr)
+            return fail(EE_ERR_INVALID_ARG, "a_idx / c_idx need counts");
+        if (counts != nullptr && (tier < 0 || tier > 2)) return fail(EE_ERR_INVALID_ARG, "tier must be 0, 1 or 2");
+        if (M == 0) return EE_OK;
+        EeGemmArgs g{a, b_nk, (uint16_t*)c, nullptr, nullptr, b_scale, a_idx, c_idx, counts, lda, ldb, ldc,
+                     M, N, K, counts ? tier : 0, sw};
+        const std::string name = sw ? "eek_gemm_w8a16_swiglu" : "eek_gemm_w8a16";
+        const Kernel* k = find_kernel(eng, name);
+        return launch(eng, name, cdiv(M, 128) * cdiv(N, 128), 1, k ? k->block : EE_BLOCK, g, stream);
+    }
     if (acc_out != nullptr && kind != EE_GEMM_I8) return fail(EE_ERR_INVALID_ARG, "acc_out is INT8 only");
     if (M < 0 || N <= 0 || K <= 0) return fail(EE_ERR_INVALID_ARG, "need M >= 0, N > 0, K > 0");
     const int64_t esz = (kind == EE_GEMM_F16) ? 2 : 1;

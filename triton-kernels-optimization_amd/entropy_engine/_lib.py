@@ -32,7 +32,7 @@ STATUS_NAMES = {0: "EE_OK", -1: "EE_ERR_INVALID_ARG", -2: "EE_ERR_IO", -3: "EE_E
 # quantiser modes / GEMM kinds / tiers
 EE_QUANT_I8_DISPATCH, EE_QUANT_I8_ENGINE, EE_QUANT_F8_ROW, EE_QUANT_F8_TENSOR = 0, 1, 2, 3
 EE_TENSOR_WS_FLOATS = 1024
-EE_GEMM_I8, EE_GEMM_F8, EE_GEMM_F16 = 0, 1, 2
+EE_GEMM_I8, EE_GEMM_F8, EE_GEMM_F16, EE_GEMM_W8A16 = 0, 1, 2, 3
 
 _p = ctypes.c_void_p
 _i32 = ctypes.c_int32

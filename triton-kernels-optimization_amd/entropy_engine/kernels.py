@@ -251,7 +251,7 @@ def prepare_weight(b_int8: torch.Tensor, b_scale: torch.Tensor) -> PackedWeight:
 
 # ---------------------------------------------------------------- GEMMs
 
-_KINDS = {"int8": _lib.EE_GEMM_I8, "fp8": _lib.EE_GEMM_F8, "fp16": _lib.EE_GEMM_F16}
+_KINDS = {"int8": _lib.EE_GEMM_I8, "fp8": _lib.EE_GEMM_F8, "fp16": _lib.EE_GEMM_F16, "w8a16": _lib.EE_GEMM_W8A16}
 
 
 def gemm(kind: str, a: torch.Tensor, b_nk: torch.Tensor, a_scale=None, b_scale=None, out=None, *,
