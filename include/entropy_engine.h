@@ -228,6 +228,28 @@ int ee_add_rmsnorm(ee_engine* eng, const void* x, int64_t ld_x, const void* y, i
 int ee_qkv_rope(ee_engine* eng, const void* qkv, int64_t ld, const void* cos_t, const void* sin_t, void* q, void* k,
                 void* v, int32_t B, int32_t S, int32_t Hq, int32_t Hkv, int32_t d, float q_scale,
                 ee_stream_t stream);
+/* The same with v written transposed for ee_attention_causal: vt [B, Hkv, d, S],
+ * row (b, h, j) holding v[.., j] of every token, and within each group of 16
+ * tokens the order 0-3, 8-11, 4-7, 12-15.  S % 16 == 0.  No counterpart in
+ * the reference (a layout of this build's fused attention). */
+int ee_qkv_rope_vt(ee_engine* eng, const void* qkv, int64_t ld, const void* cos_t, const void* sin_t, void* q,
+                   void* k, void* vt, int32_t B, int32_t S, int32_t Hq, int32_t Hkv, int32_t d, float q_scale,
+                   ee_stream_t stream);
+
+/* Causal grouped-query attention fused with the Shannon entropy of its
+ * probability rows: for batch b, query head h (kv head h / (Hq / Hkv)) and
+ * query s, over keys c <= s, x_c = fp16(q . k_c), p = softmax(x),
+ * out = fp16(sum p_c v_c) and H = ln Z - sum p_c (x_c - max x) -- the HF
+ * Llama attention whose probabilities EE/python/dispatch.py:243-245 takes the
+ * entropy of, with the entropy of softmax_entropy (EE/python/kernels.py:
+ * 264-312), without materialising the S x S scores.  q [B, Hq, S, d] already
+ * scaled (ee_qkv_rope's q_scale), k [B, Hkv, S, d], vt from ee_qkv_rope_vt;
+ * out fp16 [B*S, ld_out] token-major (head h at columns h*d ..), h f32
+ * [B, Hq, S].  d == 64, S % 64 == 0, Hq / Hkv even.  Results agree with the unfused path
+ * (fp16 scores, ee_softmax_entropy, a product with v) to fp16 rounding: the
+ * probabilities here are fp16(e^(x - m_running)) normalised at the end. */
+int ee_attention_causal(ee_engine* eng, const void* q, const void* k, const void* vt, void* out, int64_t ld_out,
+                        float* h, int32_t B, int32_t S, int32_t Hq, int32_t Hkv, int32_t d, ee_stream_t stream);
 
 /* Weight preparation: gate_w, up_w fp16 [F, H] and down_w fp16 [H, F] (the
  * nn.Linear layout, EE/test_engine.py:12-14) quantised per output channel as

@@ -136,6 +136,11 @@ def test_built_meta_lists_every_kernel_the_launcher_selects():
         assert ks[k]["block"] == 256
     for c in (1, 2, 4, 8):
         assert ks[f"eek_add_rmsnorm_c{c}"]["block"] == 256
+    # fused attention: one wave per query head, W = 4 or 2 heads per kv head; 2 stages of K + V^T (16 KB)
+    for w in (2, 4):
+        assert ks[f"eek_attn_causal_d64_w{w}"]["block"] == 64 * w
+        assert ks[f"eek_attn_causal_d64_w{w}"]["lds"] == 2 * 16384
+    assert "eek_gemm_w8a16" in ks and "eek_gemm_w8a16_swiglu" in ks
     for k in ("eek_softmax_entropy_generic", "eek_quant_generic", "eek_gemm_i8", "eek_gemm_f8", "eek_gemm_f16",
               "eek_gemm_i8_w8", "eek_gemm_f16_w8",
               "eek_gemm_i8_generic", "eek_gemm_f8_generic", "eek_gemm_f16_generic",

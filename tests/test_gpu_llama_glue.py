@@ -159,3 +159,77 @@ def test_gated_llama_forward_replays_as_a_hip_graph(ee):
 
 def cuda(a):
     return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def torch_attention_entropy(q, k, v):
+    """fp32 reference of the fused kernel on the same fp16 inputs: scores rounded
+    to fp16 (what an fp16 q k^T stores), causal softmax, out and row entropy."""
+    B, Hq, S, d = q.shape
+    G = Hq // k.shape[1]
+    kr = k.repeat_interleave(G, dim=1).float()
+    vr = v.repeat_interleave(G, dim=1).float()
+    sc = (q.float() @ kr.transpose(-1, -2)).half().float()
+    mask = torch.ones(S, S, device="cuda", dtype=torch.bool).tril()
+    sc = sc.masked_fill(~mask, float("-inf"))
+    p = torch.softmax(sc, dim=-1)
+    ls = torch.log_softmax(sc, dim=-1)
+    H = -(p * torch.where(mask, ls, torch.zeros_like(ls))).sum(-1)
+    return p @ vr, H
+
+
+@pytest.mark.parametrize("B,S,Hq,Hkv", [(2, 512, 32, 4), (1, 64, 4, 2), (2, 192, 4, 2), (1, 128, 8, 1), (3, 256, 8, 2)])
+def test_fused_attention_entropy(ee, B, S, Hq, Hkv):
+    """attention_causal (scores kept in registers, online max) against the fp32
+    reference and against the unfused path (fp16 scores, softmax_entropy kernel,
+    product with v): out within fp16 rounding of the probabilities, H within 1e-3."""
+    from entropy_engine.dispatch import _attention_entropy
+    d = 64
+    g = torch.Generator(device="cuda").manual_seed(B * S + Hq)
+    qkv = (torch.randn(B * S, (Hq + 2 * Hkv) * d, device="cuda", generator=g) * 1.5).half()
+    cos, sin = rope_tables(S, d)
+    q, k, v = ee.qkv_rope(qkv, cos, sin, B, S, Hq, Hkv, d, d ** -0.5)
+    q2, k2, vt = ee.qkv_rope(qkv, cos, sin, B, S, Hq, Hkv, d, d ** -0.5, v_transposed=True)
+    assert torch.equal(q, q2) and torch.equal(k, k2)
+    # the transposed layout: vt[b, h, j, 16 g + p] = v[b, h, 16 g + VT_ORDER[p], j]
+    order = torch.tensor(ee.VT_ORDER, device="cuda")
+    idx = (torch.arange(S // 16, device="cuda")[:, None] * 16 + order[None, :]).reshape(-1)
+    assert torch.equal(vt, v[:, :, idx, :].transpose(-1, -2))
+    out, H = ee.attention_causal(q, k, vt)
+    ref_o, ref_h = torch_attention_entropy(q, k, v)
+    o = out.view(B, S, Hq, d).transpose(1, 2).float()
+    assert torch.isfinite(o).all() and torch.isfinite(H).all()
+    assert (o - ref_o).abs().max().item() <= 1e-2 * ref_o.abs().max().item()
+    assert torch.allclose(H, ref_h, rtol=1e-3, atol=1e-3)
+    assert H[:, :, 0].abs().max().item() < 1e-6      # query 0 sees one key: H = 0
+    un_o, un_h = _attention_entropy(q, k, v, 1.0, causal=True)
+    assert (o - un_o.float()).abs().max().item() <= 1e-2 * un_o.float().abs().max().item()
+    assert torch.allclose(H, un_h, rtol=1e-3, atol=1e-3)
+
+
+def test_fused_attention_one_hot_and_uniform_rows(ee):
+    """Closed form: q = 0 gives uniform rows, H = ln(s + 1) and out = the mean of
+    v over keys <= s (grouped-query heads reading their kv head)."""
+    B, S, Hq, Hkv, d = 1, 128, 4, 2, 64
+    qkv = torch.zeros(B * S, (Hq + 2 * Hkv) * d, device="cuda", dtype=torch.float16)
+    g = torch.Generator(device="cuda").manual_seed(2)
+    qkv[:, (Hq + Hkv) * d:] = torch.randn(B * S, Hkv * d, device="cuda", generator=g).half()
+    cos = torch.ones(1, S, d, device="cuda", dtype=torch.float16)
+    sin = torch.zeros(1, S, d, device="cuda", dtype=torch.float16)
+    q, k, vt = ee.qkv_rope(qkv, cos, sin, B, S, Hq, Hkv, d, 1.0, v_transposed=True)
+    out, H = ee.attention_causal(q, k, vt)
+    s = torch.arange(S, device="cuda", dtype=torch.float32)
+    assert torch.allclose(H[0], torch.log(s + 1)[None, :].expand(Hq, S), rtol=1e-5, atol=1e-5)
+    v = qkv[:, (Hq + Hkv) * d:].float().view(S, Hkv, d)
+    mean = (torch.cumsum(v, 0) / (s + 1)[:, None, None]).repeat_interleave(Hq // Hkv, dim=1)
+    assert (out.view(S, Hq, d).float() - mean).abs().max().item() < 2e-3
+
+
+def test_fused_attention_rejects_unsupported_shapes(ee):
+    from entropy_engine import _lib
+    d = 64
+    for (S, Hq, Hkv) in ((96, 4, 2), (128, 4, 4)):          # S % 64, odd query heads per kv head
+        q = torch.zeros(1, Hq, S, d, device="cuda", dtype=torch.float16)
+        k = torch.zeros(1, Hkv, S, d, device="cuda", dtype=torch.float16)
+        vt = torch.zeros(1, Hkv, d, S, device="cuda", dtype=torch.float16)
+        with pytest.raises(_lib.EngineError):
+            ee.attention_causal(q, k, vt)

@@ -855,3 +855,8 @@ def test_entropy_gated_llama_small(ee):
     got = low.forward(ids).float()
     assert low.last_fractions.tolist() == [0, 0, B * S * (7 * L + 1)]
     assert (got - ref).abs().max() <= 1e-2 * ref.abs().max()
+    # the fused attention kernel against the unfused path (scores, softmax_entropy, product with v)
+    m.fused_attention = False
+    unfused = m.forward(ids, gated=False).float()
+    m.fused_attention = True
+    assert (fp16 - unfused).abs().max() <= 1e-2 * unfused.abs().max()

@@ -177,4 +177,17 @@ struct EeQkvRopeArgs {
     int64_t ld;
     int32_t B, S, Hq, Hkv, d;
     float q_scale;          // q is stored as fp16(rope(q) * q_scale); 1 stores rope(q)
+    int32_t v_t;            // 1: v is V^T [B, Hkv, d, S], each 16-key group stored as keys 0-3, 8-11, 4-7, 12-15
+};
+
+// Fused causal attention + row entropy (attention.hip), head_dim 64.
+struct EeAttnArgs {
+    const uint16_t* q;      // fp16 [B, Hq, S, 64], carrying the 1/sqrt(64) scaling
+    const uint16_t* k;      // fp16 [B, Hkv, S, 64]
+    const uint16_t* vt;     // fp16 [B, Hkv, 64, S], key order of eek_qkv_rope's v_t layout
+    uint16_t* out;          // fp16 [B*S, ld_out]: token-major, query head h at columns 64h .. 64h + 63
+    float* h;               // f32 [B, Hq, S]: entropy of each probability row
+    int64_t ld_out;
+    int32_t B, S, Hq, Hkv;
+    int32_t W;              // query heads (waves) per workgroup: 2 or 4, dividing Hq / Hkv
 };

@@ -99,7 +99,9 @@ extern "C" __global__ void __launch_bounds__(EE_BLOCK) eek_qkv_rope(EeQkvRopeArg
     const int cpr = d >> 4;                           // 8-element chunk pairs per head row
     const int64_t T = (int64_t)a.B * a.S;
     const int64_t n_qk = T * (a.Hq + a.Hkv) * cpr;
-    const int64_t n_v = T * a.Hkv * (d >> 3);
+    // v: 16-byte chunks of each token's heads, or with v_t one unit per 16 tokens x
+    // 8 d of a kv head, transposed in registers
+    const int64_t n_v = a.v_t ? (int64_t)a.B * a.Hkv * (a.S >> 4) * (d >> 3) : T * a.Hkv * (d >> 3);
     const int64_t stride = (int64_t)gridDim.x * EE_BLOCK;
     for (int64_t i = (int64_t)blockIdx.x * EE_BLOCK + threadIdx.x; i < n_qk + n_v; i += stride) {
         if (i < n_qk) {
@@ -126,6 +128,33 @@ extern "C" __global__ void __launch_bounds__(EE_BLOCK) eek_qkv_rope(EeQkvRopeArg
                                 : a.k + (((int64_t)b * a.Hkv + (head - a.Hq)) * a.S + s) * d;
             *(u32x4*)(dst + 8 * c) = o1;
             *(u32x4*)(dst + h + 8 * c) = o2;
+        } else if (a.v_t) {
+            // V^T [B, Hkv, d, S]: row dd holds v[.., dd] of every token; within each
+            // group of 16 tokens the stored order is 0-3, 8-11, 4-7, 12-15 (the
+            // K-slot order of the attention kernel's probability fragments).
+            const int64_t iv = i - n_qk;
+            const int c = (int)(iv % (d >> 3));
+            const int64_t r1 = iv / (d >> 3);
+            const int g = (int)(r1 % (a.S >> 4));
+            const int64_t bh = r1 / (a.S >> 4);
+            const int head = (int)(bh % a.Hkv), b = (int)(bh / a.Hkv);
+            const uint16_t* src = a.qkv + ((int64_t)b * a.S + 16 * g) * a.ld + (int64_t)(a.Hq + a.Hkv + head) * d + 8 * c;
+            u32x4 x[16];
+#pragma unroll
+            for (int j = 0; j < 16; ++j) x[j] = *(const u32x4*)(src + (int64_t)j * a.ld);
+            // stored position p holds token perm(p): chunks of 4 in the order 0, 2, 1, 3
+            constexpr int perm[16] = {0, 1, 2, 3, 8, 9, 10, 11, 4, 5, 6, 7, 12, 13, 14, 15};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;   // high or low halves
+                uint32_t w[8];
+#pragma unroll
+                for (int k = 0; k < 8; ++k)
+                    w[k] = __builtin_amdgcn_perm(x[perm[2 * k + 1]][e >> 1], x[perm[2 * k]][e >> 1], sel);
+                uint16_t* dst = a.v + (((int64_t)b * a.Hkv + head) * d + 8 * c + e) * a.S + 16 * g;
+                *(u32x4*)dst = u32x4{w[0], w[1], w[2], w[3]};
+                *(u32x4*)(dst + 8) = u32x4{w[4], w[5], w[6], w[7]};
+            }
         } else {
             const int64_t iv = i - n_qk;
             const int c = (int)(iv % (d >> 3));

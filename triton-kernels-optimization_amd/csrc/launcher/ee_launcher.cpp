@@ -830,24 +830,58 @@ EE_EXPORT int ee_add_rmsnorm(ee_engine* eng, const void* x, int64_t ld_x, const 
     return launch(eng, name, cdiv(T, EE_BLOCK / 64), 1, EE_BLOCK, a, stream);
 }
 
-EE_EXPORT int ee_qkv_rope(ee_engine* eng, const void* qkv, int64_t ld, const void* cos_t, const void* sin_t,
-                          void* q, void* k, void* v, int32_t B, int32_t S, int32_t Hq, int32_t Hkv, int32_t d,
-                          float q_scale, ee_stream_t stream) {
+static int qkv_rope_impl(ee_engine* eng, const void* qkv, int64_t ld, const void* cos_t, const void* sin_t,
+                         void* q, void* k, void* v, int32_t B, int32_t S, int32_t Hq, int32_t Hkv, int32_t d,
+                         float q_scale, int v_t, ee_stream_t stream) {
     if (eng == nullptr || qkv == nullptr || cos_t == nullptr || sin_t == nullptr || q == nullptr || k == nullptr ||
         v == nullptr)
         return fail(EE_ERR_INVALID_ARG, "NULL argument");
     if (B < 0 || S < 0 || Hq <= 0 || Hkv <= 0 || d <= 0 || ld < (int64_t)(Hq + 2 * Hkv) * d)
         return fail(EE_ERR_INVALID_ARG, "bad shape or stride");
     if (d % 16 != 0 || ld % 8 != 0) return fail(EE_ERR_UNSUPPORTED, "qkv_rope needs d % 16 == 0 and ld % 8 == 0");
+    if (v_t && S % 16 != 0) return fail(EE_ERR_UNSUPPORTED, "the transposed v layout needs S % 16 == 0");
     if (!aligned(qkv, 16) || !aligned(cos_t, 16) || !aligned(sin_t, 16) || !aligned(q, 16) || !aligned(k, 16) ||
         !aligned(v, 16))
         return fail(EE_ERR_INVALID_ARG, "misaligned pointer (16 B)");
     const int64_t T = (int64_t)B * S;
     if (T == 0) return EE_OK;
     EeQkvRopeArgs a{(const uint16_t*)qkv, (const uint16_t*)cos_t, (const uint16_t*)sin_t, (uint16_t*)q, (uint16_t*)k,
-                    (uint16_t*)v, ld, B, S, Hq, Hkv, d, q_scale};
-    const int64_t work = T * (Hq + Hkv) * (d / 16) + T * Hkv * (d / 8);
+                    (uint16_t*)v, ld, B, S, Hq, Hkv, d, q_scale, v_t};
+    const int64_t work = T * (Hq + Hkv) * (d / 16) + (v_t ? T / 16 : T) * Hkv * (d / 8);
     return launch(eng, "eek_qkv_rope", std::min<int64_t>(cdiv(work, EE_BLOCK), 16384), 1, EE_BLOCK, a, stream);
+}
+
+EE_EXPORT int ee_qkv_rope(ee_engine* eng, const void* qkv, int64_t ld, const void* cos_t, const void* sin_t,
+                          void* q, void* k, void* v, int32_t B, int32_t S, int32_t Hq, int32_t Hkv, int32_t d,
+                          float q_scale, ee_stream_t stream) {
+    return qkv_rope_impl(eng, qkv, ld, cos_t, sin_t, q, k, v, B, S, Hq, Hkv, d, q_scale, 0, stream);
+}
+
+EE_EXPORT int ee_qkv_rope_vt(ee_engine* eng, const void* qkv, int64_t ld, const void* cos_t, const void* sin_t,
+                             void* q, void* k, void* vt, int32_t B, int32_t S, int32_t Hq, int32_t Hkv, int32_t d,
+                             float q_scale, ee_stream_t stream) {
+    return qkv_rope_impl(eng, qkv, ld, cos_t, sin_t, q, k, vt, B, S, Hq, Hkv, d, q_scale, 1, stream);
+}
+
+EE_EXPORT int ee_attention_causal(ee_engine* eng, const void* q, const void* k, const void* vt, void* out,
+                                  int64_t ld_out, float* h, int32_t B, int32_t S, int32_t Hq, int32_t Hkv, int32_t d,
+                                  ee_stream_t stream) {
+    if (eng == nullptr || q == nullptr || k == nullptr || vt == nullptr || out == nullptr || h == nullptr)
+        return fail(EE_ERR_INVALID_ARG, "NULL argument");
+    if (B < 0 || S < 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv != 0 || ld_out < (int64_t)Hq * d)
+        return fail(EE_ERR_INVALID_ARG, "bad shape or stride (Hq must be a multiple of Hkv, ld_out >= Hq * d)");
+    if (d != 64 || S % 64 != 0 || ld_out % 8 != 0 || (Hq / Hkv) % 2 != 0)
+        return fail(EE_ERR_UNSUPPORTED, "the fused attention needs head_dim 64, S % 64 == 0, ld_out % 8 == 0 and "
+                                        "an even number of query heads per kv head");
+    if (!aligned(q, 16) || !aligned(k, 16) || !aligned(vt, 16) || !aligned(out, 16) || !aligned(h, 4))
+        return fail(EE_ERR_INVALID_ARG, "misaligned pointer (q, k, vt, out: 16 B; h: 4 B)");
+    if ((int64_t)B * S == 0) return EE_OK;
+    const int G = Hq / Hkv;
+    const int W = G % 4 == 0 ? 4 : 2;
+    EeAttnArgs a{(const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)vt, (uint16_t*)out, h, ld_out, B, S, Hq,
+                 Hkv, W};
+    return launch(eng, "eek_attn_causal_d64_w" + std::to_string(W), (int64_t)B * (Hq / W) * (S / 64), 1, 64 * W, a,
+                  stream);
 }
 
 EE_EXPORT int ee_mlp_prepare(ee_engine* eng, const void* gate_w, const void* up_w, const void* down_w, int64_t H,

@@ -68,6 +68,9 @@ SIGNATURES = {
     "ee_add_rmsnorm": ([_p, _p, _i64, _p, _i64, _p, _p, _i64, _p, _i64, _i64, _i64, ctypes.c_float, _p], ctypes.c_int),
     "ee_qkv_rope": ([_p, _p, _i64, _p, _p, _p, _p, _p, _i32, _i32, _i32, _i32, _i32, ctypes.c_float, _p],
                     ctypes.c_int),
+    "ee_qkv_rope_vt": ([_p, _p, _i64, _p, _p, _p, _p, _p, _i32, _i32, _i32, _i32, _i32, ctypes.c_float, _p],
+                       ctypes.c_int),
+    "ee_attention_causal": ([_p, _p, _p, _p, _p, _i64, _p, _i32, _i32, _i32, _i32, _i32, _p], ctypes.c_int),
     "ee_mlp_prepare": ([_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _p],
                        ctypes.c_int),
     "ee_mlp_workspace_bytes": ([_i64, _i64, _i64, _i32], _i64),

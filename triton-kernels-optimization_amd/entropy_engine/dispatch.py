@@ -362,7 +362,11 @@ class EntropyGatedLlama:
     one tier per layer.
 
     A token's routing entropy is the mean over heads of its attention-row
-    entropy (fused softmax+entropy kernel, causal): q/k/v of layer l use layer
+    entropy: the fused attention kernel (attention_causal: scores,
+    probabilities and entropies never leave the chip) where its shapes allow
+    (head_dim 64, S % 64 == 0, an even number of query heads per kv head; the
+    attribute fused_attention = False turns it off), else the scores, the
+    fused softmax+entropy kernel and a product with v.  q/k/v of layer l use layer
     l-1's (layer 0 runs them on the FP16 tier), o/gate/up/down use layer l's,
     and the LM head uses the last layer's.  Rows are grouped per tier into one
     launch per tier and scattered back (routed_linear); q/k/v, and gate/up, run
@@ -395,6 +399,7 @@ class EntropyGatedLlama:
             self.packed[key] = self._pack(w, swiglu=isinstance(key, tuple) and key[1] == "gu")
         self.last_fractions = None
         self._rope_cache = {}
+        self.fused_attention = True
 
     @staticmethod
     def _pack(w: torch.Tensor, swiglu: bool = False) -> K.PackedWeight:
@@ -465,6 +470,8 @@ class EntropyGatedLlama:
         Hq, Hkv, d = c["heads"], c["kv_heads"], c["head_dim"]
         x = self.p["embed"][input_ids].reshape(T, -1)                    # [T, D] fp16
         cos, sin = self._rope_tables(S, x.device)
+        # the fused attention kernel's shapes (attention_causal); others take the unfused path
+        fused_att = self.fused_attention and d == 64 and S % 64 == 0 and (Hq // Hkv) % 2 == 0
         eps = c["eps"]
         counts_log = []
         route_prev = None
@@ -473,9 +480,14 @@ class EntropyGatedLlama:
             x, xn = K.add_rmsnorm(x, self.p[f"{l}.ln1"], eps, res)
             qkv = self._linear(xn, (l, "qkv"), route_prev, gated)
             # RoPE and the head-major layouts in one pass; q carries the 1/sqrt(d) scaling
-            q, k, v = K.qkv_rope(qkv, cos, sin, B, S, Hq, Hkv, d, d ** -0.5)
-            att, H = _attention_entropy(q, k, v, 1.0, causal=True)
-            att = att.transpose(1, 2).reshape(T, Hq * d)
+            if fused_att:
+                # scores, probabilities and entropies stay on chip; att comes out token-major
+                q, k, vt = K.qkv_rope(qkv, cos, sin, B, S, Hq, Hkv, d, d ** -0.5, v_transposed=True)
+                att, H = K.attention_causal(q, k, vt)
+            else:
+                q, k, v = K.qkv_rope(qkv, cos, sin, B, S, Hq, Hkv, d, d ** -0.5)
+                att, H = _attention_entropy(q, k, v, 1.0, causal=True)
+                att = att.transpose(1, 2).reshape(T, Hq * d)
             route_cur = self._route(H.mean(dim=1).reshape(T).contiguous(), counts_log) if gated else None
             o = self._linear(att, (l, "o"), route_cur, gated)
             x, xn = K.add_rmsnorm(x, self.p[f"{l}.ln2"], eps, o)

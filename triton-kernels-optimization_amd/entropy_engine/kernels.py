@@ -448,17 +448,47 @@ def add_rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float, y: torch.Tensor | 
 
 
 def qkv_rope(qkv: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, B: int, S: int, Hq: int, Hkv: int, d: int,
-             q_scale: float = 1.0):
+             q_scale: float = 1.0, v_transposed: bool = False):
     """q [B, Hq, S, d], k, v [B, Hkv, S, d] from a fused projection output [B*S, (Hq+2Hkv)*d],
-    rotary-embedded (x*cos + rotate_half(x)*sin per fp16 op; cos/sin [S, d]); q scaled by q_scale."""
+    rotary-embedded (x*cos + rotate_half(x)*sin per fp16 op; cos/sin [S, d]); q scaled by q_scale.
+    v_transposed: the third output is attention_causal's vt [B, Hkv, d, S] instead (within each
+    16-token group the order 0-3, 8-11, 4-7, 12-15; see VT_ORDER)."""
     dev = _require_cuda(qkv, cos, sin)
     ld = _rowmajor(qkv, "qkv")
     cos = cos.reshape(S, d).contiguous()
     sin = sin.reshape(S, d).contiguous()
     q = torch.empty((B, Hq, S, d), dtype=torch.float16, device=dev)
     k = torch.empty((B, Hkv, S, d), dtype=torch.float16, device=dev)
-    v = torch.empty((B, Hkv, S, d), dtype=torch.float16, device=dev)
+    v = torch.empty((B, Hkv, d, S) if v_transposed else (B, Hkv, S, d), dtype=torch.float16, device=dev)
+    fn = _lib.lib().ee_qkv_rope_vt if v_transposed else _lib.lib().ee_qkv_rope
     with torch.cuda.device(dev):
-        check(_lib.lib().ee_qkv_rope(engine(), ptr(qkv), ld, ptr(cos), ptr(sin), ptr(q), ptr(k), ptr(v), B, S, Hq,
-                                     Hkv, d, float(q_scale), stream_handle()))
+        check(fn(engine(), ptr(qkv), ld, ptr(cos), ptr(sin), ptr(q), ptr(k), ptr(v), B, S, Hq, Hkv, d, float(q_scale),
+                 stream_handle()))
     return q, k, v
+
+
+# Token order of each 16-token group in attention_causal's vt layout: stored position p holds token VT_ORDER[p].
+VT_ORDER = (0, 1, 2, 3, 8, 9, 10, 11, 4, 5, 6, 7, 12, 13, 14, 15)
+
+
+def attention_causal(q: torch.Tensor, k: torch.Tensor, vt: torch.Tensor, out: torch.Tensor | None = None):
+    """Fused causal grouped-query attention with per-row entropy (head_dim 64):
+    q [B, Hq, S, 64] (already scaled), k [B, Hkv, S, 64], vt from qkv_rope(v_transposed=True).
+    Returns (out [B*S, Hq*64] fp16, token-major, H [B, Hq, S] f32): softmax(q k^T) v over keys <= query,
+    and each probability row's Shannon entropy."""
+    dev = _require_cuda(q, k, vt, out)
+    B, Hq, S, d = q.shape
+    Hkv = k.shape[1]
+    if k.shape != (B, Hkv, S, d) or vt.shape != (B, Hkv, d, S):
+        raise ValueError(f"shape mismatch: q {tuple(q.shape)}, k {tuple(k.shape)}, vt {tuple(vt.shape)}")
+    for t_, n in ((q, "q"), (k, "k"), (vt, "vt")):
+        if t_.dtype != torch.float16 or not t_.is_contiguous():
+            raise ValueError(f"{n} must be contiguous fp16")
+    if out is None:
+        out = torch.empty((B * S, Hq * d), dtype=torch.float16, device=dev)
+    ld_out = _rowmajor(out, "out")
+    h = torch.empty((B, Hq, S), dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        check(_lib.lib().ee_attention_causal(engine(), ptr(q), ptr(k), ptr(vt), ptr(out), ld_out, ptr(h), B, S, Hq,
+                                             Hkv, d, stream_handle()))
+    return out, h
