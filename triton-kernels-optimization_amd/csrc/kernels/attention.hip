@@ -13,11 +13,15 @@
 //
 // Keys stream through LDS in blocks of 64 (K rows and V^T rows, direct-to-LDS
 // DMA, double-buffered) with an online maximum.  Per lane and query row the
-// kernel keeps c = entries equal to the running max m, z = sum e^(x - m) over
-// the other entries and t = sum e^(x - m) (x - m), rescaled by e^(m_old - m_new)
-// when m grows; H = ln c + log1p(z / c) - t / (c + z), the cancellation-free
-// form softmax_entropy.hip uses.  The output accumulates fp16(e^(x - m)) v in
-// f32, rescaled the same way, and is divided by Z = c + z at the end.
+// kernel keeps z = sum e^(x - m) and t = sum e^(x - m) (x - m) over its keys,
+// rescaled by e^(m_old - m_new) when the running max m grows; H = ln Z - T / Z
+// over the lane pair.  (softmax_entropy.hip uses a cancellation-free form that
+// keeps full relative precision for nearly one-hot rows; here H has ~1e-7
+// absolute error there, which routing at thresholds of order 1 does not see,
+// and the per-element test that form needs would cost a third of the kernel:
+// at head_dim 64 the per-score VALU work, not the MFMAs, bounds it.)  The
+// output accumulates fp16(e^(x - m)) v in f32, rescaled the same way, and is
+// divided by Z at the end.
 //
 // Workgroup: one block of 64 queries of W query heads (W = 2 or 4 waves, one
 // head each) that share one kv head, so every K/V block staged in LDS serves W
@@ -53,16 +57,16 @@ EE_DEV void att_dma16(const void* sbase, uint32_t voff, uint32_t lds_base) {
 // the 16 rows one ds_read_b128 pass serves hit 16 distinct bank groups.
 EE_DEV uint32_t att_off(int row, int chunk) { return (uint32_t)(row * 128 + ((chunk ^ ((row >> 1) & 7)) << 4)); }
 
-// x - m for the low / high fp16 half of a packed word in one v_fma_mix_f32
-// (x * 1 + (-m): a single rounding, the value of converting x, then subtracting).
-EE_DEV float att_sub_lo(uint32_t u, float negm) {
+// (x - m) log2(e) for the low / high fp16 half of a packed word in one
+// v_fma_mix_f32: x * log2(e) + (-m log2(e)), a single rounding.
+EE_DEV float att_l2_lo(uint32_t u, float negm2) {
     float r;
-    asm("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(u), "v"(negm));
+    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(u), "v"(LOG2E), "v"(negm2));
     return r;
 }
-EE_DEV float att_sub_hi(uint32_t u, float negm) {
+EE_DEV float att_l2_hi(uint32_t u, float negm2) {
     float r;
-    asm("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(u), "v"(negm));
+    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(u), "v"(LOG2E), "v"(negm2));
     return r;
 }
 
@@ -77,7 +81,12 @@ EE_DEV void attn_causal_d64(const EeAttnArgs& a) {
     const int r32 = lane & 31, hi = lane >> 5;
     const int nqb = a.S >> 6, hgroups = a.Hq / W, G = a.Hq / a.Hkv;
     const int ngrp = a.B * hgroups;
-    const int qb = nqb - 1 - (int)blockIdx.x / ngrp;     // longest key ranges are dispatched first
+    // Query block order: the first half of the grid runs the longest key ranges
+    // (qb = nqb - 1, nqb - 2, ...), the second half the mirror images (qb = 0, 1,
+    // ...), so workgroup i + N/2, which the dispatcher places beside workgroup i
+    // (two fit per CU), brings qb' = nqb - 1 - qb: nqb + 1 key steps per CU.
+    const int rank = (int)blockIdx.x / ngrp, hrank = (nqb + 1) >> 1;
+    const int qb = rank < hrank ? nqb - 1 - rank : rank - hrank;
     const int grp = (int)blockIdx.x % ngrp;
     const int b = grp / hgroups, hg = grp % hgroups;
     const int hq = hg * W + wave, hkv = (hg * W) / G;
@@ -123,12 +132,14 @@ EE_DEV void attn_causal_d64(const EeAttnArgs& a) {
 #pragma unroll
         for (int dc = 0; dc < 4; ++dc) qf[rb][dc] = *(const u32x4*)(qrow + (rb * 32 + r32) * 64 + dc * 16 + hi * 8);
 
+    // Running row max (below every clamped score at the start), and per lane
+    // z = sum e, t = sum e * (x - m) log2(e) over the lane's keys.
     f32x16 o[2][2];
-    float m[2], c[2], z[2], t[2];
+    float m[2], z[2], t[2];
 #pragma unroll
     for (int rb = 0; rb < 2; ++rb) {
-        m[rb] = -INFINITY;
-        c[rb] = z[rb] = t[rb] = 0.0f;
+        m[rb] = -131008.0f;
+        z[rb] = t[rb] = 0.0f;
 #pragma unroll
         for (int db = 0; db < 2; ++db) o[rb][db] = f32x16{};
     }
@@ -144,11 +155,10 @@ EE_DEV void attn_causal_d64(const EeAttnArgs& a) {
 
         // scores, rounded to fp16 and packed: xh[rb][kb][w] holds keys r = 2w, 2w + 1 of
         // block (rb, kb); lane holds query 32 rb + (l & 31), key 64 st + 32 kb +
-        // 8 (r / 4) + 4 (l >> 5) + r % 4.  Masked keys (> query) and -inf scores become
-        // -65504: e = 0 and e * (x - m) = 0 without a per-element guard.
-        const bool diag = st == qb;
+        // 8 (r / 4) + 4 (l >> 5) + r % 4.  On the diagonal step, keys > query become
+        // -65504 (e = 0, e * (x - m) = 0).
         uint32_t xh[2][2][8];
-        float mx[2] = {-INFINITY, -INFINITY};
+        f16x2 mx2[2] = {f16x2{(f16)-65504.0f, (f16)-65504.0f}, f16x2{(f16)-65504.0f, (f16)-65504.0f}};
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) {
             u32x4 kf[4];
@@ -159,38 +169,41 @@ EE_DEV void attn_causal_d64(const EeAttnArgs& a) {
                 f32x16 acc = f32x16{};
 #pragma unroll
                 for (int dc = 0; dc < 4; ++dc) acc = mma16(kf[dc], qf[rb][dc], acc);
-                float v[16];
+                if (st == qb) {                       // wave-uniform: the diagonal step only
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    v[r] = f16_round(acc[r]);
-                    const int kk = kb * 32 + (r >> 2) * 8 + hi * 4 + (r & 3);
-                    if ((diag && kk > rb * 32 + r32) || v[r] < -65504.0f) v[r] = -65504.0f;
-                    mx[rb] = fmaxf(mx[rb], v[r]);
+                    for (int r = 0; r < 16; ++r) {
+                        const int kk = kb * 32 + (r >> 2) * 8 + hi * 4 + (r & 3);
+                        acc[r] = kk > rb * 32 + r32 ? -65504.0f : fmaxf(acc[r], -65504.0f);
+                    }
                 }
 #pragma unroll
-                for (int w = 0; w < 8; ++w) xh[rb][kb][w] = pack_f16x2(v[2 * w], v[2 * w + 1]);
+                for (int w = 0; w < 8; ++w) {
+                    xh[rb][kb][w] = pack_f16x2(acc[2 * w], acc[2 * w + 1]);
+                    mx2[rb] = __builtin_elementwise_max(mx2[rb], f16x2_from_bits(xh[rb][kb][w]));
+                }
             }
         }
 
         __builtin_amdgcn_sched_barrier(0);           // phases stay apart: the scheduler would hoist LDS reads
 #pragma unroll
         for (int rb = 0; rb < 2; ++rb) {
-            const float mrow = fmaxf(mx[rb], __shfl_xor(mx[rb], 32));
-            const float mn = fmaxf(m[rb], mrow);
-            // rescale to the new max: the old max entries join z
-            if (mn > m[rb]) {
-                const float alpha = __builtin_amdgcn_exp2f((m[rb] - mn) * LOG2E);   // 0 at the first step
-                const float zc = z[rb] + c[rb];
-                t[rb] = zc > 0.0f ? alpha * (t[rb] + (m[rb] - mn) * zc) : 0.0f;
-                z[rb] = alpha * zc;
-                c[rb] = 0.0f;
+            float ml = fmaxf((float)mx2[rb].x, (float)mx2[rb].y);
+            ml = fmaxf(ml, __shfl_xor(ml, 32));
+            const float mn = fmaxf(m[rb], ml);
+            // rescale to the new max (alpha = 1 if unchanged; 0 at the first step,
+            // where m starts below every score): t is kept in log2 units
+            const float d2 = (m[rb] - mn) * LOG2E;
+            const float alpha = __builtin_amdgcn_exp2f(d2);
+            t[rb] = alpha * (t[rb] + d2 * z[rb]);
+            z[rb] = alpha * z[rb];
+            if (__any(mn > m[rb])) {                  // wave vote: skip the rescale when no row max grew
 #pragma unroll
                 for (int db = 0; db < 2; ++db)
 #pragma unroll
                     for (int r = 0; r < 16; ++r) o[rb][db][r] *= alpha;
             }
             m[rb] = mn;
-            const float negm = -mn;
+            const float negm2 = -mn * LOG2E;
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -198,12 +211,10 @@ EE_DEV void attn_causal_d64(const EeAttnArgs& a) {
                     float e2[2];
 #pragma unroll
                     for (int h = 0; h < 2; ++h) {
-                        const float sv_ = h ? att_sub_hi(xh[rb][kb][w], negm) : att_sub_lo(xh[rb][kb][w], negm);
-                        const float e = __builtin_amdgcn_exp2f(sv_ * LOG2E);
-                        const bool top = sv_ == 0.0f;
-                        c[rb] += top ? 1.0f : 0.0f;
-                        z[rb] += top ? 0.0f : e;
-                        t[rb] += e * sv_;
+                        const float s2 = h ? att_l2_hi(xh[rb][kb][w], negm2) : att_l2_lo(xh[rb][kb][w], negm2);
+                        const float e = __builtin_amdgcn_exp2f(s2);
+                        z[rb] += e;
+                        t[rb] += e * s2;
                         e2[h] = e;
                     }
                     xh[rb][kb][w] = pack_f16x2(e2[0], e2[1]);   // now the fp16 probability (unnormalised)
@@ -233,11 +244,9 @@ EE_DEV void attn_causal_d64(const EeAttnArgs& a) {
     uint8_t* tile = smem + wave * 8192;               // 64 rows x 128 B of this wave's output
 #pragma unroll
     for (int rb = 0; rb < 2; ++rb) {
-        const float cs = c[rb] + __shfl_xor(c[rb], 32);
-        const float zs = z[rb] + __shfl_xor(z[rb], 32);
+        const float L = z[rb] + __shfl_xor(z[rb], 32);
         const float ts = t[rb] + __shfl_xor(t[rb], 32);
-        const float L = cs + zs;
-        const float Hs = logf(cs) + log1pf(zs / cs) - ts / L;
+        const float Hs = logf(L) - 0.69314718055994531f * ts / L;
         const int qrow_i = q0 + rb * 32 + r32;
         if (hi == 0) a.h[((int64_t)b * a.Hq + hq) * S + qrow_i] = Hs;
         const float inv = 1.0f / L;
