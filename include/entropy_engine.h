@@ -172,6 +172,14 @@ int ee_gemm(ee_engine* eng, int32_t kind, const void* a, int64_t lda, const void
  * idx = stable partition [INT8 rows | FP8 rows | FP16 rows]; counts[3]. */
 int ee_route(ee_engine* eng, const float* h, int64_t rows, double tau_low, double tau_high,
              int32_t* tier, int32_t* idx, int32_t* counts, ee_stream_t stream);
+/* The same on the mean over heads of per-head row entropies h [B, heads, S]
+ * (ee_attention_causal's entropy output): row r = b * S + s is routed on
+ * (h[b, 0, s] + ... + h[b, heads - 1, s]) / heads, summed in head order.  The
+ * reference routes on the mean of its attention entropies over heads and
+ * queries (EE/python/dispatch.py:243-245, one value per call); this keeps one
+ * value per token. */
+int ee_route_heads(ee_engine* eng, const float* h, int32_t B, int32_t heads, int32_t S, double tau_low,
+                   double tau_high, int32_t* tier, int32_t* idx, int32_t* counts, ee_stream_t stream);
 
 /* Row gather (scatter = 0: dst[r] = src[idx[off+r]]) or scatter
  * (scatter = 1: dst[idx[off+r]] = src[r]) for r < counts[tier] (or rows). */

@@ -484,6 +484,23 @@ def test_route_matches_oracle(ee, orc, R):
     assert np.array_equal(host(counts), c_ref)
 
 
+@pytest.mark.parametrize("B,Hh,S", [(8, 32, 512), (2, 4, 64), (3, 1, 100), (1, 5, 7)])
+def test_route_heads_matches_oracle(ee, orc, B, Hh, S):
+    """Routing on the per-token mean over heads: the oracle's route() applied to
+    the f32 mean summed in head order then divided (the kernel's arithmetic)."""
+    rng = np.random.default_rng(B * Hh + S)
+    H = (rng.random((B, Hh, S)) * 3).astype(np.float32)
+    acc = H[:, 0, :].copy()
+    for j in range(1, Hh):
+        acc = (acc + H[:, j, :]).astype(np.float32)
+    mean = (acc / np.float32(Hh)).astype(np.float32).reshape(-1)
+    tier, idx, counts = ee.route_heads(cuda(H), 0.41, 1.68)
+    t_ref, i_ref, c_ref = orc.route(mean, 0.41, 1.68)
+    assert np.array_equal(host(tier), t_ref)
+    assert np.array_equal(host(idx), i_ref)
+    assert np.array_equal(host(counts), c_ref)
+
+
 def test_route_reference_sweep(ee):
     ent = cuda(np.float32([0.5, 1.0, 1.5, 2.0, 2.5, 3.0, 3.5, 4.0, 4.5, 5.0]))   # EE/python/benchmark.py:386
     for (tl, th), pct in {(1.0, 2.0): [10, 20, 70], (2.0, 3.5): [30, 30, 40], (3.5, 4.5): [60, 20, 20]}.items():

@@ -95,13 +95,16 @@ struct EeRoutedGemmArgs {
 
 // Per-row routing: tier + stable partition of row indices.
 struct EeRouteArgs {
-    const float* h;
+    const float* h;         // [rows], or with heads > 1 [rows / seq, heads, seq]: row r = b * seq + s
+                            // routes on the mean over heads of h[b, :, s]
     int32_t* tier;          // [rows]
     int32_t* idx;           // [rows]: rows of tier 0, then tier 1, then tier 2
     int32_t* counts;        // [3]
     int64_t rows;
     double tau_low;
     double tau_high;
+    int32_t heads;          // 1: h is per row
+    int32_t seq;
 };
 
 // Weight preparation (offline, once per layer).

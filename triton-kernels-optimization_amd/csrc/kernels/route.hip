@@ -8,6 +8,9 @@
 // ascending order, then the FP8 rows, then the FP16 rows; counts[3] their
 // sizes.  One 1024-thread workgroup; positions come from wave ballots
 // (mbcnt = popcount of the lower lanes' votes) and a scan of 16 wave totals.
+// With heads > 1 the routed value of row r = b * seq + s is the mean over
+// heads of h[b, :, s] (per-head attention-row entropies; summed in head order,
+// then divided), so the caller needs no separate reduction.
 #include "../common/ee_device.h"
 
 EE_DEV int route_tier(float h, double tl, double th) {
@@ -24,10 +27,21 @@ extern "C" __global__ void __launch_bounds__(1024) eek_route(EeRouteArgs a) {
     __shared__ int32_t base[3];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
 
-    // pass 1: totals per tier
+    // pass 1: tiers and totals per tier
     int32_t c[3] = {0, 0, 0};
     for (int64_t r = tid; r < a.rows; r += 1024) {
-        const int t = route_tier(a.h[r], a.tau_low, a.tau_high);
+        float hv;
+        if (a.heads == 1) {
+            hv = a.h[r];
+        } else {
+            // mean over heads: ascending sum, one rounded division
+            const int64_t b = r / a.seq, sq = r % a.seq;
+            const float* hp = a.h + b * a.heads * a.seq + sq;
+            float sum = 0.0f;
+            for (int j = 0; j < a.heads; ++j) sum += hp[(int64_t)j * a.seq];
+            hv = sum / (float)a.heads;
+        }
+        const int t = route_tier(hv, a.tau_low, a.tau_high);
         a.tier[r] = t;
         c[t]++;
     }
@@ -54,7 +68,7 @@ extern "C" __global__ void __launch_bounds__(1024) eek_route(EeRouteArgs a) {
     // pass 2: stable scatter, 1024 rows per step
     for (int64_t r0 = 0; r0 < a.rows; r0 += 1024) {
         const int64_t r = r0 + tid;
-        const int t = (r < a.rows) ? route_tier(a.h[r], a.tau_low, a.tau_high) : 3;
+        const int t = (r < a.rows) ? a.tier[r] : 3;  // written by this thread in pass 1
         uint32_t pos = 0;
 #pragma unroll
         for (int k = 0; k < 3; ++k) {

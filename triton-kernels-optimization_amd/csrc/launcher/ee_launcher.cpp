@@ -672,7 +672,19 @@ EE_EXPORT int ee_route(ee_engine* eng, const float* h, int64_t rows, double tau_
     if (rows < 0 || rows > 0x7fffffff) return fail(EE_ERR_INVALID_ARG, "rows out of range");
     if (!aligned(h, 4) || !aligned(tier, 4) || !aligned(idx, 4) || !aligned(counts, 4))
         return fail(EE_ERR_INVALID_ARG, "misaligned pointer");
-    EeRouteArgs a{h, tier, idx, counts, rows, tau_low, tau_high};
+    EeRouteArgs a{h, tier, idx, counts, rows, tau_low, tau_high, 1, 1};
+    return launch(eng, "eek_route", 1, 1, 1024, a, stream);
+}
+
+EE_EXPORT int ee_route_heads(ee_engine* eng, const float* h, int32_t B, int32_t heads, int32_t S, double tau_low,
+                             double tau_high, int32_t* tier, int32_t* idx, int32_t* counts, ee_stream_t stream) {
+    if (eng == nullptr || h == nullptr || tier == nullptr || idx == nullptr || counts == nullptr)
+        return fail(EE_ERR_INVALID_ARG, "NULL argument");
+    if (B < 0 || S < 0 || heads <= 0 || (int64_t)B * S > 0x7fffffff)
+        return fail(EE_ERR_INVALID_ARG, "bad shape (B, S >= 0, heads > 0, B * S < 2^31)");
+    if (!aligned(h, 4) || !aligned(tier, 4) || !aligned(idx, 4) || !aligned(counts, 4))
+        return fail(EE_ERR_INVALID_ARG, "misaligned pointer");
+    EeRouteArgs a{h, tier, idx, counts, (int64_t)B * S, tau_low, tau_high, heads, S > 0 ? S : 1};
     return launch(eng, "eek_route", 1, 1, 1024, a, stream);
 }
 

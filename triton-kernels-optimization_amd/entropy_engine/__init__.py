@@ -12,7 +12,8 @@ from .dispatch import (TINYLLAMA_1B, EntropyDispatchedLinear, EntropyDispatchedL
 from .engine import CubinEngine, EntropyMLPEngine, HsacoEngine
 from .kernels import (VT_ORDER, PackedWeight, add_rmsnorm, attention_causal, fp8_tensor_gemm, interleave_gate_up,
                       fused_softmax_entropy, gemm, prepare_weight,
-                      qkv_rope, quantize_activations, quantize_tensor_fp8, quantize_weight_codes, route, routed_linear,
+                      qkv_rope, quantize_activations, quantize_tensor_fp8, quantize_weight_codes, route, route_heads,
+                      routed_linear,
                       row_copy,
                       silu_mul, softmax_entropy, transpose_i8, triton_fp8_gemm, triton_fp16_gemm, triton_int8_gemm)
 
@@ -20,7 +21,7 @@ __all__ = [
     "EntropyDispatchedLinear", "PipelinedEntropyDispatcher", "PrecisionTier", "RowEntropyRouter",
     "EntropyDispatchedLlamaBlock", "EntropyGatedLlama", "TINYLLAMA_1B", "build_dispatched_llama",
     "quantize_weights_int8", "tier_of", "CubinEngine", "EntropyMLPEngine", "HsacoEngine", "PackedWeight", "fused_softmax_entropy",
-    "gemm", "prepare_weight", "quantize_activations", "quantize_weight_codes", "route", "routed_linear", "row_copy",
+    "gemm", "prepare_weight", "quantize_activations", "quantize_weight_codes", "route", "route_heads", "routed_linear", "row_copy",
     "fp8_tensor_gemm", "quantize_tensor_fp8",
     "silu_mul", "add_rmsnorm", "qkv_rope", "attention_causal", "VT_ORDER", "interleave_gate_up", "softmax_entropy",
     "transpose_i8",

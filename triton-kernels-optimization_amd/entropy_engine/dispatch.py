@@ -453,8 +453,10 @@ class EntropyGatedLlama:
         idx, counts = route
         return K.routed_linear(x2d, pw, idx, counts, swiglu=swiglu)
 
-    def _route(self, h_tok: torch.Tensor, counts_log: list):
-        _, idx, counts = K.route(h_tok, self.tau_low, self.tau_high)
+    def _route_heads(self, h: torch.Tensor, counts_log: list):
+        """Route tokens on the mean over heads of their attention-row entropies
+        h [B, Hq, S] (the mean taken inside the routing kernel)."""
+        _, idx, counts = K.route_heads(h, self.tau_low, self.tau_high)
         counts_log.append(counts)
         return idx, counts
 
@@ -488,7 +490,7 @@ class EntropyGatedLlama:
                 q, k, v = K.qkv_rope(qkv, cos, sin, B, S, Hq, Hkv, d, d ** -0.5)
                 att, H = _attention_entropy(q, k, v, 1.0, causal=True)
                 att = att.transpose(1, 2).reshape(T, Hq * d)
-            route_cur = self._route(H.mean(dim=1).reshape(T).contiguous(), counts_log) if gated else None
+            route_cur = self._route_heads(H, counts_log) if gated else None
             o = self._linear(att, (l, "o"), route_cur, gated)
             x, xn = K.add_rmsnorm(x, self.p[f"{l}.ln2"], eps, o)
             act = self._linear(xn, (l, "gu"), route_cur, gated, swiglu=True)

@@ -344,6 +344,24 @@ def route(h: torch.Tensor, tau_low: float, tau_high: float):
     return tier, idx, counts
 
 
+def route_heads(h: torch.Tensor, tau_low: float, tau_high: float):
+    """route() on the per-token mean over heads of h [B, heads, S] (float32): token
+    b * S + s is routed on (h[b, 0, s] + ... + h[b, heads-1, s]) / heads, summed in
+    head order.  Returns (tier int32 [B*S], idx int32 [B*S], counts int32 [3])."""
+    dev = _require_cuda(h)
+    if h.dtype != torch.float32 or h.dim() != 3 or not h.is_contiguous():
+        raise TypeError("entropy must be a contiguous [B, heads, S] float32 tensor")
+    B, Hh, S = h.shape
+    R = B * S
+    tier = torch.empty(R, dtype=torch.int32, device=dev)
+    idx = torch.empty(R, dtype=torch.int32, device=dev)
+    counts = torch.empty(3, dtype=torch.int32, device=dev)
+    with torch.cuda.device(dev):
+        check(_lib.lib().ee_route_heads(engine(), ptr(h), B, Hh, S, float(tau_low), float(tau_high), ptr(tier),
+                                        ptr(idx), ptr(counts), stream_handle()))
+    return tier, idx, counts
+
+
 def row_copy(src: torch.Tensor, idx: torch.Tensor, counts=None, tier: int = 0, scatter: bool = False,
              out: torch.Tensor | None = None) -> torch.Tensor:
     """Gather (dst[r] = src[idx[off+r]]) or scatter (dst[idx[off+r]] = src[r]) whole rows."""
