@@ -236,17 +236,20 @@ int launch(ee_engine* e, const std::string& name, int64_t gx, int64_t gy, int bl
 
 // (VPT, WPR) for a register-resident row kernel: VPT 16-byte vectors per lane,
 // WPR wave64s per row, VPT * WPR * 512 >= len: the fewest waves per row that
-// still put min_waves waves on the chip (1024 SIMDs).  The softmax kernel takes
-// 4096 (~4 per SIMD; more did not help, and a row split costs barriers); the
-// quantisers 16384 (measured 10-15% faster at M = 4096, K = 2048 / 5632).
-bool pick_row_cfg(int64_t len, int64_t rows, int64_t forced_wpr, int& vpt, int& wpr, int64_t min_waves = 4096) {
+// still put min_waves waves on the chip (1024 SIMDs) with VPT <= max_vpt.  The
+// softmax kernel takes 4096.  The quantisers take 4096 with VPT <= 6, measured
+// from graph replays at the configs' and the Llama's shapes: [4096, 2048] 1 x 4
+// 5.0 us (4 waves x 1: 6.1), [4096, 4096] 2 x 4 8.9 (4 x 2: 10.0), [4096, 5632]
+// 2 x 6 12.4 (4 x 3: 12.8), [1024, 4096] 4 x 2 3.9 (2 x 4: 4.0).
+bool pick_row_cfg(int64_t len, int64_t rows, int64_t forced_wpr, int& vpt, int& wpr, int64_t min_waves = 4096,
+                  int max_vpt = 8) {
     const int options[3] = {1, 2, 4};
     int best = -1;
     for (int w : options) {
         if (forced_wpr && w != forced_wpr) continue;
         int v = (int)cdiv(len, 512LL * w);
         if (v < 1) v = 1;
-        if (v > 8) continue;
+        if (v > (forced_wpr ? 8 : max_vpt) && !(w == 4 && v <= 8)) continue;   // 4 waves: any VPT the kernels have
         best = w;
         if (forced_wpr || rows * w >= min_waves) break;
     }
@@ -479,7 +482,7 @@ EE_EXPORT int ee_softmax_entropy(ee_engine* eng, const void* x, void* p, float* 
 static int launch_quant(ee_engine* eng, const EeQuantArgs& a, ee_stream_t stream) {
     const bool vec_ok = aligned(a.x, 16) && aligned(a.codes, 8) && a.ld_x % 8 == 0 && a.ld_c % 8 == 0;
     int vpt = 0, wpr = 0;
-    if (vec_ok && pick_row_cfg(a.K, a.M, opt(eng, "quant_wpr"), vpt, wpr, 16384)) {
+    if (vec_ok && pick_row_cfg(a.K, a.M, opt(eng, "quant_wpr"), vpt, wpr, 4096, 6)) {
         const std::string name = "eek_quant_v" + std::to_string(vpt) + "_w" + std::to_string(wpr);
         return launch(eng, name, cdiv(a.M, 4 / wpr), 1, EE_BLOCK, a, stream);
     }
