@@ -18,8 +18,9 @@
 // over the lane pair.  (softmax_entropy.hip uses a cancellation-free form that
 // keeps full relative precision for nearly one-hot rows; here H has ~1e-7
 // absolute error there, which routing at thresholds of order 1 does not see,
-// and the per-element test that form needs would cost a third of the kernel:
-// at head_dim 64 the per-score VALU work, not the MFMAs, bounds it.)  The
+// and the per-element test that form needs (a compare, two selects and an add
+// per score) would add roughly a third to the per-score VALU work, which at
+// head_dim 64 bounds the kernel, not the MFMAs.)  The
 // output accumulates fp16(e^(x - m)) v in f32, rescaled the same way, and is
 // divided by Z at the end.
 //
