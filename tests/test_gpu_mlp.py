@@ -285,8 +285,9 @@ def pipeline(request):
 
 @pytest.mark.parametrize("M,K,F", [(300, 512, 320), (1024, 2048, 1408), (1, 128, 32)])
 def test_swiglu_gemm_equals_gemm_then_silu(ee, orc, M, K, F, pipeline):
-    """The SwiGLU epilogue (every tier, every pipeline) gives the bits of the plain
-    GEMM on the same interleaved operand followed by silu_mul."""
+    """The SwiGLU epilogue (every tier, every pipeline, and the int8-weight W8A16
+    kind) gives the bits of the plain GEMM on the same interleaved operand
+    followed by silu_mul."""
     rng = np.random.default_rng(M + K + F)
     W = (rng.standard_normal((2 * F, K)) / np.sqrt(K)).astype(np.float16)
     codes, scale = ee.quantize_weight_codes(cuda(W))
@@ -295,7 +296,7 @@ def test_swiglu_gemm_equals_gemm_then_silu(ee, orc, M, K, F, pipeline):
     ci, si = ee.quantize_activations(x, "dispatcher")
     cf, sf = ee.quantize_activations(x, "fp8")
     for kind, a, b, sa, sb in (("int8", ci, pw.i8, si, pw.scale), ("fp8", cf, pw.f8, sf, pw.scale),
-                               ("fp16", x, pw.f16, None, None)):
+                               ("fp16", x, pw.f16, None, None), ("w8a16", x, pw.i8, None, pw.scale)):
         fused = ee.gemm(kind, a, b, sa, sb, swiglu=True)
         ref = ee.silu_mul(deinterleave_cols(ee.gemm(kind, a, b, sa, sb)).contiguous())
         assert fused.shape == (M, F)
