@@ -177,11 +177,13 @@ def torch_attention_entropy(q, k, v):
     return p @ vr, H
 
 
-@pytest.mark.parametrize("B,S,Hq,Hkv", [(2, 512, 32, 4), (1, 64, 4, 2), (2, 192, 4, 2), (1, 128, 8, 1), (3, 256, 8, 2)])
+@pytest.mark.parametrize("B,S,Hq,Hkv", [(2, 512, 32, 4), (1, 64, 4, 2), (2, 192, 4, 2), (1, 128, 8, 1), (3, 256, 8, 2),
+                                       (1, 1024, 8, 2), (1, 2048, 4, 1)])
 def test_fused_attention_entropy(ee, B, S, Hq, Hkv):
     """attention_causal (scores kept in registers, online max) against the fp32
     reference and against the unfused path (fp16 scores, softmax_entropy kernel,
-    product with v): out within fp16 rounding of the probabilities, H within 1e-3."""
+    product with v): out within fp16 rounding of the probabilities; H within 1e-4
+    of the unfused path."""
     from entropy_engine.dispatch import _attention_entropy
     d = 64
     g = torch.Generator(device="cuda").manual_seed(B * S + Hq)
@@ -199,11 +201,16 @@ def test_fused_attention_entropy(ee, B, S, Hq, Hkv):
     o = out.view(B, S, Hq, d).transpose(1, 2).float()
     assert torch.isfinite(o).all() and torch.isfinite(H).all()
     assert (o - ref_o).abs().max().item() <= 1e-2 * ref_o.abs().max().item()
-    assert torch.allclose(H, ref_h, rtol=1e-3, atol=1e-3)
+    # The fp32 reference rounds its own fp32 product to fp16; where that rounding and
+    # the kernel's (another summation order) land on neighbouring fp16 values for a
+    # dominant score, a long row's H moves by a few 1e-3 (seen: 5.4e-3 at S = 2048,
+    # with the unfused path off by the same amount).  The tight check is the next one.
+    assert torch.allclose(H, ref_h, rtol=1e-3, atol=1e-2)
     assert H[:, :, 0].abs().max().item() < 1e-6      # query 0 sees one key: H = 0
+    # against the unfused path (fp16 scores from hipBLASLt, softmax_entropy): measured <= 4.3e-6
     un_o, un_h = _attention_entropy(q, k, v, 1.0, causal=True)
     assert (o - un_o.float()).abs().max().item() <= 1e-2 * un_o.float().abs().max().item()
-    assert torch.allclose(H, un_h, rtol=1e-3, atol=1e-3)
+    assert torch.allclose(H, un_h, rtol=1e-4, atol=1e-4)
 
 
 def test_fused_attention_one_hot_and_uniform_rows(ee):
