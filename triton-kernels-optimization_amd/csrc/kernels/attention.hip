@@ -40,7 +40,6 @@
 #define LOG2E 1.4426950408889634f
 #define ATT_STAGE 16384                 // K block 64 x 128 B, then V^T block 64 x 128 B
 
-#define GPTR(p) ((const void __attribute__((address_space(1)))*)(p))
 #define LPTR(p) ((void __attribute__((address_space(3)))*)(p))
 
 // 16 bytes per lane from global memory (wave-uniform base + 32-bit per-lane byte
