@@ -228,6 +228,22 @@ int ee_add_rmsnorm(ee_engine* eng, const void* x, int64_t ld_x, const void* y, i
                    void* x_out, int64_t ld_xo, void* n_out, int64_t ld_n, int64_t T, int64_t D, float eps,
                    ee_stream_t stream);
 
+/* ee_add_rmsnorm over the rows of a routing partition (idx/counts from ee_route
+ * or ee_route_heads), processed in slot order, that also writes the routed
+ * linear's INT8 and FP8 operands: slot i (source row idx[i]) of the INT8 slots
+ * [0, counts[0]) and FP8 slots [counts[0], counts[0] + counts[1]) gets its
+ * codes in codes + i * ld_c (D bytes) and its scale in scale[i] -- the bits
+ * ee_routed_linear's quantiser would write from n_out (the quantisers of
+ * EE/python/kernels.py:336-338 and :361).  FP16 slots get n_out only.  x_out
+ * and n_out are written for every row, as by ee_add_rmsnorm.  With
+ * ee_routed_gemm this removes the quantiser's launch and its read of n_out.
+ * No reference counterpart: the reference quantises inside each GEMM wrapper
+ * (EE/python/kernels.py:336-338, 361).  ld_c % 8 == 0, codes 8-byte aligned. */
+int ee_add_rmsnorm_route(ee_engine* eng, const void* x, int64_t ld_x, const void* y, int64_t ld_y, const void* w,
+                         void* x_out, int64_t ld_xo, void* n_out, int64_t ld_n, int64_t T, int64_t D, float eps,
+                         const int32_t* idx, const int32_t* counts, void* codes, int64_t ld_c, float* scale,
+                         ee_stream_t stream);
+
 /* Rotary embedding of the q and k heads of a fused q|k|v projection output
  * ([B*S, (Hq + 2*Hkv)*d], row stride ld) into head-major q [B, Hq, S, d],
  * k and v [B, Hkv, S, d]: x*cos + rotate_half(x)*sin with each op rounded to
@@ -313,6 +329,18 @@ int ee_routed_linear_swiglu(ee_engine* eng, const void* x, int64_t ld_x, int32_t
                             const int32_t* idx, const int32_t* counts, const int8_t* b_i8, const uint8_t* b_f8,
                             const void* b_f16, const float* b_scale, void* act, int64_t ld_act, void* ws_codes,
                             float* ws_scale, ee_stream_t stream);
+/* ee_routed_linear and ee_routed_linear_swiglu without their quantiser: the
+ * INT8 and FP8 slots' codes [M, K] (row stride K) and scales [M] were written
+ * beforehand, by ee_add_rmsnorm_route (the same bits as the quantiser).  x is
+ * still read for the FP16 slots.  One launch; K % 128 == 0. */
+int ee_routed_gemm(ee_engine* eng, const void* x, int64_t ld_x, int32_t M, int32_t K, int32_t N,
+                   const int32_t* idx, const int32_t* counts, const int8_t* b_i8, const uint8_t* b_f8,
+                   const void* b_f16, const float* b_scale, void* c, int64_t ldc, const void* codes,
+                   const float* scale, ee_stream_t stream);
+int ee_routed_gemm_swiglu(ee_engine* eng, const void* x, int64_t ld_x, int32_t M, int32_t K, int32_t N,
+                          const int32_t* idx, const int32_t* counts, const int8_t* b_i8, const uint8_t* b_f8,
+                          const void* b_f16, const float* b_scale, void* act, int64_t ld_act, const void* codes,
+                          const float* scale, ee_stream_t stream);
 /* Rows 0..F-1 (gate) and F..2F-1 (up) of src into the interleaved order above
  * (any row payload: int8 codes, e4m3 codes, fp16 weights, or 4-byte scales with
  * row_bytes = 4).  F % 32 == 0; not in place. */

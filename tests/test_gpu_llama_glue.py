@@ -240,3 +240,58 @@ def test_fused_attention_rejects_unsupported_shapes(ee):
         vt = torch.zeros(1, Hkv, d, S, device="cuda", dtype=torch.float16)
         with pytest.raises(_lib.EngineError):
             ee.attention_causal(q, k, vt)
+
+
+def _partition(ee, T, tl, th, seed):
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    h = torch.rand(T, device="cuda", generator=g) * 8
+    _, idx, counts = ee.route(h, tl, th)
+    return idx, counts
+
+
+@pytest.mark.parametrize("T,D,tl,th", [(4096, 2048, 2.34, 6.03), (300, 256, 2.34, 6.03), (77, 4096, 2.0, 4.0),
+                                       (64, 2048, 9.0, 9.0), (64, 2048, -1.0, 9.0), (64, 512, -1.0, -1.0)])
+def test_add_rmsnorm_route_equals_norm_then_quantiser(ee, T, D, tl, th):
+    """The slot-ordered norm writes add_rmsnorm's s and n bit for bit, and for
+    the INT8 / FP8 slots the codes and scales the routed quantisers write from
+    n (dispatcher INT8 for slots [0, c0), row-scaled e4m3 for the next c1).
+    Includes an all-zero row (zero scale: the slow conversion paths)."""
+    g = torch.Generator(device="cuda").manual_seed(T + D)
+    x = torch.randn(T, D, device="cuda", generator=g).half() * 3
+    y = torch.randn(T, D, device="cuda", generator=g).half()
+    x[3 % T] = 0
+    y[3 % T] = 0
+    w = (1 + 0.1 * torch.randn(D, device="cuda", generator=g)).half()
+    idx, counts = _partition(ee, T, tl, th, T)
+    s_ref, n_ref = ee.add_rmsnorm(x, w, 1e-5, y)
+    s, n, codes, scale = ee.add_rmsnorm_route(x, w, 1e-5, y, idx, counts)
+    assert torch.equal(s, s_ref) and torch.equal(n.view(torch.int16), n_ref.view(torch.int16))
+    c0, c1, _ = counts.tolist()
+    q8, s8 = ee.quantize_activations(n_ref, "dispatcher", idx, counts, tier=0)
+    qf, sf = ee.quantize_activations(n_ref, "fp8", idx, counts, tier=1)
+    assert torch.equal(codes[:c0], q8[:c0].view(torch.uint8))
+    assert torch.equal(scale[:c0].view(torch.int32), s8[:c0].view(torch.int32))
+    assert torch.equal(codes[c0:c0 + c1], qf[c0:c0 + c1])
+    assert torch.equal(scale[c0:c0 + c1].view(torch.int32), sf[c0:c0 + c1].view(torch.int32))
+
+
+@pytest.mark.parametrize("swiglu", [False, True])
+@pytest.mark.parametrize("T", [1000, 4096])
+def test_routed_gemm_on_prepared_codes(ee, T, swiglu):
+    """routed_linear on the codes of add_rmsnorm_route (one GEMM launch) equals
+    routed_linear with its own quantiser, bit for bit."""
+    D, N = 512, 768
+    g = torch.Generator(device="cuda").manual_seed(T)
+    x = torch.randn(T, D, device="cuda", generator=g).half()
+    y = torch.randn(T, D, device="cuda", generator=g).half()
+    w = torch.ones(D, device="cuda", dtype=torch.float16)
+    wt = (torch.randn(N, D, device="cuda", generator=g) * 0.02).half()
+    codes_w, scale_w = ee.quantize_weight_codes(wt)
+    if swiglu:
+        codes_w, scale_w = ee.interleave_gate_up(codes_w), ee.interleave_gate_up(scale_w)
+    pw = ee.PackedWeight(codes_w, scale_w).materialize()
+    idx, counts = _partition(ee, T, 2.34, 6.03, T + 1)
+    _, n, codes, scale = ee.add_rmsnorm_route(x, w, 1e-5, y, idx, counts)
+    ref = ee.routed_linear(n, pw, idx, counts, swiglu=swiglu)
+    got = ee.routed_linear(n, pw, idx, counts, swiglu=swiglu, quantized=(codes, scale))
+    assert torch.equal(got.view(torch.int16), ref.view(torch.int16))

@@ -877,3 +877,9 @@ def test_entropy_gated_llama_small(ee):
     unfused = m.forward(ids, gated=False).float()
     m.fused_attention = True
     assert (fp16 - unfused).abs().max() <= 1e-2 * unfused.abs().max()
+    # norms that write the routed linears' codes (add_rmsnorm_route + one GEMM
+    # launch) against norms followed by routed_linear's own quantiser
+    m.fused_norm_quant = False
+    plain = m.forward(ids).float()
+    m.fused_norm_quant = True
+    assert torch.equal(plain, out)

@@ -169,6 +169,15 @@ struct EeRmsNormArgs {
     float inv_d;            // f32(1 / D)
 };
 
+struct EeRmsNormRouteArgs {
+    EeRmsNormArgs n;        // as eek_add_rmsnorm; launch row i is source row idx[i]
+    const int32_t* idx;     // routing partition, slot -> row (T entries)
+    const int32_t* counts;  // rows per tier: slots [0, c0) INT8, [c0, c0 + c1) FP8, the rest FP16
+    uint8_t* codes;         // [T, D] codes of the INT8 and FP8 slots, row stride ld_c
+    float* scale;           // [T] scales of those slots
+    int64_t ld_c;
+};
+
 // eek_qkv_rope: rotary embedding of q and k and the head-major layouts.
 struct EeQkvRopeArgs {
     const uint16_t* qkv;    // fp16 [B*S, (Hq + 2*Hkv) * d]: q heads, k heads, v heads; row stride ld

@@ -8,6 +8,7 @@
 // no contraction into FMAs (which would skip the fp16 rounding of a product
 // before the add that follows it).
 #pragma clang fp contract(off)
+#include "../common/ee_quant_dev.h"
 
 // eek_add_rmsnorm: s = x + y (fp16, as torch adds fp16 tensors: f32 sum
 // rounded once to fp16), then RMSNorm as LlamaRMSNorm computes it in f32:
@@ -19,10 +20,7 @@
 // The mean's f32 sum runs in a different order than torch's reduction, so a
 // row can differ from torch in the last bit of its mean.
 template <int NC>
-EE_DEV void add_rmsnorm(const EeRmsNormArgs& a) {
-    const int lane = lane_id();
-    const int64_t row = (int64_t)blockIdx.x * (EE_BLOCK / 64) + wave_id();
-    if (row >= a.T) return;
+EE_DEV void rmsnorm_row(const EeRmsNormArgs& a, int64_t row, int lane, u32x4 (&o)[NC]) {
     const int nc = (int)(a.D >> 3);                   // 16-byte chunks per row
     const uint16_t* xr = a.x + row * a.ld_x;
     u32x4 s[NC];
@@ -54,18 +52,72 @@ EE_DEV void add_rmsnorm(const EeRmsNormArgs& a) {
         const int c = lane + 64 * i;
         if (c < nc) {
             const u32x4 w = *(const u32x4*)(a.w + 8 * c);
-            u32x4 o;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const float n0 = f16_round(f16_lo(s[i][j]) * r), n1 = f16_round(f16_hi(s[i][j]) * r);
-                o[j] = pack_f16x2(f16_lo(w[j]) * n0, f16_hi(w[j]) * n1);
+                o[i][j] = pack_f16x2(f16_lo(w[j]) * n0, f16_hi(w[j]) * n1);
             }
-            *(u32x4*)(a.n_out + row * a.ld_n + 8 * c) = o;
+            *(u32x4*)(a.n_out + row * a.ld_n + 8 * c) = o[i];
         }
     }
 }
-#define EE_RMSNORM(NC) \
-    extern "C" __global__ void __launch_bounds__(EE_BLOCK) eek_add_rmsnorm_c##NC(EeRmsNormArgs a) { add_rmsnorm<NC>(a); }
+
+template <int NC>
+EE_DEV void add_rmsnorm(const EeRmsNormArgs& a) {
+    const int64_t row = (int64_t)blockIdx.x * (EE_BLOCK / 64) + wave_id();
+    if (row >= a.T) return;
+    u32x4 o[NC];
+    rmsnorm_row<NC>(a, row, lane_id(), o);
+}
+
+// eek_add_rmsnorm_route: the same norm over the rows of a routing partition in
+// slot order (slot i is source row idx[i]; slots [0, c0) are INT8, [c0, c0 + c1)
+// FP8, the rest FP16), which also quantises the normalised rows of the INT8 and
+// FP8 slots into slot i of the routed linear's workspace: the codes and scales
+// the routed quantiser (quant.hip, EE_QUANT_ROUTED_I8_F8) would write from
+// n_out, with the same arithmetic (ee_quant_dev.h), without reading n_out back.
+template <int NC>
+EE_DEV void add_rmsnorm_route(const EeRmsNormRouteArgs& ra) {
+    const EeRmsNormArgs& a = ra.n;
+    const int lane = lane_id();
+    const int64_t slot = (int64_t)blockIdx.x * (EE_BLOCK / 64) + wave_id();
+    if (slot >= a.T) return;
+    const int64_t row = ra.idx[slot];
+    u32x4 o[NC];
+    rmsnorm_row<NC>(a, row, lane, o);
+    const int64_t c0 = ra.counts[0], c01 = c0 + ra.counts[1];
+    if (slot >= c01) return;                          // FP16 slot: the GEMM reads n_out
+    const int mode = slot < c0 ? EE_QUANT_I8_DISPATCH : EE_QUANT_F8_ROW;
+    const int nc = (int)(a.D >> 3);
+    uint32_t am = 0;
+#pragma unroll
+    for (int i = 0; i < NC; ++i)
+        if (lane + 64 * i < nc)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) am = absmax_bits(am, o[i][j]);
+    am = max(am & 0xffffu, am >> 16);
+    const float amax = f16_lo(wave_max_u32(am));
+    const RowScale rs = row_scale(mode, amax);
+    const QuantFast fast = quant_fast(mode, amax, rs);
+    uint8_t* cr = ra.codes + slot * ra.ld_c;
+#pragma unroll
+    for (int i = 0; i < NC; ++i) {
+        const int c = lane + 64 * i;
+        if (c < nc) {
+            uint32_t q[8];
+            *(u32x2*)(cr + 8 * c) = quant_chunk(mode, fast, rs, o[i], q);
+        }
+    }
+    if (lane == 0) ra.scale[slot] = rs.s;
+}
+
+#define EE_RMSNORM(NC)                                                                                       \
+    extern "C" __global__ void __launch_bounds__(EE_BLOCK) eek_add_rmsnorm_c##NC(EeRmsNormArgs a) {          \
+        add_rmsnorm<NC>(a);                                                                                  \
+    }                                                                                                        \
+    extern "C" __global__ void __launch_bounds__(EE_BLOCK) eek_add_rmsnorm_route_c##NC(EeRmsNormRouteArgs a) { \
+        add_rmsnorm_route<NC>(a);                                                                            \
+    }
 EE_RMSNORM(1)
 EE_RMSNORM(2)
 EE_RMSNORM(4)

@@ -709,7 +709,7 @@ EE_EXPORT int ee_row_copy(ee_engine* eng, const void* src, int64_t ld_src_bytes,
 static int routed_impl(ee_engine* eng, const void* x, int64_t ld_x, int32_t M, int32_t K, int32_t N,
                        const int32_t* idx, const int32_t* counts, const int8_t* b_i8, const uint8_t* b_f8,
                        const void* b_f16, const float* b_scale, void* c, int64_t ldc, void* ws_codes,
-                       float* ws_scale, int sw, ee_stream_t stream) {
+                       float* ws_scale, int sw, ee_stream_t stream, bool prequant = false) {
     if (eng == nullptr || x == nullptr || idx == nullptr || counts == nullptr || b_i8 == nullptr ||
         b_f8 == nullptr || b_f16 == nullptr || b_scale == nullptr || c == nullptr || ws_codes == nullptr ||
         ws_scale == nullptr)
@@ -726,14 +726,16 @@ static int routed_impl(ee_engine* eng, const void* x, int64_t ld_x, int32_t M, i
         !aligned(ws_codes, 16) || !aligned(ws_scale, 4) || !aligned(b_scale, 16) || !aligned(idx, 4) ||
         !aligned(counts, 4))
         return fail(EE_ERR_INVALID_ARG, "misaligned pointer");
+    if (prequant && K % 128 != 0)
+        return fail(EE_ERR_UNSUPPORTED, "the routed GEMM on prepared codes needs K % 128 == 0");
     if (M == 0) return EE_OK;
     int rc;
-    if (K % 128 == 0 && !opt(eng, "routed_unfused")) {
+    if (prequant || (K % 128 == 0 && !opt(eng, "routed_unfused"))) {
         // Two launches: one quantiser for the INT8 and FP8 slots, then the three
         // tier GEMMs as one grid (eek_gemm_routed), scattering rows through idx.
         EeQuantArgs qa{(const uint16_t*)x, ws_codes, ws_scale, idx, counts, M, K, ld_x, K, EE_QUANT_ROUTED_I8_F8, 0,
                        nullptr, 0};
-        if ((rc = launch_quant(eng, qa, stream))) return rc;
+        if (!prequant && (rc = launch_quant(eng, qa, stream))) return rc;
         EeRoutedGemmArgs ra{};
         ra.t[0] = EeGemmArgs{ws_codes, b_i8, (uint16_t*)c, nullptr, ws_scale, b_scale, nullptr, idx, counts,
                              K, K, ldc, M, N, K, EE_TIER_INT8, sw};
@@ -786,6 +788,22 @@ EE_EXPORT int ee_routed_linear_swiglu(ee_engine* eng, const void* x, int64_t ld_
                        ws_scale, 1, stream);
 }
 
+EE_EXPORT int ee_routed_gemm(ee_engine* eng, const void* x, int64_t ld_x, int32_t M, int32_t K, int32_t N,
+                             const int32_t* idx, const int32_t* counts, const int8_t* b_i8, const uint8_t* b_f8,
+                             const void* b_f16, const float* b_scale, void* c, int64_t ldc, const void* codes,
+                             const float* scale, ee_stream_t stream) {
+    return routed_impl(eng, x, ld_x, M, K, N, idx, counts, b_i8, b_f8, b_f16, b_scale, c, ldc, (void*)codes,
+                       (float*)scale, 0, stream, true);
+}
+
+EE_EXPORT int ee_routed_gemm_swiglu(ee_engine* eng, const void* x, int64_t ld_x, int32_t M, int32_t K, int32_t N,
+                                    const int32_t* idx, const int32_t* counts, const int8_t* b_i8,
+                                    const uint8_t* b_f8, const void* b_f16, const float* b_scale, void* act,
+                                    int64_t ld_act, const void* codes, const float* scale, ee_stream_t stream) {
+    return routed_impl(eng, x, ld_x, M, K, N, idx, counts, b_i8, b_f8, b_f16, b_scale, act, ld_act, (void*)codes,
+                       (float*)scale, 1, stream, true);
+}
+
 EE_EXPORT int ee_interleave_gate_up(ee_engine* eng, const void* src, int64_t ld_src_bytes, void* dst,
                                     int64_t ld_dst_bytes, int64_t F, int64_t row_bytes, ee_stream_t stream) {
     if (eng == nullptr || src == nullptr || dst == nullptr) return fail(EE_ERR_INVALID_ARG, "NULL argument");
@@ -825,9 +843,9 @@ EE_EXPORT int ee_silu_mul(ee_engine* eng, const void* gu, int64_t ld_gu, void* a
     return silu_mul_impl(eng, gu, ld_gu, act, ld_act, M, F, 0, stream);
 }
 
-EE_EXPORT int ee_add_rmsnorm(ee_engine* eng, const void* x, int64_t ld_x, const void* y, int64_t ld_y,
-                             const void* w, void* x_out, int64_t ld_xo, void* n_out, int64_t ld_n, int64_t T,
-                             int64_t D, float eps, ee_stream_t stream) {
+static int rmsnorm_args(ee_engine* eng, const void* x, int64_t ld_x, const void* y, int64_t ld_y, const void* w,
+                        void* x_out, int64_t ld_xo, void* n_out, int64_t ld_n, int64_t T, int64_t D, float eps,
+                        EeRmsNormArgs& a, const char*& name) {
     if (eng == nullptr || x == nullptr || w == nullptr || n_out == nullptr || (y != nullptr && x_out == nullptr))
         return fail(EE_ERR_INVALID_ARG, "NULL argument");
     if (T < 0 || D <= 0 || ld_x < D || ld_n < D || (y != nullptr && (ld_y < D || ld_xo < D)))
@@ -836,13 +854,38 @@ EE_EXPORT int ee_add_rmsnorm(ee_engine* eng, const void* x, int64_t ld_x, const 
         return fail(EE_ERR_UNSUPPORTED, "add_rmsnorm needs D % 8 == 0, D <= 4096 and strides that are multiples of 8");
     if (!aligned(x, 16) || !aligned(y, 16) || !aligned(w, 16) || !aligned(x_out, 16) || !aligned(n_out, 16))
         return fail(EE_ERR_INVALID_ARG, "misaligned pointer (16 B)");
-    if (T == 0) return EE_OK;
-    EeRmsNormArgs a{(const uint16_t*)x, (const uint16_t*)y, (const uint16_t*)w, (uint16_t*)x_out, (uint16_t*)n_out,
-                    T, D, ld_x, ld_y, ld_xo, ld_n, eps, 1.0f / (float)D};
+    a = EeRmsNormArgs{(const uint16_t*)x, (const uint16_t*)y, (const uint16_t*)w, (uint16_t*)x_out, (uint16_t*)n_out,
+                      T, D, ld_x, ld_y, ld_xo, ld_n, eps, 1.0f / (float)D};
     const int64_t nc = cdiv(D / 8, 64);                // 16-byte chunks per lane
-    const char* name = nc <= 1 ? "eek_add_rmsnorm_c1" : nc <= 2 ? "eek_add_rmsnorm_c2"
-                                                      : nc <= 4 ? "eek_add_rmsnorm_c4" : "eek_add_rmsnorm_c8";
-    return launch(eng, name, cdiv(T, EE_BLOCK / 64), 1, EE_BLOCK, a, stream);
+    name = nc <= 1 ? "c1" : nc <= 2 ? "c2" : nc <= 4 ? "c4" : "c8";
+    return EE_OK;
+}
+
+EE_EXPORT int ee_add_rmsnorm(ee_engine* eng, const void* x, int64_t ld_x, const void* y, int64_t ld_y,
+                             const void* w, void* x_out, int64_t ld_xo, void* n_out, int64_t ld_n, int64_t T,
+                             int64_t D, float eps, ee_stream_t stream) {
+    EeRmsNormArgs a;
+    const char* nc;
+    if (int rc = rmsnorm_args(eng, x, ld_x, y, ld_y, w, x_out, ld_xo, n_out, ld_n, T, D, eps, a, nc)) return rc;
+    if (T == 0) return EE_OK;
+    return launch(eng, std::string("eek_add_rmsnorm_") + nc, cdiv(T, EE_BLOCK / 64), 1, EE_BLOCK, a, stream);
+}
+
+EE_EXPORT int ee_add_rmsnorm_route(ee_engine* eng, const void* x, int64_t ld_x, const void* y, int64_t ld_y,
+                                   const void* w, void* x_out, int64_t ld_xo, void* n_out, int64_t ld_n, int64_t T,
+                                   int64_t D, float eps, const int32_t* idx, const int32_t* counts, void* codes,
+                                   int64_t ld_c, float* scale, ee_stream_t stream) {
+    EeRmsNormArgs a;
+    const char* nc;
+    if (int rc = rmsnorm_args(eng, x, ld_x, y, ld_y, w, x_out, ld_xo, n_out, ld_n, T, D, eps, a, nc)) return rc;
+    if (idx == nullptr || counts == nullptr || codes == nullptr || scale == nullptr)
+        return fail(EE_ERR_INVALID_ARG, "NULL argument");
+    if (ld_c < D || ld_c % 8 != 0) return fail(EE_ERR_INVALID_ARG, "bad codes stride (ld_c >= D, a multiple of 8)");
+    if (!aligned(codes, 8) || !aligned(scale, 4) || !aligned(idx, 4) || !aligned(counts, 4))
+        return fail(EE_ERR_INVALID_ARG, "misaligned pointer");
+    if (T == 0) return EE_OK;
+    EeRmsNormRouteArgs ra{a, idx, counts, (uint8_t*)codes, scale, ld_c};
+    return launch(eng, std::string("eek_add_rmsnorm_route_") + nc, cdiv(T, EE_BLOCK / 64), 1, EE_BLOCK, ra, stream);
 }
 
 static int qkv_rope_impl(ee_engine* eng, const void* qkv, int64_t ld, const void* cos_t, const void* sin_t,

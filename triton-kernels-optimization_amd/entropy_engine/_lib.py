@@ -67,6 +67,11 @@ SIGNATURES = {
                          ctypes.c_int),
     "ee_silu_mul": ([_p, _p, _i64, _p, _i64, _i64, _i64, _p], ctypes.c_int),
     "ee_add_rmsnorm": ([_p, _p, _i64, _p, _i64, _p, _p, _i64, _p, _i64, _i64, _i64, ctypes.c_float, _p], ctypes.c_int),
+    "ee_add_rmsnorm_route": ([_p, _p, _i64, _p, _i64, _p, _p, _i64, _p, _i64, _i64, _i64, ctypes.c_float, _p, _p, _p,
+                              _i64, _p, _p], ctypes.c_int),
+    "ee_routed_gemm": ([_p, _p, _i64, _i32, _i32, _i32, _p, _p, _p, _p, _p, _p, _p, _i64, _p, _p, _p], ctypes.c_int),
+    "ee_routed_gemm_swiglu": ([_p, _p, _i64, _i32, _i32, _i32, _p, _p, _p, _p, _p, _p, _p, _i64, _p, _p, _p],
+                              ctypes.c_int),
     "ee_qkv_rope": ([_p, _p, _i64, _p, _p, _p, _p, _p, _i32, _i32, _i32, _i32, _i32, ctypes.c_float, _p],
                     ctypes.c_int),
     "ee_qkv_rope_vt": ([_p, _p, _i64, _p, _p, _p, _p, _p, _i32, _i32, _i32, _i32, _i32, ctypes.c_float, _p],

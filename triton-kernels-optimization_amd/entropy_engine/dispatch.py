@@ -379,7 +379,10 @@ class EntropyGatedLlama:
     lm_head [V, D]).  RMSNorm and RoPE follow the Llama definitions, as fused
     kernels (add_rmsnorm: residual add + norm; qkv_rope: RoPE + head-major q/k/v,
     q pre-scaled by 1/sqrt(d)); SwiGLU is silu_mul; grouped-query attention
-    reads the shared k/v heads without copies."""
+    reads the shared k/v heads without copies.  A norm whose output feeds a
+    routed linear also writes that linear's INT8/FP8 operands
+    (add_rmsnorm_route; attribute fused_norm_quant = False turns it off), so the
+    linear runs without its quantiser pass."""
 
     def __init__(self, params: dict, cfg: dict, tau_low: float = 2.34, tau_high: float = 6.03):
         self.p = params
@@ -400,6 +403,7 @@ class EntropyGatedLlama:
         self.last_fractions = None
         self._rope_cache = {}
         self.fused_attention = True
+        self.fused_norm_quant = True
 
     @staticmethod
     def _pack(w: torch.Tensor, swiglu: bool = False) -> K.PackedWeight:
@@ -441,9 +445,11 @@ class EntropyGatedLlama:
             self._rope_cache[key] = (emb.cos().half().unsqueeze(0), emb.sin().half().unsqueeze(0))
         return self._rope_cache[key]
 
-    def _linear(self, x2d: torch.Tensor, key, route, gated: bool, swiglu: bool = False) -> torch.Tensor:
+    def _linear(self, x2d: torch.Tensor, key, route, gated: bool, swiglu: bool = False,
+                quantized=None) -> torch.Tensor:
         """x2d @ W^T; swiglu: W is gate|up and the result is silu(gate) * up (fused
-        into the GEMM epilogue on the gated path; a separate pass on the fp16 run)."""
+        into the GEMM epilogue on the gated path; a separate pass on the fp16 run).
+        quantized: x2d's INT8/FP8 operands under `route`, from add_rmsnorm_route."""
         if not gated:
             y = torch.matmul(x2d, self.fused[key].t())
             return K.silu_mul(y) if swiglu else y
@@ -451,7 +457,17 @@ class EntropyGatedLlama:
         if route is None:                    # no entropy yet: FP16 tier (W8A16), as the reference's default
             return K.gemm("fp16", x2d, pw.f16, swiglu=swiglu)
         idx, counts = route
-        return K.routed_linear(x2d, pw, idx, counts, swiglu=swiglu)
+        return K.routed_linear(x2d, pw, idx, counts, swiglu=swiglu, quantized=quantized)
+
+    def _norm(self, x, w, res, route, gated: bool):
+        """(x, xn, quantized): the residual add + RMSNorm; when the next linear is
+        routed (and K % 128 == 0), the same kernel writes its INT8/FP8 operands."""
+        if gated and route is not None and self.fused_norm_quant and x.shape[-1] % 128 == 0:
+            idx, counts = route
+            x, xn, codes, scale = K.add_rmsnorm_route(x, w, self.cfg["eps"], res, idx, counts)
+            return x, xn, (codes, scale)
+        x, xn = K.add_rmsnorm(x, w, self.cfg["eps"], res)
+        return x, xn, None
 
     def _route_heads(self, h: torch.Tensor, counts_log: list):
         """Route tokens on the mean over heads of their attention-row entropies
@@ -474,13 +490,12 @@ class EntropyGatedLlama:
         cos, sin = self._rope_tables(S, x.device)
         # the fused attention kernel's shapes (attention_causal); others take the unfused path
         fused_att = self.fused_attention and d == 64 and S % 64 == 0 and (Hq // Hkv) % 2 == 0
-        eps = c["eps"]
         counts_log = []
         route_prev = None
         res = None                                    # the pending residual branch, added by the next norm
         for l in range(c["layers"]):
-            x, xn = K.add_rmsnorm(x, self.p[f"{l}.ln1"], eps, res)
-            qkv = self._linear(xn, (l, "qkv"), route_prev, gated)
+            x, xn, xq = self._norm(x, self.p[f"{l}.ln1"], res, route_prev, gated)
+            qkv = self._linear(xn, (l, "qkv"), route_prev, gated, quantized=xq)
             # RoPE and the head-major layouts in one pass; q carries the 1/sqrt(d) scaling
             if fused_att:
                 # scores, probabilities and entropies stay on chip; att comes out token-major
@@ -492,12 +507,12 @@ class EntropyGatedLlama:
                 att = att.transpose(1, 2).reshape(T, Hq * d)
             route_cur = self._route_heads(H, counts_log) if gated else None
             o = self._linear(att, (l, "o"), route_cur, gated)
-            x, xn = K.add_rmsnorm(x, self.p[f"{l}.ln2"], eps, o)
-            act = self._linear(xn, (l, "gu"), route_cur, gated, swiglu=True)
+            x, xn, xq = self._norm(x, self.p[f"{l}.ln2"], o, route_cur, gated)
+            act = self._linear(xn, (l, "gu"), route_cur, gated, swiglu=True, quantized=xq)
             res = self._linear(act, (l, "down"), route_cur, gated)
             route_prev = route_cur
-        x, xn = K.add_rmsnorm(x, self.p["norm"], eps, res)
-        logits = self._linear(xn, "lm_head", route_prev, gated)
+        x, xn, xq = self._norm(x, self.p["norm"], res, route_prev, gated)
+        logits = self._linear(xn, "lm_head", route_prev, gated, quantized=xq)
         if gated:
             # rows per tier over every linear layer: each route feeds o/gate/up/down (4)
             # plus the next layer's q/k/v (3) or the LM head (1); layer 0's q/k/v run

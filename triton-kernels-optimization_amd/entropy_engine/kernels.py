@@ -380,10 +380,13 @@ def row_copy(src: torch.Tensor, idx: torch.Tensor, counts=None, tier: int = 0, s
 
 
 def routed_linear(x: torch.Tensor, pw: PackedWeight, idx: torch.Tensor, counts: torch.Tensor,
-                  out: torch.Tensor | None = None, workspace=None, swiglu: bool = False) -> torch.Tensor:
+                  out: torch.Tensor | None = None, workspace=None, swiglu: bool = False,
+                  quantized=None) -> torch.Tensor:
     """One tier per row: INT8 / FP8 / W8A16 GEMMs over the rows `idx`/`counts`
     assign them (from `route`), scattered back in place; no host sync.
-    swiglu: pw is an interleaved gate|up weight; the result is act [M, N/2]."""
+    swiglu: pw is an interleaved gate|up weight; the result is act [M, N/2].
+    quantized: (codes, scale) of x's INT8 and FP8 slots, from add_rmsnorm_route
+    (the GEMM launch alone; K % 128 == 0)."""
     dev = _require_cuda(x, idx, counts, out)
     if x.dtype != torch.float16:
         raise TypeError("x must be float16")
@@ -392,10 +395,18 @@ def routed_linear(x: torch.Tensor, pw: PackedWeight, idx: torch.Tensor, counts: 
         raise ValueError(f"K mismatch: x is {tuple(x.shape)}, weight is [{pw.N}, {pw.K}]")
     N = pw.N
     c = out if out is not None else torch.empty((M, N // 2 if swiglu else N), dtype=torch.float16, device=dev)
-    if workspace is None:
-        workspace = (torch.empty((M, K), dtype=torch.uint8, device=dev), torch.empty(M, dtype=torch.float32, device=dev))
-    ws_codes, ws_scale = workspace
-    fn = _lib.lib().ee_routed_linear_swiglu if swiglu else _lib.lib().ee_routed_linear
+    if quantized is not None:
+        ws_codes, ws_scale = quantized
+        if ws_codes.shape != (M, K) or ws_codes.dtype != torch.uint8 or not ws_codes.is_contiguous() \
+                or ws_scale.dtype != torch.float32 or ws_scale.numel() != M:
+            raise ValueError("quantized must be (uint8 [M, K] contiguous, float32 [M]) from add_rmsnorm_route")
+        fn = _lib.lib().ee_routed_gemm_swiglu if swiglu else _lib.lib().ee_routed_gemm
+    else:
+        if workspace is None:
+            workspace = (torch.empty((M, K), dtype=torch.uint8, device=dev),
+                         torch.empty(M, dtype=torch.float32, device=dev))
+        ws_codes, ws_scale = workspace
+        fn = _lib.lib().ee_routed_linear_swiglu if swiglu else _lib.lib().ee_routed_linear
     with torch.cuda.device(dev):
         check(fn(engine(), ptr(x), _rowmajor(x, "x"), M, K, N, ptr(idx), ptr(counts), ptr(pw.i8), ptr(pw.f8),
                  ptr(pw.f16), ptr(pw.scale), ptr(c), _rowmajor(c, "out"), ptr(ws_codes), ptr(ws_scale),
@@ -440,10 +451,7 @@ def silu_mul(gu: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
 
 # ---------------------------------------------------------------- Llama block elementwise work
 
-def add_rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float, y: torch.Tensor | None = None):
-    """(s, n): s = x + y (x itself when y is None), n = LlamaRMSNorm(s) with weight w,
-    each op in torch's precision; rows of the last dimension D (D % 8 == 0, D <= 4096)."""
-    dev = _require_cuda(x, w, y)
+def _rmsnorm_operands(x, w, y):
     D = x.shape[-1]
     x2 = x.reshape(-1, D)
     if x2.stride(-1) != 1 or x2.data_ptr() % 16 or (x2.shape[0] > 1 and x2.stride(0) % 8):
@@ -454,15 +462,43 @@ def add_rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float, y: torch.Tensor | 
         if y2.stride(-1) != 1 or y2.data_ptr() % 16 or (y2.shape[0] > 1 and y2.stride(0) % 8):
             y2 = y2.contiguous()
     T = x2.shape[0]
-    n = torch.empty((T, D), dtype=torch.float16, device=dev)
-    s = torch.empty((T, D), dtype=torch.float16, device=dev) if y is not None else x2
-    w = w.contiguous()
+    n = torch.empty((T, D), dtype=torch.float16, device=x.device)
+    s = torch.empty((T, D), dtype=torch.float16, device=x.device) if y is not None else x2
+    return x2, y2, s, n, w.contiguous(), T, D
+
+
+def add_rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float, y: torch.Tensor | None = None):
+    """(s, n): s = x + y (x itself when y is None), n = LlamaRMSNorm(s) with weight w,
+    each op in torch's precision; rows of the last dimension D (D % 8 == 0, D <= 4096)."""
+    dev = _require_cuda(x, w, y)
+    x2, y2, s, n, w, T, D = _rmsnorm_operands(x, w, y)
     with torch.cuda.device(dev):
         check(_lib.lib().ee_add_rmsnorm(engine(), ptr(x2), _rowmajor(x2, "x"), ptr(y2),
                                         _rowmajor(y2, "y") if y2 is not None else D, ptr(w),
                                         ptr(s) if y is not None else None, D, ptr(n), D, T, D, float(eps),
                                         stream_handle()))
     return s.view(x.shape), n.view(x.shape)
+
+
+def add_rmsnorm_route(x: torch.Tensor, w: torch.Tensor, eps: float, y: torch.Tensor | None,
+                      idx: torch.Tensor, counts: torch.Tensor):
+    """(s, n, codes, scale): add_rmsnorm's s and n, plus the routed linear's INT8
+    and FP8 operands of the rows of the partition idx/counts (from route or
+    route_heads): codes uint8 [T, D] and scale f32 [T] in slot order, the bits
+    routed_linear's quantiser writes from n.  Pass (codes, scale) to
+    routed_linear(..., quantized=...) to skip that quantiser."""
+    dev = _require_cuda(x, w, y, idx, counts)
+    x2, y2, s, n, w, T, D = _rmsnorm_operands(x, w, y)
+    if idx.dtype != torch.int32 or counts.dtype != torch.int32 or idx.numel() != T:
+        raise ValueError("idx must be int32 [T] and counts int32 [3] (from route)")
+    codes = torch.empty((T, D), dtype=torch.uint8, device=dev)
+    scale = torch.empty(T, dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        check(_lib.lib().ee_add_rmsnorm_route(engine(), ptr(x2), _rowmajor(x2, "x"), ptr(y2),
+                                              _rowmajor(y2, "y") if y2 is not None else D, ptr(w),
+                                              ptr(s) if y is not None else None, D, ptr(n), D, T, D, float(eps),
+                                              ptr(idx), ptr(counts), ptr(codes), D, ptr(scale), stream_handle()))
+    return s.view(x.shape), n.view(x.shape), codes, scale
 
 
 def qkv_rope(qkv: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, B: int, S: int, Hq: int, Hkv: int, d: int,
