@@ -34,11 +34,22 @@ extern "C" __global__ void __launch_bounds__(1024) eek_route(EeRouteArgs a) {
         if (a.heads == 1) {
             hv = a.h[r];
         } else {
-            // mean over heads: ascending sum, one rounded division
+            // mean over heads: ascending sum, one rounded division.  The loads
+            // go out 32 at a time before the adds: one workgroup walks every
+            // row, so a load-add chain would pay one memory latency per head
+            // (36 us instead of 10.6 us for [8, 32, 512]).
             const int64_t b = r / a.seq, sq = r % a.seq;
             const float* hp = a.h + b * a.heads * a.seq + sq;
             float sum = 0.0f;
-            for (int j = 0; j < a.heads; ++j) sum += hp[(int64_t)j * a.seq];
+            int j = 0;
+            for (; j + 32 <= a.heads; j += 32) {
+                float v[32];
+#pragma unroll
+                for (int u = 0; u < 32; ++u) v[u] = hp[(int64_t)(j + u) * a.seq];
+#pragma unroll
+                for (int u = 0; u < 32; ++u) sum += v[u];
+            }
+            for (; j < a.heads; ++j) sum += hp[(int64_t)j * a.seq];
             hv = sum / (float)a.heads;
         }
         const int t = route_tier(hv, a.tau_low, a.tau_high);
