@@ -155,7 +155,12 @@ extern "C" __global__ void __launch_bounds__(EE_BLOCK) eek_qkv_rope(EeQkvRopeArg
     // 8 d of a kv head, transposed in registers
     const int64_t n_v = a.v_t ? (int64_t)a.B * a.Hkv * (a.S >> 4) * (d >> 3) : T * a.Hkv * (d >> 3);
     const int64_t stride = (int64_t)gridDim.x * EE_BLOCK;
-    for (int64_t i = (int64_t)blockIdx.x * EE_BLOCK + threadIdx.x; i < n_qk + n_v; i += stride) {
+    // Work items: the v_t units first (each moves 16 rows, the longest items, so
+    // they start with the first workgroups), then the q/k chunk pairs, then the
+    // plain v chunks.
+    const int64_t n_vt = a.v_t ? n_v : 0;
+    for (int64_t i0 = (int64_t)blockIdx.x * EE_BLOCK + threadIdx.x; i0 < n_qk + n_v; i0 += stride) {
+        const int64_t i = i0 < n_vt ? i0 + n_qk : i0 - n_vt;   // index in the order q/k, v
         if (i < n_qk) {
             const int c = (int)(i % cpr);
             const int64_t th = i / cpr;
