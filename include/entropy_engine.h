@@ -126,7 +126,7 @@ int ee_quant_weight_i8(ee_engine* eng, const void* w, int64_t N, int64_t K, int6
 
 /* ---- FP8 e4m3 with one scale per tensor ------------------------------------
  * No counterpart in the reference, whose FP8 tier scales per row
- * (EE/python/kernels.py:361); BASELINE config 1 ("FP8 e4m3 with per-tensor
+ * (EE/python/kernels.py:361); benchmark config 1 ("FP8 e4m3 with per-tensor
  * amax scaling") names this scheme.  For x fp16 [M, K] (activations, or an
  * nn.Linear weight [N, K]):
  *   amax = max |x|;  s = amax / 448 (f32 division) if 0 < amax < inf, else 1;

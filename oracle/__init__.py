@@ -192,7 +192,7 @@ def quant_act_f8(a):
 
 def quant_tensor_f8(a):
     """Per-tensor FP8 e4m3 codes (uint8) + f32 scale per row (all equal): the
-    build's definition of BASELINE config 1's scheme (no reference counterpart)."""
+    build's definition of benchmark config 1's scheme (no reference counterpart)."""
     a16 = _f16_2d(a)
     M, K = a16.shape
     codes = np.empty((M, K), np.uint8)

@@ -219,7 +219,7 @@ EO_API void eo_quant_act_f8(const uint16_t* A, int64_t M, int64_t K, int64_t lda
 }
 
 /* FP8 e4m3 with one scale per tensor.  No counterpart in the reference (its
- * FP8 tier scales per row, EE/python/kernels.py:361); BASELINE config 1 names
+ * FP8 tier scales per row, EE/python/kernels.py:361); benchmark config 1 names
  * the scheme and this is the build's definition of it:
  *   amax = max |x| over the tensor (NaN propagates);
  *   s = amax / 448 (f32 division) if 0 < amax < inf, else 1;  inv = 1 / s (f32);

@@ -43,7 +43,7 @@ KNOWN = {
     },
 }
 
-# Routing thresholds of BASELINE configs 3 and 4.
+# Routing thresholds of benchmark configs 3 and 4.
 THRESHOLDS = np.float64([[0.41, 1.68], [2.34, 6.03]])
 
 

@@ -235,7 +235,7 @@ def test_softmax_entropy_tiers_in_pass(ee, orc):
 
 
 def test_softmax_entropy_full_size_properties(ee):
-    """BASELINE config 2's entropy shape [4096, 14336], log-uniform row scales:
+    """benchmark config 2's entropy shape [4096, 14336], log-uniform row scales:
     H in [0, ln S] and probabilities summing to 1 within fp16 rounding."""
     rng = np.random.default_rng(7)
     R, S = 4096, 14336
@@ -455,7 +455,7 @@ def test_w8a16_int8_weights(ee, orc, M, K, N):
 
 
 def test_gemm_full_size_sampled_rows(ee, orc):
-    """BASELINE configs 1-2 at full size (M=4096, K=4096, N=14336): INT8 int32
+    """benchmark configs 1-2 at full size (M=4096, K=4096, N=14336): INT8 int32
     accumulators bit-exact on 48 sampled rows (rows are independent)."""
     rng = np.random.default_rng(11)
     M, K, N = 4096, 4096, 14336
@@ -676,7 +676,7 @@ def _config1_inputs(rng, M, K, N):
 
 
 def test_config1_three_gemms(ee, orc):
-    """BASELINE config 1 (M = K = N = 4096; activations N(0,1) with 0.1% +-20
+    """benchmark config 1 (M = K = N = 4096; activations N(0,1) with 0.1% +-20
     outliers, weights N(0,0.02)): INT8 per-row/per-channel (fp16 output
     bit-exact), FP8 e4m3 with per-tensor amax scaling (codes and scales
     bit-exact; outputs within the 1e-2 bar of float64) and the FP16 tier
@@ -729,7 +729,7 @@ def test_fp8_per_tensor_edge_cases(ee, orc):
 # ---------------------------------------------------------------------------- config 3
 
 def test_config3_dispatcher(ee, orc):
-    """M = K = N = 4096 with row logits a seeded mixture of
+    """benchmark config 3: M = K = N = 4096 with row logits a seeded mixture of
     ~20% low / 40% mid / 40% high-entropy rows (bench.mixture_logits).
     entropy -> route under (0.41, 1.68) and under (2.34, 6.03) -> per-tier
     GEMMs on the gathered rows -> scatter.  Entropy within 1e-5 relative of

@@ -91,7 +91,7 @@ def _tensor_f8_torch(a):
 
 
 def test_quant_tensor_f8(orc):
-    """Per-tensor FP8 (BASELINE config 1's scheme; the build's own definition)."""
+    """Per-tensor FP8 (benchmark config 1's scheme; the build's own definition)."""
     rng = np.random.default_rng(30)
     for a in (_acts(rng, 64, 512, outliers=0.001),                      # config 1 style: +-20 outliers
               (rng.standard_normal((33, 100)) * 0.02).astype(np.float16),   # weight-like

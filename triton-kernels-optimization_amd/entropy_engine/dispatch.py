@@ -357,7 +357,7 @@ TINYLLAMA_1B = dict(layers=22, hidden=2048, heads=32, kv_heads=4, head_dim=64, f
 
 class EntropyGatedLlama:
     """A Llama forward in which EVERY linear layer routes each token row to the
-    INT8, FP8 or FP16 (W8A16) GEMM by entropy -- BASELINE config 4.  This
+    INT8, FP8 or FP16 (W8A16) GEMM by entropy -- benchmark config 4.  This
     extends EE/python/dispatch.py:150-260, which gates only the MLP and picks
     one tier per layer.
 

@@ -130,7 +130,7 @@ def quantize_activations(a: torch.Tensor, mode: str = "dispatcher", idx=None, co
 
 
 def quantize_tensor_fp8(x: torch.Tensor):
-    """FP8 e4m3 codes with ONE scale for the whole tensor -- BASELINE config 1's
+    """FP8 e4m3 codes with ONE scale for the whole tensor -- benchmark config 1's
     "per-tensor amax" scheme, which the reference does not have (its FP8 tier
     scales per row, EE/python/kernels.py:361):
         s = amax|x| / 448 (1 if amax is 0 or not finite); code = e4m3(f32(x) * f32(1/s)).
