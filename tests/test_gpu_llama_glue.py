@@ -295,3 +295,36 @@ def test_routed_gemm_on_prepared_codes(ee, T, swiglu):
     ref = ee.routed_linear(n, pw, idx, counts, swiglu=swiglu)
     got = ee.routed_linear(n, pw, idx, counts, swiglu=swiglu, quantized=(codes, scale))
     assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
+
+
+def test_add_rmsnorm_route_and_routed_gemm_reject_bad_arguments(ee):
+    """Host-side checks: nothing is launched for a wrong partition, a short codes
+    stride, prepared codes of the wrong shape, or K % 128 != 0."""
+    from entropy_engine import _lib
+    T, D = 64, 256
+    x = torch.randn(T, D, device="cuda").half()
+    w = torch.ones(D, device="cuda", dtype=torch.float16)
+    idx, counts = _partition(ee, T, 2.34, 6.03, 5)
+    with pytest.raises(ValueError):
+        ee.add_rmsnorm_route(x, w, 1e-5, None, idx[:-1], counts)
+    with pytest.raises(ValueError):
+        ee.add_rmsnorm_route(x, w, 1e-5, None, idx.long(), counts)
+    n = torch.empty_like(x)
+    codes = torch.empty(T, D, device="cuda", dtype=torch.uint8)
+    scale = torch.empty(T, device="cuda", dtype=torch.float32)
+    L, E, P = _lib.lib(), _lib.engine(), _lib.ptr
+    s = _lib.stream_handle()
+    rc = L.ee_add_rmsnorm_route(E, P(x), D, None, D, P(w), None, D, P(n), D, T, D, 1e-5, P(idx), P(counts),
+                                P(codes), D - 8, P(scale), s)
+    assert rc == _lib.EE_ERR_INVALID_ARG                     # ld_c < D
+    rc = L.ee_add_rmsnorm_route(E, P(x), D, None, D, P(w), None, D, P(n), D, T, D, 1e-5, None, P(counts),
+                                P(codes), D, P(scale), s)
+    assert rc == _lib.EE_ERR_INVALID_ARG                     # no partition
+    wt = (torch.randn(128, D, device="cuda") * 0.02).half()
+    pw = ee.PackedWeight(*ee.quantize_weight_codes(wt)).materialize()
+    with pytest.raises(ValueError):
+        ee.routed_linear(x, pw, idx, counts, quantized=(codes[:-1], scale))
+    x96 = torch.randn(T, 96, device="cuda").half()
+    pw96 = ee.PackedWeight(*ee.quantize_weight_codes((torch.randn(128, 96, device="cuda") * 0.02).half())).materialize()
+    with pytest.raises(_lib.EngineError):
+        ee.routed_linear(x96, pw96, idx, counts, quantized=(codes[:, :96].contiguous(), scale))
