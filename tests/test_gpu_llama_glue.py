@@ -276,10 +276,12 @@ def test_add_rmsnorm_route_equals_norm_then_quantiser(ee, T, D, tl, th):
 
 
 @pytest.mark.parametrize("swiglu", [False, True])
-@pytest.mark.parametrize("T", [1000, 4096])
-def test_routed_gemm_on_prepared_codes(ee, T, swiglu):
+@pytest.mark.parametrize("T,tl,th", [(1000, 2.34, 6.03), (4096, 2.34, 6.03), (300, 9.0, 9.0), (300, -1.0, 9.0),
+                                     (300, -1.0, -1.0)])
+def test_routed_gemm_on_prepared_codes(ee, T, tl, th, swiglu):
     """routed_linear on the codes of add_rmsnorm_route (one GEMM launch) equals
-    routed_linear with its own quantiser, bit for bit."""
+    routed_linear with its own quantiser, bit for bit; mixed and single-tier
+    partitions (all INT8, all FP8, all FP16)."""
     D, N = 512, 768
     g = torch.Generator(device="cuda").manual_seed(T)
     x = torch.randn(T, D, device="cuda", generator=g).half()
@@ -290,7 +292,7 @@ def test_routed_gemm_on_prepared_codes(ee, T, swiglu):
     if swiglu:
         codes_w, scale_w = ee.interleave_gate_up(codes_w), ee.interleave_gate_up(scale_w)
     pw = ee.PackedWeight(codes_w, scale_w).materialize()
-    idx, counts = _partition(ee, T, 2.34, 6.03, T + 1)
+    idx, counts = _partition(ee, T, tl, th, T + 1)
     _, n, codes, scale = ee.add_rmsnorm_route(x, w, 1e-5, y, idx, counts)
     ref = ee.routed_linear(n, pw, idx, counts, swiglu=swiglu)
     got = ee.routed_linear(n, pw, idx, counts, swiglu=swiglu, quantized=(codes, scale))
