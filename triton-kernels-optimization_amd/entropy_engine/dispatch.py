@@ -404,6 +404,12 @@ class EntropyGatedLlama:
         self._rope_cache = {}
         self.fused_attention = True
         self.fused_norm_quant = True
+        # rows per tier over every linear call: layer l's route feeds o/gate/up/down
+        # (4) plus layer l+1's q/k/v (3), the last layer's the LM head (1); the
+        # weights live on the device, so the per-forward tally is a few kernels, not 3 per layer
+        L = cfg["layers"]
+        self._route_weights = torch.tensor([4 + (3 if l + 1 < L else 1) for l in range(L)], dtype=torch.int64,
+                                           device=params["embed"].device).view(L, 1)
 
     @staticmethod
     def _pack(w: torch.Tensor, swiglu: bool = False) -> K.PackedWeight:
@@ -514,11 +520,10 @@ class EntropyGatedLlama:
         x, xn, xq = self._norm(x, self.p["norm"], res, route_prev, gated)
         logits = self._linear(xn, "lm_head", route_prev, gated, quantized=xq)
         if gated:
-            # rows per tier over every linear layer: each route feeds o/gate/up/down (4)
-            # plus the next layer's q/k/v (3) or the LM head (1); layer 0's q/k/v run
-            # on the FP16 tier
-            weights = [4 + (3 if i + 1 < len(counts_log) else 1) for i in range(len(counts_log))]
-            total = sum(cnt.to(torch.int64) * w for cnt, w in zip(counts_log, weights))
-            total[2] += 3 * T                         # a device op: the forward stays capturable as a HIP graph
+            # rows per tier over every linear layer (weights in _route_weights); layer
+            # 0's q/k/v run on the FP16 tier.  Device ops only: the forward stays
+            # capturable as a HIP graph.
+            total = (torch.stack(counts_log).to(torch.int64) * self._route_weights).sum(0)
+            total[2] += 3 * T
             self.last_fractions = total
         return logits.view(B, S, -1)
