@@ -89,7 +89,11 @@ int ee_engine_destroy(ee_engine* eng);
  * "gemm_persist": INT8 / FP8 GEMMs with more tiles than CUs (and the routed
  * linear's tier grid) run as persistent grids, one workgroup per CU walking
  * its tiles with the stage ring running across tile boundaries; 1 turns that
- * off, n >= 2 forces it with min(n, tiles) workgroups.  Same bits either way. */
+ * off, n >= 2 forces it with min(n, tiles) workgroups.  Same bits either way.
+ * "gemm_tile": 256 x 256-tile persistent kernels for un-routed GEMMs whose
+ * 128 x 128 grid has more tiles than CUs (automatic for INT8 and FP8, whose
+ * bits do not change); 128 forbids them, 256 forces them for every tier
+ * (the FP16 tier then sums K in the loader-wave pipeline's order). */
 int ee_engine_set_option(ee_engine* eng, const char* key, int64_t value);
 int ee_engine_device(const ee_engine* eng);
 

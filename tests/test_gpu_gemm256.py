@@ -1,0 +1,163 @@
+"""GPU parity of the 256 x 256-tile persistent GEMMs (eek_gemm256_*).
+
+They replace the 128 x 128 kernels for un-routed GEMMs with more 128-tiles
+than CUs (configs 1-2, the TinyLlama projections), so each case checks them
+against the oracle -- INT8 fp16 outputs and int32 accumulators bit-exact,
+FP8 / FP16 within 1e-2 of a float64 recompute -- and, bit for bit, against the
+128-tile kernels on the same inputs (same K order: FP8 and FP16 sum slice after
+slice in both).  Ragged shapes, one-stage K, partial tiles and several tiles
+per workgroup (forced grids, including one that is not a multiple of the 8
+XCDs) exercise the stage ring across tile boundaries.
+"""
+import numpy as np
+import pytest
+import torch
+
+from test_gpu_parity import check_close_f64, cuda, host, weights
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def ee():
+    import entropy_engine
+    return entropy_engine
+
+
+def _opt(key, value):
+    from entropy_engine import _lib
+    _lib.check(_lib.lib().ee_engine_set_option(_lib.engine(), key.encode(), value))
+
+
+class _Options:
+    def __init__(self, **kv):
+        self.kv = kv
+
+    def __enter__(self):
+        for k, v in self.kv.items():
+            _opt(k, v)
+
+    def __exit__(self, *exc):
+        for k in self.kv:
+            _opt(k, 0)
+
+
+def _operands(ee, orc, M, K, N, seed):
+    rng = np.random.default_rng(seed)
+    A = rng.standard_normal((M, K)).astype(np.float16)
+    B, bs = weights(orc, rng, N, K)
+    pw = ee.prepare_weight(cuda(B), cuda(bs)).materialize()
+    return A, B, bs, pw
+
+
+# (M, K, N, gemm_persist): 0 = automatic grid
+SHAPES = [
+    (512, 512, 512, 0),        # 4 tiles, 4 stages each
+    (300, 640, 520, 0),        # partial tiles in M and N, 5 stages
+    (520, 128, 1028, 0),       # one K stage per tile; N % 8 == 4 tail
+    (1, 256, 4, 0),            # a single row and 4 columns
+    (1024, 512, 1024, 8),      # 16 tiles on 8 workgroups: 2 tiles each, ring across tiles
+    (1024, 384, 1024, 3),      # 16 tiles on 3 workgroups (not a multiple of 8): 5-6 tiles each
+    (768, 256, 2048, 5),       # 24 tiles on 5 workgroups, 2 stages per tile
+]
+
+
+@pytest.mark.parametrize("M,K,N,grid", SHAPES)
+def test_gemm256_int8_fp8_small(ee, orc, M, K, N, grid):
+    A, B, bs, pw = _operands(ee, orc, M, K, N, M * 7 + K + N)
+    codes, a_s = orc.quant_act_i8(A, "dispatcher")
+    c8, s8 = orc.quant_act_f8(A)
+    acc = torch.empty((M, N), dtype=torch.int32, device="cuda")
+    with _Options(gemm_tile=256, gemm_persist=grid):
+        o_i8 = host(ee.gemm("int8", cuda(codes), pw.i8, cuda(a_s), cuda(bs)))
+        ee.gemm("int8", cuda(codes), pw.i8, cuda(a_s), cuda(bs), acc_out=acc)
+        o_f8 = host(ee.gemm("fp8", cuda(c8), pw.f8, cuda(s8), cuda(bs)))
+    acc_ref = orc.gemm_i8_acc(codes, B)
+    assert np.array_equal(host(acc), acc_ref)
+    assert np.array_equal(o_i8.view(np.uint16), orc.epilogue_i8(acc_ref, a_s, bs).view(np.uint16))
+    check_close_f64(o_f8, orc.gemm_f8_f64(c8, B, s8, bs))
+    with _Options(gemm_tile=128):
+        r_f8 = host(ee.gemm("fp8", cuda(c8), pw.f8, cuda(s8), cuda(bs)))
+    assert np.array_equal(o_f8.view(np.uint16), r_f8.view(np.uint16))
+
+
+@pytest.mark.parametrize("M,K,N,grid", SHAPES[:3] + SHAPES[4:6])
+def test_gemm256_fp16_small(ee, orc, M, K, N, grid):
+    """The FP16 (W8A16) tier on the 256-tile kernel: within 1e-2 of float64 and
+    bit-identical to the 128-tile loader-wave pipeline (same K order)."""
+    A, B, bs, pw = _operands(ee, orc, M, K, N, M + 5 * K + N)
+    with _Options(gemm_tile=256, gemm_persist=grid):
+        out = host(ee.gemm("fp16", cuda(A), pw.f16))
+    check_close_f64(out, orc.gemm_w8a16_f64(A, B, bs))
+    with _Options(gemm_tile=128, gemm_variant=1):
+        ref = host(ee.gemm("fp16", cuda(A), pw.f16))
+    assert np.array_equal(out.view(np.uint16), ref.view(np.uint16))
+
+
+@pytest.mark.parametrize("M,K,N", [(4096, 4096, 4096), (4096, 4096, 14336)], ids=["config1", "config2"])
+def test_gemm256_full_size(ee, orc, M, K, N):
+    """Configs 1 and 2 at full size through the production epilogue (no int32
+    debug output): INT8 fp16 outputs bit-exact and FP8 within 1e-2 of float64 on
+    sampled rows against the oracle; all outputs bit-identical to the 128-tile
+    kernels.  The automatic choice picks the 256-tile kernel at these shapes."""
+    A, B, bs, pw = _operands(ee, orc, M, K, N, 21 + N)
+    codes, a_s = orc.quant_act_i8(A, "dispatcher")
+    c8, s8 = orc.quant_act_f8(A)
+    o_i8 = host(ee.gemm("int8", cuda(codes), pw.i8, cuda(a_s), cuda(bs)))
+    o_f8 = host(ee.gemm("fp8", cuda(c8), pw.f8, cuda(s8), cuda(bs)))
+    rows = np.array([0, 1, 255, 256, 257, 1000, 2047, 2048, 3333, 4095])
+    ref = orc.epilogue_i8(orc.gemm_i8_acc(codes[rows], B), a_s[rows], bs)
+    assert np.array_equal(o_i8[rows].view(np.uint16), ref.view(np.uint16))
+    check_close_f64(o_f8[rows], orc.gemm_f8_f64(c8[rows], B, s8[rows], bs))
+    with _Options(gemm_tile=128):
+        r_i8 = host(ee.gemm("int8", cuda(codes), pw.i8, cuda(a_s), cuda(bs)))
+        r_f8 = host(ee.gemm("fp8", cuda(c8), pw.f8, cuda(s8), cuda(bs)))
+    assert np.array_equal(o_i8.view(np.uint16), r_i8.view(np.uint16))
+    assert np.array_equal(o_f8.view(np.uint16), r_f8.view(np.uint16))
+
+
+def test_gemm256_fp8_config1_per_tensor(ee, orc):
+    """Config 1's FP8 leg (per-tensor e4m3 scales of A with 0.1% outliers of 20,
+    and of the weights): the 256-tile kernel within 1e-2 of float64 on sampled
+    rows and bit-identical to the 128-tile kernel."""
+    M = K = N = 4096
+    rng = np.random.default_rng(5)
+    A = rng.standard_normal((M, K)).astype(np.float16)
+    pos = rng.choice(M * K, M * K // 1000, replace=False)
+    A.reshape(-1)[pos] = (20.0 * rng.choice([-1.0, 1.0], pos.size)).astype(np.float16)
+    W = (rng.standard_normal((N, K)) * 0.02).astype(np.float16)
+    ca, sa = orc.quant_tensor_f8(A)
+    cw, sw = orc.quant_tensor_f8(W)
+    out = host(ee.gemm("fp8", cuda(ca), cuda(cw), cuda(sa), cuda(sw)))
+    rows = np.array([0, 17, 2048, 4095])
+    ref = orc.e4m3_to_f32(ca[rows]).astype(np.float64) @ orc.e4m3_to_f32(cw).astype(np.float64).T
+    ref = ref * sa[rows].astype(np.float64)[:, None] * sw.astype(np.float64)[None, :]
+    check_close_f64(out[rows], ref)
+    with _Options(gemm_tile=128):
+        r = host(ee.gemm("fp8", cuda(ca), cuda(cw), cuda(sa), cuda(sw)))
+    assert np.array_equal(out.view(np.uint16), r.view(np.uint16))
+
+
+@pytest.mark.parametrize("M,K,F", [(4096, 2048, 5632), (600, 256, 640)])
+def test_gemm256_swiglu(ee, orc, M, K, F):
+    """The SwiGLU epilogue of the 256-tile kernels gives the bits of the 128-tile
+    SwiGLU kernels (every tier; FP16 on the loader-wave order)."""
+    rng = np.random.default_rng(M + F)
+    W = (rng.standard_normal((2 * F, K)) / np.sqrt(K)).astype(np.float16)
+    codes, scale = ee.quantize_weight_codes(cuda(W))
+    pw = ee.PackedWeight(ee.interleave_gate_up(codes), ee.interleave_gate_up(scale)).materialize()
+    x = cuda(rng.standard_normal((M, K)).astype(np.float16))
+    ci, si = ee.quantize_activations(x, "dispatcher")
+    cf, sf = ee.quantize_activations(x, "fp8")
+    for kind, a, b, sa, sb in (("int8", ci, pw.i8, si, pw.scale), ("fp8", cf, pw.f8, sf, pw.scale),
+                               ("fp16", x, pw.f16, None, None)):
+        with _Options(gemm_tile=256):
+            fused = ee.gemm(kind, a, b, sa, sb, swiglu=True)
+        with _Options(gemm_tile=128, gemm_variant=1):
+            ref = ee.gemm(kind, a, b, sa, sb, swiglu=True)
+        assert torch.equal(fused.view(torch.int16), ref.view(torch.int16)), kind
+
+
+def test_gemm256_option_rejects_bad_value(ee):
+    from entropy_engine import _lib
+    assert _lib.lib().ee_engine_set_option(_lib.engine(), b"gemm_tile", 192) == _lib.EE_ERR_INVALID_ARG

@@ -1,0 +1,156 @@
+// ee_gemm_dev.h -- building blocks shared by the MFMA GEMM kernels (gfx950):
+// the swizzled 128-byte LDS rows, the direct-to-LDS DMA and its waits, the
+// 32x32 MFMA shapes of the three tiers, the dequantising arithmetic of the
+// epilogues and the XCD-aware deal of tiles to persistent workgroups.
+#pragma once
+#include "ee_device.h"
+
+// Every epilogue multiply is its own rounded f32 operation, as in the reference.
+#pragma clang fp contract(off)
+
+#define BKB 128                         // K bytes per LDS stage row
+
+// 16-byte chunk c of LDS row r sits at chunk c ^ ((r >> 1) & 7).  gfx950's LDS
+// serves a ds_read_b128 in passes of 16 lanes over 64 banks: the 16 rows of a
+// pass then land on 16 distinct (row parity, chunk) bank groups.
+EE_DEV int swz(int row) { return (row >> 1) & 7; }
+EE_DEV uint32_t lds_off(int row, int chunk) { return (uint32_t)(row * BKB + ((chunk ^ swz(row)) << 4)); }
+
+EE_DEV i32x4 as_i32x4(u32x4 v) { return __builtin_bit_cast(i32x4, v); }
+EE_DEV f16x8 as_f16x8(u32x4 v) { return __builtin_bit_cast(f16x8, v); }
+
+#define GPTR(p) ((const void __attribute__((address_space(1)))*)(p))
+#define LPTR(p) ((void __attribute__((address_space(3)))*)(p))
+
+// 16 bytes per lane from global memory straight into LDS at lds_base + 16 * lane
+// (lds_base wave-uniform).  Issued as inline asm so that the compiler's wait
+// model contains only the kernel's ds_reads (an LDS DMA it can see makes it
+// fall back to waiting for every outstanding LDS read); the kernel tracks these
+// loads itself with explicit vmcnt waits before each stage barrier.
+EE_DEV void dma16(const uint8_t* gptr, uint32_t lds_base) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds_base), "v"(gptr) : "memory", "m0");
+}
+EE_DEV uint32_t lds_addr(const uint8_t* p) { return (uint32_t)(uintptr_t)LPTR(p); }
+// The same load with a wave-uniform 64-bit base in SGPRs and a 32-bit per-lane
+// byte offset (one VGPR per row group instead of a 64-bit address pair).
+EE_DEV void dma16s(const uint8_t* sbase, uint32_t voff, uint32_t lds_base) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds_base), "v"(voff), "s"(sbase)
+                 : "memory", "m0");
+}
+
+// s_waitcnt with only vmcnt constrained (gfx9 encoding: vmcnt[3:0] | expcnt 7 << 4 |
+// lgkmcnt 15 << 8 | vmcnt[5:4] << 14).
+#define WAITCNT_VM(n) __builtin_amdgcn_s_waitcnt((((n) & 15) | (7 << 4) | (15 << 8) | (((n) >> 4) << 14)))
+// s_waitcnt lgkmcnt(0) with vmcnt and expcnt left unconstrained.
+#define WAITCNT_LGKM0() __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14))
+
+// ---------------------------------------------------------------------------
+// Pipelined kernel: 32x32 MFMA blocks (the full-rate shapes on gfx950:
+// i8 32x32x32 and f16 32x32x16 run at twice the rate of their 16x16 forms),
+// K stages split into slices of one MFMA depth, fragments of slice s+1 read
+// from LDS while the MFMAs of slice s run.
+template <int KIND> struct Pipe;
+template <> struct Pipe<EE_GEMM_I8> {            // 32x32x32 i8: 32 K bytes per slice, 16 B per lane
+    static constexpr int SB = 32, CPF = 1;
+    typedef u32x4 frag_t;
+    typedef i32x16 acc_t;
+    static EE_DEV acc_t mma(const frag_t& b, const frag_t& a, const acc_t& c) {
+        return __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(i32x4, b), __builtin_bit_cast(i32x4, a), c, 0, 0, 0);
+    }
+};
+template <> struct Pipe<EE_GEMM_F16> {           // 32x32x16 f16: 32 K bytes per slice, 16 B per lane
+    static constexpr int SB = 32, CPF = 1;
+    typedef u32x4 frag_t;
+    typedef f32x16 acc_t;
+    static EE_DEV acc_t mma(const frag_t& b, const frag_t& a, const acc_t& c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, b), __builtin_bit_cast(f16x8, a), c, 0, 0, 0);
+    }
+};
+template <> struct Pipe<EE_GEMM_F8> {            // 32x32x64 e4m3: 64 K bytes per slice, 32 B per lane
+    static constexpr int SB = 64, CPF = 2;
+    typedef i32x8 frag_t;
+    typedef f32x16 acc_t;
+    static EE_DEV acc_t mma(const frag_t& b, const frag_t& a, const acc_t& c) {
+        return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(b, a, c, 0, 0, 0, 0, 0, 0);
+    }
+};
+
+// Dequantised value of one accumulator, as the fp16 epilogues compute it
+// (left-to-right f32 multiplies; W8A16 accumulators are the value).
+template <int KIND, typename E>
+EE_DEV float deq(E acc, float as, float bs) {
+    if constexpr (KIND == EE_GEMM_I8) {
+        float v = (float)acc;
+        v = v * as;
+        return v * bs;
+    } else if constexpr (KIND == EE_GEMM_F8) {
+        const float v = acc * as;
+        return v * bs;
+    } else {
+        return acc;
+    }
+}
+
+// One 16-byte store of C or of the SwiGLU output: non-temporal (written once,
+// read by a later kernel), 8-byte halves when the row is only 8-byte aligned.
+EE_DEV void store_row16(uint16_t* dst, const u32x4& v, bool full) {
+    if (full && ((uintptr_t)dst & 15) == 0) {
+        __builtin_nontemporal_store(v, (u32x4*)dst);
+    } else {
+        __builtin_nontemporal_store(u32x2{v[0], v[1]}, (u32x2*)dst);
+        if (full) __builtin_nontemporal_store(u32x2{v[2], v[3]}, (u32x2*)(dst + 4));
+    }
+}
+
+// Tile order and the deal of tiles to workgroups (shared by the plain and the
+// routed persistent kernels).  Logical tiles a = 0 .. nA-1 (the 1-byte-operand
+// tiles) are ordered in bands of 8 M-tiles walked along N, so 32 consecutive
+// tiles form an 8 x 4 block.  They are dealt in rounds: in a round every
+// taking workgroup gets one tile, and with G a multiple of 8 workgroup
+// b = 8j + x (on XCD x) takes position x * G/8 + j, so each XCD gets 32
+// consecutive tiles -- one 8 x 4 block, whose A and B panels its CUs share in
+// that XCD's L2.  W8A16 tiles of a routed launch (nF of them, twice the work
+// of a 1-byte tile at the same K) are dealt first, round robin: workgroups
+// b < rF get qF + 1, the others qF.  The first two rounds of 1-byte tiles then
+// go only to workgroups b >= rF, which levels the load (a static version of
+// what the hardware dispatcher does for one-tile grids).
+struct TileDeal {
+    int tiles_m, tiles_n, nA, b, G, per, rF, P, first_round;
+    __device__ __forceinline__ TileDeal(int tm_count, int tn_count, int nF, int bb, int GG)
+        : tiles_m(tm_count), tiles_n(tn_count), nA(tm_count * tn_count), b(bb), G(GG) {
+        per = (G & 7) == 0 ? G >> 3 : 0;
+        rF = nF % G;
+        P = G - rF;                                   // workgroups in rounds 0 and 1
+        first_round = (rF != 0 && b < rF) ? 2 : 0;    // heavier workgroups skip rounds 0 and 1
+    }
+    // position of this workgroup in a round in which all G take part
+    __device__ __forceinline__ int pos_all() const { return per ? (b & 7) * per + (b >> 3) : b; }
+    __device__ __forceinline__ int tile_index(int round) const {
+        if (rF == 0) return round * G + pos_all();
+        if (round < 2) return round * P + (b - rF);
+        return 2 * P + (round - 2) * G + pos_all();
+    }
+    __device__ __forceinline__ int count() const {
+        // rounds first_round, first_round+1, ... while tile_index(round) < nA
+        if (rF == 0) {
+            const int p = pos_all();
+            return p < nA ? (nA - p + G - 1) / G : 0;
+        }
+        int n = 0;
+        if (first_round == 0) {
+            for (int r = 0; r < 2; ++r) n += tile_index(r) < nA;
+            if (n < 2) return n;
+        }
+        const int p = 2 * P + pos_all();
+        return n + (p < nA ? (nA - p + G - 1) / G : 0);
+    }
+    // logical tile a -> (tm, tn): bands of 8 M-tiles, M fastest within a band
+    __device__ __forceinline__ void coords(int a, int& tm, int& tn) const {
+        const int band = a / (8 * tiles_n);
+        const int m_first = band * 8;
+        const int gsz = min(tiles_m - m_first, 8);
+        const int r = a - band * 8 * tiles_n;
+        tm = m_first + r % gsz;
+        tn = r / gsz;
+    }
+};

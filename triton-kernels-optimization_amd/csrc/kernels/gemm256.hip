@@ -1,0 +1,437 @@
+// gemm256.hip -- persistent 256 x 256-tile MFMA GEMMs of the three precision
+// tiers for gfx950 (the large-M shapes: configs 1-4).
+//
+//   EE_GEMM_I8 : int8 x int8 -> int32 (v_mfma_i32_32x32x32_i8);
+//                C = fp16((f32(acc) * a_scale[m]) * b_scale[n])     (EE/python/kernels.py:50-110)
+//   EE_GEMM_F8 : e4m3 x e4m3 -> f32 (v_mfma_scale_f32_32x32x64_f8f6f4);
+//                C = fp16((acc * a_scale[m]) * b_scale[n])           (EE/python/kernels.py:118-180)
+//   EE_GEMM_F16: fp16 x fp16 -> f32 (v_mfma_f32_32x32x16_f16); C = fp16(acc)
+//                (EE/python/kernels.py:192-246, W8A16 weights pre-dequantised)
+//
+// Why a 256 x 256 tile.  A CU computing a T x T tile streams 2T bytes of
+// operands per K byte for 2T^2 ops: at the MFMA rate of 8192 int8/fp8 ops per
+// clock a 128 x 128 tile needs 64 B/clk per CU from L2, a 256 x 256 tile 32.
+// The L1 of a gfx950 CU sustains ~38-46 B/clk from L2 (a bounded number of
+// 128-byte requests in flight over an L2 latency of ~350 clocks), so 128-wide
+// tiles are operand-stream bound and 256-wide tiles can be MFMA bound.
+//
+// Workgroup: 512 threads, 8 wave64s, two per SIMD.  Wave w owns rows
+// 128 (w >> 2) .. +127 and columns 64 (w & 3) .. +63 of the tile as 4 x 2
+// blocks of 32 x 32 (128 accumulator registers), summing K in order, slice
+// after slice -- the same K order as the 128-tile loader-wave kernels, so FP8
+// and FP16 outputs are bit-identical to theirs and INT8 to every kernel.
+//
+// LDS: a ring of two 64 KB stages (128 K bytes of 256 A rows and 256 B rows,
+// the usual 128-byte swizzled rows) plus a 4 KB epilogue slot per wave.  All
+// eight waves issue the direct-to-LDS DMA of the stages in the shadow of their
+// own MFMAs (4 A and 4 B row groups of 8 rows each per wave and stage).
+// Barrier s+1 sits before the MFMAs of stage s's last K slice: by then every
+// wave has read stage s (lgkmcnt 0) and waited for its part of stage s+1
+// (vmcnt 0), so stage s+2 is issued into stage s's buffer right after it,
+// while the last slice's MFMAs run and slice 0 of stage s+1 is read.
+//
+// Persistent grid: one workgroup per CU walks its tiles (TileDeal: 8 x 4
+// blocks of tiles per XCD per round); the stage sequence and the ring run on
+// across tile boundaries.  At a tile's end the epilogue loads the scales,
+// issues the next DMA stage, then dequantises 32 x 64 blocks through the
+// wave's LDS slot and stores 16-byte row vectors.
+#include "../common/ee_device.h"
+#include "../common/ee_gemm_dev.h"
+
+#pragma clang fp contract(off)
+
+#define T2M 256
+#define T2N 256
+#define T2_STAGE ((T2M + T2N) * BKB)      // 64 KB
+#define T2_EPI (2 * T2_STAGE)             // the ring: two stages
+#define T2_SLOT 4096                      // per-wave epilogue slot (32 x 64 fp16)
+#define T2_LDS (T2_EPI + 8 * T2_SLOT)     // 160 KB
+#define T2_THREADS 512
+
+template <int KIND, int SW>
+struct G256 {
+    typedef Pipe<KIND> P;
+    typedef typename P::acc_t acc_t;
+    typedef typename P::frag_t frag_t;
+    static constexpr int ESZ = (KIND == EE_GEMM_F16) ? 2 : 1;
+    static constexpr int NSL = BKB / P::SB;           // K slices per stage: 4 (i8, f16) or 2 (f8)
+
+    const EeGemmArgs& g;
+    uint8_t* smem;
+    TileDeal deal;
+    uint32_t lds0;
+    int lane, wave, wm, wn;
+    int nk, total;                                    // stages per tile, stages of this workgroup
+    // DMA cursor: the next stage to issue is (itile, ikt), global number iss;
+    // row group q of A (B) of that tile starts at abase + aoff[q] (bbase + boff[q]).
+    int iss, itile, ikt;
+    const uint8_t* abase;
+    const uint8_t* bbase;
+    uint32_t aoff[4], boff[4];
+    acc_t acc[4][2];
+    // fragments: A single-buffered (row block i of the next slice is read right
+    // after the last MFMA that uses row block i of this one); B double-buffered,
+    // except for FP8, whose 32-byte fragments leave room for one B buffer only
+    // (its slices run j-major, so each B block is also dead before its reload)
+    static constexpr int NB = (KIND == EE_GEMM_F8) ? 1 : 2;
+    frag_t fa[4], fb[NB][2];
+
+    __device__ __forceinline__ G256(const EeGemmArgs& g_, uint8_t* smem_, int b, int G)
+        : g(g_), smem(smem_), deal((g_.M + T2M - 1) / T2M, (g_.N + T2N - 1) / T2N, 0, b, G) {}
+
+    __device__ __forceinline__ void coords(int i, int& m0, int& n0) const {
+        int tm, tn;
+        deal.coords(deal.tile_index(deal.first_round + i), tm, tn);
+        m0 = tm * T2M;
+        n0 = tn * T2N;
+    }
+
+    // DMA rows of tile i: one global_load_lds_dwordx4 fills 8 LDS rows (1 KB);
+    // lane l lands at row 8 * grp + l / 8, physical chunk l % 8, which holds
+    // logical chunk (l % 8) ^ swz(row).  Wave w fills row groups 4w .. 4w+3 of
+    // A and of B (rows are clamped: out-of-range rows load a valid row whose
+    // results are never stored).
+    __device__ __forceinline__ void dma_tile(int i) {
+        int m0, n0;
+        coords(i, m0, n0);
+        abase = (const uint8_t*)g.a + (int64_t)m0 * g.lda * ESZ;
+        bbase = (const uint8_t*)g.b + (int64_t)n0 * g.ldb * ESZ;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int r = (wave * 4 + q) * 8 + (lane >> 3);
+            const int lchunk = (lane & 7) ^ swz(r);   // swz(T2M + r) == swz(r)
+            const int m = min(m0 + r, g.M - 1) - m0;
+            aoff[q] = (uint32_t)(m * g.lda * ESZ + lchunk * 16);
+            const int n = min(n0 + r, g.N - 1) - n0;
+            boff[q] = (uint32_t)(n * g.ldb * ESZ + lchunk * 16);
+        }
+    }
+    // Part p (0..3) of the next stage: A row group 4w+p and B row group 4w+p.
+    __device__ __forceinline__ void issue_part(int p) {
+        if (p == 0 && ikt == nk) {
+            ++itile;
+            ikt = 0;
+            dma_tile(itile);
+        }
+        const uint32_t s = lds0 + (uint32_t)((iss & 1) * T2_STAGE);
+        const uint32_t kb = (uint32_t)ikt * BKB;
+        const int grp = wave * 4 + p;
+        dma16s(abase, aoff[p] + kb, s + grp * 8 * BKB);
+        dma16s(bbase, boff[p] + kb, s + (T2M + grp * 8) * BKB);
+        if (p == 3) {
+            ++ikt;
+            ++iss;
+        }
+    }
+    __device__ __forceinline__ void issue_stage() {
+#pragma unroll
+        for (int p = 0; p < 4; ++p) issue_part(p);
+    }
+
+    // Fragments of K slice sl of the stage at st: lane l reads row (l & 31) of
+    // each 32-row block, chunk(s) sl * SB/16 + (l >> 5) * CPF (+1).
+    __device__ __forceinline__ void rd(const uint8_t* st, int sl, frag_t& f, int row) const {
+        const int c0 = sl * (P::SB / 16) + (lane >> 5) * P::CPF;
+        if constexpr (P::CPF == 1) {
+            f = *(const u32x4*)(st + lds_off(row, c0));
+        } else {
+            const u32x4 x0 = *(const u32x4*)(st + lds_off(row, c0)), x1 = *(const u32x4*)(st + lds_off(row, c0 + 1));
+            f = i32x8{(int)x0[0], (int)x0[1], (int)x0[2], (int)x0[3], (int)x1[0], (int)x1[1], (int)x1[2], (int)x1[3]};
+        }
+    }
+    __device__ __forceinline__ void rd_a(const uint8_t* st, int sl, int i) {
+        rd(st, sl, fa[i], wm * 128 + i * 32 + (lane & 31));
+    }
+    __device__ __forceinline__ void rd_b(const uint8_t* st, int sl, int buf, int j) {
+        rd(st, sl, fb[buf % NB][j], T2M + wn * 64 + j * 32 + (lane & 31));
+    }
+    // all six fragments of slice sl into fa and fb[buf]
+    __device__ __forceinline__ void rd_all(const uint8_t* st, int sl, int buf) {
+        rd_a(st, sl, 0);
+        rd_b(st, sl, buf, 0);
+        rd_b(st, sl, buf, 1);
+        rd_a(st, sl, 1);
+        rd_a(st, sl, 2);
+        rd_a(st, sl, 3);
+    }
+
+#define G2_SB() __builtin_amdgcn_sched_barrier(0)
+    // The 8 MFMAs of the current slice (B fragments in buffer C), interleaved
+    // with the reads of the next slice (from stage rs, slice rsl, when RD: B into
+    // buffer 1 - C, A row block i right after its last MFMA here) and the 4 DMA
+    // parts of the next stage (when dma).
+    template <int C, bool RD>
+    __device__ __forceinline__ void slice(const uint8_t* rs, int rsl, bool dma) {
+        if constexpr (NB == 1) {
+            slice_j(RD, rs, rsl, dma);
+            return;
+        }
+        constexpr int N = (1 - C) % NB;
+        acc[0][0] = P::mma(fb[C][0], fa[0], acc[0][0]);
+        G2_SB();
+        if (RD) { rd_b(rs, rsl, N, 0); rd_b(rs, rsl, N, 1); }
+        G2_SB();
+        acc[0][1] = P::mma(fb[C][1], fa[0], acc[0][1]);
+        G2_SB();
+        if (RD) rd_a(rs, rsl, 0);
+        G2_SB();
+        acc[1][0] = P::mma(fb[C][0], fa[1], acc[1][0]);
+        G2_SB();
+        if (dma) issue_part(0);
+        G2_SB();
+        acc[1][1] = P::mma(fb[C][1], fa[1], acc[1][1]);
+        G2_SB();
+        if (RD) rd_a(rs, rsl, 1);
+        if (dma) issue_part(1);
+        G2_SB();
+        acc[2][0] = P::mma(fb[C][0], fa[2], acc[2][0]);
+        G2_SB();
+        if (dma) issue_part(2);
+        G2_SB();
+        acc[2][1] = P::mma(fb[C][1], fa[2], acc[2][1]);
+        G2_SB();
+        if (RD) rd_a(rs, rsl, 2);
+        if (dma) issue_part(3);
+        G2_SB();
+        acc[3][0] = P::mma(fb[C][0], fa[3], acc[3][0]);
+        G2_SB();
+        acc[3][1] = P::mma(fb[C][1], fa[3], acc[3][1]);
+        G2_SB();
+        if (RD) rd_a(rs, rsl, 3);
+        G2_SB();
+    }
+
+    // The single-buffer form (FP8): MFMAs j-major; B block 0 is reread after
+    // the fourth MFMA, A block i and B block 1 after their last use.
+    __device__ __forceinline__ void slice_j(bool RD, const uint8_t* rs, int rsl, bool dma) {
+        acc[0][0] = P::mma(fb[0][0], fa[0], acc[0][0]);
+        G2_SB();
+        acc[1][0] = P::mma(fb[0][0], fa[1], acc[1][0]);
+        G2_SB();
+        acc[2][0] = P::mma(fb[0][0], fa[2], acc[2][0]);
+        G2_SB();
+        acc[3][0] = P::mma(fb[0][0], fa[3], acc[3][0]);
+        G2_SB();
+        if (RD) rd_b(rs, rsl, 0, 0);
+        G2_SB();
+        acc[0][1] = P::mma(fb[0][1], fa[0], acc[0][1]);
+        G2_SB();
+        if (RD) rd_a(rs, rsl, 0);
+        if (dma) issue_part(0);
+        G2_SB();
+        acc[1][1] = P::mma(fb[0][1], fa[1], acc[1][1]);
+        G2_SB();
+        if (RD) rd_a(rs, rsl, 1);
+        if (dma) issue_part(1);
+        G2_SB();
+        acc[2][1] = P::mma(fb[0][1], fa[2], acc[2][1]);
+        G2_SB();
+        if (RD) rd_a(rs, rsl, 2);
+        if (dma) issue_part(2);
+        G2_SB();
+        acc[3][1] = P::mma(fb[0][1], fa[3], acc[3][1]);
+        G2_SB();
+        if (RD) { rd_a(rs, rsl, 3); rd_b(rs, rsl, 0, 1); }
+        if (dma) issue_part(3);
+        G2_SB();
+    }
+
+    // Stage cs: slices 0 .. NSL-1 from buffer cs & 1; the stage starts with its
+    // slice-0 fragments in fa / fb[0] (NSL is even).  Not the tile's last stage
+    // (LAST = false): before the last slice's MFMAs, barrier cs+1, slice 0 of
+    // stage cs+1 is read and stage cs+2 is issued into this stage's buffer (when
+    // dma2).  The tile's last stage reads nothing for the next one: the
+    // epilogue and the tile change do that (run()).
+    template <bool LAST>
+    __device__ __forceinline__ void stage(int cs, bool dma2) {
+        const uint8_t* st = smem + (cs & 1) * T2_STAGE;
+#pragma unroll
+        for (int h = 0; h + 1 < NSL; h += 2) {
+            slice<0, true>(st, h + 1, false);
+            if (h + 2 < NSL) slice<1, true>(st, h + 2, false);
+        }
+        if (!LAST) {
+            G2_SB();
+            WAITCNT_VM(0);
+            WAITCNT_LGKM0();
+            asm volatile("" ::: "memory");
+            __builtin_amdgcn_s_barrier();             // barrier cs+1: stage cs+1 landed, stage cs read
+            asm volatile("" ::: "memory");
+            slice<1, true>(smem + ((cs + 1) & 1) * T2_STAGE, 0, dma2);
+        } else {
+            slice<1, false>(st, 0, false);
+        }
+    }
+
+    // Dequantise and store the tile (m0, n0) from acc through the wave's LDS
+    // slot.  Scales are loaded first; the wait for them also covers this wave's
+    // part of the next DMA stage (the one barrier cs+1 will publish).
+    __device__ __forceinline__ void epilogue(int m0, int n0) {
+        const int M = g.M, N = g.N;
+        // The lane index through an empty asm: the epilogue's addresses are then
+        // computed here instead of being hoisted out of the tile loop, where they
+        // would hold ~20 VGPRs across the K loop.
+        int lane = this->lane;
+        asm volatile("" : "+v"(lane));
+        f32x4 bs[2][4] = {};
+        float as[4] = {};
+        if constexpr (KIND != EE_GEMM_F16) {
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int n = n0 + wn * 64 + j * 32 + 8 * q + 4 * (lane >> 5);
+                    bs[j][q] = (n < N) ? *(const f32x4*)(g.b_scale + n) : f32x4{0.f, 0.f, 0.f, 0.f};
+                }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int m = m0 + wm * 128 + i * 32 + (lane & 31);
+                as[i] = (m < M) ? g.a_scale[m] : 0.0f;
+            }
+        }
+        WAITCNT_VM(0);
+        asm volatile("" ::: "memory");
+        uint8_t* slot = smem + T2_EPI + wave * T2_SLOT;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int mb = m0 + wm * 128 + i * 32;    // first row of this 32 x 64 block
+            const int nb = n0 + wn * 64;
+            if constexpr (KIND == EE_GEMM_I8) {
+                if (g.acc) {                          // debug output: int32 accumulators, direct stores
+                    const int m = mb + (lane & 31);
+                    if (m < M) {
+#pragma unroll
+                        for (int j = 0; j < 2; ++j)
+#pragma unroll
+                            for (int q = 0; q < 4; ++q) {
+                                const int n = nb + j * 32 + 8 * q + 4 * (lane >> 5);
+                                if (n < N)
+                                    *(i32x4*)(g.acc + (int64_t)m * g.ldc + n) =
+                                        i32x4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
+                                              acc[i][j][4 * q + 3]};
+                            }
+                    }
+                }
+            }
+            if constexpr (SW) {
+                // columns j = 0 (gate) and j = 1 (up) of the same 32 outputs -> act
+                // columns nb / 2 .. +31: fp16(fp16(silu(gate)) * up)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    float gv[4], uv[4];
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        gv[r] = deq<KIND>(acc[i][0][4 * q + r], as[i], bs[0][q][r]);
+                        uv[r] = deq<KIND>(acc[i][1][4 * q + r], as[i], bs[1][q][r]);
+                    }
+                    *(u32x2*)(slot + lds_off(lane & 31, q) + (lane >> 5) * 8) =
+                        u32x2{silu_mul2(pack_f16x2(gv[0], gv[1]), pack_f16x2(uv[0], uv[1])),
+                              silu_mul2(pack_f16x2(gv[2], gv[3]), pack_f16x2(uv[2], uv[3]))};
+                }
+                const int na = N >> 1;
+#pragma unroll
+                for (int k = 0; k < 2; ++k) {
+                    const int rl = k * 16 + (lane >> 2), ch = lane & 3;
+                    const u32x4 v = *(const u32x4*)(slot + lds_off(rl, ch));
+                    const int m = mb + rl;
+                    const int n = (nb >> 1) + ch * 8;
+                    if (m < M && n < na) store_row16(g.c + (int64_t)m * g.ldc + n, v, true);
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const int cl = j * 32 + 8 * q + 4 * (lane >> 5);
+                        float o[4];
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            if constexpr (KIND == EE_GEMM_F16) o[r] = acc[i][j][4 * q + r];
+                            else o[r] = deq<KIND>(acc[i][j][4 * q + r], as[i], bs[j][q][r]);
+                        }
+                        // row (lane & 31): 128 bytes = 8 chunks of 16; column cl is chunk cl / 8, half (cl / 4) & 1
+                        *(u32x2*)(slot + lds_off(lane & 31, cl >> 3) + ((cl >> 2) & 1) * 8) =
+                            u32x2{pack_f16x2(o[0], o[1]), pack_f16x2(o[2], o[3])};
+                    }
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const int rl = k * 8 + (lane >> 3), ch = lane & 7;
+                    const u32x4 v = *(const u32x4*)(slot + lds_off(rl, ch));
+                    const int m = mb + rl;
+                    const int n = nb + ch * 8;
+                    if (m < M && n < N) store_row16(g.c + (int64_t)m * g.ldc + n, v, n + 8 <= N);
+                }
+            }
+        }
+    }
+
+    __device__ __forceinline__ void zero() {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) acc[i][j] = acc_t{};
+    }
+
+    // Barrier cs (each wave has waited for its part of stage cs and finished its
+    // reads of stage cs-1), then stage cs+1 into the buffer stage cs-1 used, then
+    // slice 0 of stage cs.
+    __device__ __forceinline__ void enter(int cs) {
+        WAITCNT_LGKM0();
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        if (cs + 1 < total && iss == cs + 1) issue_stage();
+        rd_all(smem + (cs & 1) * T2_STAGE, 0, 0);
+    }
+
+    __device__ __forceinline__ void run() {
+        const int tid = threadIdx.x;
+        lane = tid & 63;
+        wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+        wm = wave >> 2;
+        wn = wave & 3;
+        const int ntiles = deal.count();
+        if (ntiles <= 0) return;                      // whole workgroup, before any barrier
+        nk = (int)((int64_t)g.K * ESZ / BKB);         // K * ESZ is a multiple of BKB here
+        total = ntiles * nk;
+        lds0 = lds_addr(smem);
+        iss = 0;
+        itile = -1;
+        ikt = nk;
+        issue_stage();                                // stage 0 -> buffer 0
+        if (total > 1) {
+            issue_stage();                            // stage 1 -> buffer 1
+            WAITCNT_VM(8);
+        } else {
+            WAITCNT_VM(0);
+        }
+        enter(0);
+        int cs = 0;
+        for (int t = 0; t < ntiles; ++t) {
+            zero();
+            for (int kt = 0; kt + 1 < nk; ++kt, ++cs) stage<false>(cs, cs + 2 < total);
+            stage<true>(cs, false);
+            int m0, n0;
+            coords(t, m0, n0);
+            epilogue(m0, n0);
+            ++cs;
+            if (cs < total) enter(cs);
+        }
+    }
+};
+
+template <int KIND, int SW>
+EE_DEV void gemm256(const EeGemmArgs& g) {
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[T2_LDS];
+    G256<KIND, SW> k(g, smem, (int)blockIdx.x, (int)gridDim.x);
+    k.run();
+}
+
+#define EE_G256_ENTRY(NAME, KIND)                                                                           \
+    extern "C" __global__ void __launch_bounds__(T2_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))   \
+    NAME(EeGemmArgs g) { gemm256<KIND, 0>(g); }                                                           \
+    extern "C" __global__ void __launch_bounds__(T2_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))   \
+    NAME##_swiglu(EeGemmArgs g) { gemm256<KIND, 1>(g); }
+EE_G256_ENTRY(eek_gemm256_i8, EE_GEMM_I8)
+EE_G256_ENTRY(eek_gemm256_f8, EE_GEMM_F8)
+EE_G256_ENTRY(eek_gemm256_f16, EE_GEMM_F16)

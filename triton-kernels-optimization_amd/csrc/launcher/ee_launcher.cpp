@@ -435,6 +435,9 @@ EE_EXPORT int ee_engine_set_option(ee_engine* eng, const char* key, int64_t valu
         if (value != 0 && value != 1) return fail(EE_ERR_INVALID_ARG, k + " must be 0 or 1");
     } else if (k == "gemm_persist") {
         if (value < 0 || value > 65535) return fail(EE_ERR_INVALID_ARG, k + " must be 0 (auto), 1 (off) or a grid >= 2");
+    } else if (k == "gemm_tile") {
+        if (value != 0 && value != 128 && value != 256)
+            return fail(EE_ERR_INVALID_ARG, k + " must be 0 (auto), 128 or 256");
     } else {
         return fail(EE_ERR_INVALID_ARG, "unknown option: " + k);
     }
@@ -633,6 +636,27 @@ static int gemm_impl(ee_engine* eng, int32_t kind, const void* a, int64_t lda, c
     const int64_t tiles = cdiv(M, 128) * cdiv(N, 128);
     std::string name = std::string(names[kind]) + (((K * esz) % 128 == 0) ? "" : "_generic");
     int64_t grid = tiles;
+    // 256 x 256 tiles (eek_gemm256_*) where the 128-tile grid would take more
+    // than one round of the CUs: they stream half the operand bytes per MFMA op.
+    // Same K order as the loader-wave kernels, so INT8 and FP8 give the same bits
+    // either way; the FP16 tier takes them only when forced ("gemm_tile" = 256),
+    // since its automatic pipeline (8-wave, split K) sums in another f32 order.
+    const int64_t tile_opt = opt(eng, "gemm_tile");
+    // (The kernels address a 256-row panel with 32-bit byte offsets.)
+    const bool off32 = 255 * std::max(lda, ldb) * esz + K * esz < (int64_t(1) << 32);
+    if ((K * esz) % 128 == 0 && counts == nullptr && tile_opt != 128 && off32 &&
+        (tile_opt == 256 || (kind != EE_GEMM_F16 && tiles > eng->cus))) {
+        static const char* names256[3] = {"eek_gemm256_i8", "eek_gemm256_f8", "eek_gemm256_f16"};
+        std::string n256 = std::string(names256[kind]) + (sw ? "_swiglu" : "");
+        const Kernel* k256 = find_kernel(eng, n256);
+        if (k256 != nullptr) {
+            const int64_t t256 = cdiv(M, 256) * cdiv(N, 256);
+            int64_t g256 = persist_grid(eng, t256);
+            if (g256 <= 0) g256 = std::min<int64_t>(t256, eng->cus >= 8 ? (eng->cus & ~7) : eng->cus);
+            if (g256 <= 0) g256 = t256;
+            return launch(eng, n256, g256, 1, k256->block, g, stream);
+        }
+    }
     if ((K * esz) % 128 == 0) {
         const int64_t v = opt(eng, "gemm_variant");
         const bool w8 = v == 2 || (v == 0 && (kind == EE_GEMM_F16 || (kind == EE_GEMM_I8 && tiles <= 256)));
