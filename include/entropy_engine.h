@@ -83,17 +83,18 @@ int ee_engine_destroy(ee_engine* eng);
  * "routed_unfused" = 1 makes ee_routed_linear use its five-launch sequence for
  * every K (for comparisons); "gemm_variant" = 1 runs every GEMM on the
  * loader-wave pipeline, 2 on the 8-wave pipeline where one exists (INT8 and
- * W8A16); automatic: 8-wave for W8A16, and for INT8 grids of at most one tile
- * per CU.  INT8 results are identical either way; the FP16 tier's f32
- * summation order follows the pipeline (the routed linear follows ee_gemm).
+ * W8A16); automatic: 8-wave for INT8 grids of at most one tile per CU.  INT8
+ * results are identical either way.  Every FP16-tier kernel sums K in one f32
+ * order (slice after slice), whatever the shape, tile size or routing, except
+ * the 8-wave form (gemm_variant = 2), which splits K between wave pairs; the
+ * routed linear follows ee_gemm's choice.
  * "gemm_persist": INT8 / FP8 GEMMs with more tiles than CUs (and the routed
  * linear's tier grid) run as persistent grids, one workgroup per CU walking
  * its tiles with the stage ring running across tile boundaries; 1 turns that
  * off, n >= 2 forces it with min(n, tiles) workgroups.  Same bits either way.
- * "gemm_tile": 256 x 256-tile persistent kernels for un-routed GEMMs whose
- * 128 x 128 grid has more tiles than CUs (automatic for INT8 and FP8, whose
- * bits do not change); 128 forbids them, 256 forces them for every tier
- * (the FP16 tier then sums K in the loader-wave pipeline's order). */
+ * "gemm_tile": 256 x 256-tile persistent kernels (plain and routed) for GEMMs
+ * whose 128 x 128 grid has more tiles than CUs (automatic; same bits); 128
+ * forbids them, 256 forces them at every size. */
 int ee_engine_set_option(ee_engine* eng, const char* key, int64_t value);
 int ee_engine_device(const ee_engine* eng);
 

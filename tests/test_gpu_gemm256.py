@@ -1,7 +1,7 @@
 """GPU parity of the 256 x 256-tile persistent GEMMs (eek_gemm256_*).
 
-They replace the 128 x 128 kernels for un-routed GEMMs with more 128-tiles
-than CUs (configs 1-2, the TinyLlama projections), so each case checks them
+They replace the 128 x 128 kernels for GEMMs and routed linears with more
+128-tiles than CUs (configs 1-4), so each case checks them
 against the oracle -- INT8 fp16 outputs and int32 accumulators bit-exact,
 FP8 / FP16 within 1e-2 of a float64 recompute -- and, bit for bit, against the
 128-tile kernels on the same inputs (same K order: FP8 and FP16 sum slice after
@@ -161,3 +161,73 @@ def test_gemm256_swiglu(ee, orc, M, K, F):
 def test_gemm256_option_rejects_bad_value(ee):
     from entropy_engine import _lib
     assert _lib.lib().ee_engine_set_option(_lib.engine(), b"gemm_tile", 192) == _lib.EE_ERR_INVALID_ARG
+
+
+# ---------------------------------------------------------------------------- routed
+
+@pytest.mark.parametrize("M,K,N,H_hi,grid", [(300, 512, 520, 3.0, 0), (700, 1024, 384, 3.0, 8), (700, 256, 264, 3.0, 3),
+                                             (129, 256, 128, 10.0, 0), (257, 512, 256, 0.3, 0), (1, 128, 64, 1.0, 0)])
+def test_gemm256_routed_equals_per_tier(ee, orc, M, K, N, H_hi, grid):
+    """The 256-tile routed grid (three phases per workgroup: FP16, INT8, FP8
+    tiles): every row equals the un-routed GEMM of its tier bit for bit, and the
+    128-tile routed grid gives the same output.  Entropy ranges make tiers
+    empty (H_hi 0.3: INT8 only; 10: mostly FP16)."""
+    rng = np.random.default_rng(M * 3 + K + N)
+    X = rng.standard_normal((M, K)).astype(np.float16)
+    B, bs = weights(orc, rng, N, K)
+    H = (rng.random(M) * H_hi).astype(np.float32)
+    pw = ee.prepare_weight(cuda(B), cuda(bs)).materialize()
+    x = cuda(X)
+    tier, idx, counts = ee.route(cuda(H), 0.41, 1.68)
+    with _Options(gemm_tile=256, gemm_persist=grid):
+        out = host(ee.routed_linear(x, pw, idx, counts)).view(np.uint16)
+    with _Options(gemm_tile=128):
+        ref128 = host(ee.routed_linear(x, pw, idx, counts)).view(np.uint16)
+    assert np.array_equal(out, ref128)
+    t = host(tier)
+    full = [ee.triton_int8_gemm(x, cuda(B), cuda(bs)), ee.triton_fp8_gemm(x, cuda(B), cuda(bs)),
+            ee.triton_fp16_gemm(x, cuda(B), cuda(bs))]
+    for k in range(3):
+        if (t == k).any():
+            assert np.array_equal(out[t == k], host(full[k]).view(np.uint16)[t == k]), f"tier {k}"
+
+
+def test_gemm256_routed_config3(ee, orc):
+    """Config 3's routed linear (M = K = N = 4096, 20/40/40 % tiers) takes the
+    256-tile routed grid automatically: rows equal the per-tier GEMMs bit for bit,
+    INT8 rows equal the oracle on sampled rows, FP8 / FP16 rows within 1e-2."""
+    M = K = N = 4096
+    rng = np.random.default_rng(3)
+    X = rng.standard_normal((M, K)).astype(np.float16)
+    B, bs = weights(orc, rng, N, K)
+    H = rng.choice(np.array([0.2, 1.0, 3.0], np.float32), M, p=[0.2, 0.4, 0.4])
+    pw = ee.prepare_weight(cuda(B), cuda(bs)).materialize()
+    x = cuda(X)
+    tier, idx, counts = ee.route(cuda(H), 0.41, 1.68)
+    out = host(ee.routed_linear(x, pw, idx, counts))
+    t = host(tier)
+    for k, fn in enumerate((ee.triton_int8_gemm, ee.triton_fp8_gemm, ee.triton_fp16_gemm)):
+        ref = host(fn(x, cuda(B), cuda(bs)))
+        assert np.array_equal(out[t == k].view(np.uint16), ref[t == k].view(np.uint16)), f"tier {k}"
+    rows = [np.nonzero(t == k)[0][[0, -1]] for k in range(3)]
+    assert np.array_equal(out[rows[0]].view(np.uint16), orc.triton_int8_gemm(X[rows[0]], B, bs).view(np.uint16))
+    check_close_f64(out[rows[1]], orc.triton_fp8_gemm_f64(X[rows[1]], B, bs))
+    check_close_f64(out[rows[2]], orc.triton_fp16_gemm_f64(X[rows[2]], B, bs))
+
+
+@pytest.mark.parametrize("M,K,F", [(4096, 2048, 1408), (600, 256, 320)])
+def test_gemm256_routed_swiglu(ee, orc, M, K, F):
+    """SwiGLU epilogue of the 256-tile routed grid: the bits of the 128-tile
+    routed SwiGLU grid."""
+    rng = np.random.default_rng(M + 7 * F)
+    W = (rng.standard_normal((2 * F, K)) / np.sqrt(K)).astype(np.float16)
+    codes, scale = ee.quantize_weight_codes(cuda(W))
+    pw = ee.PackedWeight(ee.interleave_gate_up(codes), ee.interleave_gate_up(scale)).materialize()
+    x = cuda(rng.standard_normal((M, K)).astype(np.float16))
+    h = cuda((rng.random(M) * 3).astype(np.float32))
+    _, idx, counts = ee.route(h, 0.41, 1.68)
+    with _Options(gemm_tile=256):
+        fused = ee.routed_linear(x, pw, idx, counts, swiglu=True)
+    with _Options(gemm_tile=128):
+        ref = ee.routed_linear(x, pw, idx, counts, swiglu=True)
+    assert torch.equal(fused.view(torch.int16), ref.view(torch.int16))

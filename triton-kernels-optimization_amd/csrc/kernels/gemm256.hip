@@ -48,7 +48,7 @@
 #define T2_LDS (T2_EPI + 8 * T2_SLOT)     // 160 KB
 #define T2_THREADS 512
 
-template <int KIND, int SW>
+template <int KIND, int SW, class Seq>
 struct G256 {
     typedef Pipe<KIND> P;
     typedef typename P::acc_t acc_t;
@@ -58,7 +58,9 @@ struct G256 {
 
     const EeGemmArgs& g;
     uint8_t* smem;
-    TileDeal deal;
+    const Seq& seq;                                   // tiles of this workgroup: count(), coords(i, m0, n0)
+    int M;                                            // rows (counts[tier] when routed)
+    int64_t off;                                      // partition slot of row 0 (routed), else 0
     uint32_t lds0;
     int lane, wave, wm, wn;
     int nk, total;                                    // stages per tile, stages of this workgroup
@@ -76,12 +78,12 @@ struct G256 {
     static constexpr int NB = (KIND == EE_GEMM_F8) ? 1 : 2;
     frag_t fa[4], fb[NB][2];
 
-    __device__ __forceinline__ G256(const EeGemmArgs& g_, uint8_t* smem_, int b, int G)
-        : g(g_), smem(smem_), deal((g_.M + T2M - 1) / T2M, (g_.N + T2N - 1) / T2N, 0, b, G) {}
+    __device__ __forceinline__ G256(const EeGemmArgs& g_, uint8_t* smem_, const Seq& seq_, int M_, int64_t off_)
+        : g(g_), smem(smem_), seq(seq_), M(M_), off(off_) {}
 
     __device__ __forceinline__ void coords(int i, int& m0, int& n0) const {
         int tm, tn;
-        deal.coords(deal.tile_index(deal.first_round + i), tm, tn);
+        seq.coords(i, tm, tn);
         m0 = tm * T2M;
         n0 = tn * T2N;
     }
@@ -91,17 +93,22 @@ struct G256 {
     // logical chunk (l % 8) ^ swz(row).  Wave w fills row groups 4w .. 4w+3 of
     // A and of B (rows are clamped: out-of-range rows load a valid row whose
     // results are never stored).
+    // Un-routed: offsets from the tile's first row.  Routed (g.counts): A row m
+    // is a[a_idx[off + m]] or a[off + m], offsets from the operand's start (the
+    // launcher checks that they fit 32 bits).
     __device__ __forceinline__ void dma_tile(int i) {
         int m0, n0;
         coords(i, m0, n0);
-        abase = (const uint8_t*)g.a + (int64_t)m0 * g.lda * ESZ;
+        constexpr bool routed = Seq::ROUTED;
+        abase = (const uint8_t*)g.a + (routed ? 0 : (int64_t)m0 * g.lda * ESZ);
         bbase = (const uint8_t*)g.b + (int64_t)n0 * g.ldb * ESZ;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const int r = (wave * 4 + q) * 8 + (lane >> 3);
             const int lchunk = (lane & 7) ^ swz(r);   // swz(T2M + r) == swz(r)
-            const int m = min(m0 + r, g.M - 1) - m0;
-            aoff[q] = (uint32_t)(m * g.lda * ESZ + lchunk * 16);
+            const int m = min(m0 + r, M - 1);
+            const int64_t ar = !routed ? (int64_t)(m - m0) : Seq::GATHER ? (int64_t)g.a_idx[off + m] : off + m;
+            aoff[q] = (uint32_t)(ar * g.lda * ESZ + lchunk * 16);
             const int n = min(n0 + r, g.N - 1) - n0;
             boff[q] = (uint32_t)(n * g.ldb * ESZ + lchunk * 16);
         }
@@ -267,7 +274,7 @@ struct G256 {
     // slot.  Scales are loaded first; the wait for them also covers this wave's
     // part of the next DMA stage (the one barrier cs+1 will publish).
     __device__ __forceinline__ void epilogue(int m0, int n0) {
-        const int M = g.M, N = g.N;
+        const int N = g.N;
         // The lane index through an empty asm: the epilogue's addresses are then
         // computed here instead of being hoisted out of the tile loop, where they
         // would hold ~20 VGPRs across the K loop.
@@ -286,9 +293,30 @@ struct G256 {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int m = m0 + wm * 128 + i * 32 + (lane & 31);
-                as[i] = (m < M) ? g.a_scale[m] : 0.0f;
+                as[i] = (m < M) ? g.a_scale[off + m] : 0.0f;
             }
         }
+        // C row of wave row r (0..127) of the tile, -1 beyond M.  Routed rows are
+        // scattered through c_idx: lane l loads the C rows of wave rows l and
+        // 64 + l here, with the scales, and each store round fetches its row
+        // from the lane that holds it (ds_bpermute: a cross-lane move, no LDS
+        // memory), two registers instead of a 16-entry table.
+        int32_t cr[2];
+        if constexpr (Seq::ROUTED) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int m = m0 + wm * 128 + h * 64 + lane;
+                cr[h] = (m < M) ? (g.c_idx ? g.c_idx[off + m] : m) : -1;
+            }
+        }
+        auto crow_of = [&](int r) -> int32_t {
+            if constexpr (Seq::ROUTED) {
+                return __builtin_amdgcn_ds_bpermute((r & 63) << 2, cr[r >> 6]);
+            } else {
+                const int m = m0 + wm * 128 + r;
+                return m < M ? m : -1;
+            }
+        };
         WAITCNT_VM(0);
         asm volatile("" ::: "memory");
         uint8_t* slot = smem + T2_EPI + wave * T2_SLOT;
@@ -297,7 +325,7 @@ struct G256 {
             const int mb = m0 + wm * 128 + i * 32;    // first row of this 32 x 64 block
             const int nb = n0 + wn * 64;
             if constexpr (KIND == EE_GEMM_I8) {
-                if (g.acc) {                          // debug output: int32 accumulators, direct stores
+                if (!Seq::ROUTED && g.acc) {          // debug output: int32 accumulators, direct stores
                     const int m = mb + (lane & 31);
                     if (m < M) {
 #pragma unroll
@@ -333,9 +361,9 @@ struct G256 {
                 for (int k = 0; k < 2; ++k) {
                     const int rl = k * 16 + (lane >> 2), ch = lane & 3;
                     const u32x4 v = *(const u32x4*)(slot + lds_off(rl, ch));
-                    const int m = mb + rl;
                     const int n = (nb >> 1) + ch * 8;
-                    if (m < M && n < na) store_row16(g.c + (int64_t)m * g.ldc + n, v, true);
+                    const int32_t crow = crow_of(i * 32 + rl);
+                    if (crow >= 0 && n < na) store_row16(g.c + (int64_t)crow * g.ldc + n, v, true);
                 }
             } else {
 #pragma unroll
@@ -357,9 +385,9 @@ struct G256 {
                 for (int k = 0; k < 4; ++k) {
                     const int rl = k * 8 + (lane >> 3), ch = lane & 7;
                     const u32x4 v = *(const u32x4*)(slot + lds_off(rl, ch));
-                    const int m = mb + rl;
                     const int n = nb + ch * 8;
-                    if (m < M && n < N) store_row16(g.c + (int64_t)m * g.ldc + n, v, n + 8 <= N);
+                    const int32_t crow = crow_of(i * 32 + rl);
+                    if (crow >= 0 && n < N) store_row16(g.c + (int64_t)crow * g.ldc + n, v, n + 8 <= N);
                 }
             }
         }
@@ -390,7 +418,7 @@ struct G256 {
         wave = __builtin_amdgcn_readfirstlane(tid >> 6);
         wm = wave >> 2;
         wn = wave & 3;
-        const int ntiles = deal.count();
+        const int ntiles = seq.count();
         if (ntiles <= 0) return;                      // whole workgroup, before any barrier
         nk = (int)((int64_t)g.K * ESZ / BKB);         // K * ESZ is a multiple of BKB here
         total = ntiles * nk;
@@ -420,11 +448,104 @@ struct G256 {
     }
 };
 
+// Tiles of an un-routed GEMM for workgroup b of G (TileDeal: 8 x 4 blocks per XCD).
+struct Seq256 {
+    static constexpr bool ROUTED = false, GATHER = false;
+    TileDeal d;
+    __device__ __forceinline__ Seq256(const EeGemmArgs& g, int b, int G)
+        : d((g.M + T2M - 1) / T2M, (g.N + T2N - 1) / T2N, 0, b, G) {}
+    __device__ __forceinline__ int count() const { return d.count(); }
+    __device__ __forceinline__ void coords(int i, int& tm, int& tn) const {
+        d.coords(d.tile_index(d.first_round + i), tm, tn);
+    }
+};
+
 template <int KIND, int SW>
 EE_DEV void gemm256(const EeGemmArgs& g) {
     __shared__ __attribute__((aligned(1024))) uint8_t smem[T2_LDS];
-    G256<KIND, SW> k(g, smem, (int)blockIdx.x, (int)gridDim.x);
+    const Seq256 seq(g, (int)blockIdx.x, (int)gridDim.x);
+    G256<KIND, SW, Seq256> k(g, smem, seq, g.M, 0);
     k.run();
+}
+
+// ---------------------------------------------------------------- routed
+// The routed linear's three tier GEMMs as one persistent grid on 256 x 256
+// tiles.  Tier t owns ceil(counts[t] / 256) M-tiles of its partition slots.
+// FP16 (W8A16) tiles, twice the work of a 1-byte tile at the same K, are
+// dealt first, round robin; the 1-byte tiles -- all INT8 tiles, then all FP8
+// tiles, each tier in bands of 8 M-tiles along N -- follow in TileDeal rounds
+// (workgroups holding an extra FP16 tile skip the first two).  A workgroup
+// then runs its tiles in three phases (FP16, INT8, FP8), one G256 pipeline
+// each; the tier order of the 1-byte list makes each phase a contiguous run.
+// Every tile sums K in the order of the un-routed kernels, so routed rows equal
+// ee_gemm's rows of the same tier bit for bit.
+
+// logical tile a of a tiles_m x tiles_n grid -> (tm, tn): bands of 8 M-tiles, M fastest
+EE_DEV void band_coords(int a, int tiles_m, int tiles_n, int& tm, int& tn) {
+    const int band = a / (8 * tiles_n);
+    const int m_first = band * 8;
+    const int gsz = min(tiles_m - m_first, 8);
+    const int r = a - band * 8 * tiles_n;
+    tm = m_first + r % gsz;
+    tn = r / gsz;
+}
+
+// The 1-byte tiles lo .. hi-1 of this workgroup's deal (INT8 or FP8 phase).
+struct SeqR1 {
+    static constexpr bool ROUTED = true, GATHER = false;   // codes sit at their partition slots
+    const TileDeal& d;
+    int lo, n, T0, T1, nN;
+    __device__ __forceinline__ int count() const { return n; }
+    __device__ __forceinline__ void coords(int i, int& tm, int& tn) const {
+        const int a = d.tile_index(d.first_round + lo + i);
+        if (a < T0 * nN) band_coords(a, T0, nN, tm, tn);
+        else band_coords(a - T0 * nN, T1, nN, tm, tn);
+    }
+};
+// The FP16 tiles f = b, b + G, ... < nF: M-tile f % T2, N-tile f / T2.
+struct SeqRF {
+    static constexpr bool ROUTED = true, GATHER = true;    // fp16 rows gathered from x through a_idx
+    int b, G, n, T2;
+    __device__ __forceinline__ int count() const { return n; }
+    __device__ __forceinline__ void coords(int i, int& tm, int& tn) const {
+        const int f = b + i * G;
+        tm = f % T2;
+        tn = f / T2;
+    }
+};
+
+template <int SW>
+EE_DEV void gemm256_routed(const EeRoutedGemmArgs& r) {
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[T2_LDS];
+    const int32_t* counts = r.t[0].counts;
+    const int c0 = counts[0], c1 = counts[1], c2 = counts[2];
+    const int T0 = (c0 + T2M - 1) / T2M, T1 = (c1 + T2M - 1) / T2M, T2 = (c2 + T2M - 1) / T2M;
+    const int nN = (r.t[0].N + T2N - 1) / T2N;
+    const int b = (int)blockIdx.x, G = (int)gridDim.x;
+    const int nF = T2 * nN;
+    const TileDeal d(T0 + T1, nN, nF, b, G);
+    // phase FP16
+    const SeqRF sf{b, G, b < nF ? (nF - b + G - 1) / G : 0, T2};
+    if (sf.n > 0) {
+        G256<EE_GEMM_F16, SW, SeqRF> k(r.t[2], smem, sf, c2, (int64_t)c0 + c1);
+        k.run();
+    }
+    // the 1-byte tiles: the INT8 ones come first (logical index < T0 * nN)
+    const int n1 = d.count();
+    int ni8 = 0;
+    while (ni8 < n1 && d.tile_index(d.first_round + ni8) < T0 * nN) ++ni8;
+    if (ni8 > 0) {
+        if (sf.n > 0) __syncthreads();                // the previous phase's LDS reads and DMA are done
+        const SeqR1 s8{d, 0, ni8, T0, T1, nN};
+        G256<EE_GEMM_I8, SW, SeqR1> k(r.t[0], smem, s8, c0, 0);
+        k.run();
+    }
+    if (n1 > ni8) {
+        if (sf.n > 0 || ni8 > 0) __syncthreads();
+        const SeqR1 s8{d, ni8, n1 - ni8, T0, T1, nN};
+        G256<EE_GEMM_F8, SW, SeqR1> k(r.t[1], smem, s8, c1, c0);
+        k.run();
+    }
 }
 
 #define EE_G256_ENTRY(NAME, KIND)                                                                           \
@@ -435,3 +556,11 @@ EE_DEV void gemm256(const EeGemmArgs& g) {
 EE_G256_ENTRY(eek_gemm256_i8, EE_GEMM_I8)
 EE_G256_ENTRY(eek_gemm256_f8, EE_GEMM_F8)
 EE_G256_ENTRY(eek_gemm256_f16, EE_GEMM_F16)
+extern "C" __global__ void __launch_bounds__(T2_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
+eek_gemm256_routed(EeRoutedGemmArgs r) {
+    gemm256_routed<0>(r);
+}
+extern "C" __global__ void __launch_bounds__(T2_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
+eek_gemm256_routed_swiglu(EeRoutedGemmArgs r) {
+    gemm256_routed<1>(r);
+}

@@ -628,24 +628,28 @@ static int gemm_impl(ee_engine* eng, int32_t kind, const void* a, int64_t lda, c
     // The pipelined kernels stream whole 128-byte K stages; other K take the fallback.
     // Two pipelines: loader waves + MFMA waves (eek_gemm_*), and eight waves that
     // each load and compute (eek_gemm_*_w8).  Measured on MI355X (identical data,
-    // interleaved runs): the 8-wave form is faster for W8A16 at every shape and
-    // for INT8 when the grid is at most one tile per CU (1024 x 4096 x 4096:
-    // 22.9 vs 24.9 us); with several tiles per CU the loader-wave form is ~5%
-    // faster for INT8.  FP8 keeps the loader-wave form (its 8-wave form spills).
+    // interleaved runs): the 8-wave form is faster for INT8 when the grid is at
+    // most one tile per CU (1024 x 4096 x 4096: 22.9 vs 24.9 us); with several
+    // tiles per CU the loader-wave form is ~5% faster.  FP8 keeps the loader-wave
+    // form (its 8-wave form spills).  The FP16 tier takes the loader-wave form
+    // unless gemm_variant = 2: its 8-wave form splits K between wave pairs, an f32
+    // order no other kernel (the 256 tiles, the routed grids) shares, and every
+    // FP16 row must get the same bits whatever the shape or routing.
     static const char* names[3] = {"eek_gemm_i8", "eek_gemm_f8", "eek_gemm_f16"};
     const int64_t tiles = cdiv(M, 128) * cdiv(N, 128);
     std::string name = std::string(names[kind]) + (((K * esz) % 128 == 0) ? "" : "_generic");
     int64_t grid = tiles;
     // 256 x 256 tiles (eek_gemm256_*) where the 128-tile grid would take more
     // than one round of the CUs: they stream half the operand bytes per MFMA op.
-    // Same K order as the loader-wave kernels, so INT8 and FP8 give the same bits
-    // either way; the FP16 tier takes them only when forced ("gemm_tile" = 256),
-    // since its automatic pipeline (8-wave, split K) sums in another f32 order.
+    // They sum K in the loader-wave kernels' order, so every tier gives the same
+    // bits either way (the FP16 tier's 8-wave split-K pipeline, gemm_variant 2,
+    // has its own order and keeps the 128 tiles).
     const int64_t tile_opt = opt(eng, "gemm_tile");
+    const int64_t variant = opt(eng, "gemm_variant");
     // (The kernels address a 256-row panel with 32-bit byte offsets.)
     const bool off32 = 255 * std::max(lda, ldb) * esz + K * esz < (int64_t(1) << 32);
     if ((K * esz) % 128 == 0 && counts == nullptr && tile_opt != 128 && off32 &&
-        (tile_opt == 256 || (kind != EE_GEMM_F16 && tiles > eng->cus))) {
+        !(kind == EE_GEMM_F16 && variant == 2) && (tile_opt == 256 || tiles > eng->cus)) {
         static const char* names256[3] = {"eek_gemm256_i8", "eek_gemm256_f8", "eek_gemm256_f16"};
         std::string n256 = std::string(names256[kind]) + (sw ? "_swiglu" : "");
         const Kernel* k256 = find_kernel(eng, n256);
@@ -658,8 +662,8 @@ static int gemm_impl(ee_engine* eng, int32_t kind, const void* a, int64_t lda, c
         }
     }
     if ((K * esz) % 128 == 0) {
-        const int64_t v = opt(eng, "gemm_variant");
-        const bool w8 = v == 2 || (v == 0 && (kind == EE_GEMM_F16 || (kind == EE_GEMM_I8 && tiles <= 256)));
+        const int64_t v = variant;
+        const bool w8 = v == 2 || (v == 0 && kind == EE_GEMM_I8 && tiles <= 256);
         if (w8 && find_kernel(eng, name + "_w8")) {
             name += "_w8";
         } else if (kind != EE_GEMM_F16 && counts == nullptr) {
@@ -768,8 +772,22 @@ static int routed_impl(ee_engine* eng, const void* x, int64_t ld_x, int32_t M, i
         ra.t[2] = EeGemmArgs{x, b_f16, (uint16_t*)c, nullptr, nullptr, nullptr, idx, idx, counts,
                              ld_x, K, ldc, M, N, K, EE_TIER_FP16, sw};
         ra.mt_max = (int32_t)cdiv(M, 128) + 2;
-        ra.f16_w8 = opt(eng, "gemm_variant") != 1;   // the FP16 pipeline ee_gemm picks (same f32 order)
+        ra.f16_w8 = opt(eng, "gemm_variant") == 2;   // the FP16 pipeline ee_gemm picks (same f32 order)
         const int64_t slots = (int64_t)ra.mt_max * cdiv(N, 128);
+        // Large grids: the 256 x 256-tile routed kernel (same K order in every tier).
+        // Its DMA addresses rows from the operands' starts with 32-bit offsets.
+        const int64_t tile_opt = opt(eng, "gemm_tile");
+        const bool off32 = std::max<int64_t>((int64_t)M * ld_x * 2, (int64_t)M * K) + 2 * K < (int64_t(1) << 32) &&
+                           255 * 2 * (int64_t)K + 2 * K < (int64_t(1) << 32);
+        if (!ra.f16_w8 && tile_opt != 128 && off32 && (tile_opt == 256 || slots > eng->cus)) {
+            std::string n256 = sw ? "eek_gemm256_routed_swiglu" : "eek_gemm256_routed";
+            const Kernel* k256 = find_kernel(eng, n256);
+            if (k256 != nullptr) {
+                const int64_t g256 = eng->cus >= 8 ? (eng->cus & ~7) : std::max(1, eng->cus);
+                const int64_t pv = opt(eng, "gemm_persist");
+                return launch(eng, n256, pv >= 2 ? pv : g256, 1, k256->block, ra, stream);
+            }
+        }
         const int64_t pg = ra.f16_w8 ? persist_grid(eng, slots) : 0;   // its W8A16 tiles run on Gemm8
         std::string rname = pg > 0 ? "eek_gemm_routed_persist" : "eek_gemm_routed";
         if (sw) rname += "_swiglu";
