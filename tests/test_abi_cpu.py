@@ -8,6 +8,7 @@ CPU tensors.
 import ctypes
 import json
 import os
+import subprocess
 import re
 
 import pytest
@@ -62,17 +63,60 @@ def test_engine_create_errors(L, tmp_path):
     rc, msg, _ = _create(L, str(tmp_path))
     assert rc == _lib.EE_ERR_META and "format" in msg
     meta = {"format": "entropy-engine-meta/1", "code_objects": {"gemm": {"file": "gemm.hsaco"}},
-            "kernels": {"eek_gemm_i8": {"code_object": "gemm", "block": 256, "lds": 65536}}}
+            "kernels": {"eek_gemm_i8": {"code_object": "gemm", "block": 256, "lds": 65536, "kernarg": 112}}}
     (tmp_path / "entropy_engine_meta.json").write_text(json.dumps(meta))
     rc, msg, _ = _create(L, str(tmp_path))
     assert rc == _lib.EE_ERR_IO and "Could not open code object" in msg
     (tmp_path / "gemm.hsaco").write_bytes(b"not an elf at all")
     rc, msg, _ = _create(L, str(tmp_path))
     assert rc == _lib.EE_ERR_IO and "Not an ELF" in msg
+    del meta["kernels"]["eek_gemm_i8"]["kernarg"]
+    (tmp_path / "entropy_engine_meta.json").write_text(json.dumps(meta))
+    rc, msg, _ = _create(L, str(tmp_path))
+    assert rc == _lib.EE_ERR_META and "Missing key: kernarg" in msg
     del meta["kernels"]["eek_gemm_i8"]["lds"]
     (tmp_path / "entropy_engine_meta.json").write_text(json.dumps(meta))
     rc, msg, _ = _create(L, str(tmp_path))
     assert rc == _lib.EE_ERR_META and "Missing key: lds" in msg
+
+
+# kernel name prefix -> the argument struct its entry takes (csrc/kernels/*.hip)
+_ARG_STRUCTS = [
+    ("eek_gemm256_routed", "EeRoutedGemmArgs"), ("eek_gemm_routed", "EeRoutedGemmArgs"), ("eek_gemm", "EeGemmArgs"),
+    ("eek_softmax_entropy", "EeSoftmaxArgs"), ("eek_quant", "EeQuantArgs"), ("eek_absmax_partial", "EeAbsmaxArgs"),
+    ("eek_route", "EeRouteArgs"), ("eek_transpose_i8", "EeWeightArgs"), ("eek_pack_b", "EeWeightArgs"),
+    ("eek_quant_weight", "EeWeightArgs"), ("eek_row_copy", "EeRowCopyArgs"), ("eek_silu_mul", "EeSiluMulArgs"),
+    ("eek_interleave_rows", "EeInterleaveArgs"), ("eek_add_rmsnorm_route", "EeRmsNormRouteArgs"),
+    ("eek_add_rmsnorm", "EeRmsNormArgs"), ("eek_qkv_rope", "EeQkvRopeArgs"), ("eek_attn", "EeAttnArgs"),
+]
+
+
+def _struct_sizes(tmp_path):
+    """sizeof of every argument struct on the host, from ee_kernel_args.h (plain C layout)."""
+    names = sorted(set(n for _, n in _ARG_STRUCTS))
+    src = tmp_path / "sizes.cpp"
+    src.write_text('#include <cstdio>\n#include "common/ee_kernel_args.h"\nint main() {\n' +
+                   "".join(f'  std::printf("{n} %zu\\n", sizeof({n}));\n' for n in names) + "}\n")
+    exe = tmp_path / "sizes"
+    subprocess.run(["g++", "-std=c++17", "-I", os.path.join(PKG, "csrc"), "-I", os.path.join(ROOT, "include"),
+                    str(src), "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout
+    return {l.split()[0]: int(l.split()[1]) for l in out.splitlines()}
+
+
+def test_meta_kernarg_sizes_match_the_argument_structs(tmp_path):
+    """Every kernel's by-value argument block (read from its code object's notes
+    into the meta) has the size of the struct the launcher passes it, which
+    launch() also checks before every launch."""
+    meta = json.load(open(os.path.join(PKG, "lib", "entropy_engine_meta.json")))
+    sizes = _struct_sizes(tmp_path)
+    src = open(os.path.join(PKG, "csrc", "launcher", "ee_launcher.cpp")).read()
+    assert "sizeof(Args) != k->kernarg" in src
+    for name, k in meta["kernels"].items():
+        struct = next((n for p, n in _ARG_STRUCTS if name.startswith(p) and
+                       not (p == "eek_quant" and name.startswith("eek_quant_weight"))), None)
+        assert struct is not None, f"no argument struct known for {name}"
+        assert k["kernarg"] == sizes[struct], f"{name}: meta {k['kernarg']} B, {struct} {sizes[struct]} B"
 
 
 def test_module_engine_errors(L, tmp_path):

@@ -71,13 +71,23 @@ def read_notes(hsaco: str):
     """Kernel descriptors from the code object's AMDGPU metadata note."""
     readelf = os.path.join(ROCM, "llvm", "bin", "llvm-readelf")
     text = _run([readelf, "--notes", hsaco])
-    kernels, cur = [], None
+    kernels, cur, arg_size = [], None, 0
     for line in text.splitlines():
-        m = re.match(r"\s+\.(\w+):\s+(.*)$", line)
+        m = re.match(r"\s+(?:- )?\.(\w+):\s*(.*)$", line)
         if not m:
             continue
         key, val = m.group(1), m.group(2).strip()
         if key == "args":
+            if cur is None:
+                cur = {}
+            cur["kernarg"] = 0
+            continue
+        if key == "size":                            # an entry of .args
+            arg_size = int(val)
+            continue
+        if key == "value_kind":                      # explicit arguments only (no hidden ones)
+            if val == "by_value" and cur is not None:
+                cur["kernarg"] = cur.get("kernarg", 0) + arg_size
             continue
         if key in ("group_segment_fixed_size", "max_flat_workgroup_size", "vgpr_count", "agpr_count",
                    "sgpr_count", "private_segment_fixed_size", "kernarg_segment_size", "name"):
@@ -120,7 +130,12 @@ def build(jobs: int = 8, only_host: bool = False, verbose: bool = True) -> str:
                     "lds": k["group_segment_fixed_size"],
                     "max_flat_workgroup_size": k["max_flat_workgroup_size"],
                     "vgpr": k["vgpr_count"], "agpr": k.get("agpr_count", 0), "sgpr": k.get("sgpr_count", 0),
+                    # bytes of the kernel's by-value argument block; the launcher checks
+                    # it against the size of the struct it passes
+                    "kernarg": k.get("kernarg", 0),
                 }
+                if meta["kernels"][k["name"]]["kernarg"] <= 0:
+                    raise RuntimeError(f"{k['name']}: no by-value argument block in the code object's notes")
         for name, kern in GEMM_META.items():
             d = meta["kernels"][kern]
             with open(os.path.join(LIB, name + "_meta.json"), "w") as f:

@@ -177,6 +177,7 @@ struct Kernel {
     hipFunction_t fn = nullptr;
     int block = 0;
     int lds = 0;
+    int kernarg = 0;                          // bytes of its by-value argument block (meta)
 };
 
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
@@ -225,6 +226,9 @@ int launch(ee_engine* e, const std::string& name, int64_t gx, int64_t gy, int bl
     if (block != k->block)
         return fail(EE_ERR_META, "launch block " + std::to_string(block) + " != meta block " +
                                      std::to_string(k->block) + " for " + name);
+    if ((int)sizeof(Args) != k->kernarg)
+        return fail(EE_ERR_INVALID_ARG, "argument block of " + name + " is " + std::to_string(sizeof(Args)) +
+                                            " bytes but its code object takes " + std::to_string(k->kernarg));
     int rc = check_device(e->device);
     if (rc) return rc;
     void* params[] = {&args};
@@ -333,7 +337,7 @@ EE_EXPORT int ee_engine_create(const char* lib_dir, ee_engine** out) {
     if (kns == nullptr || kns->kind != Json::OBJ) return fail(EE_ERR_META, "Missing key: kernels (" + meta_path + ")");
 
     // Validate the whole meta, then read every code object, before touching HIP.
-    struct KSpec { std::string co; int64_t block, lds; };
+    struct KSpec { std::string co; int64_t block, lds, kernarg; };
     std::map<std::string, KSpec> specs;
     for (const auto& kv : kns->obj) {
         const Json* co = kv.second.get("code_object");
@@ -341,10 +345,12 @@ EE_EXPORT int ee_engine_create(const char* lib_dir, ee_engine** out) {
             return fail(EE_ERR_META, "Missing key: code_object for kernel " + kv.first + " (" + meta_path + ")");
         if (cos->get(co->str) == nullptr)
             return fail(EE_ERR_META, "kernel " + kv.first + " names unknown code object " + co->str);
-        KSpec s{co->str, 0, 0};
+        KSpec s{co->str, 0, 0, 0};
         if ((rc = json_int(kv.second, "block", meta_path, s.block))) return rc;
         if ((rc = json_int(kv.second, "lds", meta_path, s.lds))) return rc;
+        if ((rc = json_int(kv.second, "kernarg", meta_path, s.kernarg))) return rc;
         if (s.block <= 0 || s.block > 1024) return fail(EE_ERR_META, "bad block size for " + kv.first);
+        if (s.kernarg <= 0 || s.kernarg > 4096) return fail(EE_ERR_META, "bad kernarg size for " + kv.first);
         specs[kv.first] = s;
     }
 
@@ -403,6 +409,7 @@ EE_EXPORT int ee_engine_create(const char* lib_dir, ee_engine** out) {
         }
         k.block = (int)kv.second.block;
         k.lds = lds;
+        k.kernarg = (int)kv.second.kernarg;
         e->kernels[kv.first] = k;
     }
     *out = e.release();
