@@ -334,6 +334,24 @@ int ee_routed_linear_swiglu(ee_engine* eng, const void* x, int64_t ld_x, int32_t
                             const int32_t* idx, const int32_t* counts, const int8_t* b_i8, const uint8_t* b_f8,
                             const void* b_f16, const float* b_scale, void* act, int64_t ld_act, void* ws_codes,
                             float* ws_scale, ee_stream_t stream);
+
+/* ---- allocation-free routed linear ----------------------------------------
+ * No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): ee_routed_linear without the ws_codes / ws_scale
+ * workspace.  The codes and scales live in a device array of the library
+ * (EE_NOALLOC_MAX_CODE_BYTES + 4 * EE_NOALLOC_MAX_ROWS bytes, one copy per
+ * GPU, held until the process ends), resolved once per device when an engine
+ * is created.  Nothing is allocated and nothing synchronises.  Limits:
+ * M <= EE_NOALLOC_MAX_ROWS and M * K <= EE_NOALLOC_MAX_CODE_BYTES, else
+ * EE_ERR_UNSUPPORTED.  Every call on one GPU shares the array: calls that
+ * overlap on one GPU (other streams, other threads) race.  Same results as
+ * ee_routed_linear. */
+#define EE_NOALLOC_MAX_ROWS 16384
+#define EE_NOALLOC_MAX_CODE_BYTES (32 * 1024 * 1024)
+int ee_routed_linear_noalloc(ee_engine* eng, const void* x, int64_t ld_x, int32_t M, int32_t K, int32_t N,
+                             const int32_t* idx, const int32_t* counts, const int8_t* b_i8, const uint8_t* b_f8,
+                             const void* b_f16, const float* b_scale, void* c, int64_t ldc, ee_stream_t stream);
 /* ee_routed_linear and ee_routed_linear_swiglu without their quantiser: the
  * INT8 and FP8 slots' codes [M, K] (row stride K) and scales [M] were written
  * beforehand, by ee_add_rmsnorm_route (the same bits as the quantiser).  x is

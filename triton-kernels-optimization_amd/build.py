@@ -102,12 +102,19 @@ def read_notes(hsaco: str):
 
 
 def build_host() -> str:
+    """The launcher (g++) plus ee_noalloc.hip (hipcc, host and device code: the
+    device-resident workspace of ee_routed_linear_noalloc) in one library."""
     src = os.path.join(CSRC, "launcher", "ee_launcher.cpp")
+    noalloc = os.path.join(CSRC, "launcher", "ee_noalloc.hip")
     out = os.path.join(LIB, "libentropy_engine.so")
     tmp = out + ".tmp"
+    obj = os.path.join(LIB, "ee_noalloc.o")
+    _run([_hipcc(), f"--offload-arch={ARCH}", "-c", "-O2", "-fPIC", "-std=c++17", "-fvisibility=hidden",
+          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+          "-I", INCLUDE, "-I", CSRC, noalloc, "-o", obj])
     _run(["g++", "-std=c++17", "-O2", "-fPIC", "-shared", "-fvisibility=hidden", "-Wall", "-Wextra",
           "-D__HIP_PLATFORM_AMD__", "-I", os.path.join(ROCM, "include"), "-I", INCLUDE, "-I", CSRC,
-          src, "-o", tmp, "-L", os.path.join(ROCM, "lib"), "-lamdhip64", "-Wl,--no-undefined"])
+          src, obj, "-o", tmp, "-L", os.path.join(ROCM, "lib"), "-lamdhip64", "-Wl,--no-undefined"])
     os.replace(tmp, out)
     return out
 

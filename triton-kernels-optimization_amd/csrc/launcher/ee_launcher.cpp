@@ -184,9 +184,16 @@ int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 }  // namespace
 
+// Device address and size of ee_routed_linear_noalloc's workspace array on the
+// current device (ee_noalloc.hip); returns a hipError_t value.
+extern "C" int ee_noalloc_scratch_address(void** out, int64_t* bytes);
+
 struct ee_engine {
     int device = -1;
     int cus = 0;                              // compute units: the persistent GEMM grids
+    void* scratch = nullptr;                  // this device's copy of the no-alloc workspace
+    int64_t scratch_bytes = 0;
+    int scratch_rc = 0;                       // hipError_t of its lookup
     std::vector<hipModule_t> modules;
     std::unordered_map<std::string, Kernel> kernels;
     std::unordered_map<std::string, int64_t> options;
@@ -412,6 +419,9 @@ EE_EXPORT int ee_engine_create(const char* lib_dir, ee_engine** out) {
         k.kernarg = (int)kv.second.kernarg;
         e->kernels[kv.first] = k;
     }
+    // This device's copy of ee_routed_linear_noalloc's workspace; a failed lookup
+    // only disables that entry point (it reports the HIP error).
+    e->scratch_rc = ee_noalloc_scratch_address(&e->scratch, &e->scratch_bytes);
     *out = e.release();
     return EE_OK;
 }
@@ -835,6 +845,26 @@ EE_EXPORT int ee_routed_linear_swiglu(ee_engine* eng, const void* x, int64_t ld_
                                       int64_t ld_act, void* ws_codes, float* ws_scale, ee_stream_t stream) {
     return routed_impl(eng, x, ld_x, M, K, N, idx, counts, b_i8, b_f8, b_f16, b_scale, act, ld_act, ws_codes,
                        ws_scale, 1, stream);
+}
+
+EE_EXPORT int ee_routed_linear_noalloc(ee_engine* eng, const void* x, int64_t ld_x, int32_t M, int32_t K, int32_t N,
+                                       const int32_t* idx, const int32_t* counts, const int8_t* b_i8,
+                                       const uint8_t* b_f8, const void* b_f16, const float* b_scale, void* c,
+                                       int64_t ldc, ee_stream_t stream) {
+    if (eng == nullptr) return fail(EE_ERR_INVALID_ARG, "engine must not be NULL");
+    if (M < 0 || K <= 0) return fail(EE_ERR_INVALID_ARG, "bad shape or stride");
+    if (M > EE_NOALLOC_MAX_ROWS || (int64_t)M * K > EE_NOALLOC_MAX_CODE_BYTES)
+        return fail(EE_ERR_UNSUPPORTED, "ee_routed_linear_noalloc holds at most " +
+                                            std::to_string(EE_NOALLOC_MAX_ROWS) + " rows and " +
+                                            std::to_string(EE_NOALLOC_MAX_CODE_BYTES) + " bytes of codes (M * K); got M = " +
+                                            std::to_string(M) + ", K = " + std::to_string(K));
+    if (eng->scratch == nullptr)
+        return fail(EE_ERR_HIP, std::string("no-alloc workspace unavailable: hipGetSymbolAddress failed: ") +
+                                    hipGetErrorString((hipError_t)eng->scratch_rc));
+    uint8_t* codes = (uint8_t*)eng->scratch;
+    float* scales = (float*)(codes + EE_NOALLOC_MAX_CODE_BYTES);
+    return routed_impl(eng, x, ld_x, M, K, N, idx, counts, b_i8, b_f8, b_f16, b_scale, c, ldc, codes, scales, 0,
+                       stream);
 }
 
 EE_EXPORT int ee_routed_gemm(ee_engine* eng, const void* x, int64_t ld_x, int32_t M, int32_t K, int32_t N,

@@ -32,6 +32,8 @@ STATUS_NAMES = {0: "EE_OK", -1: "EE_ERR_INVALID_ARG", -2: "EE_ERR_IO", -3: "EE_E
 # quantiser modes / GEMM kinds / tiers
 EE_QUANT_I8_DISPATCH, EE_QUANT_I8_ENGINE, EE_QUANT_F8_ROW, EE_QUANT_F8_TENSOR = 0, 1, 2, 3
 EE_TENSOR_WS_FLOATS = 1024
+EE_NOALLOC_MAX_ROWS = 16384              # ee_routed_linear_noalloc's workspace limits
+EE_NOALLOC_MAX_CODE_BYTES = 32 * 1024 * 1024
 EE_GEMM_I8, EE_GEMM_F8, EE_GEMM_F16, EE_GEMM_W8A16 = 0, 1, 2, 3
 
 _p = ctypes.c_void_p
@@ -63,6 +65,8 @@ SIGNATURES = {
     "ee_route": ([_p, _p, _i64, _f64, _f64, _p, _p, _p, _p], ctypes.c_int),
     "ee_route_heads": ([_p, _p, _i32, _i32, _i32, _f64, _f64, _p, _p, _p, _p], ctypes.c_int),
     "ee_row_copy": ([_p, _p, _i64, _p, _i64, _i64, _i64, _p, _p, _i32, _i32, _p], ctypes.c_int),
+    "ee_routed_linear_noalloc": ([_p, _p, _i64, _i32, _i32, _i32, _p, _p, _p, _p, _p, _p, _p, _i64, _p],
+                                 ctypes.c_int),
     "ee_routed_linear": ([_p, _p, _i64, _i32, _i32, _i32, _p, _p, _p, _p, _p, _p, _p, _i64, _p, _p, _p],
                          ctypes.c_int),
     "ee_silu_mul": ([_p, _p, _i64, _p, _i64, _i64, _i64, _p], ctypes.c_int),
