@@ -30,8 +30,10 @@ GEMM operands stay resident (as in the reference's loop); the HBM-bound
 entropy kernel rotates through enough input/output buffers to exceed the
 256 MB Infinity Cache ("cold", the roofline figure) and also reports the
 same-buffer ("hot") rate.
-cpu_baseline: the repository's C oracle (a port of the reference's
-arithmetic) timed on this host's cores over a bounded sample.
+cpu_baseline: the reference path's arithmetic as PyTorch CPU ops
+(oracle/torch_cpu.py: INT8 with torch._int_mm, FP8 through f32, f32 entropy)
+and the repository's C oracle, timed on this host's cores over a bounded
+sample.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
 """
@@ -298,8 +300,27 @@ def main():
                     af_b, sf_b = ee.quantize_activations(ab, "fp8")
                     run("c2_fp8", lambda: ee.gemm("fp8", af_b, pwb.f8, sf_b, pwb.scale, out=cb), primary="eager")
                 run(f"{cfg}_fp16_torch", lambda: torch.matmul(ab, Wb.t(), out=cb), primary="eager")
+                if cfg == "c1":                                        # this build's own FP16 (W8A16) tier
+                    run("c1_w8a16", lambda: ee.gemm("fp16", ab, pwb.f16, out=cb), primary="eager")
                 big[cfg] = 2.0 * Mb * Nb * Kb
                 del ab, Wb, Bb, pwb, ai_b, cb
+        # config 1's softmax + entropy: fp16 [4096, 4096] rows drawn as in config 0, with
+        # probabilities, cold (9 buffer pairs of 64 MiB > 2 x the 256 MB MALL)
+        if not only or "c1_softmax_entropy" in only:
+            R1, S1 = 4096, 4096
+            sc1 = torch.from_numpy(rng.choice(np.float32([0.25, 1.0, 4.0, 16.0]), R1))
+            L1 = (torch.randn(R1, S1, generator=torch.Generator().manual_seed(4)) * sc1[:, None]).half().to(dev)
+            c1_in = [L1] + [L1.clone() for _ in range(8)]
+            c1_out = [torch.empty_like(L1) for _ in range(9)]
+            rot1 = {"i": 0}
+
+            def ent_c1():
+                i = rot1["i"] % 9
+                rot1["i"] += 1
+                ee.softmax_entropy(c1_in[i], out_probs=c1_out[i])
+
+            run("c1_softmax_entropy", ent_c1, steps=9 * max(1, args.steps // 9), warmup=9)
+            del c1_in, c1_out, L1
         # ---- config 3: the dispatcher end to end on a mixed batch (M = K = N = 4096)
         c3 = None
         c3_names = ("c3_entropy", "c3_route", "c3_linear", "c3_end_to_end")
@@ -428,15 +449,23 @@ def main():
             "shape": "M=K=N=4096; entropy over fp16 [4096,4096] mixture logits",
         }
     for cfg, ops_b in big.items():
-        legs = ("int8", "fp8_tensor", "fp16_torch") if cfg == "c1" else ("int8", "fp8", "fp16_torch")
-        peak = {"int8": PEAK_I8_TOPS, "fp8_tensor": PEAK_F8_TFLOPS, "fp8": PEAK_F8_TFLOPS, "fp16_torch": PEAK_F16_TFLOPS}
+        legs = ("int8", "fp8_tensor", "w8a16", "fp16_torch") if cfg == "c1" else ("int8", "fp8", "fp16_torch")
+        peak = {"int8": PEAK_I8_TOPS, "fp8_tensor": PEAK_F8_TFLOPS, "fp8": PEAK_F8_TFLOPS, "w8a16": PEAK_F16_TFLOPS,
+                "fp16_torch": PEAK_F16_TFLOPS}
         kernels[f"gemm_{cfg}"] = {
             leg: {"us": results[f"{cfg}_{leg}"]["ms"] * 1e3,
                   "TOPS": ops_b / (results[f"{cfg}_{leg}"]["ms"] * 1e-3) / 1e12,
                   "frac_of_peak": ops_b / (results[f"{cfg}_{leg}"]["ms"] * 1e-3) / 1e12 / peak[leg]}
             for leg in legs}
-        kernels[f"gemm_{cfg}"]["shape"] = ("M, K, N = 4096, 4096, 4096; A with 0.1% outliers of 20; FP8 per-tensor scales"
+        kernels[f"gemm_{cfg}"]["shape"] = ("M, K, N = 4096, 4096, 4096; A with 0.1% outliers of 20; FP8 per-tensor "
+                                           "scales; w8a16 = this build's FP16 tier (fp16 A, W8A16 weights)"
                                            if cfg == "c1" else "M, K, N = 4096, 4096, 14336")
+    if "c1_softmax_entropy" in results:
+        b1 = 4096 * 4096 * 4 + 4096 * 4
+        g1 = b1 / (results["c1_softmax_entropy"]["ms"] * 1e-3) / 1e9
+        kernels["softmax_entropy_c1"] = {"us_cold": results["c1_softmax_entropy"]["ms"] * 1e3, "GBps_cold": g1,
+                                         "frac_of_hbm_cold": g1 / PEAK_HBM_GBS, "bytes_per_launch": b1,
+                                         "shape": "config 1: fp16 [4096, 4096] with probabilities, rows as config 0"}
     if mlp is not None:
         kernels["mlp_engine"] = {
             f"us_{k}": results[f"mlp_{k}"]["ms"] * 1e3 for k in ("int8", "fp8", "fp16", "routed", "torch_fp16")}
@@ -521,11 +550,13 @@ def main():
                                "accumulate, fp16 dequant); FP8 e4m3 GEMM and fused softmax+entropy fp16 "
                                "[1024,4096] in 'kernels'",
                    "M": M, "K": K, "N": N, "entropy_rows": ER, "entropy_cols": ES},
-        "roofline": {"bound": "mfma", "achieved": round(i8_launch_tops, 2), "peak": PEAK_I8_TOPS, "unit": "TFLOP/s",
+        "value_timing": "eager launches back to back, events on the launch stream (the reference's loop)",
+        "roofline": {"bound": "mfma", "achieved": round(i8_launch_tops, 2), "peak": PEAK_I8_TOPS, "unit": "TOPS",
+                     "timing": "average launch over the replay of one HIP graph of the K launches",
                      "frac": round(i8_launch_tops / PEAK_I8_TOPS, 4), "traffic": traffic,
                      "kernel": "eek_gemm_i8_w8 (8-wave INT8 pipeline, 1024x4096x4096)", "us_per_launch": round(i8_roof_ms * 1e3, 3)},
         "roofline_entropy": {"bound": "hbm", "achieved": round(ent_launch_gbs, 1), "peak": PEAK_HBM_GBS,
-                             "unit": "GB/s", "frac": round(ent_launch_gbs / PEAK_HBM_GBS, 4), "traffic": ent_traffic,
+                             "unit": "GB/s", "timing": "average launch over the replay of one HIP graph, cold", "frac": round(ent_launch_gbs / PEAK_HBM_GBS, 4), "traffic": ent_traffic,
                              "kernel": "eek_softmax_entropy_v4_w2 (cold, [1024,4096])", "us_per_launch": round(ent_roof_ms * 1e3, 3)},
         "kernels": kernels,
         "cpu_baseline": cpu,
@@ -534,35 +565,61 @@ def main():
 
 
 def cpu_baseline(A, W, L):
-    """The C oracle on this host: INT8 tier end to end (quantiser + int32 GEMM
-    + epilogue) at the full config-0 shape, repeated for >= 10 s (<= 30 s)."""
+    """The reference path's arithmetic on this host's cores, over a bounded
+    sample of the config-0 workload (~15-25 s of CPU work):
+      * oracle/torch_cpu.py, PyTorch CPU ops (BASELINE.md's CPU plan): INT8 =
+        the dispatcher quantiser + torch._int_mm + epilogue at the full
+        1024x4096x4096 shape (`value`); FP8 = e4m3 codes decoded to f32 + an f32
+        matmul on a 256-row slice; softmax+entropy in f32 on all 1024 rows;
+      * the repository's C oracle (OpenMP) on the INT8 path, beside it.
+    Threads: torch's (OMP_NUM_THREADS: the host's CPU share)."""
     import numpy as np
+    import torch
     sys.path.insert(0, ROOT)
     import oracle
+    from oracle import torch_cpu as tc
+    threads = torch.get_num_threads()
+
+    def rate(fn, seconds, cap=30.0):
+        fn()                                                           # warm
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            fn()
+            reps += 1
+            el = time.perf_counter() - t0
+            if el >= seconds or (el / reps) * (reps + 1) > cap:
+                return reps, el
+
+    a, w, lg = torch.from_numpy(A), torch.from_numpy(W), torch.from_numpy(L)
     B, bs = oracle.quantize_weights_int8(W)
-    reps, t0 = 0, time.perf_counter()
-    while True:
-        codes, a_s = oracle.quant_act_i8(A, "dispatcher")
-        oracle.epilogue_i8(oracle.gemm_i8_acc(codes, B), a_s, bs)
-        reps += 1
-        el = time.perf_counter() - t0
-        if el >= 10.0 or (el / reps) * (reps + 1) > 30.0:
-            break
-    tops = 2.0 * M * N * K * reps / el / 1e12
-    t1 = time.perf_counter()
-    ereps = 0
-    while time.perf_counter() - t1 < 2.0:
-        oracle.softmax_entropy(L)
-        ereps += 1
-    ent_gbs = (ER * ES * 4 + ER * 4) * ereps / (time.perf_counter() - t1) / 1e9
+    b, bst = torch.from_numpy(B), torch.from_numpy(bs)
+    reps_i8, el_i8 = rate(lambda: tc.triton_int8_gemm(a, b, bst), 8.0)
+    i8_tops = 2.0 * M * N * K * reps_i8 / el_i8 / 1e12
+    b8 = tc.weight_f8(b)
+    a_s = a[:256]
+    reps_f8, el_f8 = rate(lambda: tc.triton_fp8_gemm(a_s, b, bst, b8), 4.0)
+    f8_tflops = 2.0 * 256 * N * K * reps_f8 / el_f8 / 1e12
+    reps_e, el_e = rate(lambda: tc.softmax_entropy(lg), 2.0)
+    ent_gbs = (ER * ES * 4 + ER * 4) * reps_e / el_e / 1e9
+    def c_int8():
+        codes, s = oracle.quant_act_i8(A, "dispatcher")
+        return oracle.epilogue_i8(oracle.gemm_i8_acc(codes, B), s, bs)
+
+    reps_c, el_c = rate(c_int8, 5.0)
+    c_tops = 2.0 * M * N * K * reps_c / el_c / 1e12
     try:
         model = [l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo") if l.startswith("model name")][0]
     except Exception:
         model = "unknown"
-    return {"value": round(tops, 4), "unit": "TOPS", "cores": oracle.num_threads(), "kind": "port",
-            "sample": f"C oracle INT8 path (quantiser + int32 GEMM + epilogue) at the full 1024x4096x4096 shape, "
-                      f"{reps} reps in {el:.1f} s; entropy [1024,4096] {ent_gbs:.2f} GB/s; CPU {model}"}
-
+    return {"value": round(i8_tops, 4), "unit": "TOPS", "cores": threads, "kind": "port",
+            "int8_tops": round(i8_tops, 4), "fp8_tflops": round(f8_tflops, 4),
+            "entropy_gbps": round(ent_gbs, 3), "c_oracle_int8_tops": round(c_tops, 4),
+            "c_oracle_threads": oracle.num_threads(),
+            "sample": f"PyTorch-CPU restatement (oracle/torch_cpu.py), {threads} threads on {model}: INT8 dispatcher "
+                      f"quantiser + torch._int_mm + epilogue at 1024x4096x4096, {reps_i8} reps in {el_i8:.1f} s; "
+                      f"FP8 codes -> f32 matmul on 256x4096x4096, {reps_f8} reps in {el_f8:.1f} s; f32 "
+                      f"softmax+entropy [1024,4096], {reps_e} reps in {el_e:.1f} s; C oracle INT8 path "
+                      f"{reps_c} reps in {el_c:.1f} s"}
 
 if __name__ == "__main__":
     main()
