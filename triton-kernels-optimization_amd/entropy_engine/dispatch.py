@@ -278,9 +278,20 @@ class EntropyDispatchedLlamaBlock(nn.Module):
     quantity the reference computes as -sum p ln(p + 1e-10) over HF's attention
     weights (dispatch.py:243-245); the kernel's exact H = ln Z - sum p*s differs
     from it only by the 1e-10 regulariser and the fp16 rounding of p.
-    attention_mask follows HF eager attention: an additive [B, 1, S, Sk] mask,
-    or None for unmasked attention (as in the reference's own test,
-    benchmark.py:220-277).  KV caches are outside this path."""
+    attention_mask follows HF attention: an additive [B, 1, S, Sk] mask; None
+    means unmasked attention under eager attention (the reference's own test,
+    benchmark.py:220-277) and causal attention (key c of query s kept iff
+    c <= Sk - S + s) under the fused implementations, for which HF's LlamaModel
+    passes None instead of a causal mask.
+
+    KV cache (EE/python/dispatch.py:166-209, 214-247): keys and values are
+    appended to an HF Cache after RoPE (cache.update(k, v, layer_idx)) and the
+    attention runs over every cached key.  Two calling conventions: the
+    reference's -- past_key_value=..., use_cache=..., returning (hidden,) or,
+    with use_cache, (hidden, present_kv), present_kv being the updated cache or,
+    without one, the (k, v) of this call -- and HF's LlamaModel's (transformers
+    >= 5: past_key_values=..., returning the hidden tensor), so the block can
+    replace an HF decoder layer inside a stock forward or generate()."""
 
     def __init__(self, llama_block, layer_idx: int = 0):
         super().__init__()
@@ -298,12 +309,12 @@ class EntropyDispatchedLlamaBlock(nn.Module):
     def forward(self, hidden_states: torch.Tensor, dispatcher: Optional[PipelinedEntropyDispatcher] = None,
                 attention_mask: Optional[torch.Tensor] = None, position_ids: Optional[torch.Tensor] = None,
                 past_key_value=None, use_cache: bool = False, **kwargs) -> Tuple[torch.Tensor, ...]:
-        if past_key_value is not None or use_cache:
-            raise NotImplementedError("EntropyDispatchedLlamaBlock: KV caches are not supported")
+        hf_call = "past_key_values" in kwargs               # HF LlamaModel (transformers >= 5) convention
+        cache = kwargs.pop("past_key_values", None) if hf_call else past_key_value
         residual = hidden_states
         hidden_states = self.input_layernorm(hidden_states)
-        attn_output, entropy_batch, _ = self._attention_with_fused_entropy(
-            hidden_states, attention_mask=attention_mask, position_ids=position_ids, **kwargs)
+        attn_output, entropy_batch, present_kv = self._attention_with_fused_entropy(
+            hidden_states, attention_mask=attention_mask, position_ids=position_ids, cache=cache, **kwargs)
         self.layer_entropy = entropy_batch
         if dispatcher is not None:
             dispatcher.submit_entropy(entropy_batch)
@@ -315,10 +326,15 @@ class EntropyDispatchedLlamaBlock(nn.Module):
         up = self.up_proj(hidden_states, tier=tier)
         hidden_states = self.down_proj(self.act_fn(gate) * up, tier=tier)
         hidden_states = residual + hidden_states
-        return (hidden_states,)
+        if hf_call:
+            return hidden_states
+        outputs = (hidden_states,)
+        if use_cache:
+            outputs += (present_kv,)
+        return outputs
 
     def _attention_with_fused_entropy(self, hidden_states: torch.Tensor, attention_mask=None, position_ids=None,
-                                      **kwargs):
+                                      cache=None, **kwargs):
         attn = self.self_attn
         B, S, _ = hidden_states.shape
         hd = attn.head_dim
@@ -330,14 +346,26 @@ class EntropyDispatchedLlamaBlock(nn.Module):
             if self._rotary is None:
                 from transformers.models.llama.modeling_llama import LlamaRotaryEmbedding
                 self._rotary = LlamaRotaryEmbedding(config=attn.config, device=hidden_states.device)
-            if position_ids is None:
-                position_ids = torch.arange(S, device=hidden_states.device).unsqueeze(0).expand(B, -1)
+            if position_ids is None:                        # after the cached positions, if any
+                past = cache.get_seq_length(self.layer_idx) if cache is not None else 0
+                position_ids = torch.arange(past, past + S, device=hidden_states.device).unsqueeze(0).expand(B, -1)
             pe = self._rotary(hidden_states, position_ids)
         cos, sin = pe
         q, k = _rope(q, cos, sin), _rope(k, cos, sin)
-        out, H = _attention_entropy(q, k, v, attn.scaling, attention_mask)
+        if cache is not None:                               # append, then attend over every cached key
+            k, v = cache.update(k, v, self.layer_idx)
+        present = cache if cache is not None else (k, v)
+        Sk = k.shape[2]
+        causal = False
+        if attention_mask is None and S > 1 and getattr(attn.config, "_attn_implementation", "eager") != "eager":
+            if Sk == S:
+                causal = True
+            else:                                           # queries are the last S of Sk positions
+                attention_mask = torch.full((S, Sk), float("-inf"), dtype=q.dtype, device=q.device)
+                attention_mask = attention_mask.triu(Sk - S + 1).view(1, 1, S, Sk)
+        out, H = _attention_entropy(q, k, v, attn.scaling, attention_mask, causal=causal)
         out = attn.o_proj(out.transpose(1, 2).reshape(B, S, -1).contiguous())
-        return out, H.mean(dim=(1, 2)), None
+        return out, H.mean(dim=(1, 2)), present
 
 
 def build_dispatched_llama(model, tau_low: float, tau_high: float):
@@ -404,6 +432,15 @@ class EntropyGatedLlama:
         self._rope_cache = {}
         self.fused_attention = True
         self.fused_norm_quant = True
+        # Test hooks (None: off).  linear_impl(key, x2d, route, swiglu) -> y replaces
+        # the tier kernels of the gated linears (an independent restatement of their
+        # arithmetic); linear_probe(key, x2d, route, y) sees each gated linear's
+        # input, routing and output; route_replay: a list of (idx, counts), one per
+        # layer, used instead of routing (routes holds the last forward's).
+        self.linear_impl = None
+        self.linear_probe = None
+        self.route_replay = None
+        self.routes = []
         # rows per tier over every linear call: layer l's route feeds o/gate/up/down
         # (4) plus layer l+1's q/k/v (3), the last layer's the LM head (1); the
         # weights live on the device, so the per-forward tally is a few kernels, not 3 per layer
@@ -459,16 +496,24 @@ class EntropyGatedLlama:
         if not gated:
             y = torch.matmul(x2d, self.fused[key].t())
             return K.silu_mul(y) if swiglu else y
-        pw = self.packed[key]
-        if route is None:                    # no entropy yet: FP16 tier (W8A16), as the reference's default
-            return K.gemm("fp16", x2d, pw.f16, swiglu=swiglu)
-        idx, counts = route
-        return K.routed_linear(x2d, pw, idx, counts, swiglu=swiglu, quantized=quantized)
+        if self.linear_impl is not None:
+            y = self.linear_impl(key, x2d, route, swiglu)
+        else:
+            pw = self.packed[key]
+            if route is None:                # no entropy yet: FP16 tier (W8A16), as the reference's default
+                y = K.gemm("fp16", x2d, pw.f16, swiglu=swiglu)
+            else:
+                idx, counts = route
+                y = K.routed_linear(x2d, pw, idx, counts, swiglu=swiglu, quantized=quantized)
+        if self.linear_probe is not None:
+            self.linear_probe(key, x2d, route, y)
+        return y
 
     def _norm(self, x, w, res, route, gated: bool):
         """(x, xn, quantized): the residual add + RMSNorm; when the next linear is
         routed (and K % 128 == 0), the same kernel writes its INT8/FP8 operands."""
-        if gated and route is not None and self.fused_norm_quant and x.shape[-1] % 128 == 0:
+        if (gated and route is not None and self.fused_norm_quant and self.linear_impl is None
+                and x.shape[-1] % 128 == 0):
             idx, counts = route
             x, xn, codes, scale = K.add_rmsnorm_route(x, w, self.cfg["eps"], res, idx, counts)
             return x, xn, (codes, scale)
@@ -478,8 +523,12 @@ class EntropyGatedLlama:
     def _route_heads(self, h: torch.Tensor, counts_log: list):
         """Route tokens on the mean over heads of their attention-row entropies
         h [B, Hq, S] (the mean taken inside the routing kernel)."""
-        _, idx, counts = K.route_heads(h, self.tau_low, self.tau_high)
+        if self.route_replay is not None:
+            idx, counts = self.route_replay[len(counts_log)]
+        else:
+            _, idx, counts = K.route_heads(h, self.tau_low, self.tau_high)
         counts_log.append(counts)
+        self.routes.append((idx, counts))
         return idx, counts
 
     # ---------------------------------------------------------------- forward
@@ -497,6 +546,7 @@ class EntropyGatedLlama:
         # the fused attention kernel's shapes (attention_causal); others take the unfused path
         fused_att = self.fused_attention and d == 64 and S % 64 == 0 and (Hq // Hkv) % 2 == 0
         counts_log = []
+        self.routes = []
         route_prev = None
         res = None                                    # the pending residual branch, added by the next norm
         for l in range(c["layers"]):
