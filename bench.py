@@ -252,7 +252,7 @@ def main():
                 rot2["i"] += 1
                 ee.softmax_entropy(big_in[i], out_probs=big_out[i])
 
-            run("softmax_entropy_c2_cold", ent_c2, steps=3 * max(1, args.steps // 6), warmup=3)
+            run("softmax_entropy_c2_cold", ent_c2, steps=3 * max(1, args.steps // 6), warmup=6)
             del big_in, big_out
         run("quant_i8", lambda: ee.quantize_activations(a, "dispatcher", out_codes=a_i8, out_scale=s_i8))
         run("quant_f8", lambda: ee.quantize_activations(a, "fp8", out_codes=a_f8, out_scale=s_f8))

@@ -280,12 +280,29 @@ EE_DEV void softmax_entropy_generic(const EeSoftmaxArgs& a) {
         EeSoftmaxArgs a) {                                                                     \
         softmax_entropy_vec<V, W>(a);                                                          \
     }
+// The same within 64 VGPRs, for eight waves per SIMD: with 4 vectors per lane the
+// kept e values take the kernel to 65-72 VGPRs (seven waves per SIMD), and at
+// [4096, 4096] (8192 waves for 7168 slots) the last 1024 waves ran as a second
+// round: 15.1 -> 14.2 us cold at 63 VGPRs.  (Three, five, six and seven waves per
+// row do not fit 64 without spilling and keep the plain form.)
+#define EE_SE_VEC_8W(V, W)                                                                     \
+    extern "C" __global__ void __launch_bounds__(SeGeom<W>::BLOCK)                             \
+        __attribute__((amdgpu_waves_per_eu(8))) eek_softmax_entropy_v##V##_w##W(EeSoftmaxArgs a) { \
+        softmax_entropy_vec<V, W>(a);                                                          \
+    }
 #define EE_SE_VEC_W(V) EE_SE_VEC(V, 1) EE_SE_VEC(V, 2) EE_SE_VEC(V, 3) EE_SE_VEC(V, 4) \
                        EE_SE_VEC(V, 5) EE_SE_VEC(V, 6) EE_SE_VEC(V, 7) EE_SE_VEC(V, 8)
 EE_SE_VEC_W(1)
 EE_SE_VEC_W(2)
 EE_SE_VEC_W(3)
-EE_SE_VEC_W(4)
+EE_SE_VEC_8W(4, 1)
+EE_SE_VEC_8W(4, 2)
+EE_SE_VEC(4, 3)
+EE_SE_VEC_8W(4, 4)
+EE_SE_VEC(4, 5)
+EE_SE_VEC(4, 6)
+EE_SE_VEC(4, 7)
+EE_SE_VEC_8W(4, 8)
 // short rows, several per wave
 #define EE_SE_ROWS(V, R) \
     extern "C" __global__ void __launch_bounds__(EE_BLOCK) eek_softmax_entropy_v##V##_r##R(EeSoftmaxArgs a) { \
