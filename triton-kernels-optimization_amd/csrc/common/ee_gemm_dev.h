@@ -3,6 +3,8 @@
 // 32x32 MFMA shapes of the three tiers, the dequantising arithmetic of the
 // epilogues and the XCD-aware deal of tiles to persistent workgroups.
 #pragma once
+#include <type_traits>
+
 #include "ee_device.h"
 
 // Every epilogue multiply is its own rounded f32 operation, as in the reference.
@@ -50,7 +52,14 @@ EE_DEV void dma16s(const uint8_t* sbase, uint32_t voff, uint32_t lds_base) {
 // K stages split into slices of one MFMA depth, fragments of slice s+1 read
 // from LDS while the MFMAs of slice s run.
 template <int KIND> struct Pipe;
-template <> struct Pipe<EE_GEMM_I8> {            // 32x32x32 i8: 32 K bytes per slice, 16 B per lane
+// INT8 slices are 64 K bytes deep by default, as FP8's: two 32x32x32 i8 MFMAs
+// per block, on the first and second 16 bytes of each lane's 32 (lanes 0-31
+// hold K bytes 0-31 of the slice, lanes 32-63 bytes 32-63; A and B fragments
+// pair up the same K bytes, and int32 sums are exact in any order).  64 clocks
+// of MFMA per block and slice, against 32 for one 32-byte slice, cover each
+// batch of fragment reads twice as long.  The 32-byte form stays for kernels
+// whose registers the 32-byte fragments would overflow.
+struct PipeI8x32 {                               // 32x32x32 i8: 32 K bytes per slice, 16 B per lane
     static constexpr int SB = 32, CPF = 1;
     typedef u32x4 frag_t;
     typedef i32x16 acc_t;
@@ -58,6 +67,18 @@ template <> struct Pipe<EE_GEMM_I8> {            // 32x32x32 i8: 32 K bytes per 
         return __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(i32x4, b), __builtin_bit_cast(i32x4, a), c, 0, 0, 0);
     }
 };
+struct PipeI8x64 {                               // 2 x 32x32x32 i8: 64 K bytes per slice, 32 B per lane
+    static constexpr int SB = 64, CPF = 2;
+    typedef i32x8 frag_t;
+    typedef i32x16 acc_t;
+    static EE_DEV acc_t mma(const frag_t& b, const frag_t& a, const acc_t& c) {
+        const i32x4 b0{b[0], b[1], b[2], b[3]}, b1{b[4], b[5], b[6], b[7]};
+        const i32x4 a0{a[0], a[1], a[2], a[3]}, a1{a[4], a[5], a[6], a[7]};
+        return __builtin_amdgcn_mfma_i32_32x32x32_i8(b1, a1, __builtin_amdgcn_mfma_i32_32x32x32_i8(b0, a0, c, 0, 0, 0),
+                                                     0, 0, 0);
+    }
+};
+template <> struct Pipe<EE_GEMM_I8> : PipeI8x64 {};
 template <> struct Pipe<EE_GEMM_F16> {           // 32x32x16 f16: 32 K bytes per slice, 16 B per lane
     static constexpr int SB = 32, CPF = 1;
     typedef u32x4 frag_t;

@@ -146,10 +146,12 @@ EE_DEV void epilogue(const EeGemmArgs& g, const acc_t (&acc)[4][4], int m0, int 
 
 
 
-template <int KIND>
-struct Frags {
-    typename Pipe<KIND>::frag_t a[2], b[2];
+template <class P>
+struct FragsP {
+    typename P::frag_t a[2], b[2];
 };
+template <int KIND>
+using Frags = FragsP<Pipe<KIND>>;
 
 // Fragments of one K slice: lane l reads row (l & 31) of each 32-row block, K
 // chunk(s) slice * SB/16 + (l >> 5) * CPF (+1): lanes 0-31 and 32-63 cover the
@@ -862,7 +864,8 @@ EE_DEV void epilogue_blk_direct(const EeGemmArgs& g, const typename Pipe<KIND>::
 
 template <int KIND, int SW = 0>
 struct Gemm8 {
-    typedef Pipe<KIND> P;
+    // (eight waves' registers leave no room for INT8's 64-byte slices)
+    typedef std::conditional_t<KIND == EE_GEMM_I8, PipeI8x32, Pipe<KIND>> P;
     typedef typename P::acc_t acc_t;
     static constexpr int ESZ = (KIND == EE_GEMM_F16) ? 2 : 1;
     static constexpr int LOADS = 4;                    // DMA instructions per wave per stage
@@ -877,7 +880,7 @@ struct Gemm8 {
     const uint8_t* pa[2];
     const uint8_t* pb[2];
     acc_t acc[2][2];
-    Frags<KIND> fr[2];
+    FragsP<P> fr[2];
 
     __device__ __forceinline__ Gemm8(const EeGemmArgs& g_, uint8_t* smem_) : g(g_), smem(smem_) {}
 
@@ -913,8 +916,8 @@ struct Gemm8 {
         const bool more = GENERIC ? (kt + 1 < nk) : MORE;
 #pragma unroll
         for (int h = 0; h < HPS; ++h) {
-            Frags<KIND>& cur = fr[(PAR + h) & 1];
-            Frags<KIND>& nxt = fr[(PAR + h + 1) & 1];
+            FragsP<P>& cur = fr[(PAR + h) & 1];
+            FragsP<P>& nxt = fr[(PAR + h + 1) & 1];
             int dkt = -1, dp0 = 0;
             bool rd = false;
             const uint8_t* rs = s;

@@ -50,7 +50,8 @@
 
 template <int KIND, int SW, class Seq>
 struct G256 {
-    typedef Pipe<KIND> P;
+    // (the SwiGLU epilogue's registers leave no room for INT8's 32-byte fragments)
+    typedef std::conditional_t<KIND == EE_GEMM_I8 && SW, PipeI8x32, Pipe<KIND>> P;
     typedef typename P::acc_t acc_t;
     typedef typename P::frag_t frag_t;
     static constexpr int ESZ = (KIND == EE_GEMM_F16) ? 2 : 1;
@@ -75,7 +76,7 @@ struct G256 {
     // after the last MFMA that uses row block i of this one); B double-buffered,
     // except for FP8, whose 32-byte fragments leave room for one B buffer only
     // (its slices run j-major, so each B block is also dead before its reload)
-    static constexpr int NB = (KIND == EE_GEMM_F8) ? 1 : 2;
+    static constexpr int NB = (P::CPF == 2) ? 1 : 2;
     frag_t fa[4], fb[NB][2];
 
     __device__ __forceinline__ G256(const EeGemmArgs& g_, uint8_t* smem_, const Seq& seq_, int M_, int64_t off_)
