@@ -59,8 +59,10 @@ template <int KIND> struct Pipe;
 // of MFMA per block and slice, against 32 for one 32-byte slice, cover each
 // batch of fragment reads twice as long.  The 32-byte form stays for kernels
 // whose registers the 32-byte fragments would overflow.
+// Fragment chunks: lane l reads 16-byte chunk sl * SB/16 + (l >> 5) * LSTEP of its
+// row and, when CPF == 2, the chunk CSTEP after it.
 struct PipeI8x32 {                               // 32x32x32 i8: 32 K bytes per slice, 16 B per lane
-    static constexpr int SB = 32, CPF = 1;
+    static constexpr int SB = 32, CPF = 1, LSTEP = 1, CSTEP = 0;
     typedef u32x4 frag_t;
     typedef i32x16 acc_t;
     static EE_DEV acc_t mma(const frag_t& b, const frag_t& a, const acc_t& c) {
@@ -68,7 +70,7 @@ struct PipeI8x32 {                               // 32x32x32 i8: 32 K bytes per 
     }
 };
 struct PipeI8x64 {                               // 2 x 32x32x32 i8: 64 K bytes per slice, 32 B per lane
-    static constexpr int SB = 64, CPF = 2;
+    static constexpr int SB = 64, CPF = 2, LSTEP = 2, CSTEP = 1;
     typedef i32x8 frag_t;
     typedef i32x16 acc_t;
     static EE_DEV acc_t mma(const frag_t& b, const frag_t& a, const acc_t& c) {
@@ -79,16 +81,17 @@ struct PipeI8x64 {                               // 2 x 32x32x32 i8: 64 K bytes 
     }
 };
 template <> struct Pipe<EE_GEMM_I8> : PipeI8x64 {};
-template <> struct Pipe<EE_GEMM_F16> {           // 32x32x16 f16: 32 K bytes per slice, 16 B per lane
-    static constexpr int SB = 32, CPF = 1;
+struct PipeF16x32 {                              // 32x32x16 f16: 32 K bytes per slice, 16 B per lane
+    static constexpr int SB = 32, CPF = 1, LSTEP = 1, CSTEP = 0;
     typedef u32x4 frag_t;
     typedef f32x16 acc_t;
     static EE_DEV acc_t mma(const frag_t& b, const frag_t& a, const acc_t& c) {
         return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, b), __builtin_bit_cast(f16x8, a), c, 0, 0, 0);
     }
 };
+template <> struct Pipe<EE_GEMM_F16> : PipeF16x32 {};
 template <> struct Pipe<EE_GEMM_F8> {            // 32x32x64 e4m3: 64 K bytes per slice, 32 B per lane
-    static constexpr int SB = 64, CPF = 2;
+    static constexpr int SB = 64, CPF = 2, LSTEP = 2, CSTEP = 1;
     typedef i32x8 frag_t;
     typedef f32x16 acc_t;
     static EE_DEV acc_t mma(const frag_t& b, const frag_t& a, const acc_t& c) {

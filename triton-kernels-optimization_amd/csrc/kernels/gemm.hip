@@ -154,13 +154,13 @@ template <int KIND>
 using Frags = FragsP<Pipe<KIND>>;
 
 // Fragments of one K slice: lane l reads row (l & 31) of each 32-row block, K
-// chunk(s) slice * SB/16 + (l >> 5) * CPF (+1): lanes 0-31 and 32-63 cover the
-// two K halves of the slice, as the 32x32 MFMA operands expect.
+// chunk slice * SB/16 + (l >> 5) * LSTEP (and the chunk CSTEP after it when
+// CPF == 2): lanes 0-31 and 32-63 cover the two K halves of each MFMA's operand.
 template <int KIND>
 EE_DEV void read_frags(const uint8_t* s, int slice, int wm, int wn, int lane, Frags<KIND>& f) {
     typedef Pipe<KIND> P;
     const int r = lane & 31;
-    const int c0 = slice * (P::SB / 16) + (lane >> 5) * P::CPF;
+    const int c0 = slice * (P::SB / 16) + (lane >> 5) * P::LSTEP;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
         const int ra = wm * 64 + i * 32 + r, rb = BM + wn * 64 + i * 32 + r;
@@ -168,8 +168,8 @@ EE_DEV void read_frags(const uint8_t* s, int slice, int wm, int wn, int lane, Fr
             f.a[i] = *(const u32x4*)(s + lds_off(ra, c0));
             f.b[i] = *(const u32x4*)(s + lds_off(rb, c0));
         } else {
-            const u32x4 a0 = *(const u32x4*)(s + lds_off(ra, c0)), a1 = *(const u32x4*)(s + lds_off(ra, c0 + 1));
-            const u32x4 b0 = *(const u32x4*)(s + lds_off(rb, c0)), b1 = *(const u32x4*)(s + lds_off(rb, c0 + 1));
+            const u32x4 a0 = *(const u32x4*)(s + lds_off(ra, c0)), a1 = *(const u32x4*)(s + lds_off(ra, c0 + P::CSTEP));
+            const u32x4 b0 = *(const u32x4*)(s + lds_off(rb, c0)), b1 = *(const u32x4*)(s + lds_off(rb, c0 + P::CSTEP));
             f.a[i] = i32x8{(int)a0[0], (int)a0[1], (int)a0[2], (int)a0[3], (int)a1[0], (int)a1[1], (int)a1[2], (int)a1[3]};
             f.b[i] = i32x8{(int)b0[0], (int)b0[1], (int)b0[2], (int)b0[3], (int)b1[0], (int)b1[1], (int)b1[2], (int)b1[3]};
         }
@@ -960,12 +960,12 @@ struct Gemm8 {
     // One fragment of one K slice: which = 0, 1 (A row block), 2, 3 (B row block).
     __device__ __forceinline__ void read_frag(const uint8_t* s, int slice, typename P::frag_t& f, int which) const {
         const int r = lane & 31;
-        const int c0 = slice * (P::SB / 16) + (lane >> 5) * P::CPF;
+        const int c0 = slice * (P::SB / 16) + (lane >> 5) * P::LSTEP;
         const int row = which < 2 ? wm * 64 + which * 32 + r : BM + wn * 64 + (which - 2) * 32 + r;
         if constexpr (P::CPF == 1) {
             f = *(const u32x4*)(s + lds_off(row, c0));
         } else {
-            const u32x4 x0 = *(const u32x4*)(s + lds_off(row, c0)), x1 = *(const u32x4*)(s + lds_off(row, c0 + 1));
+            const u32x4 x0 = *(const u32x4*)(s + lds_off(row, c0)), x1 = *(const u32x4*)(s + lds_off(row, c0 + P::CSTEP));
             f = i32x8{(int)x0[0], (int)x0[1], (int)x0[2], (int)x0[3], (int)x1[0], (int)x1[1], (int)x1[2], (int)x1[3]};
         }
     }

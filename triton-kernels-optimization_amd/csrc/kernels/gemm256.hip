@@ -50,12 +50,12 @@
 
 template <int KIND, int SW, class Seq>
 struct G256 {
-    // (the SwiGLU epilogue's registers leave no room for INT8's 32-byte fragments)
+    // (the SwiGLU epilogue's registers leave no room for INT8's 64-byte slices)
     typedef std::conditional_t<KIND == EE_GEMM_I8 && SW, PipeI8x32, Pipe<KIND>> P;
     typedef typename P::acc_t acc_t;
     typedef typename P::frag_t frag_t;
     static constexpr int ESZ = (KIND == EE_GEMM_F16) ? 2 : 1;
-    static constexpr int NSL = BKB / P::SB;           // K slices per stage: 4 (i8, f16) or 2 (f8)
+    static constexpr int NSL = BKB / P::SB;           // K slices per stage: 4 (32-byte slices) or 2 (64-byte)
 
     const EeGemmArgs& g;
     uint8_t* smem;
@@ -137,13 +137,14 @@ struct G256 {
     }
 
     // Fragments of K slice sl of the stage at st: lane l reads row (l & 31) of
-    // each 32-row block, chunk(s) sl * SB/16 + (l >> 5) * CPF (+1).
+    // each 32-row block, chunk sl * SB/16 + (l >> 5) * LSTEP (and the chunk CSTEP
+    // after it when CPF == 2).
     __device__ __forceinline__ void rd(const uint8_t* st, int sl, frag_t& f, int row) const {
-        const int c0 = sl * (P::SB / 16) + (lane >> 5) * P::CPF;
+        const int c0 = sl * (P::SB / 16) + (lane >> 5) * P::LSTEP;
         if constexpr (P::CPF == 1) {
             f = *(const u32x4*)(st + lds_off(row, c0));
         } else {
-            const u32x4 x0 = *(const u32x4*)(st + lds_off(row, c0)), x1 = *(const u32x4*)(st + lds_off(row, c0 + 1));
+            const u32x4 x0 = *(const u32x4*)(st + lds_off(row, c0)), x1 = *(const u32x4*)(st + lds_off(row, c0 + P::CSTEP));
             f = i32x8{(int)x0[0], (int)x0[1], (int)x0[2], (int)x0[3], (int)x1[0], (int)x1[1], (int)x1[2], (int)x1[3]};
         }
     }
