@@ -94,7 +94,10 @@ int ee_engine_destroy(ee_engine* eng);
  * off, n >= 2 forces it with min(n, tiles) workgroups.  Same bits either way.
  * "gemm_tile": 256 x 256-tile persistent kernels (plain and routed) for GEMMs
  * whose 128 x 128 grid has more tiles than CUs (automatic; same bits); 128
- * forbids them, 256 forces them at every size. */
+ * forbids them, 256 forces them at every size.
+ * "gemm_tile_n": the width of those 256-row tiles: automatic (plain GEMMs take
+ * 256 x 128 where 256 x 256 tiles would keep at most half the CUs busy; the
+ * routed grid stays at 256), or 128 / 256 forced.  Same bits either way. */
 int ee_engine_set_option(ee_engine* eng, const char* key, int64_t value);
 int ee_engine_device(const ee_engine* eng);
 

@@ -1,4 +1,5 @@
-"""GPU parity of the 256 x 256-tile persistent GEMMs (eek_gemm256_*).
+"""GPU parity of the 256-row-tile persistent GEMMs (eek_gemm256_*: 256 x 256
+tiles; eek_gemm256n128_*: 256 x 128).  Every case runs at both tile widths.
 
 They replace the 128 x 128 kernels for GEMMs and routed linears with more
 128-tiles than CUs (configs 1-4), so each case checks them
@@ -62,13 +63,14 @@ SHAPES = [
 ]
 
 
+@pytest.mark.parametrize("tn", [256, 128])
 @pytest.mark.parametrize("M,K,N,grid", SHAPES)
-def test_gemm256_int8_fp8_small(ee, orc, M, K, N, grid):
+def test_gemm256_int8_fp8_small(ee, orc, M, K, N, grid, tn):
     A, B, bs, pw = _operands(ee, orc, M, K, N, M * 7 + K + N)
     codes, a_s = orc.quant_act_i8(A, "dispatcher")
     c8, s8 = orc.quant_act_f8(A)
     acc = torch.empty((M, N), dtype=torch.int32, device="cuda")
-    with _Options(gemm_tile=256, gemm_persist=grid):
+    with _Options(gemm_tile=256, gemm_tile_n=tn, gemm_persist=grid):
         o_i8 = host(ee.gemm("int8", cuda(codes), pw.i8, cuda(a_s), cuda(bs)))
         ee.gemm("int8", cuda(codes), pw.i8, cuda(a_s), cuda(bs), acc_out=acc)
         o_f8 = host(ee.gemm("fp8", cuda(c8), pw.f8, cuda(s8), cuda(bs)))
@@ -81,12 +83,13 @@ def test_gemm256_int8_fp8_small(ee, orc, M, K, N, grid):
     assert np.array_equal(o_f8.view(np.uint16), r_f8.view(np.uint16))
 
 
+@pytest.mark.parametrize("tn", [256, 128])
 @pytest.mark.parametrize("M,K,N,grid", SHAPES[:3] + SHAPES[4:6])
-def test_gemm256_fp16_small(ee, orc, M, K, N, grid):
+def test_gemm256_fp16_small(ee, orc, M, K, N, grid, tn):
     """The FP16 (W8A16) tier on the 256-tile kernel: within 1e-2 of float64 and
     bit-identical to the 128-tile loader-wave pipeline (same K order)."""
     A, B, bs, pw = _operands(ee, orc, M, K, N, M + 5 * K + N)
-    with _Options(gemm_tile=256, gemm_persist=grid):
+    with _Options(gemm_tile=256, gemm_tile_n=tn, gemm_persist=grid):
         out = host(ee.gemm("fp16", cuda(A), pw.f16))
     check_close_f64(out, orc.gemm_w8a16_f64(A, B, bs))
     with _Options(gemm_tile=128, gemm_variant=1):
@@ -99,7 +102,7 @@ def test_gemm256_full_size(ee, orc, M, K, N):
     """Configs 1 and 2 at full size through the production epilogue (no int32
     debug output): INT8 fp16 outputs bit-exact and FP8 within 1e-2 of float64 on
     sampled rows against the oracle; all outputs bit-identical to the 128-tile
-    kernels.  The automatic choice picks the 256-tile kernel at these shapes."""
+    kernels.  The automatic choice picks the 256 x 256-tile kernel at these shapes."""
     A, B, bs, pw = _operands(ee, orc, M, K, N, 21 + N)
     codes, a_s = orc.quant_act_i8(A, "dispatcher")
     c8, s8 = orc.quant_act_f8(A)
@@ -138,8 +141,9 @@ def test_gemm256_fp8_config1_per_tensor(ee, orc):
     assert np.array_equal(out.view(np.uint16), r.view(np.uint16))
 
 
+@pytest.mark.parametrize("tn", [256, 128])
 @pytest.mark.parametrize("M,K,F", [(4096, 2048, 5632), (600, 256, 640)])
-def test_gemm256_swiglu(ee, orc, M, K, F):
+def test_gemm256_swiglu(ee, orc, M, K, F, tn):
     """The SwiGLU epilogue of the 256-tile kernels gives the bits of the 128-tile
     SwiGLU kernels (every tier; FP16 on the loader-wave order)."""
     rng = np.random.default_rng(M + F)
@@ -151,7 +155,7 @@ def test_gemm256_swiglu(ee, orc, M, K, F):
     cf, sf = ee.quantize_activations(x, "fp8")
     for kind, a, b, sa, sb in (("int8", ci, pw.i8, si, pw.scale), ("fp8", cf, pw.f8, sf, pw.scale),
                                ("fp16", x, pw.f16, None, None)):
-        with _Options(gemm_tile=256):
+        with _Options(gemm_tile=256, gemm_tile_n=tn):
             fused = ee.gemm(kind, a, b, sa, sb, swiglu=True)
         with _Options(gemm_tile=128, gemm_variant=1):
             ref = ee.gemm(kind, a, b, sa, sb, swiglu=True)
@@ -161,13 +165,15 @@ def test_gemm256_swiglu(ee, orc, M, K, F):
 def test_gemm256_option_rejects_bad_value(ee):
     from entropy_engine import _lib
     assert _lib.lib().ee_engine_set_option(_lib.engine(), b"gemm_tile", 192) == _lib.EE_ERR_INVALID_ARG
+    assert _lib.lib().ee_engine_set_option(_lib.engine(), b"gemm_tile_n", 64) == _lib.EE_ERR_INVALID_ARG
 
 
 # ---------------------------------------------------------------------------- routed
 
+@pytest.mark.parametrize("tn", [256, 128])
 @pytest.mark.parametrize("M,K,N,H_hi,grid", [(300, 512, 520, 3.0, 0), (700, 1024, 384, 3.0, 8), (700, 256, 264, 3.0, 3),
                                              (129, 256, 128, 10.0, 0), (257, 512, 256, 0.3, 0), (1, 128, 64, 1.0, 0)])
-def test_gemm256_routed_equals_per_tier(ee, orc, M, K, N, H_hi, grid):
+def test_gemm256_routed_equals_per_tier(ee, orc, M, K, N, H_hi, grid, tn):
     """The 256-tile routed grid (three phases per workgroup: FP16, INT8, FP8
     tiles): every row equals the un-routed GEMM of its tier bit for bit, and the
     128-tile routed grid gives the same output.  Entropy ranges make tiers
@@ -179,7 +185,7 @@ def test_gemm256_routed_equals_per_tier(ee, orc, M, K, N, H_hi, grid):
     pw = ee.prepare_weight(cuda(B), cuda(bs)).materialize()
     x = cuda(X)
     tier, idx, counts = ee.route(cuda(H), 0.41, 1.68)
-    with _Options(gemm_tile=256, gemm_persist=grid):
+    with _Options(gemm_tile=256, gemm_tile_n=tn, gemm_persist=grid):
         out = host(ee.routed_linear(x, pw, idx, counts)).view(np.uint16)
     with _Options(gemm_tile=128):
         ref128 = host(ee.routed_linear(x, pw, idx, counts)).view(np.uint16)
@@ -216,7 +222,8 @@ def test_gemm256_routed_config3(ee, orc):
 
 
 @pytest.mark.parametrize("M,K,F", [(4096, 2048, 1408), (600, 256, 320)])
-def test_gemm256_routed_swiglu(ee, orc, M, K, F):
+@pytest.mark.parametrize("tn", [256, 128])
+def test_gemm256_routed_swiglu(ee, orc, M, K, F, tn):
     """SwiGLU epilogue of the 256-tile routed grid: the bits of the 128-tile
     routed SwiGLU grid."""
     rng = np.random.default_rng(M + 7 * F)
@@ -226,7 +233,7 @@ def test_gemm256_routed_swiglu(ee, orc, M, K, F):
     x = cuda(rng.standard_normal((M, K)).astype(np.float16))
     h = cuda((rng.random(M) * 3).astype(np.float32))
     _, idx, counts = ee.route(h, 0.41, 1.68)
-    with _Options(gemm_tile=256):
+    with _Options(gemm_tile=256, gemm_tile_n=tn):
         fused = ee.routed_linear(x, pw, idx, counts, swiglu=True)
     with _Options(gemm_tile=128):
         ref = ee.routed_linear(x, pw, idx, counts, swiglu=True)

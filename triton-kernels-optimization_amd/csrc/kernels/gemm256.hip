@@ -41,15 +41,26 @@
 #pragma clang fp contract(off)
 
 #define T2M 256
-#define T2N 256
-#define T2_STAGE ((T2M + T2N) * BKB)      // 64 KB
-#define T2_EPI (2 * T2_STAGE)             // the ring: two stages
 #define T2_SLOT 4096                      // per-wave epilogue slot (32 x 64 fp16)
-#define T2_LDS (T2_EPI + 8 * T2_SLOT)     // 160 KB
 #define T2_THREADS 512
 
-template <int KIND, int SW, class Seq>
+// Tile TN columns wide (256 or 128).  Waves: TN = 256: wm = w >> 2, wn = w & 3, 128 x 64
+// each (4 x 2 blocks); TN = 128: wm = w >> 1, wn = w & 1, 64 x 64 each (2 x 2 blocks).
+template <int TN>
+struct G2Geom {
+    static constexpr int STAGE = (T2M + TN) * BKB;    // 64 KB or 48 KB
+    static constexpr int EPI = 2 * STAGE;             // the ring: two stages
+    static constexpr int LDS = EPI + 8 * T2_SLOT;     // 160 KB or 128 KB
+    static constexpr int WR = TN == 256 ? 128 : 64;   // rows of a wave's block
+    static constexpr int NI = WR / 32;                // its 32-row blocks
+    static constexpr int WMS = TN == 256 ? 2 : 1;     // wm = w >> WMS, wn = w & (2^WMS - 1)
+    static constexpr int BG = TN / 64;                // B row groups of 8 each wave loads per stage
+};
+
+template <int KIND, int SW, class Seq, int TN = 256>
 struct G256 {
+    typedef G2Geom<TN> GE;
+    static constexpr int NI = GE::NI, WR = GE::WR;
     // (the SwiGLU epilogue's registers leave no room for INT8's 64-byte slices)
     typedef std::conditional_t<KIND == EE_GEMM_I8 && SW, PipeI8x32, Pipe<KIND>> P;
     typedef typename P::acc_t acc_t;
@@ -70,14 +81,14 @@ struct G256 {
     int iss, itile, ikt;
     const uint8_t* abase;
     const uint8_t* bbase;
-    uint32_t aoff[4], boff[4];
-    acc_t acc[4][2];
+    uint32_t aoff[4], boff[GE::BG];
+    acc_t acc[NI][2];
     // fragments: A single-buffered (row block i of the next slice is read right
     // after the last MFMA that uses row block i of this one); B double-buffered,
     // except for FP8, whose 32-byte fragments leave room for one B buffer only
     // (its slices run j-major, so each B block is also dead before its reload)
     static constexpr int NB = (P::CPF == 2) ? 1 : 2;
-    frag_t fa[4], fb[NB][2];
+    frag_t fa[NI], fb[NB][2];
 
     __device__ __forceinline__ G256(const EeGemmArgs& g_, uint8_t* smem_, const Seq& seq_, int M_, int64_t off_)
         : g(g_), smem(smem_), seq(seq_), M(M_), off(off_) {}
@@ -86,7 +97,7 @@ struct G256 {
         int tm, tn;
         seq.coords(i, tm, tn);
         m0 = tm * T2M;
-        n0 = tn * T2N;
+        n0 = tn * TN;
     }
 
     // DMA rows of tile i: one global_load_lds_dwordx4 fills 8 LDS rows (1 KB);
@@ -106,26 +117,31 @@ struct G256 {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const int r = (wave * 4 + q) * 8 + (lane >> 3);
-            const int lchunk = (lane & 7) ^ swz(r);   // swz(T2M + r) == swz(r)
+            const int lchunk = (lane & 7) ^ swz(r);
             const int m = min(m0 + r, M - 1);
             const int64_t ar = !routed ? (int64_t)(m - m0) : Seq::GATHER ? (int64_t)g.a_idx[off + m] : off + m;
             aoff[q] = (uint32_t)(ar * g.lda * ESZ + lchunk * 16);
+        }
+#pragma unroll
+        for (int q = 0; q < GE::BG; ++q) {
+            const int r = (wave * GE::BG + q) * 8 + (lane >> 3);
+            const int lchunk = (lane & 7) ^ swz(r);   // swz(T2M + r) == swz(r)
             const int n = min(n0 + r, g.N - 1) - n0;
             boff[q] = (uint32_t)(n * g.ldb * ESZ + lchunk * 16);
         }
     }
-    // Part p (0..3) of the next stage: A row group 4w+p and B row group 4w+p.
+    // Part p (0..3) of the next stage: A row group 4w+p and, for p < BG, B row group BG w + p.
     __device__ __forceinline__ void issue_part(int p) {
         if (p == 0 && ikt == nk) {
             ++itile;
             ikt = 0;
             dma_tile(itile);
         }
-        const uint32_t s = lds0 + (uint32_t)((iss & 1) * T2_STAGE);
+        const uint32_t s = lds0 + (uint32_t)((iss & 1) * GE::STAGE);
         const uint32_t kb = (uint32_t)ikt * BKB;
         const int grp = wave * 4 + p;
         dma16s(abase, aoff[p] + kb, s + grp * 8 * BKB);
-        dma16s(bbase, boff[p] + kb, s + (T2M + grp * 8) * BKB);
+        if (p < GE::BG) dma16s(bbase, boff[p] + kb, s + (T2M + (wave * GE::BG + p) * 8) * BKB);
         if (p == 3) {
             ++ikt;
             ++iss;
@@ -149,19 +165,18 @@ struct G256 {
         }
     }
     __device__ __forceinline__ void rd_a(const uint8_t* st, int sl, int i) {
-        rd(st, sl, fa[i], wm * 128 + i * 32 + (lane & 31));
+        rd(st, sl, fa[i], wm * WR + i * 32 + (lane & 31));
     }
     __device__ __forceinline__ void rd_b(const uint8_t* st, int sl, int buf, int j) {
         rd(st, sl, fb[buf % NB][j], T2M + wn * 64 + j * 32 + (lane & 31));
     }
-    // all six fragments of slice sl into fa and fb[buf]
+    // all fragments of slice sl into fa and fb[buf]
     __device__ __forceinline__ void rd_all(const uint8_t* st, int sl, int buf) {
         rd_a(st, sl, 0);
         rd_b(st, sl, buf, 0);
         rd_b(st, sl, buf, 1);
-        rd_a(st, sl, 1);
-        rd_a(st, sl, 2);
-        rd_a(st, sl, 3);
+#pragma unroll
+        for (int i = 1; i < NI; ++i) rd_a(st, sl, i);
     }
 
 #define G2_SB() __builtin_amdgcn_sched_barrier(0)
@@ -172,7 +187,11 @@ struct G256 {
     template <int C, bool RD>
     __device__ __forceinline__ void slice(const uint8_t* rs, int rsl, bool dma) {
         if constexpr (NB == 1) {
-            slice_j(RD, rs, rsl, dma);
+            if constexpr (NI == 2) slice_j2(RD, rs, rsl, dma);
+            else slice_j(RD, rs, rsl, dma);
+            return;
+        } else if constexpr (NI == 2) {
+            slice2<C>(RD, rs, rsl, dma);
             return;
         }
         constexpr int N = (1 - C) % NB;
@@ -207,6 +226,48 @@ struct G256 {
         acc[3][1] = P::mma(fb[C][1], fa[3], acc[3][1]);
         G2_SB();
         if (RD) rd_a(rs, rsl, 3);
+        G2_SB();
+    }
+
+    // Two row blocks (64 x 64 per wave): the same interleave over 4 MFMAs, the four
+    // load parts of the next stage after the first two.
+    template <int C>
+    __device__ __forceinline__ void slice2(bool RD, const uint8_t* rs, int rsl, bool dma) {
+        constexpr int N = (1 - C) % NB;
+        acc[0][0] = P::mma(fb[C][0], fa[0], acc[0][0]);
+        G2_SB();
+        if (RD) { rd_b(rs, rsl, N, 0); rd_b(rs, rsl, N, 1); }
+        G2_SB();
+        acc[0][1] = P::mma(fb[C][1], fa[0], acc[0][1]);
+        G2_SB();
+        if (RD) rd_a(rs, rsl, 0);
+        if (dma) { issue_part(0); issue_part(1); }
+        G2_SB();
+        acc[1][0] = P::mma(fb[C][0], fa[1], acc[1][0]);
+        G2_SB();
+        if (dma) { issue_part(2); issue_part(3); }
+        G2_SB();
+        acc[1][1] = P::mma(fb[C][1], fa[1], acc[1][1]);
+        G2_SB();
+        if (RD) rd_a(rs, rsl, 1);
+        G2_SB();
+    }
+    __device__ __forceinline__ void slice_j2(bool RD, const uint8_t* rs, int rsl, bool dma) {
+        acc[0][0] = P::mma(fb[0][0], fa[0], acc[0][0]);
+        G2_SB();
+        acc[1][0] = P::mma(fb[0][0], fa[1], acc[1][0]);
+        G2_SB();
+        if (RD) rd_b(rs, rsl, 0, 0);
+        G2_SB();
+        acc[0][1] = P::mma(fb[0][1], fa[0], acc[0][1]);
+        G2_SB();
+        if (RD) rd_a(rs, rsl, 0);
+        if (dma) { issue_part(0); issue_part(1); }
+        G2_SB();
+        acc[1][1] = P::mma(fb[0][1], fa[1], acc[1][1]);
+        G2_SB();
+        if (RD) { rd_a(rs, rsl, 1); rd_b(rs, rsl, 0, 1); }
+        if (dma) { issue_part(2); issue_part(3); }
         G2_SB();
     }
 
@@ -253,7 +314,7 @@ struct G256 {
     // epilogue and the tile change do that (run()).
     template <bool LAST>
     __device__ __forceinline__ void stage(int cs, bool dma2) {
-        const uint8_t* st = smem + (cs & 1) * T2_STAGE;
+        const uint8_t* st = smem + (cs & 1) * GE::STAGE;
 #pragma unroll
         for (int h = 0; h + 1 < NSL; h += 2) {
             slice<0, true>(st, h + 1, false);
@@ -266,7 +327,7 @@ struct G256 {
             asm volatile("" ::: "memory");
             __builtin_amdgcn_s_barrier();             // barrier cs+1: stage cs+1 landed, stage cs read
             asm volatile("" ::: "memory");
-            slice<1, true>(smem + ((cs + 1) & 1) * T2_STAGE, 0, dma2);
+            slice<1, true>(smem + ((cs + 1) & 1) * GE::STAGE, 0, dma2);
         } else {
             slice<1, false>(st, 0, false);
         }
@@ -283,7 +344,7 @@ struct G256 {
         int lane = this->lane;
         asm volatile("" : "+v"(lane));
         f32x4 bs[2][4] = {};
-        float as[4] = {};
+        float as[NI] = {};
         if constexpr (KIND != EE_GEMM_F16) {
 #pragma unroll
             for (int j = 0; j < 2; ++j)
@@ -293,8 +354,8 @@ struct G256 {
                     bs[j][q] = (n < N) ? *(const f32x4*)(g.b_scale + n) : f32x4{0.f, 0.f, 0.f, 0.f};
                 }
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int m = m0 + wm * 128 + i * 32 + (lane & 31);
+            for (int i = 0; i < NI; ++i) {
+                const int m = m0 + wm * WR + i * 32 + (lane & 31);
                 as[i] = (m < M) ? g.a_scale[off + m] : 0.0f;
             }
         }
@@ -303,11 +364,11 @@ struct G256 {
         // 64 + l here, with the scales, and each store round fetches its row
         // from the lane that holds it (ds_bpermute: a cross-lane move, no LDS
         // memory), two registers instead of a 16-entry table.
-        int32_t cr[2];
+        int32_t cr[WR / 64];
         if constexpr (Seq::ROUTED) {
 #pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const int m = m0 + wm * 128 + h * 64 + lane;
+            for (int h = 0; h < WR / 64; ++h) {
+                const int m = m0 + wm * WR + h * 64 + lane;
                 cr[h] = (m < M) ? (g.c_idx ? g.c_idx[off + m] : m) : -1;
             }
         }
@@ -315,16 +376,16 @@ struct G256 {
             if constexpr (Seq::ROUTED) {
                 return __builtin_amdgcn_ds_bpermute((r & 63) << 2, cr[r >> 6]);
             } else {
-                const int m = m0 + wm * 128 + r;
+                const int m = m0 + wm * WR + r;
                 return m < M ? m : -1;
             }
         };
         WAITCNT_VM(0);
         asm volatile("" ::: "memory");
-        uint8_t* slot = smem + T2_EPI + wave * T2_SLOT;
+        uint8_t* slot = smem + GE::EPI + wave * T2_SLOT;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int mb = m0 + wm * 128 + i * 32;    // first row of this 32 x 64 block
+        for (int i = 0; i < NI; ++i) {
+            const int mb = m0 + wm * WR + i * 32;     // first row of this 32 x 64 block
             const int nb = n0 + wn * 64;
             if constexpr (KIND == EE_GEMM_I8) {
                 if (!Seq::ROUTED && g.acc) {          // debug output: int32 accumulators, direct stores
@@ -397,7 +458,7 @@ struct G256 {
 
     __device__ __forceinline__ void zero() {
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < NI; ++i)
 #pragma unroll
             for (int j = 0; j < 2; ++j) acc[i][j] = acc_t{};
     }
@@ -411,15 +472,15 @@ struct G256 {
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
         if (cs + 1 < total && iss == cs + 1) issue_stage();
-        rd_all(smem + (cs & 1) * T2_STAGE, 0, 0);
+        rd_all(smem + (cs & 1) * GE::STAGE, 0, 0);
     }
 
     __device__ __forceinline__ void run() {
         const int tid = threadIdx.x;
         lane = tid & 63;
         wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-        wm = wave >> 2;
-        wn = wave & 3;
+        wm = wave >> GE::WMS;
+        wn = wave & ((1 << GE::WMS) - 1);
         const int ntiles = seq.count();
         if (ntiles <= 0) return;                      // whole workgroup, before any barrier
         nk = (int)((int64_t)g.K * ESZ / BKB);         // K * ESZ is a multiple of BKB here
@@ -431,7 +492,9 @@ struct G256 {
         issue_stage();                                // stage 0 -> buffer 0
         if (total > 1) {
             issue_stage();                            // stage 1 -> buffer 1
-            WAITCNT_VM(8);
+            // stage 0 landed; stage 1's loads (4 A + BG B per wave) may stay in flight
+            if constexpr (GE::BG == 4) WAITCNT_VM(8);
+            else WAITCNT_VM(6);
         } else {
             WAITCNT_VM(0);
         }
@@ -451,22 +514,23 @@ struct G256 {
 };
 
 // Tiles of an un-routed GEMM for workgroup b of G (TileDeal: 8 x 4 blocks per XCD).
+template <int TN>
 struct Seq256 {
     static constexpr bool ROUTED = false, GATHER = false;
     TileDeal d;
     __device__ __forceinline__ Seq256(const EeGemmArgs& g, int b, int G)
-        : d((g.M + T2M - 1) / T2M, (g.N + T2N - 1) / T2N, 0, b, G) {}
+        : d((g.M + T2M - 1) / T2M, (g.N + TN - 1) / TN, 0, b, G) {}
     __device__ __forceinline__ int count() const { return d.count(); }
     __device__ __forceinline__ void coords(int i, int& tm, int& tn) const {
         d.coords(d.tile_index(d.first_round + i), tm, tn);
     }
 };
 
-template <int KIND, int SW>
+template <int KIND, int SW, int TN>
 EE_DEV void gemm256(const EeGemmArgs& g) {
-    __shared__ __attribute__((aligned(1024))) uint8_t smem[T2_LDS];
-    const Seq256 seq(g, (int)blockIdx.x, (int)gridDim.x);
-    G256<KIND, SW, Seq256> k(g, smem, seq, g.M, 0);
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[G2Geom<TN>::LDS];
+    const Seq256<TN> seq(g, (int)blockIdx.x, (int)gridDim.x);
+    G256<KIND, SW, Seq256<TN>, TN> k(g, smem, seq, g.M, 0);
     k.run();
 }
 
@@ -516,20 +580,20 @@ struct SeqRF {
     }
 };
 
-template <int SW>
+template <int SW, int TN>
 EE_DEV void gemm256_routed(const EeRoutedGemmArgs& r) {
-    __shared__ __attribute__((aligned(1024))) uint8_t smem[T2_LDS];
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[G2Geom<TN>::LDS];
     const int32_t* counts = r.t[0].counts;
     const int c0 = counts[0], c1 = counts[1], c2 = counts[2];
     const int T0 = (c0 + T2M - 1) / T2M, T1 = (c1 + T2M - 1) / T2M, T2 = (c2 + T2M - 1) / T2M;
-    const int nN = (r.t[0].N + T2N - 1) / T2N;
+    const int nN = (r.t[0].N + TN - 1) / TN;
     const int b = (int)blockIdx.x, G = (int)gridDim.x;
     const int nF = T2 * nN;
     const TileDeal d(T0 + T1, nN, nF, b, G);
     // phase FP16
     const SeqRF sf{b, G, b < nF ? (nF - b + G - 1) / G : 0, T2};
     if (sf.n > 0) {
-        G256<EE_GEMM_F16, SW, SeqRF> k(r.t[2], smem, sf, c2, (int64_t)c0 + c1);
+        G256<EE_GEMM_F16, SW, SeqRF, TN> k(r.t[2], smem, sf, c2, (int64_t)c0 + c1);
         k.run();
     }
     // the 1-byte tiles: the INT8 ones come first (logical index < T0 * nN)
@@ -539,30 +603,33 @@ EE_DEV void gemm256_routed(const EeRoutedGemmArgs& r) {
     if (ni8 > 0) {
         if (sf.n > 0) __syncthreads();                // the previous phase's LDS reads and DMA are done
         const SeqR1 s8{d, 0, ni8, T0, T1, nN};
-        G256<EE_GEMM_I8, SW, SeqR1> k(r.t[0], smem, s8, c0, 0);
+        G256<EE_GEMM_I8, SW, SeqR1, TN> k(r.t[0], smem, s8, c0, 0);
         k.run();
     }
     if (n1 > ni8) {
         if (sf.n > 0 || ni8 > 0) __syncthreads();
         const SeqR1 s8{d, ni8, n1 - ni8, T0, T1, nN};
-        G256<EE_GEMM_F8, SW, SeqR1> k(r.t[1], smem, s8, c1, c0);
+        G256<EE_GEMM_F8, SW, SeqR1, TN> k(r.t[1], smem, s8, c1, c0);
         k.run();
     }
 }
 
-#define EE_G256_ENTRY(NAME, KIND)                                                                           \
+#define EE_G256_ENTRY(NAME, KIND, TN)                                                                       \
     extern "C" __global__ void __launch_bounds__(T2_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))   \
-    NAME(EeGemmArgs g) { gemm256<KIND, 0>(g); }                                                           \
+    NAME(EeGemmArgs g) { gemm256<KIND, 0, TN>(g); }                                                       \
     extern "C" __global__ void __launch_bounds__(T2_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))   \
-    NAME##_swiglu(EeGemmArgs g) { gemm256<KIND, 1>(g); }
-EE_G256_ENTRY(eek_gemm256_i8, EE_GEMM_I8)
-EE_G256_ENTRY(eek_gemm256_f8, EE_GEMM_F8)
-EE_G256_ENTRY(eek_gemm256_f16, EE_GEMM_F16)
-extern "C" __global__ void __launch_bounds__(T2_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
-eek_gemm256_routed(EeRoutedGemmArgs r) {
-    gemm256_routed<0>(r);
-}
-extern "C" __global__ void __launch_bounds__(T2_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))
-eek_gemm256_routed_swiglu(EeRoutedGemmArgs r) {
-    gemm256_routed<1>(r);
-}
+    NAME##_swiglu(EeGemmArgs g) { gemm256<KIND, 1, TN>(g); }
+EE_G256_ENTRY(eek_gemm256_i8, EE_GEMM_I8, 256)
+EE_G256_ENTRY(eek_gemm256_f8, EE_GEMM_F8, 256)
+EE_G256_ENTRY(eek_gemm256_f16, EE_GEMM_F16, 256)
+// 256 x 128 tiles
+EE_G256_ENTRY(eek_gemm256n128_i8, EE_GEMM_I8, 128)
+EE_G256_ENTRY(eek_gemm256n128_f8, EE_GEMM_F8, 128)
+EE_G256_ENTRY(eek_gemm256n128_f16, EE_GEMM_F16, 128)
+#define EE_G256_ROUTED_ENTRY(NAME, TN)                                                                      \
+    extern "C" __global__ void __launch_bounds__(T2_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))   \
+    NAME(EeRoutedGemmArgs r) { gemm256_routed<0, TN>(r); }                                                \
+    extern "C" __global__ void __launch_bounds__(T2_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2)))   \
+    NAME##_swiglu(EeRoutedGemmArgs r) { gemm256_routed<1, TN>(r); }
+EE_G256_ROUTED_ENTRY(eek_gemm256_routed, 256)
+EE_G256_ROUTED_ENTRY(eek_gemm256n128_routed, 128)

@@ -472,6 +472,9 @@ EE_EXPORT int ee_engine_set_option(ee_engine* eng, const char* key, int64_t valu
     } else if (k == "gemm_tile") {
         if (value != 0 && value != 128 && value != 256)
             return fail(EE_ERR_INVALID_ARG, k + " must be 0 (auto), 128 or 256");
+    } else if (k == "gemm_tile_n") {
+        if (value != 0 && value != 128 && value != 256)
+            return fail(EE_ERR_INVALID_ARG, k + " must be 0 (auto), 128 or 256");
     } else {
         return fail(EE_ERR_INVALID_ARG, "unknown option: " + k);
     }
@@ -685,13 +688,25 @@ static int gemm_impl(ee_engine* eng, int32_t kind, const void* a, int64_t lda, c
     if ((K * esz) % 128 == 0 && counts == nullptr && tile_opt != 128 && off32 &&
         !(kind == EE_GEMM_F16 && variant == 2) && (tile_opt == 256 || tiles > eng->cus)) {
         static const char* names256[3] = {"eek_gemm256_i8", "eek_gemm256_f8", "eek_gemm256_f16"};
-        std::string n256 = std::string(names256[kind]) + (sw ? "_swiglu" : "");
+        static const char* names128[3] = {"eek_gemm256n128_i8", "eek_gemm256n128_f8", "eek_gemm256n128_f16"};
+        // Tile width: 256 x 128 where the 256 x 256 grid would keep at most half the CUs
+        // busy.  Measured (eager, same box): 4096 x 2048 x 2048 INT8 22.5 against 27.6 us,
+        // 4096 x 5632 x 2048 51.5 against 61.1 (FP8 -17%); but at N = 2560 (160 tiles of
+        // 256 x 256) 37.6 against 28.1, and a 256 x 256 grid whose last round is half
+        // full (4096 x 14336: 3.5 rounds) is still faster than 7 rounds of 256 x 128
+        // tiles (229 against 253 us): those stream 1.5x the bytes per MFMA op.
+        // Option "gemm_tile_n": 0 auto, 128 or 256 forced.
+        const int64_t tn_opt = opt(eng, "gemm_tile_n");
+        const int64_t gcu = eng->cus >= 8 ? (eng->cus & ~7) : eng->cus;
+        const int64_t t256 = cdiv(M, 256) * cdiv(N, 256), t128 = cdiv(M, 256) * cdiv(N, 128);
+        const bool narrow = tn_opt == 128 || (tn_opt == 0 && 2 * t256 <= gcu);
+        std::string n256 = std::string(narrow ? names128[kind] : names256[kind]) + (sw ? "_swiglu" : "");
         const Kernel* k256 = find_kernel(eng, n256);
         if (k256 != nullptr) {
-            const int64_t t256 = cdiv(M, 256) * cdiv(N, 256);
-            int64_t g256 = persist_grid(eng, t256);
-            if (g256 <= 0) g256 = std::min<int64_t>(t256, eng->cus >= 8 ? (eng->cus & ~7) : eng->cus);
-            if (g256 <= 0) g256 = t256;
+            const int64_t tt = narrow ? t128 : t256;
+            int64_t g256 = persist_grid(eng, tt);
+            if (g256 <= 0) g256 = std::min<int64_t>(tt, gcu);
+            if (g256 <= 0) g256 = tt;
             return launch(eng, n256, g256, 1, k256->block, g, stream);
         }
     }
@@ -814,7 +829,10 @@ static int routed_impl(ee_engine* eng, const void* x, int64_t ld_x, int32_t M, i
         const bool off32 = std::max<int64_t>((int64_t)M * ld_x * 2, (int64_t)M * K) + 2 * K < (int64_t(1) << 32) &&
                            255 * 2 * (int64_t)K + 2 * K < (int64_t(1) << 32);
         if (!ra.f16_w8 && tile_opt != 128 && off32 && (tile_opt == 256 || slots > eng->cus)) {
-            std::string n256 = sw ? "eek_gemm256_routed_swiglu" : "eek_gemm256_routed";
+            // (256 x 256 tiles unless option gemm_tile_n = 128: the tiers' row counts, which
+            // decide the rounds, are on the device)
+            std::string n256 = opt(eng, "gemm_tile_n") == 128 ? "eek_gemm256n128_routed" : "eek_gemm256_routed";
+            if (sw) n256 += "_swiglu";
             const Kernel* k256 = find_kernel(eng, n256);
             if (k256 != nullptr) {
                 const int64_t g256 = eng->cus >= 8 ? (eng->cus & ~7) : std::max(1, eng->cus);
