@@ -323,7 +323,8 @@ def main():
             del c1_in, c1_out, L1
         # ---- config 3: the dispatcher end to end on a mixed batch (M = K = N = 4096)
         c3 = None
-        c3_names = ("c3_entropy", "c3_route", "c3_linear", "c3_end_to_end")
+        c3_names = ("c3_entropy", "c3_route", "c3_linear", "c3_end_to_end", "c3_routed_gemm", "c3_tier_i8",
+                    "c3_tier_f8", "c3_tier_f16")
         if not only or any(n in only for n in c3_names):
             M3 = K3 = N3 = 4096
             L3, _ = mixture_logits(rng, M3, K3)
@@ -351,8 +352,23 @@ def main():
             run("c3_route", lambda: ee.route(h3, 0.41, 1.68))
             run("c3_linear", lambda: ee.routed_linear(x3, pw3, idx3, counts3, out=out3, workspace=ws3))
             run("c3_end_to_end", c3_all)
+            # the routed GEMM launch alone (on the codes its quantiser left in the workspace)
+            # against the three tiers' own GEMMs on the same partitioned rows
+            ee.routed_linear(x3, pw3, idx3, counts3, out=out3, workspace=ws3)
+            n0, n1, n2 = counts3.cpu().tolist()
+            codes3, scale3 = ws3
+            x16_3 = x3[idx3[n0 + n1:].long()].contiguous()
+            o_t = [torch.empty((max(n, 1), N3), dtype=torch.float16, device=dev) for n in (n0, n1, n2)]
+            run("c3_routed_gemm", lambda: ee.routed_linear(x3, pw3, idx3, counts3, out=out3, quantized=(codes3, scale3)))
+            if n0:
+                run("c3_tier_i8", lambda: ee.gemm("int8", codes3[:n0], pw3.i8, scale3[:n0], pw3.scale, out=o_t[0]))
+            if n1:
+                run("c3_tier_f8", lambda: ee.gemm("fp8", codes3[n0:n0 + n1], pw3.f8, scale3[n0:n0 + n1], pw3.scale,
+                                                  out=o_t[1]))
+            if n2:
+                run("c3_tier_f16", lambda: ee.gemm("fp16", x16_3, pw3.f16, out=o_t[2]))
             c3 = {"routing_fractions": fr, "thresholds_timed": [0.41, 1.68],
-                  "ops": 2.0 * M3 * N3 * K3}
+                  "ops": 2.0 * M3 * N3 * K3, "rows": [n0, n1, n2]}
         # ---- the fused MLP engine at EE/test_engine.py:10's shape (B, S, H, Inter = 1, 1024, 2048, 5632)
         mlp = None
         mlp_names = ("mlp_int8", "mlp_fp8", "mlp_fp16", "mlp_routed", "mlp_torch_fp16")
@@ -448,6 +464,15 @@ def main():
             "routing_fractions_int8_fp8_fp16": c3["routing_fractions"],
             "shape": "M=K=N=4096; entropy over fp16 [4096,4096] mixture logits",
         }
+        if "c3_routed_gemm" in results:
+            tiers = [results[f"c3_tier_{t}"]["ms"] * 1e3 for t in ("i8", "f8", "f16") if f"c3_tier_{t}" in results]
+            kernels["dispatcher_c3"].update({
+                "us_routed_gemm": results["c3_routed_gemm"]["ms"] * 1e3,
+                "us_per_tier_gemms": tiers, "us_per_tier_gemm_sum": sum(tiers),
+                "routed_over_per_tier_sum": results["c3_routed_gemm"]["ms"] * 1e3 / sum(tiers),
+                "rows_per_tier": c3["rows"],
+                "note": "routed GEMM launch alone (codes from its quantiser) vs the three tiers' own GEMMs on the "
+                        "same partitioned rows, each a separate launch"})
     for cfg, ops_b in big.items():
         legs = ("int8", "fp8_tensor", "w8a16", "fp16_torch") if cfg == "c1" else ("int8", "fp8", "fp16_torch")
         peak = {"int8": PEAK_I8_TOPS, "fp8_tensor": PEAK_F8_TFLOPS, "fp8": PEAK_F8_TFLOPS, "w8a16": PEAK_F16_TFLOPS,
