@@ -198,6 +198,39 @@ def test_gemm256_routed_equals_per_tier(ee, orc, M, K, N, H_hi, grid, tn):
             assert np.array_equal(out[t == k], host(full[k]).view(np.uint16)[t == k]), f"tier {k}"
 
 
+@pytest.mark.parametrize("N,sw", [(2048, False), (2560, False), (1024, True)])
+def test_gemm256_routed_sparse_fp16_halves(ee, orc, N, sw):
+    """Config 4's mix (2.3 / 95.8 / 1.9 % of 4096 rows): one sparse FP16 M-tile per
+    column, which the routed grid runs as 256 x 128 halves.  Every row equals the
+    128-tile routed grid's and, per tier, the un-routed GEMM of its tier bit for
+    bit."""
+    M, K = 4096, 512
+    rng = np.random.default_rng(N + sw)
+    u = rng.random(M)
+    H = np.where(u < 0.023, 0.1, np.where(u < 0.981, 1.0, 9.0)).astype(np.float32)
+    if sw:
+        W = (rng.standard_normal((2 * N, K)) / np.sqrt(K)).astype(np.float16)
+        codes, scale = ee.quantize_weight_codes(cuda(W))
+        pw = ee.PackedWeight(ee.interleave_gate_up(codes), ee.interleave_gate_up(scale)).materialize()
+    else:
+        B, bs = weights(orc, rng, N, K)
+        pw = ee.prepare_weight(cuda(B), cuda(bs)).materialize()
+    x = cuda(rng.standard_normal((M, K)).astype(np.float16))
+    tier, idx, counts = ee.route(cuda(H), 0.5, 5.0)
+    assert all(c > 0 for c in counts.tolist())
+    with _Options(gemm_tile=256):
+        out = host(ee.routed_linear(x, pw, idx, counts, swiglu=sw)).view(np.uint16)
+    with _Options(gemm_tile=128):
+        ref128 = host(ee.routed_linear(x, pw, idx, counts, swiglu=sw)).view(np.uint16)
+    assert np.array_equal(out, ref128)
+    if not sw:
+        t = host(tier)
+        full = [ee.triton_int8_gemm(x, cuda(B), cuda(bs)), ee.triton_fp8_gemm(x, cuda(B), cuda(bs)),
+                ee.triton_fp16_gemm(x, cuda(B), cuda(bs))]
+        for k in range(3):
+            assert np.array_equal(out[t == k], host(full[k]).view(np.uint16)[t == k]), f"tier {k}"
+
+
 def test_gemm256_routed_config3(ee, orc):
     """Config 3's routed linear (M = K = N = 4096, 20/40/40 % tiers) takes the
     256-tile routed grid automatically: rows equal the per-tier GEMMs bit for bit,

@@ -133,26 +133,27 @@ EE_DEV void store_row16(uint16_t* dst, const u32x4& v, bool full) {
 // taking workgroup gets one tile, and with G a multiple of 8 workgroup
 // b = 8j + x (on XCD x) takes position x * G/8 + j, so each XCD gets 32
 // consecutive tiles -- one 8 x 4 block, whose A and B panels its CUs share in
-// that XCD's L2.  W8A16 tiles of a routed launch (nF of them, twice the work
-// of a 1-byte tile at the same K) are dealt first, round robin: workgroups
-// b < rF get qF + 1, the others qF.  The first two rounds of 1-byte tiles then
-// go only to workgroups b >= rF, which levels the load (a static version of
-// what the hardware dispatcher does for one-tile grids).
+// that XCD's L2.  W8A16 tiles of a routed launch (nF of them, each worth `skip`
+// 1-byte tiles: 2 for a 256 x 256 tile, 1 for a 256 x 128 half) are dealt
+// first, round robin: workgroups b < rF get qF + 1, the others qF.  The first
+// `skip` rounds of 1-byte tiles then go only to workgroups b >= rF, which levels
+// the load (a static version of what the hardware dispatcher does for one-tile
+// grids).
 struct TileDeal {
-    int tiles_m, tiles_n, nA, b, G, per, rF, P, first_round;
-    __device__ __forceinline__ TileDeal(int tm_count, int tn_count, int nF, int bb, int GG)
-        : tiles_m(tm_count), tiles_n(tn_count), nA(tm_count * tn_count), b(bb), G(GG) {
+    int tiles_m, tiles_n, nA, b, G, per, rF, P, first_round, skip;
+    __device__ __forceinline__ TileDeal(int tm_count, int tn_count, int nF, int bb, int GG, int sk = 2)
+        : tiles_m(tm_count), tiles_n(tn_count), nA(tm_count * tn_count), b(bb), G(GG), skip(sk) {
         per = (G & 7) == 0 ? G >> 3 : 0;
         rF = nF % G;
-        P = G - rF;                                   // workgroups in rounds 0 and 1
-        first_round = (rF != 0 && b < rF) ? 2 : 0;    // heavier workgroups skip rounds 0 and 1
+        P = G - rF;                                   // workgroups in the first `skip` rounds
+        first_round = (rF != 0 && b < rF) ? skip : 0; // heavier workgroups skip those rounds
     }
     // position of this workgroup in a round in which all G take part
     __device__ __forceinline__ int pos_all() const { return per ? (b & 7) * per + (b >> 3) : b; }
     __device__ __forceinline__ int tile_index(int round) const {
         if (rF == 0) return round * G + pos_all();
-        if (round < 2) return round * P + (b - rF);
-        return 2 * P + (round - 2) * G + pos_all();
+        if (round < skip) return round * P + (b - rF);
+        return skip * P + (round - skip) * G + pos_all();
     }
     __device__ __forceinline__ int count() const {
         // rounds first_round, first_round+1, ... while tile_index(round) < nA
@@ -162,10 +163,10 @@ struct TileDeal {
         }
         int n = 0;
         if (first_round == 0) {
-            for (int r = 0; r < 2; ++r) n += tile_index(r) < nA;
-            if (n < 2) return n;
+            for (int r = 0; r < skip; ++r) n += tile_index(r) < nA;
+            if (n < skip) return n;
         }
-        const int p = 2 * P + pos_all();
+        const int p = skip * P + pos_all();
         return n + (p < nA ? (nA - p + G - 1) / G : 0);
     }
     // logical tile a -> (tm, tn): bands of 8 M-tiles, M fastest within a band

@@ -586,15 +586,37 @@ EE_DEV void gemm256_routed(const EeRoutedGemmArgs& r) {
     const int32_t* counts = r.t[0].counts;
     const int c0 = counts[0], c1 = counts[1], c2 = counts[2];
     const int T0 = (c0 + T2M - 1) / T2M, T1 = (c1 + T2M - 1) / T2M, T2 = (c2 + T2M - 1) / T2M;
-    const int nN = (r.t[0].N + TN - 1) / TN;
+    const int N = r.t[0].N;
+    const int nN = (N + TN - 1) / TN;
     const int b = (int)blockIdx.x, G = (int)gridDim.x;
-    const int nF = T2 * nN;
-    const TileDeal d(T0 + T1, nN, nF, b, G);
+    // W8A16 tiles: 256 x TN, or 256 x 128 halves where that shortens the estimated
+    // makespan (in 1-byte-tile units: a full W8A16 tile costs 2, a half ~1.15, as
+    // measured).  A few FP16 rows -- one M-tile per column, as at config 4 -- then
+    // no longer set the grid's length at twice a 1-byte tile's time.  Every
+    // workgroup reads the same counts, so every workgroup makes the same choice.
+    int nF = T2 * nN, skip = 2;
+    bool half = false;
+    if constexpr (TN == 256) {
+        const int nFh = T2 * ((N + 127) / 128), nA = (T0 + T1) * nN;
+        const int full20 = 20 * max(2 * ((nF + G - 1) / G), (2 * nF + nA + G - 1) / G);
+        const int half20 = max(23 * ((nFh + G - 1) / G), 20 * (((23 * nFh + 19) / 20 + nA + G - 1) / G));
+        if (nF > 0 && half20 < full20) {
+            half = true;
+            nF = nFh;
+            skip = 1;
+        }
+    }
+    const TileDeal d(T0 + T1, nN, nF, b, G, skip);
     // phase FP16
     const SeqRF sf{b, G, b < nF ? (nF - b + G - 1) / G : 0, T2};
     if (sf.n > 0) {
-        G256<EE_GEMM_F16, SW, SeqRF, TN> k(r.t[2], smem, sf, c2, (int64_t)c0 + c1);
-        k.run();
+        if (half) {
+            G256<EE_GEMM_F16, SW, SeqRF, 128> k(r.t[2], smem, sf, c2, (int64_t)c0 + c1);
+            k.run();
+        } else {
+            G256<EE_GEMM_F16, SW, SeqRF, TN> k(r.t[2], smem, sf, c2, (int64_t)c0 + c1);
+            k.run();
+        }
     }
     // the 1-byte tiles: the INT8 ones come first (logical index < T0 * nN)
     const int n1 = d.count();
