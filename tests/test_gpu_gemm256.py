@@ -8,7 +8,8 @@ FP8 / FP16 within 1e-2 of a float64 recompute -- and, bit for bit, against the
 128-tile kernels on the same inputs (same K order: FP8 and FP16 sum slice after
 slice in both).  Ragged shapes, one-stage K, partial tiles and several tiles
 per workgroup (forced grids, including one that is not a multiple of the 8
-XCDs) exercise the stage ring across tile boundaries.
+XCDs) exercise the stage ring across tile boundaries; grids whose last round
+is at most half full run that round as 256 x 128 halves.
 """
 import numpy as np
 import pytest
@@ -60,6 +61,9 @@ SHAPES = [
     (1024, 512, 1024, 8),      # 16 tiles on 8 workgroups: 2 tiles each, ring across tiles
     (1024, 384, 1024, 3),      # 16 tiles on 3 workgroups (not a multiple of 8): 5-6 tiles each
     (768, 256, 2048, 5),       # 24 tiles on 5 workgroups, 2 stages per tile
+    # last round at most half full: it runs as 256 x 128 halves (256-wide tiles only)
+    (512, 512, 2432, 8),       # 20 tiles on 8: 2 full rounds, 8 halves (one past N: skipped)
+    (300, 640, 1800, 13),      # 16 tiles on 13: 1 round, 6 halves; partial in M and N
 ]
 
 
@@ -84,7 +88,7 @@ def test_gemm256_int8_fp8_small(ee, orc, M, K, N, grid, tn):
 
 
 @pytest.mark.parametrize("tn", [256, 128])
-@pytest.mark.parametrize("M,K,N,grid", SHAPES[:3] + SHAPES[4:6])
+@pytest.mark.parametrize("M,K,N,grid", SHAPES[:3] + SHAPES[4:6] + SHAPES[7:])
 def test_gemm256_fp16_small(ee, orc, M, K, N, grid, tn):
     """The FP16 (W8A16) tier on the 256-tile kernel: within 1e-2 of float64 and
     bit-identical to the 128-tile loader-wave pipeline (same K order)."""
@@ -142,10 +146,11 @@ def test_gemm256_fp8_config1_per_tensor(ee, orc):
 
 
 @pytest.mark.parametrize("tn", [256, 128])
-@pytest.mark.parametrize("M,K,F", [(4096, 2048, 5632), (600, 256, 640)])
-def test_gemm256_swiglu(ee, orc, M, K, F, tn):
+@pytest.mark.parametrize("M,K,F,grid", [(4096, 2048, 5632, 0), (600, 256, 640, 0), (512, 256, 1216, 8)])
+def test_gemm256_swiglu(ee, orc, M, K, F, grid, tn):
     """The SwiGLU epilogue of the 256-tile kernels gives the bits of the 128-tile
-    SwiGLU kernels (every tier; FP16 on the loader-wave order)."""
+    SwiGLU kernels (every tier; FP16 on the loader-wave order).  The forced grid
+    of 8 leaves the last round half full: 256 x 128 halves."""
     rng = np.random.default_rng(M + F)
     W = (rng.standard_normal((2 * F, K)) / np.sqrt(K)).astype(np.float16)
     codes, scale = ee.quantize_weight_codes(cuda(W))
@@ -155,7 +160,7 @@ def test_gemm256_swiglu(ee, orc, M, K, F, tn):
     cf, sf = ee.quantize_activations(x, "fp8")
     for kind, a, b, sa, sb in (("int8", ci, pw.i8, si, pw.scale), ("fp8", cf, pw.f8, sf, pw.scale),
                                ("fp16", x, pw.f16, None, None)):
-        with _Options(gemm_tile=256, gemm_tile_n=tn):
+        with _Options(gemm_tile=256, gemm_tile_n=tn, gemm_persist=grid):
             fused = ee.gemm(kind, a, b, sa, sb, swiglu=True)
         with _Options(gemm_tile=128, gemm_variant=1):
             ref = ee.gemm(kind, a, b, sa, sb, swiglu=True)

@@ -513,23 +513,65 @@ struct G256 {
     }
 };
 
-// Tiles of an un-routed GEMM for workgroup b of G (TileDeal: 8 x 4 blocks per XCD).
+// Tiles of an un-routed GEMM for workgroup b of G (TileDeal: 8 x 4 blocks per XCD),
+// at most `cap` rounds of them.
 template <int TN>
 struct Seq256 {
     static constexpr bool ROUTED = false, GATHER = false;
     TileDeal d;
-    __device__ __forceinline__ Seq256(const EeGemmArgs& g, int b, int G)
-        : d((g.M + T2M - 1) / T2M, (g.N + TN - 1) / TN, 0, b, G) {}
-    __device__ __forceinline__ int count() const { return d.count(); }
+    int cap;
+    __device__ __forceinline__ Seq256(const EeGemmArgs& g, int b, int G, int cap_ = 0x7fffffff)
+        : d((g.M + T2M - 1) / T2M, (g.N + TN - 1) / TN, 0, b, G), cap(cap_) {}
+    __device__ __forceinline__ int count() const { return min(d.count(), cap); }
     __device__ __forceinline__ void coords(int i, int& tm, int& tn) const {
         d.coords(d.tile_index(d.first_round + i), tm, tn);
     }
 };
+// One 256 x 128 tile (tm, tn in 128-column units), or none.
+struct Seq256Half {
+    static constexpr bool ROUTED = false, GATHER = false;
+    int n, tm, tn;
+    __device__ __forceinline__ int count() const { return n; }
+    __device__ __forceinline__ void coords(int, int& tm_, int& tn_) const {
+        tm_ = tm;
+        tn_ = tn;
+    }
+};
 
+// A grid of 256 x 256 tiles whose last round is at most half full (config 2:
+// 896 tiles on 256 CUs, 3.5 rounds) runs that round as 256 x 128 halves, one
+// per workgroup: the full rounds first, then the halves, in the same tile
+// order (both halves of a tile on one XCD).  The halves sum K in the same
+// order, so the output bits do not change.
 template <int KIND, int SW, int TN>
 EE_DEV void gemm256(const EeGemmArgs& g) {
     __shared__ __attribute__((aligned(1024))) uint8_t smem[G2Geom<TN>::LDS];
-    const Seq256<TN> seq(g, (int)blockIdx.x, (int)gridDim.x);
+    const int b = (int)blockIdx.x, G = (int)gridDim.x;
+    const Seq256<TN> seq(g, b, G);
+    if constexpr (TN == 256) {
+        const int nT = seq.d.nA, full = nT / G, rem = nT - full * G;
+        if (rem > 0 && 2 * rem <= G) {
+            if (full > 0) {
+                const Seq256<TN> s1(g, b, G, full);
+                G256<KIND, SW, Seq256<TN>, TN> k(g, smem, s1, g.M, 0);
+                k.run();
+                __syncthreads();                      // every wave's reads of the ring and its slot are done
+            }
+            const int h = seq.d.pos_all();            // positions 0 .. G-1, one per workgroup
+            Seq256Half sh{0, 0, 0};
+            if (h < 2 * rem) {
+                int tm, tn;
+                seq.d.coords(full * G + (h >> 1), tm, tn);
+                const int tn2 = 2 * tn + (h & 1);
+                if (tn2 * 128 < g.N) sh = Seq256Half{1, tm, tn2};
+            }
+            if (sh.n > 0) {
+                G256<KIND, SW, Seq256Half, 128> k(g, smem, sh, g.M, 0);
+                k.run();
+            }
+            return;
+        }
+    }
     G256<KIND, SW, Seq256<TN>, TN> k(g, smem, seq, g.M, 0);
     k.run();
 }
