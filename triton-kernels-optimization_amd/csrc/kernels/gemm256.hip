@@ -67,6 +67,26 @@ struct G256 {
     typedef typename P::frag_t frag_t;
     static constexpr int ESZ = (KIND == EE_GEMM_F16) ? 2 : 1;
     static constexpr int NSL = BKB / P::SB;           // K slices per stage: 4 (32-byte slices) or 2 (64-byte)
+    // DMA parts of stage s+2 issued in each slice of the window from barrier s+1
+    // (slice w = 0: the last slice of stage s; w >= 1: slice w-1 of stage s+1).
+    // All four are issued before barrier s+2 waits for them.  FP16 (four slices
+    // per stage) spreads them over two slices: 2.5% faster at configs 1-2 than
+    // all four in the first; the 1-byte kinds, with two slices per stage, keep
+    // them in the first (spread, the last loads land late: 3-8% slower).
+    static constexpr int dma_count(int w) {
+        if constexpr (KIND == EE_GEMM_F16) {
+            constexpr int c[4] = {2, 2, 0, 0};
+            return c[w];
+        } else {
+            return w == 0 ? 4 : 0;
+        }
+    }
+    static constexpr int dma_first(int w) {
+        int f = 0;
+        for (int i = 0; i < w; ++i) f += dma_count(i);
+        return f;
+    }
+    static_assert(dma_first(NSL) == 4, "every DMA part is issued within its window");
 
     const EeGemmArgs& g;
     uint8_t* smem;
@@ -79,6 +99,7 @@ struct G256 {
     // DMA cursor: the next stage to issue is (itile, ikt), global number iss;
     // row group q of A (B) of that tile starts at abase + aoff[q] (bbase + boff[q]).
     int iss, itile, ikt;
+    bool dmaon;                                       // the stage being issued is still issuing
     const uint8_t* abase;
     const uint8_t* bbase;
     uint32_t aoff[4], boff[GE::BG];
@@ -180,18 +201,23 @@ struct G256 {
     }
 
 #define G2_SB() __builtin_amdgcn_sched_barrier(0)
+    // Part p0 + k of the stage being issued, at the k-th DMA position of a slice
+    // (k < np), while dmaon.
+    __device__ __forceinline__ void dma_at(int k, int p0, int np) {
+        if (k < np && dmaon) issue_part(p0 + k);
+    }
     // The 8 MFMAs of the current slice (B fragments in buffer C), interleaved
     // with the reads of the next slice (from stage rs, slice rsl, when RD: B into
-    // buffer 1 - C, A row block i right after its last MFMA here) and the 4 DMA
-    // parts of the next stage (when dma).
+    // buffer 1 - C, A row block i right after its last MFMA here) and DMA parts
+    // p0 .. p0+np-1 of the stage being issued.
     template <int C, bool RD>
-    __device__ __forceinline__ void slice(const uint8_t* rs, int rsl, bool dma) {
+    __device__ __forceinline__ void slice(const uint8_t* rs, int rsl, int p0, int np) {
         if constexpr (NB == 1) {
-            if constexpr (NI == 2) slice_j2(RD, rs, rsl, dma);
-            else slice_j(RD, rs, rsl, dma);
+            if constexpr (NI == 2) slice_j2(RD, rs, rsl, p0, np);
+            else slice_j(RD, rs, rsl, p0, np);
             return;
         } else if constexpr (NI == 2) {
-            slice2<C>(RD, rs, rsl, dma);
+            slice2<C>(RD, rs, rsl, p0, np);
             return;
         }
         constexpr int N = (1 - C) % NB;
@@ -205,21 +231,21 @@ struct G256 {
         G2_SB();
         acc[1][0] = P::mma(fb[C][0], fa[1], acc[1][0]);
         G2_SB();
-        if (dma) issue_part(0);
+        dma_at(0, p0, np);
         G2_SB();
         acc[1][1] = P::mma(fb[C][1], fa[1], acc[1][1]);
         G2_SB();
         if (RD) rd_a(rs, rsl, 1);
-        if (dma) issue_part(1);
+        dma_at(1, p0, np);
         G2_SB();
         acc[2][0] = P::mma(fb[C][0], fa[2], acc[2][0]);
         G2_SB();
-        if (dma) issue_part(2);
+        dma_at(2, p0, np);
         G2_SB();
         acc[2][1] = P::mma(fb[C][1], fa[2], acc[2][1]);
         G2_SB();
         if (RD) rd_a(rs, rsl, 2);
-        if (dma) issue_part(3);
+        dma_at(3, p0, np);
         G2_SB();
         acc[3][0] = P::mma(fb[C][0], fa[3], acc[3][0]);
         G2_SB();
@@ -232,7 +258,7 @@ struct G256 {
     // Two row blocks (64 x 64 per wave): the same interleave over 4 MFMAs, the four
     // load parts of the next stage after the first two.
     template <int C>
-    __device__ __forceinline__ void slice2(bool RD, const uint8_t* rs, int rsl, bool dma) {
+    __device__ __forceinline__ void slice2(bool RD, const uint8_t* rs, int rsl, int p0, int np) {
         constexpr int N = (1 - C) % NB;
         acc[0][0] = P::mma(fb[C][0], fa[0], acc[0][0]);
         G2_SB();
@@ -241,18 +267,20 @@ struct G256 {
         acc[0][1] = P::mma(fb[C][1], fa[0], acc[0][1]);
         G2_SB();
         if (RD) rd_a(rs, rsl, 0);
-        if (dma) { issue_part(0); issue_part(1); }
+        dma_at(0, p0, np);
+        dma_at(1, p0, np);
         G2_SB();
         acc[1][0] = P::mma(fb[C][0], fa[1], acc[1][0]);
         G2_SB();
-        if (dma) { issue_part(2); issue_part(3); }
+        dma_at(2, p0, np);
+        dma_at(3, p0, np);
         G2_SB();
         acc[1][1] = P::mma(fb[C][1], fa[1], acc[1][1]);
         G2_SB();
         if (RD) rd_a(rs, rsl, 1);
         G2_SB();
     }
-    __device__ __forceinline__ void slice_j2(bool RD, const uint8_t* rs, int rsl, bool dma) {
+    __device__ __forceinline__ void slice_j2(bool RD, const uint8_t* rs, int rsl, int p0, int np) {
         acc[0][0] = P::mma(fb[0][0], fa[0], acc[0][0]);
         G2_SB();
         acc[1][0] = P::mma(fb[0][0], fa[1], acc[1][0]);
@@ -262,18 +290,20 @@ struct G256 {
         acc[0][1] = P::mma(fb[0][1], fa[0], acc[0][1]);
         G2_SB();
         if (RD) rd_a(rs, rsl, 0);
-        if (dma) { issue_part(0); issue_part(1); }
+        dma_at(0, p0, np);
+        dma_at(1, p0, np);
         G2_SB();
         acc[1][1] = P::mma(fb[0][1], fa[1], acc[1][1]);
         G2_SB();
         if (RD) { rd_a(rs, rsl, 1); rd_b(rs, rsl, 0, 1); }
-        if (dma) { issue_part(2); issue_part(3); }
+        dma_at(2, p0, np);
+        dma_at(3, p0, np);
         G2_SB();
     }
 
     // The single-buffer form (FP8): MFMAs j-major; B block 0 is reread after
     // the fourth MFMA, A block i and B block 1 after their last use.
-    __device__ __forceinline__ void slice_j(bool RD, const uint8_t* rs, int rsl, bool dma) {
+    __device__ __forceinline__ void slice_j(bool RD, const uint8_t* rs, int rsl, int p0, int np) {
         acc[0][0] = P::mma(fb[0][0], fa[0], acc[0][0]);
         G2_SB();
         acc[1][0] = P::mma(fb[0][0], fa[1], acc[1][0]);
@@ -287,22 +317,22 @@ struct G256 {
         acc[0][1] = P::mma(fb[0][1], fa[0], acc[0][1]);
         G2_SB();
         if (RD) rd_a(rs, rsl, 0);
-        if (dma) issue_part(0);
+        dma_at(0, p0, np);
         G2_SB();
         acc[1][1] = P::mma(fb[0][1], fa[1], acc[1][1]);
         G2_SB();
         if (RD) rd_a(rs, rsl, 1);
-        if (dma) issue_part(1);
+        dma_at(1, p0, np);
         G2_SB();
         acc[2][1] = P::mma(fb[0][1], fa[2], acc[2][1]);
         G2_SB();
         if (RD) rd_a(rs, rsl, 2);
-        if (dma) issue_part(2);
+        dma_at(2, p0, np);
         G2_SB();
         acc[3][1] = P::mma(fb[0][1], fa[3], acc[3][1]);
         G2_SB();
         if (RD) { rd_a(rs, rsl, 3); rd_b(rs, rsl, 0, 1); }
-        if (dma) issue_part(3);
+        dma_at(3, p0, np);
         G2_SB();
     }
 
@@ -317,8 +347,8 @@ struct G256 {
         const uint8_t* st = smem + (cs & 1) * GE::STAGE;
 #pragma unroll
         for (int h = 0; h + 1 < NSL; h += 2) {
-            slice<0, true>(st, h + 1, false);
-            if (h + 2 < NSL) slice<1, true>(st, h + 2, false);
+            slice<0, true>(st, h + 1, dma_first(h + 1), dma_count(h + 1));
+            if (h + 2 < NSL) slice<1, true>(st, h + 2, dma_first(h + 2), dma_count(h + 2));
         }
         if (!LAST) {
             G2_SB();
@@ -327,9 +357,11 @@ struct G256 {
             asm volatile("" ::: "memory");
             __builtin_amdgcn_s_barrier();             // barrier cs+1: stage cs+1 landed, stage cs read
             asm volatile("" ::: "memory");
-            slice<1, true>(smem + ((cs + 1) & 1) * GE::STAGE, 0, dma2);
+            dmaon = dma2;
+            slice<1, true>(smem + ((cs + 1) & 1) * GE::STAGE, 0, dma_first(0), dma_count(0));
         } else {
-            slice<1, false>(st, 0, false);
+            slice<1, false>(st, 0, 0, 0);
+            dmaon = false;
         }
     }
 
@@ -467,6 +499,7 @@ struct G256 {
     // reads of stage cs-1), then stage cs+1 into the buffer stage cs-1 used, then
     // slice 0 of stage cs.
     __device__ __forceinline__ void enter(int cs) {
+        dmaon = false;
         WAITCNT_LGKM0();
         asm volatile("" ::: "memory");
         __builtin_amdgcn_s_barrier();
@@ -489,6 +522,7 @@ struct G256 {
         iss = 0;
         itile = -1;
         ikt = nk;
+        dmaon = false;
         issue_stage();                                // stage 0 -> buffer 0
         if (total > 1) {
             issue_stage();                            // stage 1 -> buffer 1
