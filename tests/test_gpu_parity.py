@@ -484,7 +484,7 @@ def test_route_matches_oracle(ee, orc, R):
     assert np.array_equal(host(counts), c_ref)
 
 
-@pytest.mark.parametrize("B,Hh,S", [(8, 32, 512), (2, 4, 64), (3, 1, 100), (1, 5, 7)])
+@pytest.mark.parametrize("B,Hh,S", [(8, 32, 512), (2, 4, 64), (3, 1, 100), (1, 5, 7), (3, 40, 2001)])
 def test_route_heads_matches_oracle(ee, orc, B, Hh, S):
     """Routing on the per-token mean over heads: the oracle's route() applied to
     the f32 mean summed in head order then divided (the kernel's arithmetic)."""

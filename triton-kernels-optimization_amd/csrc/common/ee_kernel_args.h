@@ -103,7 +103,7 @@ struct EeRouteArgs {
     int64_t rows;
     double tau_low;
     double tau_high;
-    int32_t heads;          // 1: h is per row
+    int32_t heads;          // 1: h is per row; 0 (eek_route): tier[] already holds the tiers
     int32_t seq;
 };
 

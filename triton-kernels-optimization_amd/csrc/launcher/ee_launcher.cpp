@@ -765,6 +765,13 @@ EE_EXPORT int ee_route_heads(ee_engine* eng, const float* h, int32_t B, int32_t 
     if (!aligned(h, 4) || !aligned(tier, 4) || !aligned(idx, 4) || !aligned(counts, 4))
         return fail(EE_ERR_INVALID_ARG, "misaligned pointer");
     EeRouteArgs a{h, tier, idx, counts, (int64_t)B * S, tau_low, tau_high, heads, S > 0 ? S : 1};
+    if (heads == 1) return launch(eng, "eek_route", 1, 1, 1024, a, stream);
+    // the per-row head means and tiers over the whole grid, then the partition
+    if (a.rows > 0) {
+        const int rc = launch(eng, "eek_route_heads_tier", cdiv(a.rows, EE_BLOCK), 1, EE_BLOCK, a, stream);
+        if (rc != EE_OK) return rc;
+    }
+    a.heads = 0;
     return launch(eng, "eek_route", 1, 1, 1024, a, stream);
 }
 
