@@ -105,7 +105,10 @@ def time_steps(fn, steps: int, warmup: int, use_graph: bool, stream, repeats: in
     `warmup` launches, then more until `fn` has kept the GPU busy for `warm_s`
     seconds: after the host-side setup between legs the GPU has idled, and it
     takes ~0.1 s of load to reach its steady clock (the C0 INT8 GEMM measured
-    24.8, 23.0, then 22.2 us in three back-to-back timings straight after idle)."""
+    24.8, 23.0, then 22.2 us in three back-to-back timings straight after idle).
+    A captured graph is likewise replayed for `warm_s` before the timed
+    replays: the first replays of the run's first graph ran the C0 INT8 GEMM
+    at ~25.5 us per launch against 22 us eager, the same after the warm-up."""
     import torch
     t0 = time.perf_counter()
     for _ in range(warmup):
@@ -122,8 +125,12 @@ def time_steps(fn, steps: int, warmup: int, use_graph: bool, stream, repeats: in
             with torch.cuda.graph(graph, stream=stream):
                 for _ in range(steps):
                     fn()
-            graph.replay()                      # untimed replay
-            torch.cuda.synchronize()
+            t1 = time.perf_counter()            # untimed replays, for warm_s as well
+            while True:
+                graph.replay()
+                torch.cuda.synchronize()
+                if time.perf_counter() - t1 >= warm_s:
+                    break
         except Exception as e:                  # capture unsupported -> eager only
             print(f"# graph capture failed ({type(e).__name__}: {e}); timing eager launches", file=sys.stderr)
             graph = None
