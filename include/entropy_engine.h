@@ -242,9 +242,11 @@ int ee_add_rmsnorm(ee_engine* eng, const void* x, int64_t ld_x, const void* y, i
  * [0, counts[0]) and FP8 slots [counts[0], counts[0] + counts[1]) gets its
  * codes in codes + i * ld_c (D bytes) and its scale in scale[i] -- the bits
  * ee_routed_linear's quantiser would write from n_out (the quantisers of
- * EE/python/kernels.py:336-338 and :361).  FP16 slots get n_out only.  x_out
- * and n_out are written for every row, as by ee_add_rmsnorm.  With
- * ee_routed_gemm this removes the quantiser's launch and its read of n_out.
+ * EE/python/kernels.py:336-338 and :361).  FP16 slots get n_out only: the
+ * INT8 and FP8 slots' rows of n_out are left unwritten (their normalised
+ * values reach the GEMM as those codes).  x_out is written for every row, as
+ * by ee_add_rmsnorm.  With ee_routed_gemm this removes the quantiser's launch,
+ * its read of n_out, and the write of n_out for the quantised rows.
  * No reference counterpart: the reference quantises inside each GEMM wrapper
  * (EE/python/kernels.py:336-338, 361).  ld_c % 8 == 0, codes 8-byte aligned. */
 int ee_add_rmsnorm_route(ee_engine* eng, const void* x, int64_t ld_x, const void* y, int64_t ld_y, const void* w,

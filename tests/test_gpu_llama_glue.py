@@ -252,10 +252,11 @@ def _partition(ee, T, tl, th, seed):
 @pytest.mark.parametrize("T,D,tl,th", [(4096, 2048, 2.34, 6.03), (300, 256, 2.34, 6.03), (77, 4096, 2.0, 4.0),
                                        (64, 2048, 9.0, 9.0), (64, 2048, -1.0, 9.0), (64, 512, -1.0, -1.0)])
 def test_add_rmsnorm_route_equals_norm_then_quantiser(ee, T, D, tl, th):
-    """The slot-ordered norm writes add_rmsnorm's s and n bit for bit, and for
-    the INT8 / FP8 slots the codes and scales the routed quantisers write from
-    n (dispatcher INT8 for slots [0, c0), row-scaled e4m3 for the next c1).
-    Includes an all-zero row (zero scale: the slow conversion paths)."""
+    """The slot-ordered norm writes add_rmsnorm's s bit for bit, its n for the
+    FP16 slots' rows (and no other row of n), and for the INT8 / FP8 slots the
+    codes and scales the routed quantisers write from n (dispatcher INT8 for
+    slots [0, c0), row-scaled e4m3 for the next c1).  Includes an all-zero row
+    (zero scale: the slow conversion paths)."""
     g = torch.Generator(device="cuda").manual_seed(T + D)
     x = torch.randn(T, D, device="cuda", generator=g).half() * 3
     y = torch.randn(T, D, device="cuda", generator=g).half()
@@ -264,9 +265,15 @@ def test_add_rmsnorm_route_equals_norm_then_quantiser(ee, T, D, tl, th):
     w = (1 + 0.1 * torch.randn(D, device="cuda", generator=g)).half()
     idx, counts = _partition(ee, T, tl, th, T)
     s_ref, n_ref = ee.add_rmsnorm(x, w, 1e-5, y)
-    s, n, codes, scale = ee.add_rmsnorm_route(x, w, 1e-5, y, idx, counts)
-    assert torch.equal(s, s_ref) and torch.equal(n.view(torch.int16), n_ref.view(torch.int16))
     c0, c1, _ = counts.tolist()
+    n_out = torch.full((T, D), -7.0, dtype=torch.float16, device="cuda")
+    s, n, codes, scale = ee.add_rmsnorm_route(x, w, 1e-5, y, idx, counts, n_out=n_out)
+    assert n.data_ptr() == n_out.data_ptr()
+    fp16_rows = idx[c0 + c1:].long()
+    quant_rows = idx[:c0 + c1].long()
+    assert torch.equal(s, s_ref)
+    assert torch.equal(n[fp16_rows].view(torch.int16), n_ref[fp16_rows].view(torch.int16))
+    assert bool((n[quant_rows] == -7.0).all())
     q8, s8 = ee.quantize_activations(n_ref, "dispatcher", idx, counts, tier=0)
     qf, sf = ee.quantize_activations(n_ref, "fp8", idx, counts, tier=1)
     assert torch.equal(codes[:c0], q8[:c0].view(torch.uint8))
@@ -279,8 +286,9 @@ def test_add_rmsnorm_route_equals_norm_then_quantiser(ee, T, D, tl, th):
 @pytest.mark.parametrize("T,tl,th", [(1000, 2.34, 6.03), (4096, 2.34, 6.03), (300, 9.0, 9.0), (300, -1.0, 9.0),
                                      (300, -1.0, -1.0)])
 def test_routed_gemm_on_prepared_codes(ee, T, tl, th, swiglu):
-    """routed_linear on the codes of add_rmsnorm_route (one GEMM launch) equals
-    routed_linear with its own quantiser, bit for bit; mixed and single-tier
+    """routed_linear on the codes of add_rmsnorm_route (one GEMM launch; it reads
+    only the FP16 slots' rows of the route's n) equals routed_linear with its
+    own quantiser on add_rmsnorm's n, bit for bit; mixed and single-tier
     partitions (all INT8, all FP8, all FP16)."""
     D, N = 512, 768
     g = torch.Generator(device="cuda").manual_seed(T)
@@ -293,8 +301,9 @@ def test_routed_gemm_on_prepared_codes(ee, T, tl, th, swiglu):
         codes_w, scale_w = ee.interleave_gate_up(codes_w), ee.interleave_gate_up(scale_w)
     pw = ee.PackedWeight(codes_w, scale_w).materialize()
     idx, counts = _partition(ee, T, tl, th, T + 1)
+    _, n_ref = ee.add_rmsnorm(x, w, 1e-5, y)
     _, n, codes, scale = ee.add_rmsnorm_route(x, w, 1e-5, y, idx, counts)
-    ref = ee.routed_linear(n, pw, idx, counts, swiglu=swiglu)
+    ref = ee.routed_linear(n_ref, pw, idx, counts, swiglu=swiglu)
     got = ee.routed_linear(n, pw, idx, counts, swiglu=swiglu, quantized=(codes, scale))
     assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
 

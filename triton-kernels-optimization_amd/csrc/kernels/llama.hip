@@ -20,7 +20,7 @@
 // The mean's f32 sum runs in a different order than torch's reduction, so a
 // row can differ from torch in the last bit of its mean.
 template <int NC>
-EE_DEV void rmsnorm_row(const EeRmsNormArgs& a, int64_t row, int lane, u32x4 (&o)[NC]) {
+EE_DEV void rmsnorm_row(const EeRmsNormArgs& a, int64_t row, int lane, u32x4 (&o)[NC], bool store_n = true) {
     const int nc = (int)(a.D >> 3);                   // 16-byte chunks per row
     const uint16_t* xr = a.x + row * a.ld_x;
     u32x4 s[NC];
@@ -57,7 +57,7 @@ EE_DEV void rmsnorm_row(const EeRmsNormArgs& a, int64_t row, int lane, u32x4 (&o
                 const float n0 = f16_round(f16_lo(s[i][j]) * r), n1 = f16_round(f16_hi(s[i][j]) * r);
                 o[i][j] = pack_f16x2(f16_lo(w[j]) * n0, f16_hi(w[j]) * n1);
             }
-            *(u32x4*)(a.n_out + row * a.ld_n + 8 * c) = o[i];
+            if (store_n) *(u32x4*)(a.n_out + row * a.ld_n + 8 * c) = o[i];
         }
     }
 }
@@ -76,6 +76,7 @@ EE_DEV void add_rmsnorm(const EeRmsNormArgs& a) {
 // FP8 slots into slot i of the routed linear's workspace: the codes and scales
 // the routed quantiser (quant.hip, EE_QUANT_ROUTED_I8_F8) would write from
 // n_out, with the same arithmetic (ee_quant_dev.h), without reading n_out back.
+// n_out receives the FP16 slots' rows only, the ones the routed GEMM reads.
 template <int NC>
 EE_DEV void add_rmsnorm_route(const EeRmsNormRouteArgs& ra) {
     const EeRmsNormArgs& a = ra.n;
@@ -83,9 +84,9 @@ EE_DEV void add_rmsnorm_route(const EeRmsNormRouteArgs& ra) {
     const int64_t slot = (int64_t)blockIdx.x * (EE_BLOCK / 64) + wave_id();
     if (slot >= a.T) return;
     const int64_t row = ra.idx[slot];
-    u32x4 o[NC];
-    rmsnorm_row<NC>(a, row, lane, o);
     const int64_t c0 = ra.counts[0], c01 = c0 + ra.counts[1];
+    u32x4 o[NC];
+    rmsnorm_row<NC>(a, row, lane, o, slot >= c01);
     if (slot >= c01) return;                          // FP16 slot: the GEMM reads n_out
     const int mode = slot < c0 ? EE_QUANT_I8_DISPATCH : EE_QUANT_F8_ROW;
     const int nc = (int)(a.D >> 3);

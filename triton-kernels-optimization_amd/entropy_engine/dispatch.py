@@ -511,9 +511,11 @@ class EntropyGatedLlama:
 
     def _norm(self, x, w, res, route, gated: bool):
         """(x, xn, quantized): the residual add + RMSNorm; when the next linear is
-        routed (and K % 128 == 0), the same kernel writes its INT8/FP8 operands."""
+        routed (and K % 128 == 0), the same kernel writes its INT8/FP8 operands,
+        and xn then holds only the FP16 rows (a linear probe gets every row: the
+        separate norm and quantiser, which give the same bits)."""
         if (gated and route is not None and self.fused_norm_quant and self.linear_impl is None
-                and x.shape[-1] % 128 == 0):
+                and self.linear_probe is None and x.shape[-1] % 128 == 0):
             idx, counts = route
             x, xn, codes, scale = K.add_rmsnorm_route(x, w, self.cfg["eps"], res, idx, counts)
             return x, xn, (codes, scale)

@@ -481,16 +481,22 @@ def add_rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float, y: torch.Tensor | 
 
 
 def add_rmsnorm_route(x: torch.Tensor, w: torch.Tensor, eps: float, y: torch.Tensor | None,
-                      idx: torch.Tensor, counts: torch.Tensor):
-    """(s, n, codes, scale): add_rmsnorm's s and n, plus the routed linear's INT8
+                      idx: torch.Tensor, counts: torch.Tensor, n_out: torch.Tensor | None = None):
+    """(s, n, codes, scale): add_rmsnorm's s, plus the routed linear's INT8
     and FP8 operands of the rows of the partition idx/counts (from route or
     route_heads): codes uint8 [T, D] and scale f32 [T] in slot order, the bits
-    routed_linear's quantiser writes from n.  Pass (codes, scale) to
+    routed_linear's quantiser writes from add_rmsnorm's n.  n holds add_rmsnorm's
+    rows for the FP16 slots only (the others are not written; n_out, fp16 [T, D]
+    contiguous, receives them when given).  Pass (codes, scale) to
     routed_linear(..., quantized=...) to skip that quantiser."""
-    dev = _require_cuda(x, w, y, idx, counts)
+    dev = _require_cuda(x, w, y, idx, counts, n_out)
     x2, y2, s, n, w, T, D = _rmsnorm_operands(x, w, y)
     if idx.dtype != torch.int32 or counts.dtype != torch.int32 or idx.numel() != T:
         raise ValueError("idx must be int32 [T] and counts int32 [3] (from route)")
+    if n_out is not None:
+        if n_out.dtype != torch.float16 or tuple(n_out.shape) != (T, D) or not n_out.is_contiguous():
+            raise ValueError("n_out must be a contiguous float16 [T, D] tensor")
+        n = n_out
     codes = torch.empty((T, D), dtype=torch.uint8, device=dev)
     scale = torch.empty(T, dtype=torch.float32, device=dev)
     with torch.cuda.device(dev):
