@@ -167,6 +167,45 @@ def test_gemm256_swiglu(ee, orc, M, K, F, grid, tn):
         assert torch.equal(fused.view(torch.int16), ref.view(torch.int16)), kind
 
 
+def _sweep_cases(n=24, seed=2024):
+    """Seeded shapes and forced grids: ragged M and N, K of 1-12 stages, grids of
+    1-37 workgroups (multiples of 8 and not), so that rounds end full, half full
+    (256 x 128 halves) or otherwise."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(n):
+        M = int(rng.integers(1, 1300))
+        N = int(rng.integers(1, 700)) * 4
+        K = int(rng.integers(1, 13)) * 128
+        grid = int(rng.choice([1, 2, 3, 5, 7, 8, 13, 16, 24, 37]))
+        out.append((M, K, N, grid))
+    return out
+
+
+@pytest.mark.parametrize("M,K,N,grid", _sweep_cases())
+def test_gemm256_seeded_sweep(ee, orc, M, K, N, grid):
+    """256 x 256-tile kernels on seeded shapes and grids: INT8 int32 accumulators
+    equal the oracle's; INT8, FP8 and FP16 outputs equal the 128-tile kernels'
+    bit for bit."""
+    A, B, bs, pw = _operands(ee, orc, M, K, N, M * 31 + K + N + grid)
+    codes, a_s = orc.quant_act_i8(A, "dispatcher")
+    c8, s8 = orc.quant_act_f8(A)
+    acc = torch.empty((M, N), dtype=torch.int32, device="cuda")
+    with _Options(gemm_tile=256, gemm_persist=grid):
+        ee.gemm("int8", cuda(codes), pw.i8, cuda(a_s), cuda(bs), acc_out=acc)
+        o_i8 = host(ee.gemm("int8", cuda(codes), pw.i8, cuda(a_s), cuda(bs)))
+        o_f8 = host(ee.gemm("fp8", cuda(c8), pw.f8, cuda(s8), cuda(bs)))
+        o_f16 = host(ee.gemm("fp16", cuda(A), pw.f16))
+    assert np.array_equal(host(acc), orc.gemm_i8_acc(codes, B))
+    with _Options(gemm_tile=128, gemm_variant=1):
+        r_i8 = host(ee.gemm("int8", cuda(codes), pw.i8, cuda(a_s), cuda(bs)))
+        r_f8 = host(ee.gemm("fp8", cuda(c8), pw.f8, cuda(s8), cuda(bs)))
+        r_f16 = host(ee.gemm("fp16", cuda(A), pw.f16))
+    assert np.array_equal(o_i8.view(np.uint16), r_i8.view(np.uint16))
+    assert np.array_equal(o_f8.view(np.uint16), r_f8.view(np.uint16))
+    assert np.array_equal(o_f16.view(np.uint16), r_f16.view(np.uint16))
+
+
 def test_gemm256_option_rejects_bad_value(ee):
     from entropy_engine import _lib
     assert _lib.lib().ee_engine_set_option(_lib.engine(), b"gemm_tile", 192) == _lib.EE_ERR_INVALID_ARG
