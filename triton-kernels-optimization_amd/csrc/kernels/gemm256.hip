@@ -28,7 +28,8 @@
 // Barrier s+1 sits before the MFMAs of stage s's last K slice: by then every
 // wave has read stage s (lgkmcnt 0) and waited for its part of stage s+1
 // (vmcnt 0), so stage s+2 is issued into stage s's buffer right after it,
-// while the last slice's MFMAs run and slice 0 of stage s+1 is read.
+// while the last slice's MFMAs run and slice 0 of stage s+1 is read (FP16:
+// half of it there, half during the next slice).
 //
 // Persistent grid: one workgroup per CU walks its tiles (TileDeal: 8 x 4
 // blocks of tiles per XCD per round); the stage sequence and the ring run on
@@ -339,9 +340,10 @@ struct G256 {
     // Stage cs: slices 0 .. NSL-1 from buffer cs & 1; the stage starts with its
     // slice-0 fragments in fa / fb[0] (NSL is even).  Not the tile's last stage
     // (LAST = false): before the last slice's MFMAs, barrier cs+1, slice 0 of
-    // stage cs+1 is read and stage cs+2 is issued into this stage's buffer (when
-    // dma2).  The tile's last stage reads nothing for the next one: the
-    // epilogue and the tile change do that (run()).
+    // stage cs+1 is read and stage cs+2 starts into this stage's buffer (when
+    // dma2; its parts go out over the slices dma_count gives).  The tile's last
+    // stage reads nothing for the next one: the epilogue and the tile change do
+    // that (run()).
     template <bool LAST>
     __device__ __forceinline__ void stage(int cs, bool dma2) {
         const uint8_t* st = smem + (cs & 1) * GE::STAGE;
