@@ -552,3 +552,50 @@ def attention_causal(q: torch.Tensor, k: torch.Tensor, vt: torch.Tensor, out: to
         check(_lib.lib().ee_attention_causal(engine(), ptr(q), ptr(k), ptr(vt), ptr(out), ld_out, ptr(h), B, S, Hq,
                                              Hkv, d, stream_handle()))
     return out, h
+
+
+# ---------------------------------------------------------------- hardware probes
+
+PROBE_KINDS = {"stream": 0, "lds": 1, "mfma_i8": 2, "mfma_f8": 3, "stream_own": 4}
+_PROBE_ITERS = {"stream": 2048, "lds": 4096, "mfma_i8": 4096, "mfma_f8": 2048, "stream_own": 256}
+_PROBE_UNITS = {"stream": "bytes/clock/CU", "lds": "bytes/clock/CU", "mfma_i8": "clocks/MFMA",
+                "mfma_f8": "clocks/MFMA", "stream_own": "bytes/clock/CU"}
+
+
+def probe(kind: str, iters: int | None = None, grid: int | None = None, window: int | None = None) -> dict:
+    """One hardware rate of the current GPU, measured by probe.hip (ee_probe):
+    "stream" -- direct-to-LDS load bytes per clock per CU from L2-resident data
+    (each XCD's workgroups share one `window`-byte window); "stream_own" -- the
+    same with a window per workgroup (default 8 MiB: nothing shared, so the
+    stream comes from the MALL or HBM); "lds" -- ds_read_b128
+    bytes per clock per CU; "mfma_i8" / "mfma_f8" -- clocks per 32x32 MFMA per
+    SIMD with two waves on it.  One workgroup of 512 threads per CU by default.
+    Returns the median over workgroups of the rate and of the shader clock (MHz,
+    s_memtime against the 100 MHz s_memrealtime), after one untimed launch."""
+    if kind not in PROBE_KINDS:
+        raise ValueError(f"probe kind must be one of {sorted(PROBE_KINDS)}")
+    dev = torch.device("cuda", torch.cuda.current_device())
+    k = PROBE_KINDS[kind]
+    grid = grid or torch.cuda.get_device_properties(dev).multi_processor_count
+    iters = iters or _PROBE_ITERS[kind]
+    window = window or (8 << 20 if kind == "stream_own" else 1 << 19)
+    nwin = grid if kind == "stream_own" else 8
+    src = torch.ones(nwin * window, dtype=torch.uint8, device=dev) if kind.startswith("stream") else None
+    times = torch.zeros(grid * 4, dtype=torch.int64, device=dev)
+    sink = torch.empty(grid * 512, dtype=torch.int32, device=dev)
+    with torch.cuda.device(dev):
+        for _ in range(2):                       # the first launch warms L2 and the clock
+            check(_lib.lib().ee_probe(engine(), k, ptr(src), window, iters, grid, ptr(times), ptr(sink),
+                                      stream_handle()))
+        torch.cuda.synchronize()
+    t = times.view(grid, 4).cpu().double()
+    clk = t[:, 1] - t[:, 0]
+    us = (t[:, 3] - t[:, 2]) / 100.0
+    if kind.startswith("stream"):
+        rate = iters * 32768.0 / clk
+    elif kind == "lds":
+        rate = 512 * 16 * 8.0 * iters / clk
+    else:
+        rate = clk / (iters * 4 * 2.0)
+    return {"kind": kind, "value": round(float(rate.median()), 2), "unit": _PROBE_UNITS[kind],
+            "sclk_mhz": round(float((clk / us).median()), 0), "grid": grid, "iters": iters}
