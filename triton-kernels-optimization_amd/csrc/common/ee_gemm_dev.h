@@ -1,6 +1,6 @@
 // ee_gemm_dev.h -- building blocks shared by the MFMA GEMM kernels (gfx950):
 // the swizzled 128-byte LDS rows, the direct-to-LDS DMA and its waits, the
-// 32x32 MFMA shapes of the three tiers, the dequantising arithmetic of the
+// MFMA shapes of the three tiers, the dequantising arithmetic of the
 // epilogues and the XCD-aware deal of tiles to persistent workgroups.
 #pragma once
 #include <type_traits>
@@ -47,11 +47,23 @@ EE_DEV void dma16s(const uint8_t* sbase, uint32_t voff, uint32_t lds_base) {
 #define WAITCNT_LGKM0() __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14))
 
 // ---------------------------------------------------------------------------
-// Pipelined kernel: 32x32 MFMA blocks (the full-rate shapes on gfx950:
-// i8 32x32x32 and f16 32x32x16 run at twice the rate of their 16x16 forms),
-// K stages split into slices of one MFMA depth, fragments of slice s+1 read
-// from LDS while the MFMAs of slice s run.
+// Pipelined kernels: 32x32 blocks of C, K stages split into slices of one
+// MFMA depth, fragments of slice s+1 read from LDS while the MFMAs of slice s
+// run.  A block is one 32x32 MFMA per slice, or four 16x16 ones (PipeI8x16).
 template <int KIND> struct Pipe;
+// Where a lane's accumulators sit in its 32x32 block: registers 4q .. 4q+3 hold
+// rows (A side, m) row_of(q, l) and columns (B side, n) col_of(q, l) .. +3.
+// A lane's quarters span NRQ distinct rows (quarter q: the rq(q)-th) and NCQ
+// distinct column groups (the cq(q)-th), which size the epilogue's scales.
+// 32x32 MFMAs: every register of lane l is row l & 31; columns 8q + 4 (l >> 5).
+struct Lay32 {
+    static constexpr bool SUB16 = false;
+    static constexpr int NRQ = 1, NCQ = 4;
+    static EE_DEV int rq(int) { return 0; }
+    static EE_DEV int cq(int q) { return q; }
+    static EE_DEV int row_of(int, int lane) { return lane & 31; }
+    static EE_DEV int col_of(int q, int lane) { return 8 * q + 4 * (lane >> 5); }
+};
 // INT8 slices are 64 K bytes deep by default, as FP8's: two 32x32x32 i8 MFMAs
 // per block, on the first and second 16 bytes of each lane's 32 (lanes 0-31
 // hold K bytes 0-31 of the slice, lanes 32-63 bytes 32-63; A and B fragments
@@ -61,7 +73,7 @@ template <int KIND> struct Pipe;
 // whose registers the 32-byte fragments would overflow.
 // Fragment chunks: lane l reads 16-byte chunk sl * SB/16 + (l >> 5) * LSTEP of its
 // row and, when CPF == 2, the chunk CSTEP after it.
-struct PipeI8x32 {                               // 32x32x32 i8: 32 K bytes per slice, 16 B per lane
+struct PipeI8x32 : Lay32 {                       // 32x32x32 i8: 32 K bytes per slice, 16 B per lane
     static constexpr int SB = 32, CPF = 1, LSTEP = 1, CSTEP = 0;
     typedef u32x4 frag_t;
     typedef i32x16 acc_t;
@@ -69,7 +81,7 @@ struct PipeI8x32 {                               // 32x32x32 i8: 32 K bytes per 
         return __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(i32x4, b), __builtin_bit_cast(i32x4, a), c, 0, 0, 0);
     }
 };
-struct PipeI8x64 {                               // 2 x 32x32x32 i8: 64 K bytes per slice, 32 B per lane
+struct PipeI8x64 : Lay32 {                       // 2 x 32x32x32 i8: 64 K bytes per slice, 32 B per lane
     static constexpr int SB = 64, CPF = 2, LSTEP = 2, CSTEP = 1;
     typedef i32x8 frag_t;
     typedef i32x16 acc_t;
@@ -81,7 +93,43 @@ struct PipeI8x64 {                               // 2 x 32x32x32 i8: 64 K bytes 
     }
 };
 template <> struct Pipe<EE_GEMM_I8> : PipeI8x64 {};
-struct PipeF16x32 {                              // 32x32x16 f16: 32 K bytes per slice, 16 B per lane
+// INT8 as 16x16x64 i8 MFMAs: per 64-byte slice a 32x32 block is four of them
+// (the same MFMA time as two 32x32x32).  Fragment half h (registers 4h .. 4h+3)
+// holds rows 16h + (l & 15) of the block, K bytes 16 (l >> 4) .. +15 of the
+// slice, for A and B alike; accumulator quarter q is the 16 x 16 sub-block of
+// A half q & 1 and B half q >> 1, lane l holding its row l & 15 and columns
+// 4 (l >> 4) .. +3.  Measured on MI355X (a sustained MFMA + fragment-read
+// loop, identical rates in clocks): the 16x16 forms run at a 9-13% higher
+// shader clock under the power limit than the 32x32 forms of the same work.
+// The four quarters of one block's accumulators; element e is register e & 3 of quarter e >> 2.
+struct I32x4x4 {
+    i32x4 q[4];
+    __device__ __forceinline__ int32_t operator[](int e) const { return q[e >> 2][e & 3]; }
+};
+// The two 16-row halves of one fragment.
+struct I32x4x2 {
+    i32x4 h[2];
+};
+struct PipeI8x16 {
+    static constexpr int SB = 64, CPF = 2, LSTEP = 0, CSTEP = 0;
+    static constexpr bool SUB16 = true;
+    typedef I32x4x2 frag_t;
+    typedef I32x4x4 acc_t;
+    static EE_DEV acc_t mma(const frag_t& b, const frag_t& a, const acc_t& c) {
+        acc_t r;
+        r.q[0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(b.h[0], a.h[0], c.q[0], 0, 0, 0);
+        r.q[1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(b.h[0], a.h[1], c.q[1], 0, 0, 0);
+        r.q[2] = __builtin_amdgcn_mfma_i32_16x16x64_i8(b.h[1], a.h[0], c.q[2], 0, 0, 0);
+        r.q[3] = __builtin_amdgcn_mfma_i32_16x16x64_i8(b.h[1], a.h[1], c.q[3], 0, 0, 0);
+        return r;
+    }
+    static constexpr int NRQ = 2, NCQ = 2;
+    static EE_DEV int rq(int q) { return q & 1; }
+    static EE_DEV int cq(int q) { return q >> 1; }
+    static EE_DEV int row_of(int q, int lane) { return (q & 1) * 16 + (lane & 15); }
+    static EE_DEV int col_of(int q, int lane) { return (q >> 1) * 16 + 4 * (lane >> 4); }
+};
+struct PipeF16x32 : Lay32 {                      // 32x32x16 f16: 32 K bytes per slice, 16 B per lane
     static constexpr int SB = 32, CPF = 1, LSTEP = 1, CSTEP = 0;
     typedef u32x4 frag_t;
     typedef f32x16 acc_t;
@@ -90,7 +138,7 @@ struct PipeF16x32 {                              // 32x32x16 f16: 32 K bytes per
     }
 };
 template <> struct Pipe<EE_GEMM_F16> : PipeF16x32 {};
-template <> struct Pipe<EE_GEMM_F8> {            // 32x32x64 e4m3: 64 K bytes per slice, 32 B per lane
+template <> struct Pipe<EE_GEMM_F8> : Lay32 {    // 32x32x64 e4m3: 64 K bytes per slice, 32 B per lane
     static constexpr int SB = 64, CPF = 2, LSTEP = 2, CSTEP = 1;
     typedef i32x8 frag_t;
     typedef f32x16 acc_t;

@@ -1,7 +1,9 @@
 // gemm256.hip -- persistent 256 x 256-tile MFMA GEMMs of the three precision
 // tiers for gfx950 (the large-M shapes: configs 1-4).
 //
-//   EE_GEMM_I8 : int8 x int8 -> int32 (v_mfma_i32_32x32x32_i8);
+//   EE_GEMM_I8 : int8 x int8 -> int32 (v_mfma_i32_16x16x64_i8, four per 32x32 block
+//                and 64-byte K slice: the same MFMA time as the 32x32x32 form at a
+//                lower power draw; SwiGLU keeps 32x32x32 on 32-byte slices);
 //                C = fp16((f32(acc) * a_scale[m]) * b_scale[n])     (EE/python/kernels.py:50-110)
 //   EE_GEMM_F8 : e4m3 x e4m3 -> f32 (v_mfma_scale_f32_32x32x64_f8f6f4);
 //                C = fp16((acc * a_scale[m]) * b_scale[n])           (EE/python/kernels.py:118-180)
@@ -62,8 +64,9 @@ template <int KIND, int SW, class Seq, int TN = 256>
 struct G256 {
     typedef G2Geom<TN> GE;
     static constexpr int NI = GE::NI, WR = GE::WR;
-    // (the SwiGLU epilogue's registers leave no room for INT8's 64-byte slices)
-    typedef std::conditional_t<KIND == EE_GEMM_I8 && SW, PipeI8x32, Pipe<KIND>> P;
+    // INT8: 16x16x64 MFMAs (PipeI8x16), or 32-byte 32x32x32 slices for SwiGLU,
+    // whose epilogue registers leave no room for 64-byte slices
+    typedef std::conditional_t<KIND == EE_GEMM_I8, std::conditional_t<SW != 0, PipeI8x32, PipeI8x16>, Pipe<KIND>> P;
     typedef typename P::acc_t acc_t;
     typedef typename P::frag_t frag_t;
     static constexpr int ESZ = (KIND == EE_GEMM_F16) ? 2 : 1;
@@ -111,6 +114,7 @@ struct G256 {
     // (its slices run j-major, so each B block is also dead before its reload)
     static constexpr int NB = (P::CPF == 2) ? 1 : 2;
     frag_t fa[NI], fb[NB][2];
+    uint32_t fo[2];                                   // SUB16: byte of row l & 15, chunk 4 sl + (l >> 4)
 
     __device__ __forceinline__ G256(const EeGemmArgs& g_, uint8_t* smem_, const Seq& seq_, int M_, int64_t off_)
         : g(g_), smem(smem_), seq(seq_), M(M_), off(off_) {}
@@ -133,6 +137,11 @@ struct G256 {
     __device__ __forceinline__ void dma_tile(int i) {
         int m0, n0;
         coords(i, m0, n0);
+        // SUB16: the lane index through an empty asm, so that the lane-dependent
+        // parts of the offsets are computed here rather than held across the K
+        // loop (the 16x16 form's registers have no room for them)
+        int lane = this->lane;
+        if constexpr (P::SUB16) asm volatile("" : "+v"(lane));
         constexpr bool routed = Seq::ROUTED;
         abase = (const uint8_t*)g.a + (routed ? 0 : (int64_t)m0 * g.lda * ESZ);
         bbase = (const uint8_t*)g.b + (int64_t)n0 * g.ldb * ESZ;
@@ -142,14 +151,28 @@ struct G256 {
             const int lchunk = (lane & 7) ^ swz(r);
             const int m = min(m0 + r, M - 1);
             const int64_t ar = !routed ? (int64_t)(m - m0) : Seq::GATHER ? (int64_t)g.a_idx[off + m] : off + m;
-            aoff[q] = (uint32_t)(ar * g.lda * ESZ + lchunk * 16);
+            if constexpr (P::SUB16) {
+                // the low 32 bits in 32-bit registers (the launcher checks that the
+                // offsets fit): a 64-bit multiply-add would hold register pairs
+                uint32_t pr = (uint32_t)ar * (uint32_t)(g.lda * ESZ);
+                asm volatile("" : "+v"(pr));
+                aoff[q] = pr + (uint32_t)(lchunk * 16);
+            } else {
+                aoff[q] = (uint32_t)(ar * g.lda * ESZ + lchunk * 16);
+            }
         }
 #pragma unroll
         for (int q = 0; q < GE::BG; ++q) {
             const int r = (wave * GE::BG + q) * 8 + (lane >> 3);
             const int lchunk = (lane & 7) ^ swz(r);   // swz(T2M + r) == swz(r)
             const int n = min(n0 + r, g.N - 1) - n0;
-            boff[q] = (uint32_t)(n * g.ldb * ESZ + lchunk * 16);
+            if constexpr (P::SUB16) {
+                uint32_t pr = (uint32_t)n * (uint32_t)(g.ldb * ESZ);
+                asm volatile("" : "+v"(pr));
+                boff[q] = pr + (uint32_t)(lchunk * 16);
+            } else {
+                boff[q] = (uint32_t)(n * g.ldb * ESZ + lchunk * 16);
+            }
         }
     }
     // Part p (0..3) of the next stage: A row group 4w+p and, for p < BG, B row group BG w + p.
@@ -186,11 +209,25 @@ struct G256 {
             f = i32x8{(int)x0[0], (int)x0[1], (int)x0[2], (int)x0[3], (int)x1[0], (int)x1[1], (int)x1[2], (int)x1[3]};
         }
     }
+    // 16x16x64 fragments (SUB16) of the 32-row block at row0 (a multiple of 16, so
+    // swz(row0 + x) == swz(x)): rows row0 + (l & 15) and row0 + 16 + (l & 15),
+    // chunk 4 sl + (l >> 4), at byte fo[sl] of the block's first row and 2 KB on.
+    __device__ __forceinline__ void rd16(const uint8_t* st, int sl, frag_t& f, int row0) const {
+        // (the offset through an empty asm: each read adds it to the block's base
+        // instead of the compiler holding a hoisted address per block and buffer)
+        uint32_t o = fo[sl];
+        asm volatile("" : "+v"(o));
+        const uint8_t* p = st + row0 * BKB + o;
+        f.h[0] = *(const i32x4*)p;
+        f.h[1] = *(const i32x4*)(p + 16 * BKB);
+    }
     __device__ __forceinline__ void rd_a(const uint8_t* st, int sl, int i) {
-        rd(st, sl, fa[i], wm * WR + i * 32 + (lane & 31));
+        if constexpr (P::SUB16) rd16(st, sl, fa[i], wm * WR + i * 32);
+        else rd(st, sl, fa[i], wm * WR + i * 32 + (lane & 31));
     }
     __device__ __forceinline__ void rd_b(const uint8_t* st, int sl, int buf, int j) {
-        rd(st, sl, fb[buf % NB][j], T2M + wn * 64 + j * 32 + (lane & 31));
+        if constexpr (P::SUB16) rd16(st, sl, fb[buf % NB][j], T2M + wn * 64 + j * 32);
+        else rd(st, sl, fb[buf % NB][j], T2M + wn * 64 + j * 32 + (lane & 31));
     }
     // all fragments of slice sl into fa and fb[buf]
     __device__ __forceinline__ void rd_all(const uint8_t* st, int sl, int buf) {
@@ -370,7 +407,7 @@ struct G256 {
     // Dequantise and store the tile (m0, n0) from acc through the wave's LDS
     // slot.  Scales are loaded first; the wait for them also covers this wave's
     // part of the next DMA stage (the one barrier cs+1 will publish).
-    __device__ __forceinline__ void epilogue(int m0, int n0) {
+    __device__ __forceinline__ void epilogue32(int m0, int n0) {
         const int N = g.N;
         // The lane index through an empty asm: the epilogue's addresses are then
         // computed here instead of being hoisted out of the tile loop, where they
@@ -490,6 +527,132 @@ struct G256 {
         }
     }
 
+    // epilogue32 for the 16x16 accumulator layout (SUB16): quarter q of block (i, j)
+    // holds rows row_of(q) and columns j * 32 + col_of(q) .. +3 of the block, whose
+    // scales are bs[j][cq(q)] and as[rq(q)].  Lane l loads the row scales of wave
+    // rows l and 64 + l (with the next stage's wait) and each block's lanes fetch
+    // theirs from the lanes holding them (ds_bpermute).
+    __device__ __forceinline__ void epilogue16(int m0, int n0) {
+        G2_SB();                                      // nothing of it moves up among the last MFMAs
+        const int N = g.N;
+        int lane = this->lane;                        // (not hoisted out of the tile loop)
+        asm volatile("" : "+v"(lane));
+        f32x4 bs[2][P::NCQ] = {};
+        float asv[WR / 64] = {};
+        if constexpr (KIND != EE_GEMM_F16) {
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int c = 0; c < P::NCQ; ++c) {      // column group c: quarters 2c, 2c + 1
+                    const int n = n0 + wn * 64 + j * 32 + P::col_of(2 * c, lane);
+                    bs[j][c] = (n < N) ? *(const f32x4*)(g.b_scale + n) : f32x4{0.f, 0.f, 0.f, 0.f};
+                }
+#pragma unroll
+            for (int h = 0; h < WR / 64; ++h) {
+                const int m = m0 + wm * WR + h * 64 + lane;
+                asv[h] = (m < M) ? g.a_scale[off + m] : 0.0f;
+            }
+        }
+        int32_t cr[WR / 64];                          // C rows, as in epilogue32
+        if constexpr (Seq::ROUTED) {
+#pragma unroll
+            for (int h = 0; h < WR / 64; ++h) {
+                const int m = m0 + wm * WR + h * 64 + lane;
+                cr[h] = (m < M) ? (g.c_idx ? g.c_idx[off + m] : m) : -1;
+            }
+        }
+        auto crow_of = [&](int r) -> int32_t {
+            if constexpr (Seq::ROUTED) {
+                return __builtin_amdgcn_ds_bpermute((r & 63) << 2, cr[r >> 6]);
+            } else {
+                const int m = m0 + wm * WR + r;
+                return m < M ? m : -1;
+            }
+        };
+        WAITCNT_VM(0);
+        asm volatile("" ::: "memory");
+        uint8_t* slot = smem + GE::EPI + wave * T2_SLOT;
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const int mb = m0 + wm * WR + i * 32;     // first row of this 32 x 64 block
+            const int nb = n0 + wn * 64;
+            float as[P::NRQ] = {};
+            if constexpr (KIND != EE_GEMM_F16)
+#pragma unroll
+                for (int h = 0; h < P::NRQ; ++h) {
+                    const int r = i * 32 + P::row_of(h, lane);
+                    as[h] = __int_as_float(__builtin_amdgcn_ds_bpermute((r & 63) << 2, __float_as_int(asv[r >> 6])));
+                }
+            if constexpr (KIND == EE_GEMM_I8) {
+                if (!Seq::ROUTED && g.acc) {          // debug output: int32 accumulators, direct stores
+#pragma unroll
+                    for (int j = 0; j < 2; ++j)
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) {
+                            const int m = mb + P::row_of(q, lane), n = nb + j * 32 + P::col_of(q, lane);
+                            if (m < M && n < N)
+                                *(i32x4*)(g.acc + (int64_t)m * g.ldc + n) =
+                                    i32x4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
+                                          acc[i][j][4 * q + 3]};
+                        }
+                }
+            }
+            if constexpr (SW) {
+                // gate (j = 0) and up (j = 1) of the same 32 outputs -> act columns nb / 2 .. +31
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    float gv[4], uv[4];
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        gv[r] = deq<KIND>(acc[i][0][4 * q + r], as[P::rq(q)], bs[0][P::cq(q)][r]);
+                        uv[r] = deq<KIND>(acc[i][1][4 * q + r], as[P::rq(q)], bs[1][P::cq(q)][r]);
+                    }
+                    const int ca = P::col_of(q, lane);
+                    *(u32x2*)(slot + lds_off(P::row_of(q, lane), ca >> 3) + ((ca >> 2) & 1) * 8) =
+                        u32x2{silu_mul2(pack_f16x2(gv[0], gv[1]), pack_f16x2(uv[0], uv[1])),
+                              silu_mul2(pack_f16x2(gv[2], gv[3]), pack_f16x2(uv[2], uv[3]))};
+                }
+                const int na = N >> 1;
+#pragma unroll
+                for (int k = 0; k < 2; ++k) {
+                    const int rl = k * 16 + (lane >> 2), ch = lane & 3;
+                    const u32x4 v = *(const u32x4*)(slot + lds_off(rl, ch));
+                    const int n = (nb >> 1) + ch * 8;
+                    const int32_t crow = crow_of(i * 32 + rl);
+                    if (crow >= 0 && n < na) store_row16(g.c + (int64_t)crow * g.ldc + n, v, true);
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const int cl = j * 32 + P::col_of(q, lane);
+                        float o[4];
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            if constexpr (KIND == EE_GEMM_F16) o[r] = acc[i][j][4 * q + r];
+                            else o[r] = deq<KIND>(acc[i][j][4 * q + r], as[P::rq(q)], bs[j][P::cq(q)][r]);
+                        }
+                        *(u32x2*)(slot + lds_off(P::row_of(q, lane), cl >> 3) + ((cl >> 2) & 1) * 8) =
+                            u32x2{pack_f16x2(o[0], o[1]), pack_f16x2(o[2], o[3])};
+                    }
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const int rl = k * 8 + (lane >> 3), ch = lane & 7;
+                    const u32x4 v = *(const u32x4*)(slot + lds_off(rl, ch));
+                    const int n = nb + ch * 8;
+                    const int32_t crow = crow_of(i * 32 + rl);
+                    if (crow >= 0 && n < N) store_row16(g.c + (int64_t)crow * g.ldc + n, v, n + 8 <= N);
+                }
+            }
+        }
+    }
+
+    __device__ __forceinline__ void epilogue(int m0, int n0) {
+        if constexpr (P::SUB16) epilogue16(m0, n0);
+        else epilogue32(m0, n0);
+    }
+
     __device__ __forceinline__ void zero() {
 #pragma unroll
         for (int i = 0; i < NI; ++i)
@@ -516,6 +679,9 @@ struct G256 {
         wave = __builtin_amdgcn_readfirstlane(tid >> 6);
         wm = wave >> GE::WMS;
         wn = wave & ((1 << GE::WMS) - 1);
+        if constexpr (P::SUB16)
+#pragma unroll
+            for (int sl = 0; sl < 2; ++sl) fo[sl] = lds_off(lane & 15, sl * 4 + (lane >> 4));
         const int ntiles = seq.count();
         if (ntiles <= 0) return;                      // whole workgroup, before any barrier
         nk = (int)((int64_t)g.K * ESZ / BKB);         // K * ESZ is a multiple of BKB here
