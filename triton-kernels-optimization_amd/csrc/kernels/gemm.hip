@@ -688,6 +688,15 @@ EE_DEV void xchg_put(uint8_t* slot, const acc_t& v, int lane) {
         *(u32x4*)(slot + (q * 64 + lane) * 16) = u32x4{w[0], w[1], w[2], w[3]};
     }
 }
+EE_DEV void xchg_put(uint8_t* slot, const I32x4x4& v, int lane) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) *(u32x4*)(slot + (q * 64 + lane) * 16) = __builtin_bit_cast(u32x4, v.q[q]);
+}
+template <int KIND>
+EE_DEV void xchg_add(const uint8_t* slot, I32x4x4& v, int lane) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) v.q[q] += __builtin_bit_cast(i32x4, *(const u32x4*)(slot + (q * 64 + lane) * 16));
+}
 template <int KIND, typename acc_t>
 EE_DEV void xchg_add(const uint8_t* slot, acc_t& v, int lane) {
 #pragma unroll
@@ -862,10 +871,86 @@ EE_DEV void epilogue_blk_direct(const EeGemmArgs& g, const typename Pipe<KIND>::
         }
 }
 
+// The 16x16x64 accumulator layout (PipeI8x16): register 4q + r of column block
+// j of row block rb holds row rb*32 + row_of(q, l), column j*32 + col_of(q, l) + r
+// of the quadrant; a lane needs two row scales and two column-scale vectors per j.
+struct TileScales16 {
+    f32x4 bs[2][2];
+    float as[2];
+};
+template <class P>
+EE_DEV void load_scales_blk16(const EeGemmArgs& g, int m0, int n0, int M, int64_t off, int wm, int wn, int rb,
+                              int lane, TileScales16& sc) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            const int n = n0 + wn * 64 + j * 32 + P::col_of(2 * c, lane);
+            sc.bs[j][c] = (n < g.N) ? *(const f32x4*)(g.b_scale + n) : f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int m = m0 + wm * 64 + rb * 32 + P::row_of(h, lane);
+        sc.as[h] = (m < M) ? g.a_scale[off + m] : 0.0f;
+    }
+}
+// epilogue_blk_lds (INT8, no SwiGLU) for that layout.
+template <class P>
+EE_DEV void epilogue_blk_lds16(const EeGemmArgs& g, const I32x4x4 (&acc)[2], const TileScales16& sc, uint8_t* tile,
+                               int m0, int n0, int M, int64_t off, int wm, int wn, int rb, int lane) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int cl = j * 32 + P::col_of(q, lane);
+            float o[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) o[r] = deq<EE_GEMM_I8>(acc[j][4 * q + r], sc.as[P::rq(q)], sc.bs[j][P::cq(q)][r]);
+            *(u32x2*)(tile + lds_off(P::row_of(q, lane), cl >> 3) + ((cl >> 2) & 1) * 8) =
+                u32x2{pack_f16x2(o[0], o[1]), pack_f16x2(o[2], o[3])};
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int rl = k * 8 + (lane >> 3), ch = lane & 7;
+        const u32x4 v = *(const u32x4*)(tile + lds_off(rl, ch));
+        const int m = m0 + wm * 64 + rb * 32 + rl;
+        const int n = n0 + wn * 64 + ch * 8;
+        if (m >= M || n >= g.N) continue;
+        const int64_t crow = g.c_idx ? (int64_t)g.c_idx[off + m] : (int64_t)m;
+        store_row16(g.c + crow * g.ldc + n, v, n + 8 <= g.N);
+    }
+}
+// epilogue_blk_direct (int32 accumulators requested) for that layout.
+template <class P>
+EE_DEV void epilogue_blk_direct16(const EeGemmArgs& g, const I32x4x4 (&acc)[2], int m0, int n0, int M, int64_t off,
+                                  int wm, int wn, int rb, int lane) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int m = m0 + wm * 64 + rb * 32 + P::row_of(q, lane);
+            const int n = n0 + wn * 64 + j * 32 + P::col_of(q, lane);
+            if (m >= M || n >= g.N) continue;
+            const int64_t crow = g.c_idx ? (int64_t)g.c_idx[off + m] : (int64_t)m;
+            const float as = g.a_scale[off + m];
+            float o[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                float v = (float)acc[j][4 * q + r];
+                v = v * as;
+                o[r] = v * g.b_scale[n + r];
+            }
+            *(u32x2*)(g.c + crow * g.ldc + n) = u32x2{pack_f16x2(o[0], o[1]), pack_f16x2(o[2], o[3])};
+            if (g.acc) *(i32x4*)(g.acc + crow * g.ldc + n) = acc[j].q[q];
+        }
+}
+
 template <int KIND, int SW = 0>
 struct Gemm8 {
-    // (eight waves' registers leave no room for INT8's 64-byte slices)
-    typedef std::conditional_t<KIND == EE_GEMM_I8, PipeI8x32, Pipe<KIND>> P;
+    // INT8: 16x16x64 MFMAs on 64-byte slices, or (SwiGLU, whose epilogue
+    // registers leave no room for 64-byte fragments) 32x32x32 on 32-byte slices
+    typedef std::conditional_t<KIND == EE_GEMM_I8, std::conditional_t<SW != 0, PipeI8x32, PipeI8x16>, Pipe<KIND>> P;
     typedef typename P::acc_t acc_t;
     static constexpr int ESZ = (KIND == EE_GEMM_F16) ? 2 : 1;
     static constexpr int LOADS = 4;                    // DMA instructions per wave per stage
@@ -959,14 +1044,22 @@ struct Gemm8 {
     }
     // One fragment of one K slice: which = 0, 1 (A row block), 2, 3 (B row block).
     __device__ __forceinline__ void read_frag(const uint8_t* s, int slice, typename P::frag_t& f, int which) const {
-        const int r = lane & 31;
-        const int c0 = slice * (P::SB / 16) + (lane >> 5) * P::LSTEP;
-        const int row = which < 2 ? wm * 64 + which * 32 + r : BM + wn * 64 + (which - 2) * 32 + r;
-        if constexpr (P::CPF == 1) {
-            f = *(const u32x4*)(s + lds_off(row, c0));
+        if constexpr (P::SUB16) {                     // rows base + (l & 15), +16; chunk 4 slice + (l >> 4)
+            const int base = which < 2 ? wm * 64 + which * 32 : BM + wn * 64 + (which - 2) * 32;
+            const int r = base + (lane & 15), c = slice * 4 + (lane >> 4);
+            f.h[0] = *(const i32x4*)(s + lds_off(r, c));
+            f.h[1] = *(const i32x4*)(s + lds_off(r + 16, c));   // swz(r + 16) == swz(r)
         } else {
-            const u32x4 x0 = *(const u32x4*)(s + lds_off(row, c0)), x1 = *(const u32x4*)(s + lds_off(row, c0 + P::CSTEP));
-            f = i32x8{(int)x0[0], (int)x0[1], (int)x0[2], (int)x0[3], (int)x1[0], (int)x1[1], (int)x1[2], (int)x1[3]};
+            const int r = lane & 31;
+            const int c0 = slice * (P::SB / 16) + (lane >> 5) * P::LSTEP;
+            const int row = which < 2 ? wm * 64 + which * 32 + r : BM + wn * 64 + (which - 2) * 32 + r;
+            if constexpr (P::CPF == 1) {
+                f = *(const u32x4*)(s + lds_off(row, c0));
+            } else {
+                const u32x4 x0 = *(const u32x4*)(s + lds_off(row, c0)),
+                            x1 = *(const u32x4*)(s + lds_off(row, c0 + P::CSTEP));
+                f = i32x8{(int)x0[0], (int)x0[1], (int)x0[2], (int)x0[3], (int)x1[0], (int)x1[1], (int)x1[2], (int)x1[3]};
+            }
         }
     }
     // The last five stages (kt0 = nk - 5 .. nk - 1, nk >= 6), first one of parity P0.
@@ -994,8 +1087,11 @@ struct Gemm8 {
 
         // Scales of the wave's final block first: they are the oldest loads the
         // first stage wait covers.
-        TileScales sc;
-        if (!g.acc) load_scales_blk<KIND>(g, m0, n0, M, off, wm, wn, kq, lane, sc);
+        std::conditional_t<P::SUB16, TileScales16, TileScales> sc;
+        if (!g.acc) {
+            if constexpr (P::SUB16) load_scales_blk16<P>(g, m0, n0, M, off, wm, wn, kq, lane, sc);
+            else load_scales_blk<KIND>(g, m0, n0, M, off, wm, wn, kq, lane, sc);
+        }
         // DMA: one global_load_lds_dwordx4 fills 8 LDS rows (1 KB): lane l lands at
         // row r = 8*grp + l/8, physical chunk l%8, which holds logical chunk
         // (l%8) ^ swz(r).  Wave w fills row groups 2w, 2w+1 of A and of B.
@@ -1078,10 +1174,12 @@ struct Gemm8 {
             for (int j = 0; j < 2; ++j) xchg_add<KIND>(src + j * 4096, blk[j], lane);
         }
         if (g.acc) {
-            epilogue_blk_direct<KIND>(g, blk, m0, n0, M, off, wm, wn, kq, lane);
+            if constexpr (P::SUB16) epilogue_blk_direct16<P>(g, blk, m0, n0, M, off, wm, wn, kq, lane);
+            else epilogue_blk_direct<KIND>(g, blk, m0, n0, M, off, wm, wn, kq, lane);
         } else {
             uint8_t* tile = smem + (nk % NSTAGE) * LDS_STAGE + wave * 4096;
-            epilogue_blk_lds<KIND, SW>(g, blk, sc, tile, m0, n0, M, off, wm, wn, kq, lane);
+            if constexpr (P::SUB16) epilogue_blk_lds16<P>(g, blk, sc, tile, m0, n0, M, off, wm, wn, kq, lane);
+            else epilogue_blk_lds<KIND, SW>(g, blk, sc, tile, m0, n0, M, off, wm, wn, kq, lane);
         }
     }
 };
