@@ -22,6 +22,15 @@ def test_probe_rates_in_range(ee, kind, lo, hi):
     assert 300 < r["sclk_mhz"] < 3500, r
 
 
+@pytest.mark.parametrize("kind", ["frag_i8_32x32", "frag_i8_16x16", "frag_f16_32x32", "frag_f16_16x16"])
+def test_probe_fragment_loops(ee, kind):
+    # 8 MFMAs of 32 clocks (or 16 of 16) per wave and iteration, two waves per
+    # SIMD: at least 512 clocks per iteration, and not far above
+    r = ee.probe(kind, iters=512)
+    assert 500 < r["value"] < 4000, r
+    assert 300 < r["sclk_mhz"] < 3500, r
+
+
 def test_probe_on_few_workgroups(ee):
     r = ee.probe("stream", iters=64, grid=3, window=65536)
     assert r["grid"] == 3 and r["value"] > 0
@@ -34,7 +43,9 @@ def test_probe_rejects_bad_arguments(ee):
     sink = torch.zeros(4 * 512, dtype=torch.int32, device="cuda")
     src = torch.zeros(8 * 32768, dtype=torch.uint8, device="cuda")
     P = lambda t: t.data_ptr()
-    assert L.ee_probe(E, 5, None, 0, 1, 1, P(times), P(sink), None) == _lib.EE_ERR_INVALID_ARG       # kind
+    assert L.ee_probe(E, 9, None, 0, 1, 1, P(times), P(sink), None) == _lib.EE_ERR_INVALID_ARG       # kind
+    assert L.ee_probe(E, 5, None, 1 << 20, 1, 1, P(times), P(sink), None) == _lib.EE_ERR_INVALID_ARG # no src
+    assert L.ee_probe(E, 6, P(src), 65536, 1, 1, P(times), P(sink), None) == _lib.EE_ERR_INVALID_ARG # src < 1 MiB
     assert L.ee_probe(E, 4, None, 32768, 1, 1, P(times), P(sink), None) == _lib.EE_ERR_INVALID_ARG   # no src
     assert L.ee_probe(E, 0, None, 32768, 1, 1, P(times), P(sink), None) == _lib.EE_ERR_INVALID_ARG   # no src
     assert L.ee_probe(E, 0, P(src), 1000, 1, 1, P(times), P(sink), None) == _lib.EE_ERR_INVALID_ARG  # window

@@ -93,26 +93,38 @@ struct PipeI8x64 : Lay32 {                       // 2 x 32x32x32 i8: 64 K bytes 
     }
 };
 template <> struct Pipe<EE_GEMM_I8> : PipeI8x64 {};
-// INT8 as 16x16x64 i8 MFMAs: per 64-byte slice a 32x32 block is four of them
-// (the same MFMA time as two 32x32x32).  Fragment half h (registers 4h .. 4h+3)
-// holds rows 16h + (l & 15) of the block, K bytes 16 (l >> 4) .. +15 of the
-// slice, for A and B alike; accumulator quarter q is the 16 x 16 sub-block of
-// A half q & 1 and B half q >> 1, lane l holding its row l & 15 and columns
-// 4 (l >> 4) .. +3.  Measured on MI355X (a sustained MFMA + fragment-read
-// loop, identical rates in clocks): the 16x16 forms run at a 9-13% higher
-// shader clock under the power limit than the 32x32 forms of the same work.
+// 16x16 MFMAs on 64-byte K slices (INT8 16x16x64 i8, FP16 16x16x32 f16): a
+// 32x32 block of a slice is four of them, the same MFMA time as the 32x32
+// forms.  Fragment half h holds rows 16h + (l & 15) of the block, K bytes
+// 16 (l >> 4) .. +15 of the slice, for A and B alike; accumulator quarter q is
+// the 16 x 16 sub-block of A half q & 1 and B half q >> 1, lane l holding its
+// row l & 15 and columns 4 (l >> 4) .. +3.  Measured on MI355X (probe.hip's
+// fragment loops: the same clocks per iteration either way), the 16x16 forms
+// run at a 9-13% higher shader clock under the power limit than the 32x32
+// forms of the same work.
+struct Lay16 {
+    static constexpr bool SUB16 = true;
+    static constexpr int NRQ = 2, NCQ = 2;
+    static EE_DEV int rq(int q) { return q & 1; }
+    static EE_DEV int cq(int q) { return q >> 1; }
+    static EE_DEV int row_of(int q, int lane) { return (q & 1) * 16 + (lane & 15); }
+    static EE_DEV int col_of(int q, int lane) { return (q >> 1) * 16 + 4 * (lane >> 4); }
+};
 // The four quarters of one block's accumulators; element e is register e & 3 of quarter e >> 2.
 struct I32x4x4 {
     i32x4 q[4];
     __device__ __forceinline__ int32_t operator[](int e) const { return q[e >> 2][e & 3]; }
 };
+struct F32x4x4 {
+    f32x4 q[4];
+    __device__ __forceinline__ float operator[](int e) const { return q[e >> 2][e & 3]; }
+};
 // The two 16-row halves of one fragment.
 struct I32x4x2 {
     i32x4 h[2];
 };
-struct PipeI8x16 {
+struct PipeI8x16 : Lay16 {
     static constexpr int SB = 64, CPF = 2, LSTEP = 0, CSTEP = 0;
-    static constexpr bool SUB16 = true;
     typedef I32x4x2 frag_t;
     typedef I32x4x4 acc_t;
     static EE_DEV acc_t mma(const frag_t& b, const frag_t& a, const acc_t& c) {
@@ -123,11 +135,22 @@ struct PipeI8x16 {
         r.q[3] = __builtin_amdgcn_mfma_i32_16x16x64_i8(b.h[1], a.h[1], c.q[3], 0, 0, 0);
         return r;
     }
-    static constexpr int NRQ = 2, NCQ = 2;
-    static EE_DEV int rq(int q) { return q & 1; }
-    static EE_DEV int cq(int q) { return q >> 1; }
-    static EE_DEV int row_of(int q, int lane) { return (q & 1) * 16 + (lane & 15); }
-    static EE_DEV int col_of(int q, int lane) { return (q >> 1) * 16 + 4 * (lane >> 4); }
+};
+struct PipeF16x16 : Lay16 {                       // 16x16x32 f16: 64 K bytes (32 elements) per slice
+    static constexpr int SB = 64, CPF = 2, LSTEP = 0, CSTEP = 0;
+    typedef I32x4x2 frag_t;
+    typedef F32x4x4 acc_t;
+    static EE_DEV f32x4 m16(const i32x4& b, const i32x4& a, const f32x4& c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, b), __builtin_bit_cast(f16x8, a), c, 0, 0, 0);
+    }
+    static EE_DEV acc_t mma(const frag_t& b, const frag_t& a, const acc_t& c) {
+        acc_t r;
+        r.q[0] = m16(b.h[0], a.h[0], c.q[0]);
+        r.q[1] = m16(b.h[0], a.h[1], c.q[1]);
+        r.q[2] = m16(b.h[1], a.h[0], c.q[2]);
+        r.q[3] = m16(b.h[1], a.h[1], c.q[3]);
+        return r;
+    }
 };
 struct PipeF16x32 : Lay32 {                      // 32x32x16 f16: 32 K bytes per slice, 16 B per lane
     static constexpr int SB = 32, CPF = 1, LSTEP = 1, CSTEP = 0;
@@ -137,7 +160,7 @@ struct PipeF16x32 : Lay32 {                      // 32x32x16 f16: 32 K bytes per
         return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, b), __builtin_bit_cast(f16x8, a), c, 0, 0, 0);
     }
 };
-template <> struct Pipe<EE_GEMM_F16> : PipeF16x32 {};
+template <> struct Pipe<EE_GEMM_F16> : PipeF16x16 {};
 template <> struct Pipe<EE_GEMM_F8> : Lay32 {    // 32x32x64 e4m3: 64 K bytes per slice, 32 B per lane
     static constexpr int SB = 64, CPF = 2, LSTEP = 2, CSTEP = 1;
     typedef i32x8 frag_t;

@@ -156,22 +156,35 @@ using Frags = FragsP<Pipe<KIND>>;
 // Fragments of one K slice: lane l reads row (l & 31) of each 32-row block, K
 // chunk slice * SB/16 + (l >> 5) * LSTEP (and the chunk CSTEP after it when
 // CPF == 2): lanes 0-31 and 32-63 cover the two K halves of each MFMA's operand.
+// 16x16 pipes (SUB16): rows (l & 15) and 16 + (l & 15) of each block, chunk 4 slice + (l >> 4).
 template <int KIND>
 EE_DEV void read_frags(const uint8_t* s, int slice, int wm, int wn, int lane, Frags<KIND>& f) {
     typedef Pipe<KIND> P;
-    const int r = lane & 31;
-    const int c0 = slice * (P::SB / 16) + (lane >> 5) * P::LSTEP;
+    if constexpr (P::SUB16) {
+        const int c = slice * 4 + (lane >> 4), r = lane & 15;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int ra = wm * 64 + i * 32 + r, rb = BM + wn * 64 + i * 32 + r;
-        if constexpr (P::CPF == 1) {
-            f.a[i] = *(const u32x4*)(s + lds_off(ra, c0));
-            f.b[i] = *(const u32x4*)(s + lds_off(rb, c0));
-        } else {
-            const u32x4 a0 = *(const u32x4*)(s + lds_off(ra, c0)), a1 = *(const u32x4*)(s + lds_off(ra, c0 + P::CSTEP));
-            const u32x4 b0 = *(const u32x4*)(s + lds_off(rb, c0)), b1 = *(const u32x4*)(s + lds_off(rb, c0 + P::CSTEP));
-            f.a[i] = i32x8{(int)a0[0], (int)a0[1], (int)a0[2], (int)a0[3], (int)a1[0], (int)a1[1], (int)a1[2], (int)a1[3]};
-            f.b[i] = i32x8{(int)b0[0], (int)b0[1], (int)b0[2], (int)b0[3], (int)b1[0], (int)b1[1], (int)b1[2], (int)b1[3]};
+        for (int i = 0; i < 2; ++i) {
+            const int ra = wm * 64 + i * 32 + r, rb = BM + wn * 64 + i * 32 + r;   // swz(x + 16) == swz(x)
+            f.a[i].h[0] = *(const i32x4*)(s + lds_off(ra, c));
+            f.a[i].h[1] = *(const i32x4*)(s + lds_off(ra + 16, c));
+            f.b[i].h[0] = *(const i32x4*)(s + lds_off(rb, c));
+            f.b[i].h[1] = *(const i32x4*)(s + lds_off(rb + 16, c));
+        }
+    } else {
+        const int r = lane & 31;
+        const int c0 = slice * (P::SB / 16) + (lane >> 5) * P::LSTEP;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int ra = wm * 64 + i * 32 + r, rb = BM + wn * 64 + i * 32 + r;
+            if constexpr (P::CPF == 1) {
+                f.a[i] = *(const u32x4*)(s + lds_off(ra, c0));
+                f.b[i] = *(const u32x4*)(s + lds_off(rb, c0));
+            } else {
+                const u32x4 a0 = *(const u32x4*)(s + lds_off(ra, c0)), a1 = *(const u32x4*)(s + lds_off(ra, c0 + P::CSTEP));
+                const u32x4 b0 = *(const u32x4*)(s + lds_off(rb, c0)), b1 = *(const u32x4*)(s + lds_off(rb, c0 + P::CSTEP));
+                f.a[i] = i32x8{(int)a0[0], (int)a0[1], (int)a0[2], (int)a0[3], (int)a1[0], (int)a1[1], (int)a1[2], (int)a1[3]};
+                f.b[i] = i32x8{(int)b0[0], (int)b0[1], (int)b0[2], (int)b0[3], (int)b1[0], (int)b1[1], (int)b1[2], (int)b1[3]};
+            }
         }
     }
 }
@@ -190,14 +203,31 @@ EE_DEV void mma_all(const Frags<KIND>& f, typename Pipe<KIND>::acc_t (&acc)[2][2
 template <int KIND>
 EE_DEV void interleave() {
     __builtin_amdgcn_sched_group_barrier(0x100, 4 * Pipe<KIND>::CPF, 0);   // DS read
-    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);                     // MFMA
+    __builtin_amdgcn_sched_group_barrier(0x008, Pipe<KIND>::SUB16 ? 16 : 4, 0);   // MFMA
 }
 
 // 32x32 epilogue: lane l, register r of block (i, j) holds
 // C[m0 + wm*64 + 32i + (l & 31)][n0 + wn*64 + 32j + 8*(r/4) + 4*(l >> 5) + r%4].
-template <int KIND>
-EE_DEV void epilogue32(const EeGemmArgs& g, const typename Pipe<KIND>::acc_t (&acc)[2][2], int m0, int n0, int M,
+template <int KIND, class P = Pipe<KIND>>
+EE_DEV void epilogue32(const EeGemmArgs& g, const typename P::acc_t (&acc)[2][2], int m0, int n0, int M,
                        int64_t off, int wm, int wn, int lane) {
+    if constexpr (P::SUB16) {                         // (FP16: no scales) quarter q at row_of(q), col_of(q)
+        static_assert(KIND == EE_GEMM_F16, "16x16 loader-wave epilogues are FP16's");
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int m = m0 + wm * 64 + i * 32 + P::row_of(q, lane);
+                    const int n = n0 + wn * 64 + j * 32 + P::col_of(q, lane);
+                    if (m >= M || n >= g.N) continue;
+                    const int64_t crow = g.c_idx ? (int64_t)g.c_idx[off + m] : (int64_t)m;
+                    *(u32x2*)(g.c + crow * g.ldc + n) = u32x2{pack_f16x2(acc[i][j][4 * q], acc[i][j][4 * q + 1]),
+                                                              pack_f16x2(acc[i][j][4 * q + 2], acc[i][j][4 * q + 3])};
+                }
+        return;
+    } else {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
         const int m = m0 + wm * 64 + i * 32 + (lane & 31);
@@ -233,6 +263,7 @@ EE_DEV void epilogue32(const EeGemmArgs& g, const typename Pipe<KIND>::acc_t (&a
                 }
             }
         }
+    }
     }
 }
 
@@ -275,10 +306,24 @@ EE_DEV void load_scales(const EeGemmArgs& g, int m0, int n0, int M, int64_t off,
 // act = fp16(fp16(silu(fp16(gate))) * fp16(up)), the fp16 gate and up being
 // exactly what the plain epilogue would store.  The 64 x 32 act block goes
 // through the wave's LDS region to act columns (n0 + 64 wn) / 2 ...
-template <int KIND>
-EE_DEV void epilogue32_lds_swiglu(const EeGemmArgs& g, const typename Pipe<KIND>::acc_t (&acc)[2][2],
+template <int KIND, class P = Pipe<KIND>>
+EE_DEV void epilogue32_lds_swiglu(const EeGemmArgs& g, const typename P::acc_t (&acc)[2][2],
                                   const TileScales& sc, uint8_t* tile, int m0, int n0, int M, int64_t off, int wm,
                                   int wn, int lane) {
+    if constexpr (P::SUB16) {                         // FP16: act column col_of(q) of row row_of(q)
+        static_assert(KIND == EE_GEMM_F16, "16x16 loader-wave epilogues are FP16's");
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int rl = i * 32 + P::row_of(q, lane), ca = P::col_of(q, lane);
+                *(u32x2*)(tile + lds_off(rl, ca >> 3) + ((ca >> 2) & 1) * 8) =
+                    u32x2{silu_mul2(pack_f16x2(acc[i][0][4 * q], acc[i][0][4 * q + 1]),
+                                    pack_f16x2(acc[i][1][4 * q], acc[i][1][4 * q + 1])),
+                          silu_mul2(pack_f16x2(acc[i][0][4 * q + 2], acc[i][0][4 * q + 3]),
+                                    pack_f16x2(acc[i][1][4 * q + 2], acc[i][1][4 * q + 3]))};
+            }
+    } else {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
         const int rl = i * 32 + (lane & 31);
@@ -296,6 +341,7 @@ EE_DEV void epilogue32_lds_swiglu(const EeGemmArgs& g, const typename Pipe<KIND>
                       silu_mul2(pack_f16x2(gv[2], gv[3]), pack_f16x2(uv[2], uv[3]))};
         }
     }
+    }
     const int na = g.N >> 1;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
@@ -309,13 +355,27 @@ EE_DEV void epilogue32_lds_swiglu(const EeGemmArgs& g, const typename Pipe<KIND>
     }
 }
 
-template <int KIND, int SW>
-EE_DEV void epilogue32_lds(const EeGemmArgs& g, const typename Pipe<KIND>::acc_t (&acc)[2][2], const TileScales& sc,
+template <int KIND, int SW, class P = Pipe<KIND>>
+EE_DEV void epilogue32_lds(const EeGemmArgs& g, const typename P::acc_t (&acc)[2][2], const TileScales& sc,
                            uint8_t* tile, int m0, int n0, int M, int64_t off, int wm, int wn, int lane) {
     if constexpr (SW) {
-        epilogue32_lds_swiglu<KIND>(g, acc, sc, tile, m0, n0, M, off, wm, wn, lane);
+        epilogue32_lds_swiglu<KIND, P>(g, acc, sc, tile, m0, n0, M, off, wm, wn, lane);
         return;
     }
+    if constexpr (P::SUB16) {                         // FP16: quarter q at row_of(q), col_of(q)
+        static_assert(KIND == EE_GEMM_F16, "16x16 loader-wave epilogues are FP16's");
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int rl = i * 32 + P::row_of(q, lane), cl = j * 32 + P::col_of(q, lane);
+                    *(u32x2*)(tile + lds_off(rl, cl >> 3) + ((cl >> 2) & 1) * 8) =
+                        u32x2{pack_f16x2(acc[i][j][4 * q], acc[i][j][4 * q + 1]),
+                              pack_f16x2(acc[i][j][4 * q + 2], acc[i][j][4 * q + 3])};
+                }
+    } else {
     // 1. dequantise and write: lane l holds rows i*32 + (l & 31), columns j*32 + 8q + 4(l >> 5) + 0..3.
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
@@ -344,6 +404,7 @@ EE_DEV void epilogue32_lds(const EeGemmArgs& g, const typename Pipe<KIND>::acc_t
                     u32x2{pack_f16x2(o[0], o[1]), pack_f16x2(o[2], o[3])};
             }
         }
+    }
     }
     // 2. read back row-contiguous and store (each wave reads only its own region)
 #pragma unroll
@@ -661,7 +722,7 @@ EE_DEV void gemm_tile_w8a16(const EeGemmArgs& g, int tm, int tn, uint8_t* smem) 
     for (int kt = 0; kt + 1 < nk; ++kt) stage(kt, true);
     stage(nk - 1, false);
     uint8_t* tile = smem + W8_EPI + wave * (64 * BKB);
-    epilogue32_lds<EE_GEMM_F16, SW>(g, acc, sc, tile, m0, n0, M, off, wm, wn, lane);
+    epilogue32_lds<EE_GEMM_F16, SW, PipeF16x32>(g, acc, sc, tile, m0, n0, M, off, wm, wn, lane);   // 32x32 layout
 }
 
 template <int SW>
@@ -696,6 +757,15 @@ template <int KIND>
 EE_DEV void xchg_add(const uint8_t* slot, I32x4x4& v, int lane) {
 #pragma unroll
     for (int q = 0; q < 4; ++q) v.q[q] += __builtin_bit_cast(i32x4, *(const u32x4*)(slot + (q * 64 + lane) * 16));
+}
+EE_DEV void xchg_put(uint8_t* slot, const F32x4x4& v, int lane) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) *(u32x4*)(slot + (q * 64 + lane) * 16) = __builtin_bit_cast(u32x4, v.q[q]);
+}
+template <int KIND>
+EE_DEV void xchg_add(const uint8_t* slot, F32x4x4& v, int lane) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) v.q[q] += __builtin_bit_cast(f32x4, *(const u32x4*)(slot + (q * 64 + lane) * 16));
 }
 template <int KIND, typename acc_t>
 EE_DEV void xchg_add(const uint8_t* slot, acc_t& v, int lane) {
@@ -878,26 +948,58 @@ struct TileScales16 {
     f32x4 bs[2][2];
     float as[2];
 };
-template <class P>
+template <int KIND, class P>
 EE_DEV void load_scales_blk16(const EeGemmArgs& g, int m0, int n0, int M, int64_t off, int wm, int wn, int rb,
                               int lane, TileScales16& sc) {
+    if constexpr (KIND != EE_GEMM_F16) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int c = 0; c < 2; ++c) {
-            const int n = n0 + wn * 64 + j * 32 + P::col_of(2 * c, lane);
-            sc.bs[j][c] = (n < g.N) ? *(const f32x4*)(g.b_scale + n) : f32x4{0.f, 0.f, 0.f, 0.f};
+            for (int c = 0; c < 2; ++c) {
+                const int n = n0 + wn * 64 + j * 32 + P::col_of(2 * c, lane);
+                sc.bs[j][c] = (n < g.N) ? *(const f32x4*)(g.b_scale + n) : f32x4{0.f, 0.f, 0.f, 0.f};
+            }
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int m = m0 + wm * 64 + rb * 32 + P::row_of(h, lane);
+            sc.as[h] = (m < M) ? g.a_scale[off + m] : 0.0f;
         }
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        const int m = m0 + wm * 64 + rb * 32 + P::row_of(h, lane);
-        sc.as[h] = (m < M) ? g.a_scale[off + m] : 0.0f;
     }
 }
-// epilogue_blk_lds (INT8, no SwiGLU) for that layout.
-template <class P>
-EE_DEV void epilogue_blk_lds16(const EeGemmArgs& g, const I32x4x4 (&acc)[2], const TileScales16& sc, uint8_t* tile,
-                               int m0, int n0, int M, int64_t off, int wm, int wn, int rb, int lane) {
+// epilogue_blk_lds (and its SwiGLU form) for that layout.
+template <int KIND, int SW, class P>
+EE_DEV void epilogue_blk_lds16(const EeGemmArgs& g, const typename P::acc_t (&acc)[2], const TileScales16& sc,
+                               uint8_t* tile, int m0, int n0, int M, int64_t off, int wm, int wn, int rb, int lane) {
+    // (the lane through an empty asm: addresses derived from it are computed here,
+    // not merged with the K loop's and held across it)
+    asm volatile("" : "+v"(lane));
+    if constexpr (SW) {                               // gate (j = 0) and up (j = 1) -> act columns (n0 + 64 wn) / 2 ..
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            float gv[4], uv[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                gv[r] = deq<KIND>(acc[0][4 * q + r], sc.as[P::rq(q)], sc.bs[0][P::cq(q)][r]);
+                uv[r] = deq<KIND>(acc[1][4 * q + r], sc.as[P::rq(q)], sc.bs[1][P::cq(q)][r]);
+            }
+            const int ca = P::col_of(q, lane);
+            *(u32x2*)(tile + lds_off(P::row_of(q, lane), ca >> 3) + ((ca >> 2) & 1) * 8) =
+                u32x2{silu_mul2(pack_f16x2(gv[0], gv[1]), pack_f16x2(uv[0], uv[1])),
+                      silu_mul2(pack_f16x2(gv[2], gv[3]), pack_f16x2(uv[2], uv[3]))};
+        }
+        const int na = g.N >> 1;
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const int rl = k * 16 + (lane >> 2), ch = lane & 3;
+            const u32x4 v = *(const u32x4*)(tile + lds_off(rl, ch));
+            const int m = m0 + wm * 64 + rb * 32 + rl;
+            const int n = ((n0 + wn * 64) >> 1) + ch * 8;
+            if (m >= M || n >= na) continue;
+            const int64_t crow = g.c_idx ? (int64_t)g.c_idx[off + m] : (int64_t)m;
+            store_row16(g.c + crow * g.ldc + n, v, true);
+        }
+        return;
+    }
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
 #pragma unroll
@@ -905,7 +1007,7 @@ EE_DEV void epilogue_blk_lds16(const EeGemmArgs& g, const I32x4x4 (&acc)[2], con
             const int cl = j * 32 + P::col_of(q, lane);
             float o[4];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) o[r] = deq<EE_GEMM_I8>(acc[j][4 * q + r], sc.as[P::rq(q)], sc.bs[j][P::cq(q)][r]);
+            for (int r = 0; r < 4; ++r) o[r] = deq<KIND>(acc[j][4 * q + r], sc.as[P::rq(q)], sc.bs[j][P::cq(q)][r]);
             *(u32x2*)(tile + lds_off(P::row_of(q, lane), cl >> 3) + ((cl >> 2) & 1) * 8) =
                 u32x2{pack_f16x2(o[0], o[1]), pack_f16x2(o[2], o[3])};
         }
@@ -921,10 +1023,10 @@ EE_DEV void epilogue_blk_lds16(const EeGemmArgs& g, const I32x4x4 (&acc)[2], con
         store_row16(g.c + crow * g.ldc + n, v, n + 8 <= g.N);
     }
 }
-// epilogue_blk_direct (int32 accumulators requested) for that layout.
-template <class P>
-EE_DEV void epilogue_blk_direct16(const EeGemmArgs& g, const I32x4x4 (&acc)[2], int m0, int n0, int M, int64_t off,
-                                  int wm, int wn, int rb, int lane) {
+// epilogue_blk_direct (int32 accumulators requested, INT8) for that layout.
+template <int KIND, class P>
+EE_DEV void epilogue_blk_direct16(const EeGemmArgs& g, const typename P::acc_t (&acc)[2], int m0, int n0, int M,
+                                  int64_t off, int wm, int wn, int rb, int lane) {
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
@@ -933,16 +1035,14 @@ EE_DEV void epilogue_blk_direct16(const EeGemmArgs& g, const I32x4x4 (&acc)[2], 
             const int n = n0 + wn * 64 + j * 32 + P::col_of(q, lane);
             if (m >= M || n >= g.N) continue;
             const int64_t crow = g.c_idx ? (int64_t)g.c_idx[off + m] : (int64_t)m;
-            const float as = g.a_scale[off + m];
+            const float as = (KIND == EE_GEMM_F16) ? 0.0f : g.a_scale[off + m];
             float o[4];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                float v = (float)acc[j][4 * q + r];
-                v = v * as;
-                o[r] = v * g.b_scale[n + r];
-            }
+            for (int r = 0; r < 4; ++r) o[r] = deq<KIND>(acc[j][4 * q + r], as, KIND == EE_GEMM_F16 ? 0.0f : g.b_scale[n + r]);
             *(u32x2*)(g.c + crow * g.ldc + n) = u32x2{pack_f16x2(o[0], o[1]), pack_f16x2(o[2], o[3])};
-            if (g.acc) *(i32x4*)(g.acc + crow * g.ldc + n) = acc[j].q[q];
+            if constexpr (KIND == EE_GEMM_I8) {
+                if (g.acc) *(i32x4*)(g.acc + crow * g.ldc + n) = acc[j].q[q];
+            }
         }
 }
 
@@ -966,6 +1066,7 @@ struct Gemm8 {
     const uint8_t* pb[2];
     acc_t acc[2][2];
     FragsP<P> fr[2];
+    uint32_t fo16;                                     // SUB16: byte of row l & 15, chunk (l >> 4) of slice 0
 
     __device__ __forceinline__ Gemm8(const EeGemmArgs& g_, uint8_t* smem_) : g(g_), smem(smem_) {}
 
@@ -1045,10 +1146,15 @@ struct Gemm8 {
     // One fragment of one K slice: which = 0, 1 (A row block), 2, 3 (B row block).
     __device__ __forceinline__ void read_frag(const uint8_t* s, int slice, typename P::frag_t& f, int which) const {
         if constexpr (P::SUB16) {                     // rows base + (l & 15), +16; chunk 4 slice + (l >> 4)
+            // (base % 16 == 0: swz(base + x) == swz(x); the lane's offset for the slice goes
+            // through an empty asm, so that each read adds it to the block's base rather
+            // than the compiler holding a hoisted address per block and buffer)
             const int base = which < 2 ? wm * 64 + which * 32 : BM + wn * 64 + (which - 2) * 32;
-            const int r = base + (lane & 15), c = slice * 4 + (lane >> 4);
-            f.h[0] = *(const i32x4*)(s + lds_off(r, c));
-            f.h[1] = *(const i32x4*)(s + lds_off(r + 16, c));   // swz(r + 16) == swz(r)
+            uint32_t o = fo16 ^ (uint32_t)((slice & 1) << 6);  // chunk 4 + c ^ s == (c ^ s) ^ 4 for c < 4
+            asm volatile("" : "+v"(o));
+            const uint8_t* p = s + base * BKB + o;
+            f.h[0] = *(const i32x4*)p;
+            f.h[1] = *(const i32x4*)(p + 16 * BKB);
         } else {
             const int r = lane & 31;
             const int c0 = slice * (P::SB / 16) + (lane >> 5) * P::LSTEP;
@@ -1079,6 +1185,7 @@ struct Gemm8 {
         kq = wave >> 2;
         wm = (wave >> 1) & 1;
         wn = wave & 1;
+        if constexpr (P::SUB16) fo16 = lds_off(lane & 15, lane >> 4);
         const int M = g.counts ? g.counts[g.tier] : g.M;
         const int64_t off = g.counts ? tier_offset(g.counts, g.tier) : 0;
         const int m0 = tm * BM, n0 = tn * BN;
@@ -1089,7 +1196,7 @@ struct Gemm8 {
         // first stage wait covers.
         std::conditional_t<P::SUB16, TileScales16, TileScales> sc;
         if (!g.acc) {
-            if constexpr (P::SUB16) load_scales_blk16<P>(g, m0, n0, M, off, wm, wn, kq, lane, sc);
+            if constexpr (P::SUB16) load_scales_blk16<KIND, P>(g, m0, n0, M, off, wm, wn, kq, lane, sc);
             else load_scales_blk<KIND>(g, m0, n0, M, off, wm, wn, kq, lane, sc);
         }
         // DMA: one global_load_lds_dwordx4 fills 8 LDS rows (1 KB): lane l lands at
@@ -1174,11 +1281,11 @@ struct Gemm8 {
             for (int j = 0; j < 2; ++j) xchg_add<KIND>(src + j * 4096, blk[j], lane);
         }
         if (g.acc) {
-            if constexpr (P::SUB16) epilogue_blk_direct16<P>(g, blk, m0, n0, M, off, wm, wn, kq, lane);
+            if constexpr (P::SUB16) epilogue_blk_direct16<KIND, P>(g, blk, m0, n0, M, off, wm, wn, kq, lane);
             else epilogue_blk_direct<KIND>(g, blk, m0, n0, M, off, wm, wn, kq, lane);
         } else {
             uint8_t* tile = smem + (nk % NSTAGE) * LDS_STAGE + wave * 4096;
-            if constexpr (P::SUB16) epilogue_blk_lds16<P>(g, blk, sc, tile, m0, n0, M, off, wm, wn, kq, lane);
+            if constexpr (P::SUB16) epilogue_blk_lds16<KIND, SW, P>(g, blk, sc, tile, m0, n0, M, off, wm, wn, kq, lane);
             else epilogue_blk_lds<KIND, SW>(g, blk, sc, tile, m0, n0, M, off, wm, wn, kq, lane);
         }
     }

@@ -73,12 +73,12 @@ struct G256 {
     static constexpr int NSL = BKB / P::SB;           // K slices per stage: 4 (32-byte slices) or 2 (64-byte)
     // DMA parts of stage s+2 issued in each slice of the window from barrier s+1
     // (slice w = 0: the last slice of stage s; w >= 1: slice w-1 of stage s+1).
-    // All four are issued before barrier s+2 waits for them.  FP16 (four slices
-    // per stage) spreads them over two slices: 2.5% faster at configs 1-2 than
-    // all four in the first; the 1-byte kinds, with two slices per stage, keep
-    // them in the first (spread, the last loads land late: 3-8% slower).
+    // All four are issued before barrier s+2 waits for them.  With four slices
+    // per stage (32-byte slices) they spread over two: 2.5% faster for FP16 at
+    // configs 1-2 than all four in the first; with two slices per stage they go
+    // in the first (spread, the last loads land late: 3-8% slower).
     static constexpr int dma_count(int w) {
-        if constexpr (KIND == EE_GEMM_F16) {
+        if constexpr (NSL == 4) {
             constexpr int c[4] = {2, 2, 0, 0};
             return c[w];
         } else {
@@ -114,7 +114,7 @@ struct G256 {
     // (its slices run j-major, so each B block is also dead before its reload)
     static constexpr int NB = (P::CPF == 2) ? 1 : 2;
     frag_t fa[NI], fb[NB][2];
-    uint32_t fo[2];                                   // SUB16: byte of row l & 15, chunk 4 sl + (l >> 4)
+    uint32_t fo;                                      // SUB16: byte of row l & 15, chunk (l >> 4) of slice 0
 
     __device__ __forceinline__ G256(const EeGemmArgs& g_, uint8_t* smem_, const Seq& seq_, int M_, int64_t off_)
         : g(g_), smem(smem_), seq(seq_), M(M_), off(off_) {}
@@ -211,11 +211,12 @@ struct G256 {
     }
     // 16x16x64 fragments (SUB16) of the 32-row block at row0 (a multiple of 16, so
     // swz(row0 + x) == swz(x)): rows row0 + (l & 15) and row0 + 16 + (l & 15),
-    // chunk 4 sl + (l >> 4), at byte fo[sl] of the block's first row and 2 KB on.
+    // chunk 4 sl + (l >> 4), at byte fo ^ 64 sl of the block's first row and 2 KB on
+    // (chunk 4 + c ^ s == (c ^ s) ^ 4 for c < 4: slice 1's offset flips bit 6).
     __device__ __forceinline__ void rd16(const uint8_t* st, int sl, frag_t& f, int row0) const {
         // (the offset through an empty asm: each read adds it to the block's base
         // instead of the compiler holding a hoisted address per block and buffer)
-        uint32_t o = fo[sl];
+        uint32_t o = fo ^ (uint32_t)(sl << 6);
         asm volatile("" : "+v"(o));
         const uint8_t* p = st + row0 * BKB + o;
         f.h[0] = *(const i32x4*)p;
@@ -679,9 +680,7 @@ struct G256 {
         wave = __builtin_amdgcn_readfirstlane(tid >> 6);
         wm = wave >> GE::WMS;
         wn = wave & ((1 << GE::WMS) - 1);
-        if constexpr (P::SUB16)
-#pragma unroll
-            for (int sl = 0; sl < 2; ++sl) fo[sl] = lds_off(lane & 15, sl * 4 + (lane >> 4));
+        if constexpr (P::SUB16) fo = lds_off(lane & 15, lane >> 4);
         const int ntiles = seq.count();
         if (ntiles <= 0) return;                      // whole workgroup, before any barrier
         nk = (int)((int64_t)g.K * ESZ / BKB);         // K * ESZ is a multiple of BKB here
@@ -750,7 +749,9 @@ EE_DEV void gemm256(const EeGemmArgs& g) {
     __shared__ __attribute__((aligned(1024))) uint8_t smem[G2Geom<TN>::LDS];
     const int b = (int)blockIdx.x, G = (int)gridDim.x;
     const Seq256<TN> seq(g, b, G);
-    if constexpr (TN == 256) {
+    // (not for FP16 SwiGLU: a second pipeline instance in the kernel takes its
+    // registers past 256; its grids run the last round as 256 x 256 tiles)
+    if constexpr (TN == 256 && !(SW && KIND == EE_GEMM_F16)) {
         const int nT = seq.d.nA, full = nT / G, rem = nT - full * G;
         if (rem > 0 && 2 * rem <= G) {
             if (full > 0) {

@@ -9,6 +9,13 @@
 //   eek_probe_mfma_i8   v_mfma_i32_32x32x32_i8, four independent accumulators per
 //                       wave, two waves per SIMD: clocks per MFMA
 //   eek_probe_mfma_f8   v_mfma_scale_f32_32x32x64_f8f6f4, the same way
+//   eek_probe_frag_*    the GEMMs' inner loop without their memory stream: each
+//                       wave reads its fragments of a 64 x 64 block from LDS
+//                       (random operands from src) and runs the MFMAs on them,
+//                       as 32x32 MFMAs (i8 32x32x32, f16 32x32x16) or as the
+//                       16x16 ones of the same work (i8 16x16x64, f16 16x16x32):
+//                       clocks per iteration and, over a run long enough for the
+//                       power limit to settle, the shader clock each holds
 //
 // Workgroups of 512 threads (8 waves, two per SIMD, as the GEMM kernels).
 // Thread 0 reads s_memtime (shader clock) and s_memrealtime (100 MHz) after a
@@ -118,3 +125,109 @@ extern "C" __global__ void __launch_bounds__(PR_THREADS) eek_probe_mfma_f8(EePro
     a.sink[(int64_t)blockIdx.x * PR_THREADS + t] =
         __builtin_bit_cast(uint32_t, c0[0] + c1[5] + c2[10] + c3[15]);
 }
+
+// Fragment loops.  Iteration k: each wave reads 8 16-byte fragments per lane
+// (1 KB apart, at 4 KB k + 512 wave + 16 lane modulo the 64 KB the workgroup
+// copied from src block b % 16) and issues MFMAs over a 64 x 64 block worth
+// 2 * 64 * 64 * 64 int8 ops or 2 * 64 * 64 * 32 f16 flops: 8 32x32 or 16 16x16.
+__device__ __forceinline__ i32x4 frag_rd(const uint8_t* s, uint32_t o) { return *(const i32x4*)(s + (o & 0xFFF0u)); }
+
+template <int V>
+__device__ __forceinline__ void probe_frag(const EeProbeArgs& a) {
+    __shared__ __attribute__((aligned(1024))) uint8_t s[65536];
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const uint8_t* blk = a.src + (int64_t)(blockIdx.x & 15) * 65536;
+    for (int i = t * 16; i < 65536; i += PR_THREADS * 16) *(i32x4*)(s + i) = *(const i32x4*)(blk + i);
+    __syncthreads();
+    const uint32_t lb = (uint32_t)(lane * 16 + wave * 512);
+    uint32_t out = 0;
+    if (t == 0) probe_times(a, 0, __builtin_amdgcn_s_memtime(), __builtin_amdgcn_s_memrealtime());
+    if constexpr (V == 0) {                           // i8 32x32x32: K 64 per iteration
+        i32x16 c[2][2] = {};
+        for (int k = 0; k < a.iters; ++k) {
+            const uint32_t o = lb + (uint32_t)k * 4096u;
+            i32x4 x[2][2], y[2][2];
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int i = 0; i < 2; ++i) {
+                    x[h][i] = frag_rd(s, o + (h * 4 + i) * 1024);
+                    y[h][i] = frag_rd(s, o + (h * 4 + 2 + i) * 1024);
+                }
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+#pragma unroll
+                    for (int j = 0; j < 2; ++j) c[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(x[h][i], y[h][j], c[i][j], 0, 0, 0);
+        }
+        out = (uint32_t)(c[0][0][0] ^ c[0][1][3] ^ c[1][0][7] ^ c[1][1][15]);
+    } else if constexpr (V == 1) {                    // i8 16x16x64: K 64
+        i32x4 c[4][4] = {};
+        for (int k = 0; k < a.iters; ++k) {
+            const uint32_t o = lb + (uint32_t)k * 4096u;
+            i32x4 x[4], y[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                x[i] = frag_rd(s, o + i * 1024);
+                y[i] = frag_rd(s, o + (4 + i) * 1024);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) c[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(x[i], y[j], c[i][j], 0, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) out ^= (uint32_t)c[i][j][(i + j) & 3];
+    } else if constexpr (V == 2) {                    // f16 32x32x16: K 32
+        f32x16 c[2][2] = {};
+        for (int k = 0; k < a.iters; ++k) {
+            const uint32_t o = lb + (uint32_t)k * 4096u;
+            f16x8 x[2][2], y[2][2];
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int i = 0; i < 2; ++i) {
+                    x[h][i] = __builtin_bit_cast(f16x8, frag_rd(s, o + (h * 4 + i) * 1024));
+                    y[h][i] = __builtin_bit_cast(f16x8, frag_rd(s, o + (h * 4 + 2 + i) * 1024));
+                }
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+#pragma unroll
+                    for (int j = 0; j < 2; ++j) c[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(x[h][i], y[h][j], c[i][j], 0, 0, 0);
+        }
+        out = __float_as_uint(c[0][0][0] + c[0][1][3] + c[1][0][7] + c[1][1][15]);
+    } else {                                          // f16 16x16x32: K 32
+        f32x4 c[4][4] = {};
+        for (int k = 0; k < a.iters; ++k) {
+            const uint32_t o = lb + (uint32_t)k * 4096u;
+            f16x8 x[4], y[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                x[i] = __builtin_bit_cast(f16x8, frag_rd(s, o + i * 1024));
+                y[i] = __builtin_bit_cast(f16x8, frag_rd(s, o + (4 + i) * 1024));
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) c[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(x[i], y[j], c[i][j], 0, 0, 0);
+        }
+        float f = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) f += c[i][j][(i + j) & 3];
+        out = __float_as_uint(f);
+    }
+    __syncthreads();
+    if (t == 0) probe_times(a, 1, __builtin_amdgcn_s_memtime(), __builtin_amdgcn_s_memrealtime());
+    a.sink[(int64_t)blockIdx.x * PR_THREADS + t] = out;
+}
+extern "C" __global__ void __launch_bounds__(PR_THREADS) eek_probe_frag_i8_32(EeProbeArgs a) { probe_frag<0>(a); }
+extern "C" __global__ void __launch_bounds__(PR_THREADS) eek_probe_frag_i8_16(EeProbeArgs a) { probe_frag<1>(a); }
+extern "C" __global__ void __launch_bounds__(PR_THREADS) eek_probe_frag_f16_32(EeProbeArgs a) { probe_frag<2>(a); }
+extern "C" __global__ void __launch_bounds__(PR_THREADS) eek_probe_frag_f16_16(EeProbeArgs a) { probe_frag<3>(a); }
