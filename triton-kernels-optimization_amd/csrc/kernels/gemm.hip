@@ -1,33 +1,37 @@
-// gemm.hip -- MFMA GEMMs of the three precision tiers for gfx950.
+// gemm.hip -- MFMA GEMMs of the three precision tiers for gfx950: the 128 x 128
+// tile kernels (config 0, small grids, routed tiers; the 256 x 256 ones are in
+// gemm256.hip).
 //
-//   EE_GEMM_I8 : int8 x int8 -> int32 on v_mfma_i32_16x16x64_i8;
-//                C = fp16((f32(acc) * a_scale[m]) * b_scale[n])
+//   EE_GEMM_I8 : int8 x int8 -> int32; C = fp16((f32(acc) * a_scale[m]) * b_scale[n])
 //                (EE/python/kernels.py:50-110)
-//   EE_GEMM_F8 : e4m3 x e4m3 -> f32 on v_mfma_f32_16x16x128_f8f6f4;
-//                C = fp16((acc * a_scale[m]) * b_scale[n])
+//   EE_GEMM_F8 : e4m3 x e4m3 -> f32; C = fp16((acc * a_scale[m]) * b_scale[n])
 //                (EE/python/kernels.py:118-180; codes from quant.hip)
-//   EE_GEMM_F16: fp16 x fp16 -> f32 on v_mfma_f32_16x16x32_f16; C = fp16(acc)
+//   EE_GEMM_F16: fp16 x fp16 -> f32; C = fp16(acc)
 //                (EE/python/kernels.py:192-246; W8A16 weights pre-dequantised
 //                bit-exactly by eek_pack_b_f16)
 //
 // Operands: A [M, K] and B [N, K], both K-contiguous, which is the order the
-// MFMA register fragments want (16 consecutive K bytes per lane).
-// Tiling: a 256-thread workgroup computes a 128 x 128 tile of C; its four
-// wave64s each own a 64 x 64 quadrant as 4 x 4 MFMA 16x16 blocks.  K advances
-// in 128-byte stages.  LDS rows are 128 bytes; 16-byte chunk c of row r sits at
-// chunk c ^ (r & 7), so the eight lanes one ds_read_b128 pass serves hit eight
-// distinct 16-byte bank groups.
+// MFMA register fragments want (16 consecutive K bytes per lane and operand).
 //
-// eek_gemm_{i8,f8,f16}: four LDS stages (128 KB) filled by direct-to-LDS
-// global_load_lds_dwordx4 (no VGPR staging), three stages in flight while the
-// fourth is consumed: each wave waits only for its own oldest stage
-// (s_waitcnt vmcnt), then one s_barrier publishes it to the workgroup.
-// Needs K * elem_size to be a multiple of 128 bytes.
-// eek_gemm_{i8,f8,f16}_generic: two register-staged LDS buffers and a
-// zero-filled K tail, for K that is only a multiple of 16 bytes.
+// Pipelined kernels (K * elem_size a multiple of 128 bytes): a 512-thread
+// workgroup computes a 128 x 128 tile of C as four 64 x 64 quadrants of 32 x 32
+// blocks; K advances in 128-byte stages that direct-to-LDS loads
+// (global_load_lds_dwordx4, no VGPR staging) stream into a ring of LDS stages;
+// LDS rows are 128 bytes, 16-byte chunk c of row r at chunk c ^ ((r >> 1) & 7).
+// Per block and K slice the MFMAs are the pipes of ee_gemm_dev.h: INT8 four
+// 16x16x64 (8-wave) or two 32x32x32 (loader-wave, persistent) per 64-byte
+// slice, FP8 one 32x32x64, FP16 four 16x16x32.
+//   eek_gemm_{i8,f8,f16}: loader waves (4 compute waves + 4 DMA waves);
+//   eek_gemm_{i8,f16}_w8: 8 waves that each compute and load (Gemm8);
+//   eek_gemm_{i8,f8}_persist, eek_gemm_routed[_persist]: persistent and routed grids;
+//   eek_gemm_w8a16: the FP16 tier on int8 weight codes dequantised in registers.
+// eek_gemm_{i8,f8,f16}_generic (K a multiple of 16 bytes only): 256 threads,
+// two register-staged LDS buffers and a zero-filled K tail; each wave owns a
+// 64 x 64 quadrant as 4 x 4 blocks of 16x16 MFMAs (16x16x64 i8, 16x16x128
+// e4m3, 16x16x32 f16).
 //
 // The MFMA is issued with B as its first operand, so each lane ends up with
-// four consecutive columns of one row of C -> one 8-byte store per block.
+// rows of C and four consecutive columns of each (one 8-byte store).
 // Routing: with a device row count counts[tier] (off = rows of lower tiers),
 // A row m is a[a_idx[off + m]] (gather from the activations) or, without
 // a_idx, a[off + m] (the quantiser's partition slot), a_scale is read at
