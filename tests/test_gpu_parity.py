@@ -140,6 +140,31 @@ def test_softmax_entropy_rows_per_wave(ee, orc, R, S, causal, rpw):
         _lib.check(L.ee_engine_set_option(_lib.engine(), b"se_rpw", 0))
 
 
+@pytest.mark.parametrize("R,S,causal", [(300, 4096, False), (130, 14336, True), (1029, 512, False)])
+def test_softmax_entropy_nontemporal_loads(ee, orc, R, S, causal):
+    """Option se_nt: the logits read with non-temporal loads (2) or plain ones
+    (1) give the same bits, both equal to the oracle's to its tolerance; the
+    option rejects other values."""
+    from entropy_engine import _lib
+    rng = np.random.default_rng(R + S)
+    X = logits_rows(rng, R, S)
+    H_ref, P_ref = orc.softmax_entropy(X, causal=causal)
+    L, E = _lib.lib(), _lib.engine()
+    out = {}
+    try:
+        for v in (1, 2):
+            _lib.check(L.ee_engine_set_option(E, b"se_nt", v))
+            p, h, _ = ee.softmax_entropy(cuda(X), causal=causal)
+            out[v] = (host(p), host(h))
+    finally:
+        _lib.check(L.ee_engine_set_option(E, b"se_nt", 0))
+    check_entropy(out[2][1], H_ref)
+    check_probs(out[2][0], P_ref)
+    assert np.array_equal(out[1][1].view(np.uint32), out[2][1].view(np.uint32))
+    assert np.array_equal(out[1][0].view(np.uint16), out[2][0].view(np.uint16))
+    assert L.ee_engine_set_option(E, b"se_nt", 3) == _lib.EE_ERR_INVALID_ARG
+
+
 def test_softmax_entropy_max_in_several_waves(ee, orc):
     """Rows whose maximum (and its ties) sit in different waves of the row, near
     one-hot rows, and +-0 maxima: the waves holding the max take the counting

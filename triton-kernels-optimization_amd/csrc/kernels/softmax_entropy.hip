@@ -63,7 +63,8 @@ EE_DEV float sub_hi(uint32_t u, float negm) {
 // The row's registers: lane l of wave wr of the row holds 16-byte vectors
 // j = 0 .. VPT-1 at column ((j * WPR + wr) * 64 + l) * 8; entries past the row
 // (or past the causal limit) read as -inf and are not loaded.
-template <int VPT, int WPR>
+// NT: non-temporal loads (the _nt kernels: logits read once from HBM).
+template <int VPT, int WPR, bool NT = false>
 EE_DEV void se_load(const EeSoftmaxArgs& a, int64_t r, int wr, int lane, u32x4 (&v)[VPT]) {
     const int S = a.S;
     const int nvalid = a.causal ? min(S, (int)(r % S) + 1) : S;
@@ -72,7 +73,8 @@ EE_DEV void se_load(const EeSoftmaxArgs& a, int64_t r, int wr, int lane, u32x4 (
     for (int j = 0; j < VPT; ++j) {
         const int c0 = ((j * WPR + wr) * 64 + lane) * 8;
         if (c0 + 8 <= nvalid) {
-            v[j] = *(const u32x4*)(xr + c0);
+            if constexpr (NT) v[j] = __builtin_nontemporal_load((const u32x4*)(xr + c0));
+            else v[j] = *(const u32x4*)(xr + c0);
         } else {
             uint16_t e[8];
 #pragma unroll
@@ -200,7 +202,7 @@ EE_DEV void se_process(const EeSoftmaxArgs& a, u32x4 (&v)[VPT], int64_t row, boo
     }
 }
 
-template <int VPT, int WPR>
+template <int VPT, int WPR, bool NT = false>
 EE_DEV void softmax_entropy_vec(const EeSoftmaxArgs& a) {
     typedef SeGeom<WPR> G;
     __shared__ float red[G::RPB * WPR][4];
@@ -211,7 +213,7 @@ EE_DEV void softmax_entropy_vec(const EeSoftmaxArgs& a) {
     const bool valid = row < a.rows;
     const int64_t r = valid ? row : a.rows - 1;    // keep every wave in the barriers
     u32x4 v[VPT];
-    se_load<VPT, WPR>(a, r, wr, lane, v);
+    se_load<VPT, WPR, NT>(a, r, wr, lane, v);
     se_process<VPT, WPR>(a, v, row, valid, w, wr, lane, red);
 }
 
@@ -290,6 +292,14 @@ EE_DEV void softmax_entropy_generic(const EeSoftmaxArgs& a) {
         __attribute__((amdgpu_waves_per_eu(8))) eek_softmax_entropy_v##V##_w##W(EeSoftmaxArgs a) { \
         softmax_entropy_vec<V, W>(a);                                                          \
     }
+// Non-temporal twins of the multi-wave layouts, for logits too large to have
+// stayed in cache (the launcher's choice): from HBM 3-5% faster, from the caches
+// ~13% slower (configs 0-2, measured both ways).
+#define EE_SE_VEC_NT(V, W, EPU)                                                                \
+    extern "C" __global__ void __launch_bounds__(SeGeom<W>::BLOCK)                             \
+        __attribute__((amdgpu_waves_per_eu(EPU))) eek_softmax_entropy_v##V##_w##W##_nt(EeSoftmaxArgs a) { \
+        softmax_entropy_vec<V, W, true>(a);                                                    \
+    }
 #define EE_SE_VEC_W(V) EE_SE_VEC(V, 1) EE_SE_VEC(V, 2) EE_SE_VEC(V, 3) EE_SE_VEC(V, 4) \
                        EE_SE_VEC(V, 5) EE_SE_VEC(V, 6) EE_SE_VEC(V, 7) EE_SE_VEC(V, 8)
 EE_SE_VEC_W(1)
@@ -316,6 +326,13 @@ EE_SE_VEC(5, 8)
 EE_SE_VEC(6, 8)
 EE_SE_VEC(7, 8)
 EE_SE_VEC(8, 8)
+EE_SE_VEC_NT(4, 2, 8)
+EE_SE_VEC_NT(4, 4, 8)
+EE_SE_VEC_NT(4, 8, 8)
+EE_SE_VEC_NT(5, 8, 1)
+EE_SE_VEC_NT(6, 8, 1)
+EE_SE_VEC_NT(7, 8, 1)
+EE_SE_VEC_NT(8, 8, 1)
 
 extern "C" __global__ void __launch_bounds__(EE_BLOCK) eek_softmax_entropy_generic(EeSoftmaxArgs a) {
     softmax_entropy_generic(a);

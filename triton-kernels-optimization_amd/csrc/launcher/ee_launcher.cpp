@@ -457,6 +457,8 @@ EE_EXPORT int ee_engine_set_option(ee_engine* eng, const char* key, int64_t valu
     const std::string k(key);
     if (k == "se_wpr") {
         if (value < 0 || value > 8) return fail(EE_ERR_INVALID_ARG, k + " must be 0 (auto) or 1..8");
+    } else if (k == "se_nt") {
+        if (value < 0 || value > 2) return fail(EE_ERR_INVALID_ARG, k + " must be 0 (auto), 1 (off) or 2 (on)");
     } else if (k == "se_rpw") {
         if (value != 0 && value != 1 && value != 2 && value != 4)
             return fail(EE_ERR_INVALID_ARG, k + " must be 0 (auto), 1, 2 or 4");
@@ -496,6 +498,12 @@ EE_EXPORT int ee_softmax_entropy(ee_engine* eng, const void* x, void* p, float* 
         return fail(EE_ERR_INVALID_ARG, "misaligned pointer");
     if (rows == 0) return EE_OK;
     EeSoftmaxArgs a{(const uint16_t*)x, (uint16_t*)p, h, tier, rows, ld_x, ld_p, S, causal, tau_low, tau_high};
+    // Non-temporal loads of the logits (the _nt kernels of the multi-wave layouts; option
+    // "se_nt": 0 auto, 1 off, 2 on): from HBM they are 3-5% faster, from the caches ~13%
+    // slower (measured at configs 0-2), so automatic takes them where the logits alone are
+    // 64 MiB or more, too large to have stayed in the 256 MB MALL beside the probabilities.
+    const int64_t nt_opt = opt(eng, "se_nt");
+    const bool nt = nt_opt == 2 || (nt_opt == 0 && rows * ld_x * 2 >= (int64_t(64) << 20));
     const bool vec_ok = aligned(x, 16) && aligned(p, 16) && ld_x % 8 == 0 && (p == nullptr || ld_p % 8 == 0);
     int vpt = 0, wpr = 0;
     if (vec_ok && pick_se_cfg(S, rows, opt(eng, "se_wpr"), vpt, wpr)) {
@@ -510,7 +518,8 @@ EE_EXPORT int ee_softmax_entropy(ee_engine* eng, const void* x, void* p, float* 
             if (rpw > 1 && find_kernel(eng, rname))
                 return launch(eng, rname, cdiv(rows, 4LL * rpw), 1, EE_BLOCK, a, stream);
         }
-        const std::string name = "eek_softmax_entropy_v" + std::to_string(vpt) + "_w" + std::to_string(wpr);
+        std::string name = "eek_softmax_entropy_v" + std::to_string(vpt) + "_w" + std::to_string(wpr);
+        if (nt && find_kernel(eng, name + "_nt")) name += "_nt";
         const int rpb = wpr == 1 ? 4 : (wpr == 2 ? 2 : 1);      // rows per block (kernel's SeGeom)
         const Kernel* k = find_kernel(eng, name);
         return launch(eng, name, cdiv(rows, rpb), 1, k ? k->block : rpb * wpr * 64, a, stream);
