@@ -315,3 +315,47 @@ def test_gemm256_routed_swiglu(ee, orc, M, K, F, tn):
     with _Options(gemm_tile=128):
         ref = ee.routed_linear(x, pw, idx, counts, swiglu=True)
     assert torch.equal(fused.view(torch.int16), ref.view(torch.int16))
+
+
+# ---------------------------------------------------------------------------- 128-tile pipelines
+
+def _sweep128_cases(n=16, seed=77):
+    """Seeded ragged shapes for the 128 x 128-tile pipelines: grids of at most
+    one tile per CU (the 8-wave INT8 kernel's automatic range) and K of 1-12
+    stages (the 8-wave kernel peels its first stage and its last five)."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(n):
+        M = int(rng.integers(1, 700))
+        N = int(rng.integers(1, 400)) * 4
+        K = int(rng.integers(1, 13)) * 128
+        out.append((M, K, N))
+    return out
+
+
+@pytest.mark.parametrize("M,K,N", _sweep128_cases())
+def test_gemm128_seeded_sweep(ee, orc, M, K, N):
+    """The 128-tile INT8 and FP16 pipelines on seeded shapes: the 8-wave INT8
+    kernel (16x16x64 MFMAs) gives the oracle's int32 accumulators and the
+    loader-wave kernel's (32x32x32) fp16 outputs bit for bit; FP16 on the
+    loader-wave kernel (16x16x32) equals the 256-tile kernel bit for bit and,
+    like the 8-wave FP16 kernel (its own split-K f32 order), is within 1e-2 of
+    the float64 recompute."""
+    A, B, bs, pw = _operands(ee, orc, M, K, N, M * 7 + K + N)
+    codes, a_s = orc.quant_act_i8(A, "dispatcher")
+    acc = torch.empty((M, N), dtype=torch.int32, device="cuda")
+    with _Options(gemm_tile=128, gemm_variant=2):
+        ee.gemm("int8", cuda(codes), pw.i8, cuda(a_s), cuda(bs), acc_out=acc)
+        o8w = host(ee.gemm("int8", cuda(codes), pw.i8, cuda(a_s), cuda(bs)))
+        f16w = host(ee.gemm("fp16", cuda(A), pw.f16))
+    assert np.array_equal(host(acc), orc.gemm_i8_acc(codes, B))
+    with _Options(gemm_tile=128, gemm_variant=1):
+        o8l = host(ee.gemm("int8", cuda(codes), pw.i8, cuda(a_s), cuda(bs)))
+        f16l = host(ee.gemm("fp16", cuda(A), pw.f16))
+    assert np.array_equal(o8w.view(np.uint16), o8l.view(np.uint16))
+    with _Options(gemm_tile=256):
+        f16g = host(ee.gemm("fp16", cuda(A), pw.f16))
+    assert np.array_equal(f16l.view(np.uint16), f16g.view(np.uint16))
+    ref = orc.gemm_w8a16_f64(A, B, bs)
+    check_close_f64(f16l, ref)
+    check_close_f64(f16w, ref)
