@@ -1052,9 +1052,8 @@ EE_DEV void epilogue_blk_direct16(const EeGemmArgs& g, const typename P::acc_t (
 
 template <int KIND, int SW = 0>
 struct Gemm8 {
-    // INT8: 16x16x64 MFMAs on 64-byte slices, or (SwiGLU, whose epilogue
-    // registers leave no room for 64-byte fragments) 32x32x32 on 32-byte slices
-    typedef std::conditional_t<KIND == EE_GEMM_I8, std::conditional_t<SW != 0, PipeI8x32, PipeI8x16>, Pipe<KIND>> P;
+    // INT8: 16x16x64 MFMAs on 64-byte slices (PipeI8x16)
+    typedef std::conditional_t<KIND == EE_GEMM_I8, PipeI8x16, Pipe<KIND>> P;
     typedef typename P::acc_t acc_t;
     static constexpr int ESZ = (KIND == EE_GEMM_F16) ? 2 : 1;
     static constexpr int LOADS = 4;                    // DMA instructions per wave per stage

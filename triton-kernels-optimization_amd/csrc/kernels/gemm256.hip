@@ -3,11 +3,12 @@
 //
 //   EE_GEMM_I8 : int8 x int8 -> int32 (v_mfma_i32_16x16x64_i8, four per 32x32 block
 //                and 64-byte K slice: the same MFMA time as the 32x32x32 form at a
-//                lower power draw; SwiGLU keeps 32x32x32 on 32-byte slices);
+//                lower power draw);
 //                C = fp16((f32(acc) * a_scale[m]) * b_scale[n])     (EE/python/kernels.py:50-110)
 //   EE_GEMM_F8 : e4m3 x e4m3 -> f32 (v_mfma_scale_f32_32x32x64_f8f6f4);
 //                C = fp16((acc * a_scale[m]) * b_scale[n])           (EE/python/kernels.py:118-180)
-//   EE_GEMM_F16: fp16 x fp16 -> f32 (v_mfma_f32_32x32x16_f16); C = fp16(acc)
+//   EE_GEMM_F16: fp16 x fp16 -> f32 (v_mfma_f32_16x16x32_f16, four per 32x32 block
+//                and 64-byte K slice); C = fp16(acc)
 //                (EE/python/kernels.py:192-246, W8A16 weights pre-dequantised)
 //
 // Why a 256 x 256 tile.  A CU computing a T x T tile streams 2T bytes of
@@ -64,9 +65,8 @@ template <int KIND, int SW, class Seq, int TN = 256>
 struct G256 {
     typedef G2Geom<TN> GE;
     static constexpr int NI = GE::NI, WR = GE::WR;
-    // INT8: 16x16x64 MFMAs (PipeI8x16), or 32-byte 32x32x32 slices for SwiGLU,
-    // whose epilogue registers leave no room for 64-byte slices
-    typedef std::conditional_t<KIND == EE_GEMM_I8, std::conditional_t<SW != 0, PipeI8x32, PipeI8x16>, Pipe<KIND>> P;
+    // INT8: 16x16x64 MFMAs on 64-byte slices (PipeI8x16)
+    typedef std::conditional_t<KIND == EE_GEMM_I8, PipeI8x16, Pipe<KIND>> P;
     typedef typename P::acc_t acc_t;
     typedef typename P::frag_t frag_t;
     static constexpr int ESZ = (KIND == EE_GEMM_F16) ? 2 : 1;
