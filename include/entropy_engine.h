@@ -94,9 +94,10 @@ int ee_engine_destroy(ee_engine* eng);
  * linear's tier grid) run as persistent grids, one workgroup per CU walking
  * its tiles with the stage ring running across tile boundaries; 1 turns that
  * off, n >= 2 forces it with min(n, tiles) workgroups.  Same bits either way.
- * "gemm_tile": 256 x 256-tile persistent kernels (plain and routed) for GEMMs
- * whose 128 x 128 grid has more tiles than CUs (automatic; same bits); 128
- * forbids them, 256 forces them at every size.
+ * "gemm_tile": 256 x 256-tile persistent kernels for plain GEMMs whose
+ * 128 x 128 grid has more tiles than CUs, and for routed linears where the
+ * 256 x 256 grid takes at most 1/2.1 of the 128 x 128 grid's rounds of the CUs
+ * (automatic; same bits); 128 forbids them, 256 forces them at every size.
  * "gemm_tile_n": the width of those 256-row tiles: automatic (plain GEMMs take
  * 256 x 128 where 256 x 256 tiles would keep at most half the CUs busy; the
  * routed grid stays at 256), or 128 / 256 forced.  Same bits either way. */

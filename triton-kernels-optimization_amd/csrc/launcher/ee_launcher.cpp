@@ -867,7 +867,19 @@ static int routed_impl(ee_engine* eng, const void* x, int64_t ld_x, int32_t M, i
         const int64_t tile_opt = opt(eng, "gemm_tile");
         const bool off32 = std::max<int64_t>((int64_t)M * ld_x * 2, (int64_t)M * K) + 2 * K < (int64_t(1) << 32) &&
                            255 * 2 * (int64_t)K + 2 * K < (int64_t(1) << 32);
-        if (!ra.f16_w8 && tile_opt != 128 && off32 && (tile_opt == 256 || slots > eng->cus)) {
+        // Automatic choice: 256 x 256 tiles where they take fewer rounds of the CUs
+        // at the cost of a round, ~2.1x that of a 128 x 128 round for 4x the work
+        // (measured at K = 2048..5632: INT8 15 against 31 us at K = 2048, 31 against
+        // 60 at K = 5632).  Tile counts take one partial M-tile beside the full ones
+        // (the tiers' row counts are on the device).  Same bits either way.  Measured
+        // on a 20/40/40 % tier mix, 128 tiles against 256: 1024 x 4096 x 4096 47 against
+        // 59 us, 2048 x 5632 x 2048 60 against 82, 128 x 2048 x 11264 SwiGLU 31 against
+        // 34 (all INT8: 23 / 47, 30 / 60, 12 / 34).
+        const int64_t cu = std::max(1, eng->cus);
+        const int64_t r128 = cdiv((cdiv(M, 128) + 1) * cdiv(N, 128), cu);
+        const int64_t r256 = cdiv((cdiv(M, 256) + 1) * cdiv(N, 256), cu);
+        const bool big = 10 * r128 > 21 * r256;
+        if (!ra.f16_w8 && tile_opt != 128 && off32 && (tile_opt == 256 || big)) {
             // (256 x 256 tiles unless option gemm_tile_n = 128: the tiers' row counts, which
             // decide the rounds, are on the device)
             std::string n256 = opt(eng, "gemm_tile_n") == 128 ? "eek_gemm256n128_routed" : "eek_gemm256_routed";
