@@ -317,6 +317,33 @@ def test_gemm256_routed_swiglu(ee, orc, M, K, F, tn):
     assert torch.equal(fused.view(torch.int16), ref.view(torch.int16))
 
 
+# (M, K, N, swiglu): the automatic routed grid is 128 x 128 tiles for the first three
+# (1-2 rounds of 128-tiles against 1 round of 256-tiles on 256 CUs) and 256 x 256
+# tiles for the last two (3+ rounds against 1)
+@pytest.mark.parametrize("M,K,N,sw", [(128, 256, 11264, True), (1024, 512, 4096, False), (2048, 384, 2048, False),
+                                      (4096, 256, 2048, False), (4096, 256, 2816, True)])
+@pytest.mark.parametrize("mix", [(1.0, 0.0, 0.0), (0.2, 0.4, 0.4)])
+def test_routed_automatic_tile_choice(ee, orc, M, K, N, sw, mix):
+    """The routed linear's automatic tile size (from the rounds of the CUs each
+    grid takes) gives the bits of both forced sizes, plain and SwiGLU, with all
+    rows INT8 and with a 20/40/40 % tier mix."""
+    rng = np.random.default_rng(M + K + N + int(sw))
+    W = (rng.standard_normal((N, K)) / np.sqrt(K)).astype(np.float16)
+    codes, scale = ee.quantize_weight_codes(cuda(W))
+    if sw:
+        codes, scale = ee.interleave_gate_up(codes), ee.interleave_gate_up(scale)
+    pw = ee.PackedWeight(codes, scale).materialize()
+    x = cuda(rng.standard_normal((M, K)).astype(np.float16))
+    H = rng.choice(np.array([0.2, 1.0, 3.0], np.float32), M, p=list(mix))
+    _, idx, counts = ee.route(cuda(H), 0.41, 1.68)
+    outs = []
+    for tile in (0, 128, 256):
+        with _Options(gemm_tile=tile):
+            outs.append(host(ee.routed_linear(x, pw, idx, counts, swiglu=sw)).view(np.uint16))
+    assert np.array_equal(outs[0], outs[1])
+    assert np.array_equal(outs[0], outs[2])
+
+
 # ---------------------------------------------------------------------------- 128-tile pipelines
 
 def _sweep128_cases(n=16, seed=77):
