@@ -69,18 +69,10 @@ struct Lay32 {
 // hold K bytes 0-31 of the slice, lanes 32-63 bytes 32-63; A and B fragments
 // pair up the same K bytes, and int32 sums are exact in any order).  64 clocks
 // of MFMA per block and slice, against 32 for one 32-byte slice, cover each
-// batch of fragment reads twice as long.  The 32-byte form stays for kernels
-// whose registers the 32-byte fragments would overflow.
+// batch of fragment reads twice as long.  (The 8-wave and 256-tile kernels run
+// the same slices as 16x16x64 MFMAs: PipeI8x16 below.)
 // Fragment chunks: lane l reads 16-byte chunk sl * SB/16 + (l >> 5) * LSTEP of its
 // row and, when CPF == 2, the chunk CSTEP after it.
-struct PipeI8x32 : Lay32 {                       // 32x32x32 i8: 32 K bytes per slice, 16 B per lane
-    static constexpr int SB = 32, CPF = 1, LSTEP = 1, CSTEP = 0;
-    typedef u32x4 frag_t;
-    typedef i32x16 acc_t;
-    static EE_DEV acc_t mma(const frag_t& b, const frag_t& a, const acc_t& c) {
-        return __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(i32x4, b), __builtin_bit_cast(i32x4, a), c, 0, 0, 0);
-    }
-};
 struct PipeI8x64 : Lay32 {                       // 2 x 32x32x32 i8: 64 K bytes per slice, 32 B per lane
     static constexpr int SB = 64, CPF = 2, LSTEP = 2, CSTEP = 1;
     typedef i32x8 frag_t;
