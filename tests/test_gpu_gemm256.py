@@ -317,6 +317,33 @@ def test_gemm256_routed_swiglu(ee, orc, M, K, F, tn):
     assert torch.equal(fused.view(torch.int16), ref.view(torch.int16))
 
 
+# (M, K, N): 128-tile routed grids that fit one round of the CUs with every FP16 tile
+# split into two 128 x 64 halves (N % 128 of 0, 64, 32, 96, 4: the last half past N
+# or partial)
+@pytest.mark.parametrize("M,K,N", [(1024, 512, 2048), (700, 256, 1984), (300, 384, 1056), (129, 128, 96),
+                                   (1000, 640, 1540)])
+def test_routed_fp16_half_tiles(ee, orc, M, K, N):
+    """The routed grid's FP16 tiles as 128 x 64 halves: every row equals its
+    tier's un-routed GEMM bit for bit (the FP16 one runs whole 128 x 128 tiles),
+    and FP16 rows are within 1e-2 of the oracle's float64 recompute."""
+    rng = np.random.default_rng(M + N)
+    X = rng.standard_normal((M, K)).astype(np.float16)
+    B, bs = weights(orc, rng, N, K)
+    H = rng.choice(np.array([0.2, 1.0, 3.0], np.float32), M, p=[0.2, 0.4, 0.4])
+    pw = ee.prepare_weight(cuda(B), cuda(bs)).materialize()
+    x = cuda(X)
+    tier, idx, counts = ee.route(cuda(H), 0.41, 1.68)
+    with _Options(gemm_tile=128):
+        out = host(ee.routed_linear(x, pw, idx, counts))
+    t = host(tier)
+    assert (t == 2).any()
+    for k, fn in enumerate((ee.triton_int8_gemm, ee.triton_fp8_gemm, ee.triton_fp16_gemm)):
+        ref = host(fn(x, cuda(B), cuda(bs)))
+        assert np.array_equal(out[t == k].view(np.uint16), ref[t == k].view(np.uint16)), f"tier {k}"
+    rows = np.nonzero(t == 2)[0][[0, -1]]
+    check_close_f64(out[rows], orc.triton_fp16_gemm_f64(X[rows], B, bs))
+
+
 # (M, K, N, swiglu): the automatic routed grid is 128 x 128 tiles for the first three
 # (1-2 rounds of 128-tiles against 1 round of 256-tiles on 256 CUs) and 256 x 256
 # tiles for the last two (3+ rounds against 1)

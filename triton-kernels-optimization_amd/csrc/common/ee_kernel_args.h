@@ -87,6 +87,8 @@ struct EeRoutedGemmArgs {
     EeGemmArgs t[3];
     int32_t mt_max;
     int32_t f16_w8;         // 1: the FP16 tier runs the 8-wave pipeline (as ee_gemm does)
+    int32_t f16_half_cus;   // > 0: FP16 tiles may run as 128 x 64 halves on this many CUs (eek_gemm_routed)
+    int32_t pad_;
 };
 
 // Internal quantiser mode of the routed linear: partition slots below counts[0]

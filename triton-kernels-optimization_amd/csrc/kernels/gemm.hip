@@ -161,9 +161,11 @@ using Frags = FragsP<Pipe<KIND>>;
 // chunk slice * SB/16 + (l >> 5) * LSTEP (and the chunk CSTEP after it when
 // CPF == 2): lanes 0-31 and 32-63 cover the two K halves of each MFMA's operand.
 // 16x16 pipes (SUB16): rows (l & 15) and 16 + (l & 15) of each block, chunk 4 slice + (l >> 4).
-template <int KIND>
+// JB: 32-column B blocks of the wave (2, or 1 in the 64-wide FP16 tiles).
+template <int KIND, int JB = 2>
 EE_DEV void read_frags(const uint8_t* s, int slice, int wm, int wn, int lane, Frags<KIND>& f) {
     typedef Pipe<KIND> P;
+    static_assert(JB == 2 || P::SUB16, "one-block waves are the 16x16 pipes'");
     if constexpr (P::SUB16) {
         const int c = slice * 4 + (lane >> 4), r = lane & 15;
 #pragma unroll
@@ -171,8 +173,14 @@ EE_DEV void read_frags(const uint8_t* s, int slice, int wm, int wn, int lane, Fr
             const int ra = wm * 64 + i * 32 + r, rb = BM + wn * 64 + i * 32 + r;   // swz(x + 16) == swz(x)
             f.a[i].h[0] = *(const i32x4*)(s + lds_off(ra, c));
             f.a[i].h[1] = *(const i32x4*)(s + lds_off(ra + 16, c));
-            f.b[i].h[0] = *(const i32x4*)(s + lds_off(rb, c));
-            f.b[i].h[1] = *(const i32x4*)(s + lds_off(rb + 16, c));
+            if constexpr (JB == 2) {
+                f.b[i].h[0] = *(const i32x4*)(s + lds_off(rb, c));
+                f.b[i].h[1] = *(const i32x4*)(s + lds_off(rb + 16, c));
+            } else if (i == 0) {                      // the wave's one block: B rows 32 wn ..
+                const int rb1 = BM + wn * 32 + r;
+                f.b[0].h[0] = *(const i32x4*)(s + lds_off(rb1, c));
+                f.b[0].h[1] = *(const i32x4*)(s + lds_off(rb1 + 16, c));
+            }
         }
     } else {
         const int r = lane & 31;
@@ -193,21 +201,21 @@ EE_DEV void read_frags(const uint8_t* s, int slice, int wm, int wn, int lane, Fr
     }
 }
 
-template <int KIND>
+template <int KIND, int JB = 2>
 EE_DEV void mma_all(const Frags<KIND>& f, typename Pipe<KIND>::acc_t (&acc)[2][2]) {
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = Pipe<KIND>::mma(f.b[j], f.a[i], acc[i][j]);
+        for (int j = 0; j < JB; ++j) acc[i][j] = Pipe<KIND>::mma(f.b[j], f.a[i], acc[i][j]);
 }
 
 // Scheduling groups for one slice: all LDS reads of the next slice first (4
 // ds_read_b128, 8 for the 32-byte e4m3 fragments), then the 4 MFMAs of the
 // current slice, which cover the reads' latency before the next slice waits.
-template <int KIND>
+template <int KIND, int JB = 2>
 EE_DEV void interleave() {
-    __builtin_amdgcn_sched_group_barrier(0x100, 4 * Pipe<KIND>::CPF, 0);   // DS read
-    __builtin_amdgcn_sched_group_barrier(0x008, Pipe<KIND>::SUB16 ? 16 : 4, 0);   // MFMA
+    __builtin_amdgcn_sched_group_barrier(0x100, (2 + JB) * Pipe<KIND>::CPF, 0);   // DS read
+    __builtin_amdgcn_sched_group_barrier(0x008, (Pipe<KIND>::SUB16 ? 8 : 2) * JB, 0);   // MFMA
 }
 
 // 32x32 epilogue: lane l, register r of block (i, j) holds
@@ -359,9 +367,11 @@ EE_DEV void epilogue32_lds_swiglu(const EeGemmArgs& g, const typename P::acc_t (
     }
 }
 
-template <int KIND, int SW, class P = Pipe<KIND>>
+// JB = 1: the wave's 64 x 32 block of a 64-wide FP16 tile (columns n0 + 32 wn ..).
+template <int KIND, int SW, class P = Pipe<KIND>, int JB = 2>
 EE_DEV void epilogue32_lds(const EeGemmArgs& g, const typename P::acc_t (&acc)[2][2], const TileScales& sc,
                            uint8_t* tile, int m0, int n0, int M, int64_t off, int wm, int wn, int lane) {
+    static_assert(JB == 2 || (P::SUB16 && SW == 0), "one-block waves: 16x16 FP16, no SwiGLU");
     if constexpr (SW) {
         epilogue32_lds_swiglu<KIND, P>(g, acc, sc, tile, m0, n0, M, off, wm, wn, lane);
         return;
@@ -371,7 +381,7 @@ EE_DEV void epilogue32_lds(const EeGemmArgs& g, const typename P::acc_t (&acc)[2
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
-            for (int j = 0; j < 2; ++j)
+            for (int j = 0; j < JB; ++j)
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     const int rl = i * 32 + P::row_of(q, lane), cl = j * 32 + P::col_of(q, lane);
@@ -410,13 +420,14 @@ EE_DEV void epilogue32_lds(const EeGemmArgs& g, const typename P::acc_t (&acc)[2
         }
     }
     }
-    // 2. read back row-contiguous and store (each wave reads only its own region)
+    // 2. read back row-contiguous and store (each wave reads only its own region:
+    //    64 rows of 4 JB chunks of 16 bytes)
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        const int rl = k * 8 + (lane >> 3), ch = lane & 7;
+    for (int k = 0; k < 4 * JB; ++k) {
+        const int rl = k * (16 / JB) + (lane >> (JB + 1)), ch = lane & (4 * JB - 1);
         const u32x4 v = *(const u32x4*)(tile + lds_off(rl, ch));
         const int m = m0 + wm * 64 + rl;
-        const int n = n0 + wn * 64 + ch * 8;
+        const int n = n0 + wn * (32 * JB) + ch * 8;
         if (m >= M || n >= g.N) continue;
         const int64_t crow = g.c_idx ? (int64_t)g.c_idx[off + m] : (int64_t)m;
         uint16_t* dst = g.c + crow * g.ldc + n;
@@ -442,20 +453,29 @@ EE_DEV void epilogue32_lds(const EeGemmArgs& g, const typename P::acc_t (&acc)[2
 
 // One 128 x 128 C tile (tile coordinates tm, tn) of the pipelined GEMM;
 // smem is the workgroup's NSTAGE * LDS_STAGE bytes of LDS (1 KB aligned).
-template <int KIND, int SW = 0>
+// TNW = 64: a 128 x 64 tile (tn counts 64-column tiles), FP16 without SwiGLU only:
+// each compute wave owns 64 x 32, the loaders fetch 64 B rows.  The same MFMAs on
+// the same K slices in the same order as the 128-wide tile, so the same bits.
+template <int KIND, int SW = 0, int TNW = BN>
 EE_DEV void gemm_tile(const EeGemmArgs& g, int tm, int tn, uint8_t* smem) {
     typedef Pipe<KIND> P;
     typedef typename P::acc_t acc_t;
+    static_assert(TNW == BN || (TNW == 64 && KIND == EE_GEMM_F16 && SW == 0), "64-wide tiles: FP16, no SwiGLU");
     constexpr int ESZ = (KIND == EE_GEMM_F16) ? 2 : 1;
-    constexpr int LOADS = 8;                          // DMA instructions per loader wave per stage (4 A + 4 B)
+    constexpr int BG = TNW / 32;                      // B row groups of 8 per loader wave
+    constexpr int JB = TNW / 64;                      // 32-column blocks per compute wave
+    constexpr int LOADS = 4 + BG;                     // DMA instructions per loader wave per stage (4 A + BG B)
     constexpr int NSL = BKB / P::SB;                  // K slices per stage (4 or 2)
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int M = g.counts ? g.counts[g.tier] : g.M;
     const int64_t off = g.counts ? tier_offset(g.counts, g.tier) : 0;
-    const int m0 = tm * BM, n0 = tn * BN;
+    const int m0 = tm * BM, n0 = tn * TNW;
     if (m0 >= M) return;                              // whole workgroup, before any barrier
+    if constexpr (TNW != BN) {
+        if (n0 >= g.N) return;
+    }
     const int nk = (int)((int64_t)g.K * ESZ / BKB);   // K * ESZ is a multiple of BKB here
 
     if (wave >= 4) {
@@ -473,8 +493,14 @@ EE_DEV void gemm_tile(const EeGemmArgs& g, int tm, int tn, uint8_t* smem) {
             const int m = min(m0 + r, M - 1);
             const int64_t ar = g.a_idx ? (int64_t)g.a_idx[off + m] : off + m;
             pa[i] = (const uint8_t*)g.a + ar * g.lda * ESZ + lchunk * 16;
-            const int n = min(n0 + r, g.N - 1);
-            pb[i] = (const uint8_t*)g.b + (int64_t)n * g.ldb * ESZ + lchunk * 16;
+            if constexpr (BG == 4) {
+                const int n = min(n0 + r, g.N - 1);
+                pb[i] = (const uint8_t*)g.b + (int64_t)n * g.ldb * ESZ + lchunk * 16;
+            } else if (i < BG) {                      // B row groups 2 lw, 2 lw + 1
+                const int rb = (lw * BG + i) * 8 + lrow;
+                const int n = min(n0 + rb, g.N - 1);
+                pb[i] = (const uint8_t*)g.b + (int64_t)n * g.ldb * ESZ + ((lane & 7) ^ swz(rb)) * 16;
+            }
         }
         auto issue = [&](int kt) {
             const uint32_t s = lds_addr(smem) + (uint32_t)((kt % NSTAGE) * LDS_STAGE);
@@ -483,7 +509,8 @@ EE_DEV void gemm_tile(const EeGemmArgs& g, int tm, int tn, uint8_t* smem) {
             for (int i = 0; i < 4; ++i) {
                 const int grp = lw * 4 + i;
                 dma16(pa[i] + kb, s + grp * 8 * BKB);
-                dma16(pb[i] + kb, s + (BM + grp * 8) * BKB);
+                if constexpr (BG == 4) dma16(pb[i] + kb, s + (BM + grp * 8) * BKB);
+                else if (i < BG) dma16(pb[i] + kb, s + (BM + (lw * BG + i) * 8) * BKB);
             }
         };
 #pragma unroll
@@ -537,7 +564,7 @@ EE_DEV void gemm_tile(const EeGemmArgs& g, int tm, int tn, uint8_t* smem) {
             Frags<KIND>& cur = (sl & 1) ? f1 : f0;
             Frags<KIND>& nxt = (sl & 1) ? f0 : f1;
             if (sl + 1 < NSL) {
-                read_frags<KIND>(s, sl + 1, wm, wn, lane, nxt);
+                read_frags<KIND, JB>(s, sl + 1, wm, wn, lane, nxt);
             } else if (more) {
                 // keep the previous slice's MFMAs ahead of this wait: they cover its latency
                 __builtin_amdgcn_sched_barrier(0);
@@ -545,23 +572,26 @@ EE_DEV void gemm_tile(const EeGemmArgs& g, int tm, int tn, uint8_t* smem) {
                 asm volatile("" ::: "memory");
                 __builtin_amdgcn_s_barrier();         // barrier kt+1: stage kt+1 has landed
                 asm volatile("" ::: "memory");
-                read_frags<KIND>(smem + ((kt + 1) % NSTAGE) * LDS_STAGE, 0, wm, wn, lane, nxt);
+                read_frags<KIND, JB>(smem + ((kt + 1) % NSTAGE) * LDS_STAGE, 0, wm, wn, lane, nxt);
             }
-            mma_all<KIND>(cur, acc);
-            interleave<KIND>();
+            mma_all<KIND, JB>(cur, acc);
+            interleave<KIND, JB>();
         }
     };
     __builtin_amdgcn_s_barrier();                     // barrier 0: stage 0 has landed
     asm volatile("" ::: "memory");
-    read_frags<KIND>(smem, 0, wm, wn, lane, f0);
+    read_frags<KIND, JB>(smem, 0, wm, wn, lane, f0);
     for (int kt = 0; kt + 1 < nk; ++kt) stage(kt, true);
     stage(nk - 1, false);
-    if (g.acc) {
+    // Buffer nk % NSTAGE is free: no DMA is in flight after the last barrier
+    // (the loaders waited for all of theirs before it), and its last stage,
+    // nk - NSTAGE, was read before barrier nk - NSTAGE + 1.
+    if constexpr (TNW != BN) {                        // FP16: no int32 accumulator output
+        uint8_t* tile = smem + (nk % NSTAGE) * LDS_STAGE + wave * (64 * BKB);
+        epilogue32_lds<KIND, SW, P, JB>(g, acc, sc, tile, m0, n0, M, off, wm, wn, lane);
+    } else if (g.acc) {
         epilogue32<KIND>(g, acc, m0, n0, M, off, wm, wn, lane);
     } else {
-        // Buffer nk % NSTAGE is free: no DMA is in flight after the last barrier
-        // (the loaders waited for all of theirs before it), and its last stage,
-        // nk - NSTAGE, was read before barrier nk - NSTAGE + 1.
         uint8_t* tile = smem + (nk % NSTAGE) * LDS_STAGE + wave * (64 * BKB);
         epilogue32_lds<KIND, SW>(g, acc, sc, tile, m0, n0, M, off, wm, wn, lane);
     }
@@ -1573,6 +1603,11 @@ EE_GEMM_ENTRY(eek_gemm_w8a16, body_w8a16)
 // an M-tile never mixes tiers; workgroups past the last tile exit at once.
 // The grid holds r.mt_max = ceil(M / 128) + 2 M-tile slots (the sum of the
 // three ceilings is at most that) times ceil(N / 128) N-tiles.
+// FP16 halves (r.f16_half_cus > 0, no SwiGLU): an FP16 tile costs two 1-byte
+// tiles, so where the grid with each FP16 tile split into two 128 x 64 tiles
+// still fits one round of the r.f16_half_cus CUs, the FP16 tier takes two M-tile
+// indices per M-tile, one per column half (mt_max then counts them: at most
+// 2 ceil(M / 128) + 2).  Same bits: the halves sum K exactly as the whole tile.
 template <int SW>
 EE_DEV void gemm_routed(const EeRoutedGemmArgs& r) {
     __shared__ __attribute__((aligned(1024))) uint8_t smem[NSTAGE * LDS_STAGE];
@@ -1582,6 +1617,14 @@ EE_DEV void gemm_routed(const EeRoutedGemmArgs& r) {
     const int T2 = (counts[2] + BM - 1) / BM;
     int tm, tn;
     tile_of((int)blockIdx.x, (int)gridDim.x, r.mt_max, tm, tn);
+    if constexpr (SW == 0) {
+        const int nN = (r.t[2].N + BN - 1) / BN;
+        if (r.f16_half_cus > 0 && T2 > 0 && (T0 + T1 + 2 * T2) * nN <= r.f16_half_cus && tm >= T0 + T1) {
+            const int v = tm - T0 - T1;
+            if (v < 2 * T2) gemm_tile<EE_GEMM_F16, 0, 64>(r.t[2], v >> 1, 2 * tn + (v & 1), smem);
+            return;
+        }
+    }
     if (tm < T0) gemm_tile<EE_GEMM_I8, SW>(r.t[0], tm, tn, smem);
     else if (tm < T0 + T1) gemm_tile<EE_GEMM_F8, SW>(r.t[1], tm - T0, tn, smem);
     else if (tm < T0 + T1 + T2) {
