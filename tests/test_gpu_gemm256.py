@@ -319,9 +319,10 @@ def test_gemm256_routed_swiglu(ee, orc, M, K, F, tn):
 
 # (M, K, N): 128-tile routed grids that fit one round of the CUs with every FP16 tile
 # split into two 128 x 64 halves (N % 128 of 0, 64, 32, 96, 4: the last half past N
-# or partial)
+# or partial), and one whose whole-tile grid takes between one and two rounds
+# (2048 rows: 4 + 7 + 7 M-tiles x 16)
 @pytest.mark.parametrize("M,K,N", [(1024, 512, 2048), (700, 256, 1984), (300, 384, 1056), (129, 128, 96),
-                                   (1000, 640, 1540)])
+                                   (1000, 640, 1540), (2048, 256, 2048)])
 def test_routed_fp16_half_tiles(ee, orc, M, K, N):
     """The routed grid's FP16 tiles as 128 x 64 halves: every row equals its
     tier's un-routed GEMM bit for bit (the FP16 one runs whole 128 x 128 tiles),

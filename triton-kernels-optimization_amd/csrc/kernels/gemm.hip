@@ -1604,10 +1604,15 @@ EE_GEMM_ENTRY(eek_gemm_w8a16, body_w8a16)
 // The grid holds r.mt_max = ceil(M / 128) + 2 M-tile slots (the sum of the
 // three ceilings is at most that) times ceil(N / 128) N-tiles.
 // FP16 halves (r.f16_half_cus > 0, no SwiGLU): an FP16 tile costs two 1-byte
-// tiles, so where the grid with each FP16 tile split into two 128 x 64 tiles
-// still fits one round of the r.f16_half_cus CUs, the FP16 tier takes two M-tile
-// indices per M-tile, one per column half (mt_max then counts them: at most
-// 2 ceil(M / 128) + 2).  Same bits: the halves sum K exactly as the whole tile.
+// tiles, so the FP16 tier takes two M-tile indices per M-tile, one per 128 x 64
+// column half (mt_max then counts them: at most 2 ceil(M / 128) + 2), where the
+// grid with the halves fits one round of the r.f16_half_cus CUs, or where the
+// whole-tile grid takes between one and two rounds (its FP16 tiles then set a
+// ragged second round).  Measured on MI355X, 20/40/40 % tiers: 1024 x 4096 x
+// 4096 52.5 -> 47.0 us, 2048 x 5632 x 2048 67.4 -> 62.8; but halves that push a
+// one-round grid into a second round lose (1024 x 2048 x 2560: 23.4 -> 27.8),
+// and past two rounds the halves' extra operand stream outweighs the balance.
+// Same bits: the halves sum K exactly as the whole tile.
 template <int SW>
 EE_DEV void gemm_routed(const EeRoutedGemmArgs& r) {
     __shared__ __attribute__((aligned(1024))) uint8_t smem[NSTAGE * LDS_STAGE];
@@ -1619,7 +1624,8 @@ EE_DEV void gemm_routed(const EeRoutedGemmArgs& r) {
     tile_of((int)blockIdx.x, (int)gridDim.x, r.mt_max, tm, tn);
     if constexpr (SW == 0) {
         const int nN = (r.t[2].N + BN - 1) / BN;
-        if (r.f16_half_cus > 0 && T2 > 0 && (T0 + T1 + 2 * T2) * nN <= r.f16_half_cus && tm >= T0 + T1) {
+        const int wf = (T0 + T1 + T2) * nN, wh = (T0 + T1 + 2 * T2) * nN, cus = r.f16_half_cus;
+        if (cus > 0 && T2 > 0 && (wh <= cus || (wf > cus && wf <= 2 * cus)) && tm >= T0 + T1) {
             const int v = tm - T0 - T1;
             if (v < 2 * T2) gemm_tile<EE_GEMM_F16, 0, 64>(r.t[2], v >> 1, 2 * tn + (v & 1), smem);
             return;

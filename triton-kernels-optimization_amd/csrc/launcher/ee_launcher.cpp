@@ -892,11 +892,12 @@ static int routed_impl(ee_engine* eng, const void* x, int64_t ld_x, int32_t M, i
             }
         }
         const int64_t pg = ra.f16_w8 ? persist_grid(eng, slots) : 0;   // its W8A16 tiles run on Gemm8
-        // FP16 tiles as 128 x 64 halves where the grid still fits one round of the CUs
-        // (decided in the kernel from the tier counts): possible only where one M-tile
-        // per 128 rows does.  The grid then holds the halves' M-tile slots too.
+        // FP16 tiles as 128 x 64 halves where the grid then fits one round of the CUs or
+        // the whole-tile grid takes one to two rounds (decided in the kernel from the
+        // tier counts): possible only where one M-tile per 128 rows takes at most two
+        // rounds.  The grid then holds the halves' M-tile slots too.
         int64_t grid = pg > 0 ? pg : slots;
-        if (pg == 0 && !sw && !ra.f16_w8 && cdiv(M, 128) * cdiv(N, 128) <= eng->cus) {
+        if (pg == 0 && !sw && !ra.f16_w8 && cdiv(M, 128) * cdiv(N, 128) <= 2 * (int64_t)eng->cus) {
             ra.mt_max = (int32_t)(2 * cdiv(M, 128) + 2);
             ra.f16_half_cus = eng->cus;
             grid = (int64_t)ra.mt_max * cdiv(N, 128);
