@@ -627,7 +627,7 @@ def main():
 def cpu_baseline(A, W, L):
     """The reference path's arithmetic on this host's cores, over a bounded
     sample of the config-0 workload (~15-25 s of CPU work):
-      * oracle/torch_cpu.py, PyTorch CPU ops (BASELINE.md's CPU plan): INT8 =
+      * oracle/torch_cpu.py, PyTorch CPU ops (the reference's own CPU path): INT8 =
         the dispatcher quantiser + torch._int_mm + epilogue at the full
         1024x4096x4096 shape (`value`); FP8 = e4m3 codes decoded to f32 + an f32
         matmul on a 256-row slice; softmax+entropy in f32 on all 1024 rows;
