@@ -100,9 +100,16 @@ int ee_engine_destroy(ee_engine* eng);
  * (automatic; same bits); 128 forbids them, 256 forces them at every size.
  * "gemm_tile_n": the width of those 256-row tiles: automatic (plain GEMMs take
  * 256 x 128 where 256 x 256 tiles would keep at most half the CUs busy; the
- * routed grid stays at 256), or 128 / 256 forced.  Same bits either way. */
+ * routed grid stays at 256), or 128 / 256 forced.  Same bits either way.
+ * "gemm_waves": the pipeline of those 256-row tiles: 8 waves (each a 128 x 64
+ * block) or 4 waves (each a 128 x 128 block, accumulators in AGPRs; tiles of
+ * at least two K stages); 0 automatic.  Same bits either way. */
 int ee_engine_set_option(ee_engine* eng, const char* key, int64_t value);
 int ee_engine_device(const ee_engine* eng);
+/* Name of the last kernel the calling thread launched through an ee_* entry
+ * point ("" before the first).  A diagnostic with no counterpart in the
+ * reference: tests use it to check which pipeline the launcher picked. */
+const char* ee_last_kernel(void);
 
 /* ---- a1/a2: fused softmax + entropy ---------------------------------------
  * Replaces fused_softmax_entropy_kernel + launcher (EE/python/kernels.py:

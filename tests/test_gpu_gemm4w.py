@@ -1,0 +1,207 @@
+"""GPU parity of the four-wave 256-row-tile GEMMs (eek_gemm4w_*: 256 x 256
+tiles, eek_gemm4wn128_*: 256 x 128; one wave per SIMD owning a 128 x 128 or
+128 x 64 quarter of the tile, accumulators in AGPRs).
+
+They run the 8-wave 256-tile kernels' tiles, deal and per-block K order, so
+every case checks them bit for bit against those kernels (gemm_waves = 8) and
+against the oracle: INT8 int32 accumulators and fp16 outputs bit-exact, FP8 /
+FP16 within 1e-2 of a float64 recompute.  The shapes cover ragged M and N,
+tiles of two to twelve K stages, several tiles per workgroup on forced grids
+(the stage ring and the tile-parity scale areas across tile boundaries, the
+re-issued stages past a workgroup's last tile), grids whose last round runs as
+256 x 128 halves, and the SwiGLU epilogue.  Each case asserts, through
+ee_last_kernel, that the four-wave kernel is the one that ran.
+"""
+import numpy as np
+import pytest
+import torch
+
+from test_gpu_parity import check_close_f64, cuda, host, weights
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def ee():
+    import entropy_engine
+    return entropy_engine
+
+
+def _opt(key, value):
+    from entropy_engine import _lib
+    _lib.check(_lib.lib().ee_engine_set_option(_lib.engine(), key.encode(), value))
+
+
+class _Options:
+    def __init__(self, **kv):
+        self.kv = kv
+
+    def __enter__(self):
+        for k, v in self.kv.items():
+            _opt(k, v)
+
+    def __exit__(self, *exc):
+        for k in self.kv:
+            _opt(k, 0)
+
+
+def _last_kernel():
+    from entropy_engine import _lib
+    return _lib.lib().ee_last_kernel().decode()
+
+
+def _operands(ee, orc, M, K, N, seed):
+    rng = np.random.default_rng(seed)
+    A = rng.standard_normal((M, K)).astype(np.float16)
+    B, bs = weights(orc, rng, N, K)
+    pw = ee.prepare_weight(cuda(B), cuda(bs)).materialize()
+    return A, B, bs, pw
+
+
+def _run_tiers(ee, A, codes, a_s, c8, s8, bs, pw, acc=None, **opts):
+    """INT8, FP8 and FP16 outputs under opts (and the INT8 int32 accumulators
+    into acc); returns them with the names of the kernels that ran."""
+    names = []
+    with _Options(**opts):
+        if acc is not None:
+            ee.gemm("int8", cuda(codes), pw.i8, cuda(a_s), cuda(bs), acc_out=acc)
+            names.append(_last_kernel())
+        o_i8 = host(ee.gemm("int8", cuda(codes), pw.i8, cuda(a_s), cuda(bs)))
+        names.append(_last_kernel())
+        o_f8 = host(ee.gemm("fp8", cuda(c8), pw.f8, cuda(s8), cuda(bs)))
+        names.append(_last_kernel())
+        o_f16 = host(ee.gemm("fp16", cuda(A), pw.f16))
+        names.append(_last_kernel())
+    return o_i8, o_f8, o_f16, names
+
+
+# (M, K, N, gemm_persist): 0 = automatic grid
+SHAPES = [
+    (512, 512, 512, 0),        # 4 tiles, 4 stages each
+    (300, 640, 520, 0),        # partial tiles in M and N, 5 stages
+    (520, 256, 1028, 0),       # two K stages per tile; N % 8 == 4 tail
+    (1, 256, 4, 0),            # a single row and 4 columns
+    (1024, 512, 1024, 8),      # 16 tiles on 8 workgroups: 2 tiles each, ring across tiles
+    (1024, 384, 1024, 3),      # 16 tiles on 3 workgroups (not a multiple of 8): 5-6 tiles each
+    (768, 256, 2048, 5),       # 24 tiles on 5 workgroups, 2 stages per tile
+    (1300, 1536, 900, 2),      # 24 tiles on 2 workgroups, 12 stages per tile
+    # last round at most half full: it runs as 256 x 128 halves (256-wide tiles only)
+    (512, 512, 2432, 8),       # 20 tiles on 8: 2 full rounds, 8 halves (one past N: skipped)
+    (300, 640, 1800, 13),      # 16 tiles on 13: 1 round, 6 halves; partial in M and N
+]
+
+
+@pytest.mark.parametrize("tn", [256, 128])
+@pytest.mark.parametrize("M,K,N,grid", SHAPES)
+def test_gemm4w_small(ee, orc, M, K, N, grid, tn):
+    A, B, bs, pw = _operands(ee, orc, M, K, N, M * 7 + K + N)
+    codes, a_s = orc.quant_act_i8(A, "dispatcher")
+    c8, s8 = orc.quant_act_f8(A)
+    acc = torch.empty((M, N), dtype=torch.int32, device="cuda")
+    o_i8, o_f8, o_f16, names = _run_tiers(ee, A, codes, a_s, c8, s8, bs, pw, acc,
+                                          gemm_tile=256, gemm_tile_n=tn, gemm_persist=grid, gemm_waves=4)
+    assert all("gemm4w" in n for n in names), names
+    acc_ref = orc.gemm_i8_acc(codes, B)
+    assert np.array_equal(host(acc), acc_ref)
+    assert np.array_equal(o_i8.view(np.uint16), orc.epilogue_i8(acc_ref, a_s, bs).view(np.uint16))
+    check_close_f64(o_f8, orc.gemm_f8_f64(c8, B, s8, bs))
+    check_close_f64(o_f16, orc.gemm_w8a16_f64(A, B, bs))
+    r_i8, r_f8, r_f16, rn = _run_tiers(ee, A, codes, a_s, c8, s8, bs, pw,
+                                       gemm_tile=256, gemm_tile_n=tn, gemm_persist=grid, gemm_waves=8)
+    assert all("gemm256" in n for n in rn), rn
+    assert np.array_equal(o_i8.view(np.uint16), r_i8.view(np.uint16))
+    assert np.array_equal(o_f8.view(np.uint16), r_f8.view(np.uint16))
+    assert np.array_equal(o_f16.view(np.uint16), r_f16.view(np.uint16))
+
+
+def test_gemm4w_one_stage_falls_back(ee, orc):
+    """Tiles of a single K stage (K * element size = 128) keep the 8-wave kernel."""
+    A, B, bs, pw = _operands(ee, orc, 520, 128, 1028, 3)
+    codes, a_s = orc.quant_act_i8(A, "dispatcher")
+    with _Options(gemm_tile=256, gemm_waves=4):
+        out = host(ee.gemm("int8", cuda(codes), pw.i8, cuda(a_s), cuda(bs)))
+        assert "gemm256" in _last_kernel()
+    acc_ref = orc.gemm_i8_acc(codes, B)
+    assert np.array_equal(out.view(np.uint16), orc.epilogue_i8(acc_ref, a_s, bs).view(np.uint16))
+
+
+@pytest.mark.parametrize("M,K,N", [(4096, 4096, 4096), (4096, 4096, 14336)], ids=["config1", "config2"])
+def test_gemm4w_full_size(ee, orc, M, K, N):
+    """Configs 1 and 2 at full size through the production epilogue: INT8 fp16
+    outputs bit-exact and FP8 / FP16 within 1e-2 of float64 on sampled rows
+    against the oracle; every output bit-identical to the 8-wave kernels'."""
+    A, B, bs, pw = _operands(ee, orc, M, K, N, 21 + N)
+    codes, a_s = orc.quant_act_i8(A, "dispatcher")
+    c8, s8 = orc.quant_act_f8(A)
+    o_i8, o_f8, o_f16, names = _run_tiers(ee, A, codes, a_s, c8, s8, bs, pw, gemm_waves=4)
+    assert all("gemm4w" in n for n in names), names
+    rows = np.array([0, 1, 255, 256, 257, 1000, 2047, 2048, 3333, 4095])
+    ref = orc.epilogue_i8(orc.gemm_i8_acc(codes[rows], B), a_s[rows], bs)
+    assert np.array_equal(o_i8[rows].view(np.uint16), ref.view(np.uint16))
+    check_close_f64(o_f8[rows], orc.gemm_f8_f64(c8[rows], B, s8[rows], bs))
+    check_close_f64(o_f16[rows], orc.gemm_w8a16_f64(A[rows], B, bs))
+    r_i8, r_f8, r_f16, _ = _run_tiers(ee, A, codes, a_s, c8, s8, bs, pw, gemm_waves=8)
+    assert np.array_equal(o_i8.view(np.uint16), r_i8.view(np.uint16))
+    assert np.array_equal(o_f8.view(np.uint16), r_f8.view(np.uint16))
+    assert np.array_equal(o_f16.view(np.uint16), r_f16.view(np.uint16))
+
+
+@pytest.mark.parametrize("tn", [256, 128])
+@pytest.mark.parametrize("M,K,F,grid", [(4096, 2048, 5632, 0), (600, 256, 640, 0), (512, 256, 1216, 8)])
+def test_gemm4w_swiglu(ee, orc, M, K, F, grid, tn):
+    """The four-wave SwiGLU epilogue gives the bits of the 8-wave one (every
+    tier).  The forced grid of 8 leaves the last round half full: 256 x 128
+    halves."""
+    rng = np.random.default_rng(M + F)
+    W = (rng.standard_normal((2 * F, K)) / np.sqrt(K)).astype(np.float16)
+    codes, scale = ee.quantize_weight_codes(cuda(W))
+    pw = ee.PackedWeight(ee.interleave_gate_up(codes), ee.interleave_gate_up(scale)).materialize()
+    x = cuda(rng.standard_normal((M, K)).astype(np.float16))
+    ci, si = ee.quantize_activations(x, "dispatcher")
+    cf, sf = ee.quantize_activations(x, "fp8")
+    for kind, a, b, sa, sb in (("int8", ci, pw.i8, si, pw.scale), ("fp8", cf, pw.f8, sf, pw.scale),
+                               ("fp16", x, pw.f16, None, None)):
+        with _Options(gemm_tile=256, gemm_tile_n=tn, gemm_persist=grid, gemm_waves=4):
+            fused = ee.gemm(kind, a, b, sa, sb, swiglu=True)
+            assert "gemm4w" in _last_kernel()
+        with _Options(gemm_tile=256, gemm_tile_n=tn, gemm_persist=grid, gemm_waves=8):
+            ref = ee.gemm(kind, a, b, sa, sb, swiglu=True)
+        assert torch.equal(fused.view(torch.int16), ref.view(torch.int16)), kind
+
+
+def _sweep_cases(n=24, seed=4044):
+    """Seeded shapes and forced grids: ragged M and N, K of 2-12 stages, grids of
+    1-37 workgroups (multiples of 8 and not)."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(n):
+        M = int(rng.integers(1, 1300))
+        N = int(rng.integers(1, 700)) * 4
+        K = int(rng.integers(2, 13)) * 128
+        grid = int(rng.choice([1, 2, 3, 5, 7, 8, 13, 16, 24, 37]))
+        out.append((M, K, N, grid))
+    return out
+
+
+@pytest.mark.parametrize("M,K,N,grid", _sweep_cases())
+def test_gemm4w_seeded_sweep(ee, orc, M, K, N, grid):
+    """Four-wave kernels on seeded shapes and grids: INT8 int32 accumulators equal
+    the oracle's; INT8, FP8 and FP16 outputs equal the 8-wave kernels' bit for bit."""
+    A, B, bs, pw = _operands(ee, orc, M, K, N, M * 31 + K + N + grid)
+    codes, a_s = orc.quant_act_i8(A, "dispatcher")
+    c8, s8 = orc.quant_act_f8(A)
+    acc = torch.empty((M, N), dtype=torch.int32, device="cuda")
+    o_i8, o_f8, o_f16, names = _run_tiers(ee, A, codes, a_s, c8, s8, bs, pw, acc,
+                                          gemm_tile=256, gemm_persist=grid, gemm_waves=4)
+    assert all("gemm4w" in n for n in names), names
+    assert np.array_equal(host(acc), orc.gemm_i8_acc(codes, B))
+    r_i8, r_f8, r_f16, _ = _run_tiers(ee, A, codes, a_s, c8, s8, bs, pw, gemm_tile=256, gemm_persist=grid,
+                                      gemm_waves=8)
+    assert np.array_equal(o_i8.view(np.uint16), r_i8.view(np.uint16))
+    assert np.array_equal(o_f8.view(np.uint16), r_f8.view(np.uint16))
+    assert np.array_equal(o_f16.view(np.uint16), r_f16.view(np.uint16))
+
+
+def test_gemm4w_option_rejects_bad_value(ee):
+    from entropy_engine import _lib
+    assert _lib.lib().ee_engine_set_option(_lib.engine(), b"gemm_waves", 6) == _lib.EE_ERR_INVALID_ARG

@@ -33,6 +33,11 @@ EE_DEV void dma16(const uint8_t* gptr, uint32_t lds_base) {
     asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds_base), "v"(gptr) : "memory", "m0");
 }
 EE_DEV uint32_t lds_addr(const uint8_t* p) { return (uint32_t)(uintptr_t)LPTR(p); }
+// 4 bytes per lane from global memory into LDS at lds_base + 4 * lane (per-row
+// scales and row indices of a tile, staged beside its operands).
+EE_DEV void dma4(const void* gptr, uint32_t lds_base) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, off" ::"s"(lds_base), "v"(gptr) : "memory", "m0");
+}
 // The same load with a wave-uniform 64-bit base in SGPRs and a 32-bit per-lane
 // byte offset (one VGPR per row group instead of a 64-bit address pair).
 EE_DEV void dma16s(const uint8_t* sbase, uint32_t voff, uint32_t lds_base) {

@@ -1,0 +1,570 @@
+// gemm4w.hip -- persistent 256 x 256-tile MFMA GEMMs of the three precision
+// tiers on four waves per workgroup (gfx950): one wave per SIMD, each wave
+// owning a 128 x 128 quarter of the tile with its accumulators in AGPRs.
+//
+//   EE_GEMM_I8 : int8 x int8 -> int32 (v_mfma_i32_16x16x64_i8, four per 32x32 block
+//                and 64-byte K slice);
+//                C = fp16((f32(acc) * a_scale[m]) * b_scale[n])     (EE/python/kernels.py:50-110)
+//   EE_GEMM_F8 : e4m3 x e4m3 -> f32 (v_mfma_scale_f32_32x32x64_f8f6f4);
+//                C = fp16((acc * a_scale[m]) * b_scale[n])           (EE/python/kernels.py:118-180)
+//   EE_GEMM_F16: fp16 x fp16 -> f32 (v_mfma_f32_16x16x32_f16, four per 32x32 block
+//                and 64-byte K slice); C = fp16(acc)
+//                (EE/python/kernels.py:192-246, W8A16 weights pre-dequantised)
+//
+// Why four waves.  The eight-wave 256-tile pipeline (gemm256.hip) gives each
+// wave a 128 x 64 block, so every A row of a stage is read from LDS by four
+// waves and every B row by two: 192 KB of fragment reads per 64 KB stage.  A
+// 128 x 128 block per wave has each stage row read by two waves: 128 KB per
+// stage, and each fragment read feeds twice the MFMAs.  The 16 blocks of
+// 32 x 32 take all 256 AGPRs as accumulators; the fragments of two K slices
+// (double buffered) and the DMA offsets fit in the 256 architectural VGPRs.
+// With one wave per SIMD the wave's own instruction stream keeps the matrix
+// core busy: each 64-byte K slice is 1024 clocks of MFMA (64 16x16x64 i8, 64
+// 16x16x32 f16 or 16 32x32x64 e4m3) into which the reads of the next slice's
+// 8 fragments and the direct-to-LDS loads of a stage are interleaved.
+//
+// Every 32 x 32 block sums its K slices in order with the MFMA and fragment
+// layout of the other pipelines (ee_gemm_dev.h), so FP8 and FP16 outputs are
+// bit-identical to the 8-wave 256-tile and the 128-tile kernels, and INT8 to
+// every kernel.
+//
+// LDS: a ring of two 64 KB stages (128 K bytes of 256 A rows and 256 B rows,
+// the 128-byte swizzled rows of ee_gemm_dev.h), a 4 KB epilogue slot per wave,
+// and two 3 KB scale areas.  Stage s: slice 0's MFMAs read slice 1's
+// fragments; barrier s+1 (every wave has read stage s and waited for its part
+// of stage s+1); slice 1's MFMAs issue stage s+2 into stage s's buffer and
+// read slice 0 of stage s+1.  Every stage runs this one schedule, across tile
+// boundaries too: the epilogue of a tile runs between two stages, with the
+// next tile's first stage landed and its slice-0 fragments in registers.
+//
+// The epilogue issues no loads: a tile's row scales, column scales and
+// (routed) C row numbers are DMA'd into the scale area of its parity with the
+// tile's first stage, and read back from LDS.  Outputs are dequantised in
+// registers, staged through the wave's slot 32 x 64 at a time and stored as
+// row-contiguous 16-byte vectors.
+//
+// Persistent grid: one workgroup per CU walks its tiles (TileDeal: 8 x 4
+// blocks of tiles per XCD per round).
+#include "../common/ee_device.h"
+#include "../common/ee_gemm_dev.h"
+#include "../common/ee_gemm_seq.h"
+
+#pragma clang fp contract(off)
+
+#define G4_THREADS 256
+
+// Tile 256 x TN (TN = 256 or 128).  Wave w owns rows 128 (w >> 1) .. +127 and
+// columns (TN / 2) (w & 1) .. + TN / 2 - 1 as 4 x NJ blocks of 32 x 32.
+template <int TN>
+struct G4Geom {
+    static constexpr int STAGE = (T2M + TN) * BKB;    // 64 KB or 48 KB
+    static constexpr int SLOTS = 2 * STAGE;           // after the ring of two stages
+    static constexpr int SLOT = 32 * 64 * 2;          // 32 rows x 64 fp16 columns per wave
+    static constexpr int SCALES = SLOTS + 4 * SLOT;   // two scale areas (tile parity)
+    static constexpr int SA = 0, SB = T2M * 4, SC = SB + TN * 4;   // a_scale, b_scale, C rows
+    static constexpr int SCALE_SZ = SC + T2M * 4;
+    static constexpr int LDS = SCALES + 2 * SCALE_SZ; // 150 KB or 117 KB
+    static constexpr int WC = TN / 2;                 // columns of a wave's block
+    static constexpr int NJ = WC / 32;                // its 32-column blocks
+    static constexpr int AG = 8;                      // A row groups (of 8 rows) per wave and stage
+    static constexpr int BG = TN / 32;                // B row groups per wave and stage
+    static constexpr int PARTS = AG + BG;             // DMA instructions per wave and stage
+};
+
+template <int KIND, int SW, class Seq, int TN = 256>
+struct G4 {
+    typedef G4Geom<TN> GE;
+    static constexpr int NJ = GE::NJ, WC = GE::WC;
+    typedef std::conditional_t<KIND == EE_GEMM_I8, PipeI8x16, Pipe<KIND>> P;
+    typedef typename P::acc_t acc_t;
+    typedef typename P::frag_t frag_t;
+    static constexpr int ESZ = (KIND == EE_GEMM_F16) ? 2 : 1;
+    static_assert(BKB / P::SB == 2, "two K slices per stage");
+    static_assert(NJ % 2 == 0, "the epilogue stores pairs of 32-column blocks");
+    static constexpr int NBLK = 4 * NJ;               // 32 x 32 blocks per wave
+    static constexpr int NFR = 4 + NJ;                // fragments per slice
+
+    const EeGemmArgs& g;
+    uint8_t* smem;
+    const Seq& seq;
+    int M;                                            // rows (counts[tier] when routed)
+    int64_t off;                                      // partition slot of row 0 (routed), else 0
+    uint32_t lds0;
+    int lane, wave, wm, wn;
+    int nk, ntiles;                                   // stages per tile (>= 2), tiles of this workgroup
+    // DMA cursor: the next stage to issue is (itile, ikt), global number iss.
+    int iss, itile, ikt;
+    const uint8_t* abase;
+    const uint8_t* bbase;
+    uint32_t aoff[GE::AG], boff[GE::BG];
+    acc_t acc[4][NJ];
+    struct Frags {
+        frag_t a[4], b[NJ];
+    } fr[2];
+
+    __device__ __forceinline__ G4(const EeGemmArgs& g_, uint8_t* smem_, const Seq& seq_, int M_, int64_t off_)
+        : g(g_), smem(smem_), seq(seq_), M(M_), off(off_) {}
+
+    __device__ __forceinline__ void coords(int i, int& m0, int& n0) const {
+        int tm, tn;
+        seq.coords(i, tm, tn);
+        m0 = tm * T2M;
+        n0 = tn * TN;
+    }
+
+    // DMA rows of tile i: one global_load_lds_dwordx4 fills 8 LDS rows (1 KB);
+    // lane l lands at row 8 * grp + l / 8, physical chunk l % 8, which holds
+    // logical chunk (l % 8) ^ swz(row).  Wave w fills A row groups 8w .. 8w+7
+    // and B row groups BG w .. BG w + BG-1 (rows clamped to the operand: rows
+    // beyond it load a valid row whose results are never stored).  Un-routed:
+    // offsets from the tile's first row; routed: A row m is a[a_idx[off + m]] or
+    // a[off + m], offsets from the operand's start (the launcher checks that
+    // they fit 32 bits).  Then the tile's scales and C rows into the scale area
+    // of its parity: wave w takes rows 64w .. 64w+63 and, for w < TN / 64,
+    // columns 64w .. 64w+63 (clamped likewise).
+    __device__ __forceinline__ void dma_tile(int i) {
+        int m0, n0;
+        coords(i, m0, n0);
+        int lane = this->lane;
+        asm volatile("" : "+v"(lane));                // lane-dependent offsets computed here, not hoisted
+        constexpr bool routed = Seq::ROUTED;
+        abase = (const uint8_t*)g.a + (routed ? 0 : (int64_t)m0 * g.lda * ESZ);
+        bbase = (const uint8_t*)g.b + (int64_t)n0 * g.ldb * ESZ;
+#pragma unroll
+        for (int q = 0; q < GE::AG; ++q) {
+            const int r = (wave * GE::AG + q) * 8 + (lane >> 3);
+            const int lchunk = (lane & 7) ^ swz(r);
+            const int m = min(m0 + r, M - 1);
+            const int64_t ar = !routed ? (int64_t)(m - m0) : Seq::GATHER ? (int64_t)g.a_idx[off + m] : off + m;
+            uint32_t pr = (uint32_t)ar * (uint32_t)(g.lda * ESZ);
+            asm volatile("" : "+v"(pr));
+            aoff[q] = pr + (uint32_t)(lchunk * 16);
+        }
+#pragma unroll
+        for (int q = 0; q < GE::BG; ++q) {
+            const int r = (wave * GE::BG + q) * 8 + (lane >> 3);
+            const int lchunk = (lane & 7) ^ swz(r);   // swz(T2M + r) == swz(r)
+            const int n = min(n0 + r, g.N - 1) - n0;
+            uint32_t pr = (uint32_t)n * (uint32_t)(g.ldb * ESZ);
+            asm volatile("" : "+v"(pr));
+            boff[q] = pr + (uint32_t)(lchunk * 16);
+        }
+        const uint32_t sa = lds0 + (uint32_t)(GE::SCALES + (i & 1) * GE::SCALE_SZ);
+        const int mr = min(m0 + wave * 64 + lane, M - 1);
+        if constexpr (KIND != EE_GEMM_F16) {
+            dma4(g.a_scale + off + mr, sa + GE::SA + wave * 256);
+            if (wave < TN / 64) dma4(g.b_scale + min(n0 + wave * 64 + lane, g.N - 1), sa + GE::SB + wave * 256);
+        }
+        if constexpr (routed)
+            if (g.c_idx) dma4(g.c_idx + off + mr, sa + GE::SC + wave * 256);
+    }
+    // Part P (0 .. PARTS-1) of the next stage: A row group 8w + P, then B row
+    // group BG w + P - 8: one s_add writing m0 (the part's LDS rows) and the
+    // load, from the stage's SGPR base (operand start + K offset of the stage)
+    // and the lane's row offset.  Past the workgroup's last stage the cursor
+    // re-issues its last tile's stages (valid rows, into ring buffers nobody
+    // reads again), so that every stage runs one schedule; run() waits for
+    // them before the workgroup ends.
+    template <int PT>
+    __device__ __forceinline__ void issue_part() {
+        if constexpr (PT == 0) {
+            if (ikt == nk) {
+                ikt = 0;
+                if (itile + 1 < ntiles) {
+                    ++itile;
+                    dma_tile(itile);
+                }
+            }
+        }
+        const uint32_t s = lds0 + (uint32_t)((iss & 1) * GE::STAGE);
+        const uint32_t kb = (uint32_t)ikt * BKB;
+        if constexpr (PT < GE::AG)
+            dma16_at<PT * 8 * BKB>(abase + kb, aoff[PT], s + wave * (GE::AG * 8 * BKB));
+        else
+            dma16_at<(PT - GE::AG) * 8 * BKB>(bbase + kb, boff[PT - GE::AG], s + (T2M + wave * GE::BG * 8) * BKB);
+        if constexpr (PT == GE::PARTS - 1) {
+            ++ikt;
+            ++iss;
+        }
+    }
+    template <int OFF>
+    static __device__ __forceinline__ void dma16_at(const uint8_t* sbase, uint32_t voff, uint32_t lds_sgpr) {
+        asm volatile("s_add_u32 m0, %0, %3\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds_sgpr), "v"(voff), "s"(sbase),
+                     "i"(OFF)
+                     : "memory", "m0", "scc");
+    }
+    template <int PT = 0>
+    __device__ __forceinline__ void issue_stage() {
+        if constexpr (PT < GE::PARTS) {
+            issue_part<PT>();
+            issue_stage<PT + 1>();
+        }
+    }
+
+    // Fragments of K slice SL from the stage at st.  Byte offsets from a stage's
+    // start, per slice (offA / offB, set up in run()):
+    // SUB16: rows row0 + (l & 15) and row0 + 16 + (l & 15), chunk 4 SL + (l >> 4)
+    // (swz(row0 + x) == swz(x) for row0 % 32 == 0);
+    // 32x32 forms: row row0 + (l & 31), chunk SL * SB/16 + (l >> 5) * LSTEP and
+    // the chunk CSTEP after it (offsets x = 0, 1).
+    // Fragment K: 0..3 A row block K (rows 128 wm + 32 K), 4.. B row block K - 4
+    // (rows 256 + WC wn + 32 (K - 4)); each read takes the block's offset as its
+    // immediate.
+    static constexpr int XR = P::SUB16 ? 1 : 2;
+    uint32_t offA[2][XR], offB[2][XR];
+    template <int SL, int K>
+    __device__ __forceinline__ void rd_frag(const uint8_t* st, Frags& f) {
+        constexpr int rel = (K < 4 ? K : K - 4) * 32 * BKB;
+        uint32_t o0, o1 = 0;
+        if constexpr (K < 4) {
+            o0 = offA[SL][0];
+            if constexpr (XR == 2) o1 = offA[SL][XR - 1];
+        } else {
+            o0 = offB[SL][0];
+            if constexpr (XR == 2) o1 = offB[SL][XR - 1];
+        }
+        frag_t v;
+        if constexpr (P::SUB16) {
+            const uint8_t* q = st + o0 + rel;
+            v.h[0] = *(const i32x4*)q;
+            v.h[1] = *(const i32x4*)(q + 16 * BKB);
+        } else {
+            const u32x4 x0 = *(const u32x4*)(st + o0 + rel), x1 = *(const u32x4*)(st + o1 + rel);
+            v = i32x8{(int)x0[0], (int)x0[1], (int)x0[2], (int)x0[3], (int)x1[0], (int)x1[1], (int)x1[2], (int)x1[3]};
+        }
+        if constexpr (K < 4) f.a[K] = v;
+        else f.b[K - 4] = v;
+    }
+    template <int SL, int K = 0>
+    __device__ __forceinline__ void rd_all(const uint8_t* st, Frags& f) {
+        if constexpr (K < NFR) {
+            rd_frag<SL, K>(st, f);
+            rd_all<SL, K + 1>(st, f);
+        }
+    }
+
+#define G4_SB() __builtin_amdgcn_sched_barrier(0)
+    // MFMA Q of block (I, J) on fragments f: SUB16 blocks are four 16x16 MFMAs
+    // (quarter Q: B half Q >> 1, A half Q & 1), exactly PipeI8x16 / PipeF16x16's
+    // mma; the 32x32 forms are one.
+    static constexpr int NQ = P::SUB16 ? 4 : 1;       // MFMAs per block
+    static constexpr int NM = NBLK * NQ;              // MFMAs per slice
+    template <int I, int J, int Q>
+    __device__ __forceinline__ void mma_q(const Frags& f) {
+        if constexpr (!P::SUB16) {
+            acc[I][J] = P::mma(f.b[J], f.a[I], acc[I][J]);
+        } else if constexpr (KIND == EE_GEMM_I8) {
+            acc[I][J].q[Q] = __builtin_amdgcn_mfma_i32_16x16x64_i8(f.b[J].h[Q >> 1], f.a[I].h[Q & 1], acc[I][J].q[Q], 0, 0, 0);
+        } else {
+            acc[I][J].q[Q] = P::m16(f.b[J].h[Q >> 1], f.a[I].h[Q & 1], acc[I][J].q[Q]);
+        }
+    }
+    // Fragment read order: by first use in the next slice (a0 b0 .. b3, then a1 .. a3).
+    static constexpr int rd_order(int r) { return r == 0 ? 0 : r <= NJ ? 3 + r : r - NJ; }
+    // The ops of a slice: RD: the NFR fragment reads of the next slice; DMA: the
+    // PARTS parts of the stage being issued.  With both, two parts then one
+    // read, repeated; op o goes after MFMA (o * span) / n, span = 3/4 of the
+    // slice's MFMAs when reading (the last reads land before the next slice).
+    static constexpr int n_ops(bool rd, bool dma) { return (rd ? NFR : 0) + (dma ? GE::PARTS : 0); }
+    static constexpr int op_at(int m, bool rd, bool dma) {   // first op after MFMA m (m may be NM: the end)
+        const int n = n_ops(rd, dma), span = rd ? (NM * 3) / 4 : NM;
+        // ops o with (o * span) / n < m ... count them: smallest o with o * span >= m * n
+        return m >= span ? n : (m * n + span - 1) / span;
+    }
+    template <int SL, bool RD, bool DMA, int O>
+    __device__ __forceinline__ void op(const uint8_t* rs, Frags& nf) {
+        if constexpr (RD && DMA) {
+            constexpr int g = O / 3, k = O % 3;           // groups of (part, part, read)
+            static_assert(GE::PARTS == 2 * NFR, "two parts per fragment read");
+            if constexpr (k < 2) issue_part<2 * g + k>();
+            else rd_frag<SL, rd_order(g)>(rs, nf);
+        } else if constexpr (RD) {
+            rd_frag<SL, rd_order(O)>(rs, nf);
+        } else if constexpr (DMA) {
+            issue_part<O>();
+        }
+    }
+    template <int SL, bool RD, bool DMA, int O, int OE>
+    __device__ __forceinline__ void ops(const uint8_t* rs, Frags& nf) {
+        if constexpr (O < OE) {
+            op<SL, RD, DMA, O>(rs, nf);
+            ops<SL, RD, DMA, O + 1, OE>(rs, nf);
+        }
+    }
+    // The MFMAs of one K slice on fragments fr[C], block row by block row, one
+    // MFMA at a time with the slice's ops between them (RD: slice SL of the stage
+    // at rs into fr[1 - C]).
+    template <int C, int SL, bool RD, bool DMA, int MI = 0>
+    __device__ __forceinline__ void slice(const uint8_t* rs) {
+        if constexpr (MI < NM) {
+            constexpr int b = MI / NQ, q = MI % NQ;
+            mma_q<b / NJ, b % NJ, q>(fr[C]);
+            G4_SB();
+            ops<SL, RD, DMA, op_at(MI, RD, DMA), op_at(MI + 1, RD, DMA)>(rs, fr[1 - C]);
+            G4_SB();
+            slice<C, SL, RD, DMA, MI + 1>(rs);
+        }
+    }
+
+    // Stage cs from buffer cs & 1; its slice-0 fragments are in fr[0].  Slice 0's
+    // MFMAs read slice 1 into fr[1]; barrier cs+1 (stage cs+1 landed, stage cs
+    // read); slice 1's MFMAs issue stage cs+2 and, RD, read slice 0 of stage
+    // cs+1 into fr[0].  A tile's last stage reads nothing: the fragments of the
+    // next tile's first stage are read after the epilogue, so that they do not
+    // hold registers through it.
+    template <bool RD>
+    __device__ __forceinline__ void stage(int cs) {
+        slice<0, 1, true, false>(smem + (cs & 1) * GE::STAGE);
+        G4_SB();
+        WAITCNT_VM(0);
+        WAITCNT_LGKM0();
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();                 // barrier cs+1: stage cs+1 landed, stage cs read
+        asm volatile("" ::: "memory");
+        slice<1, 0, RD, true>(smem + ((cs + 1) & 1) * GE::STAGE);
+        G4_SB();
+    }
+
+    // Dequantise and store tile t (m0, n0): for each 32-row block and pair of
+    // 32-column blocks, quarter q of block (i, j) holds rows row_of(q) and
+    // columns j * 32 + col_of(q) .. +3 of the block; they are dequantised with
+    // the row's a_scale and the four columns' b_scale (from the tile's scale
+    // area), written to the wave's slot as fp16 and stored as 16-byte row
+    // vectors.  SwiGLU: blocks 2p (gate) and 2p + 1 (up) hold the same 32
+    // outputs; their act values fp16(fp16(silu(gate)) * up) are staged instead.
+    static constexpr int q_of_cq(int c) { return P::SUB16 ? 2 * c : c; }
+    __device__ __forceinline__ void epilogue(int t) {
+        int m0, n0;
+        coords(t, m0, n0);
+        const int N = g.N;
+        int lane = this->lane;
+        asm volatile("" : "+v"(lane));                // epilogue addresses computed here, not hoisted
+        const int nb = n0 + wn * WC;                  // first column of the wave's block
+        const uint8_t* sc = smem + GE::SCALES + (t & 1) * GE::SCALE_SZ;
+        uint8_t* slot = smem + GE::SLOTS + wave * GE::SLOT;
+        auto crow_of = [&](int r) -> int32_t {        // C row of wave row r (0..127), -1 beyond M
+            const int m = m0 + wm * 128 + r;
+            if (m >= M) return -1;
+            if constexpr (Seq::ROUTED)
+                if (g.c_idx) return *(const int32_t*)(sc + GE::SC + (wm * 128 + r) * 4);
+            return m;
+        };
+        auto bsc = [&](int j, int c) -> f32x4 {       // b_scale of column group c of block j
+            if constexpr (KIND == EE_GEMM_F16) return f32x4{1.f, 1.f, 1.f, 1.f};
+            else return *(const f32x4*)(sc + GE::SB + (wn * WC + j * 32 + P::col_of(q_of_cq(c), lane)) * 4);
+        };
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            G4_SB();                                  // one block row's accumulators at a time
+            const int mb = m0 + wm * 128 + i * 32;    // first row of this 32-row block
+            float as[P::NRQ] = {};
+            if constexpr (KIND != EE_GEMM_F16)
+#pragma unroll
+                for (int h = 0; h < P::NRQ; ++h)
+                    as[h] = *(const float*)(sc + GE::SA + (wm * 128 + i * 32 + P::row_of(h, lane)) * 4);
+            if constexpr (KIND == EE_GEMM_I8) {
+                if (!Seq::ROUTED && g.acc) {          // debug output: int32 accumulators, direct stores
+#pragma unroll
+                    for (int j = 0; j < NJ; ++j)
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) {
+                            const int m = mb + P::row_of(q, lane), n = nb + j * 32 + P::col_of(q, lane);
+                            if (m < M && n < N)
+                                *(i32x4*)(g.acc + (int64_t)m * g.ldc + n) =
+                                    i32x4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
+                                          acc[i][j][4 * q + 3]};
+                        }
+                }
+            }
+            if constexpr (SW) {
+#pragma unroll
+                for (int pr = 0; pr < NJ / 2; ++pr) {
+                    f32x4 bg[P::NCQ], bu[P::NCQ];
+#pragma unroll
+                    for (int c = 0; c < P::NCQ; ++c) {
+                        bg[c] = bsc(2 * pr, c);
+                        bu[c] = bsc(2 * pr + 1, c);
+                    }
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        float gv[4], uv[4];
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            gv[r] = deq<KIND>(acc[i][2 * pr][4 * q + r], as[P::rq(q)], bg[P::cq(q)][r]);
+                            uv[r] = deq<KIND>(acc[i][2 * pr + 1][4 * q + r], as[P::rq(q)], bu[P::cq(q)][r]);
+                        }
+                        const int ca = pr * 32 + P::col_of(q, lane);
+                        *(u32x2*)(slot + lds_off(P::row_of(q, lane), ca >> 3) + ((ca >> 2) & 1) * 8) =
+                            u32x2{silu_mul2(pack_f16x2(gv[0], gv[1]), pack_f16x2(uv[0], uv[1])),
+                                  silu_mul2(pack_f16x2(gv[2], gv[3]), pack_f16x2(uv[2], uv[3]))};
+                    }
+                }
+                constexpr int CPR = NJ * 2;           // 16-byte chunks per act row (NJ * 16 columns)
+                constexpr int RPR = 64 / CPR;         // rows per store round
+                const int na = N >> 1;
+#pragma unroll
+                for (int k = 0; k < 32 / RPR; ++k) {
+                    const int rl = k * RPR + lane / CPR, ch = lane % CPR;
+                    const u32x4 v = *(const u32x4*)(slot + lds_off(rl, ch));
+                    const int n = (nb >> 1) + ch * 8;
+                    const int32_t crow = crow_of(i * 32 + rl);
+                    if (crow >= 0 && n < na) store_row16(g.c + (int64_t)crow * g.ldc + n, v, true);
+                }
+            } else {
+#pragma unroll
+                for (int jp = 0; jp < NJ / 2; ++jp) {
+                    G4_SB();
+#pragma unroll
+                    for (int jj = 0; jj < 2; ++jj) {
+                        const int j = 2 * jp + jj;
+                        f32x4 bs[P::NCQ];
+#pragma unroll
+                        for (int c = 0; c < P::NCQ; ++c) bs[c] = bsc(j, c);
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) {
+                            const int cl = jj * 32 + P::col_of(q, lane);
+                            float o[4];
+#pragma unroll
+                            for (int r = 0; r < 4; ++r) {
+                                if constexpr (KIND == EE_GEMM_F16) o[r] = acc[i][j][4 * q + r];
+                                else o[r] = deq<KIND>(acc[i][j][4 * q + r], as[P::rq(q)], bs[P::cq(q)][r]);
+                            }
+                            *(u32x2*)(slot + lds_off(P::row_of(q, lane), cl >> 3) + ((cl >> 2) & 1) * 8) =
+                                u32x2{pack_f16x2(o[0], o[1]), pack_f16x2(o[2], o[3])};
+                        }
+                    }
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        const int rl = k * 8 + (lane >> 3), ch = lane & 7;
+                        const u32x4 v = *(const u32x4*)(slot + lds_off(rl, ch));
+                        const int n = nb + jp * 64 + ch * 8;
+                        const int32_t crow = crow_of(i * 32 + rl);
+                        if (crow >= 0 && n < N) store_row16(g.c + (int64_t)crow * g.ldc + n, v, n + 8 <= N);
+                    }
+                }
+            }
+        }
+    }
+
+    // Zero accumulators, each 4-register group through an empty asm that keeps it
+    // in AGPRs: without it hipcc shares one zero group among the first MFMAs of
+    // a tile and then copies accumulators between AGPRs and VGPRs at the top of
+    // every stage.
+    template <typename V>
+    static __device__ __forceinline__ V zero4() {
+        V z = {};
+        asm volatile("" : "+a"(z));
+        return z;
+    }
+    __device__ __forceinline__ void zero() {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) {
+                if constexpr (P::SUB16) {
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) acc[i][j].q[q] = zero4<std::remove_reference_t<decltype(acc[i][j].q[q])>>();
+                } else {
+                    acc[i][j] = zero4<acc_t>();
+                }
+            }
+    }
+
+    __device__ __forceinline__ void run() {
+        const int tid = threadIdx.x;
+        lane = tid & 63;
+        wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+        wm = wave >> 1;
+        wn = wave & 1;
+#pragma unroll
+        for (int sl = 0; sl < 2; ++sl)
+#pragma unroll
+            for (int x = 0; x < XR; ++x) {
+                uint32_t o;
+                if constexpr (P::SUB16) o = lds_off(lane & 15, lane >> 4) ^ (uint32_t)(sl << 6);
+                else o = lds_off(lane & 31, sl * (P::SB / 16) + (lane >> 5) * P::LSTEP + x * P::CSTEP);
+                uint32_t oa = (uint32_t)(wm * 128 * BKB) + o, ob = (uint32_t)((T2M + wn * WC) * BKB) + o;
+                asm volatile("" : "+v"(oa), "+v"(ob));
+                offA[sl][x] = oa;
+                offB[sl][x] = ob;
+            }
+        ntiles = seq.count();
+        if (ntiles <= 0) return;                      // whole workgroup, before any barrier
+        nk = (int)((int64_t)g.K * ESZ / BKB);         // a multiple of BKB, at least 2 stages (launcher)
+        lds0 = lds_addr(smem);
+        iss = 0;
+        itile = -1;
+        ikt = nk;
+        issue_stage();                                // stage 0 (and tile 0's scales) -> buffer 0
+        issue_stage();                                // stage 1 -> buffer 1
+        WAITCNT_VM(GE::PARTS);                        // stage 0 landed; stage 1 may stay in flight
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();                 // barrier 0
+        asm volatile("" ::: "memory");
+        rd_all<0>(smem, fr[0]);
+        int cs = 0;
+        for (int t = 0; t < ntiles; ++t) {
+            zero();
+            for (int kt = 0; kt + 1 < nk; ++kt, ++cs) stage<true>(cs);
+            stage<false>(cs);
+            ++cs;
+            epilogue(t);
+            if (t + 1 < ntiles) {                     // slice 0 of the next tile's first stage (landed)
+                G4_SB();
+                rd_all<0>(smem + (cs & 1) * GE::STAGE, fr[0]);
+            }
+        }
+        WAITCNT_VM(0);                                // the re-issued stages have landed
+    }
+};
+
+// A grid of 256 x 256 tiles whose last round is at most half full (config 2:
+// 896 tiles on 256 CUs, 3.5 rounds) runs that round as 256 x 128 halves, one
+// per workgroup: the full rounds first, then the halves, in the same tile
+// order (both halves of a tile on one XCD).  The halves sum K in the same
+// order, so the output bits do not change.
+template <int KIND, int SW, int TN>
+EE_DEV void gemm4w(const EeGemmArgs& g) {
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[G4Geom<TN>::LDS];
+    const int b = (int)blockIdx.x, G = (int)gridDim.x;
+    const Seq256<TN> seq(g, b, G);
+    if constexpr (TN == 256) {
+        const int nT = seq.d.nA, full = nT / G, rem = nT - full * G;
+        if (rem > 0 && 2 * rem <= G) {
+            if (full > 0) {
+                const Seq256<TN> s1(g, b, G, full);
+                G4<KIND, SW, Seq256<TN>, TN> k(g, smem, s1, g.M, 0);
+                k.run();
+                __syncthreads();                      // every wave's reads of the ring, slots and scales are done
+            }
+            const int h = seq.d.pos_all();            // positions 0 .. G-1, one per workgroup
+            Seq256Half sh{0, 0, 0};
+            if (h < 2 * rem) {
+                int tm, tn;
+                seq.d.coords(full * G + (h >> 1), tm, tn);
+                const int tn2 = 2 * tn + (h & 1);
+                if (tn2 * 128 < g.N) sh = Seq256Half{1, tm, tn2};
+            }
+            if (sh.n > 0) {
+                G4<KIND, SW, Seq256Half, 128> k(g, smem, sh, g.M, 0);
+                k.run();
+            }
+            return;
+        }
+    }
+    G4<KIND, SW, Seq256<TN>, TN> k(g, smem, seq, g.M, 0);
+    k.run();
+}
+
+#define EE_G4_ENTRY(NAME, KIND, TN)                                                                        \
+    extern "C" __global__ void __launch_bounds__(G4_THREADS) __attribute__((amdgpu_waves_per_eu(1, 1)))   \
+    NAME(EeGemmArgs g) { gemm4w<KIND, 0, TN>(g); }                                                        \
+    extern "C" __global__ void __launch_bounds__(G4_THREADS) __attribute__((amdgpu_waves_per_eu(1, 1)))   \
+    NAME##_swiglu(EeGemmArgs g) { gemm4w<KIND, 1, TN>(g); }
+EE_G4_ENTRY(eek_gemm4w_i8, EE_GEMM_I8, 256)
+EE_G4_ENTRY(eek_gemm4w_f8, EE_GEMM_F8, 256)
+EE_G4_ENTRY(eek_gemm4w_f16, EE_GEMM_F16, 256)
+// 256 x 128 tiles
+EE_G4_ENTRY(eek_gemm4wn128_i8, EE_GEMM_I8, 128)
+EE_G4_ENTRY(eek_gemm4wn128_f8, EE_GEMM_F8, 128)
+EE_G4_ENTRY(eek_gemm4wn128_f16, EE_GEMM_F16, 128)

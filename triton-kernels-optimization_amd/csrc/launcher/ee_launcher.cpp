@@ -223,6 +223,9 @@ const Kernel* find_kernel(const ee_engine* e, const std::string& name) {
     return it == e->kernels.end() ? nullptr : &it->second;
 }
 
+// Name of the last kernel this thread launched through launch() (ee_last_kernel).
+thread_local std::string t_last_kernel;
+
 template <typename Args>
 int launch(ee_engine* e, const std::string& name, int64_t gx, int64_t gy, int block, Args args,
            ee_stream_t stream) {
@@ -242,6 +245,7 @@ int launch(ee_engine* e, const std::string& name, int64_t gx, int64_t gy, int bl
     EE_HIP(hipModuleLaunchKernel(k->fn, (unsigned)gx, (unsigned)gy, 1, (unsigned)block, 1, 1, 0,
                                  (hipStream_t)stream, params, nullptr),
            "hipModuleLaunchKernel(" + name + ")");
+    t_last_kernel = name;
     return EE_OK;
 }
 
@@ -477,6 +481,9 @@ EE_EXPORT int ee_engine_set_option(ee_engine* eng, const char* key, int64_t valu
     } else if (k == "gemm_tile_n") {
         if (value != 0 && value != 128 && value != 256)
             return fail(EE_ERR_INVALID_ARG, k + " must be 0 (auto), 128 or 256");
+    } else if (k == "gemm_waves") {
+        if (value != 0 && value != 4 && value != 8)
+            return fail(EE_ERR_INVALID_ARG, k + " must be 0 (auto), 4 or 8");
     } else {
         return fail(EE_ERR_INVALID_ARG, "unknown option: " + k);
     }
@@ -485,6 +492,8 @@ EE_EXPORT int ee_engine_set_option(ee_engine* eng, const char* key, int64_t valu
 }
 
 EE_EXPORT int ee_engine_device(const ee_engine* eng) { return eng ? eng->device : -1; }
+
+EE_EXPORT const char* ee_last_kernel(void) { return t_last_kernel.c_str(); }
 
 EE_EXPORT int ee_softmax_entropy(ee_engine* eng, const void* x, void* p, float* h, int64_t rows, int32_t S,
                                  int64_t ld_x, int64_t ld_p, int32_t causal, int32_t* tier, double tau_low,
@@ -710,6 +719,16 @@ static int gemm_impl(ee_engine* eng, int32_t kind, const void* a, int64_t lda, c
         const int64_t t256 = cdiv(M, 256) * cdiv(N, 256), t128 = cdiv(M, 256) * cdiv(N, 128);
         const bool narrow = tn_opt == 128 || (tn_opt == 0 && 2 * t256 <= gcu);
         std::string n256 = std::string(narrow ? names128[kind] : names256[kind]) + (sw ? "_swiglu" : "");
+        // Four waves per workgroup, each a 128 x (tile width / 2) quarter of the tile
+        // (eek_gemm4w*: the same tiles, deal and K order, so the same bits), where a
+        // tile has at least two K stages.  Option "gemm_waves": 0 auto, 4 or 8.
+        static const char* names4w[3] = {"eek_gemm4w_i8", "eek_gemm4w_f8", "eek_gemm4w_f16"};
+        static const char* names4w128[3] = {"eek_gemm4wn128_i8", "eek_gemm4wn128_f8", "eek_gemm4wn128_f16"};
+        const int64_t waves_opt = opt(eng, "gemm_waves");
+        if (waves_opt == 4 && K * esz >= 256) {
+            const std::string n4 = std::string(narrow ? names4w128[kind] : names4w[kind]) + (sw ? "_swiglu" : "");
+            if (find_kernel(eng, n4) != nullptr) n256 = n4;
+        }
         const Kernel* k256 = find_kernel(eng, n256);
         if (k256 != nullptr) {
             const int64_t tt = narrow ? t128 : t256;

@@ -48,6 +48,7 @@ SIGNATURES = {
     "ee_engine_destroy": ([_p], ctypes.c_int),
     "ee_engine_set_option": ([_p, ctypes.c_char_p, _i64], ctypes.c_int),
     "ee_engine_device": ([_p], ctypes.c_int),
+    "ee_last_kernel": ([], ctypes.c_char_p),
     "ee_softmax_entropy": ([_p, _p, _p, _p, _i64, _i32, _i64, _i64, _i32, _p, _f64, _f64, _p], ctypes.c_int),
     "ee_quant_act": ([_p, _p, _i64, _i64, _i64, _i32, _p, _i64, _p, _p, _p, _i32, _p], ctypes.c_int),
     "ee_quant_weight_i8": ([_p, _p, _i64, _i64, _i64, _p, _i64, _p, _p], ctypes.c_int),
