@@ -101,9 +101,10 @@ int ee_engine_destroy(ee_engine* eng);
  * "gemm_tile_n": the width of those 256-row tiles: automatic (plain GEMMs take
  * 256 x 128 where 256 x 256 tiles would keep at most half the CUs busy; the
  * routed grid stays at 256), or 128 / 256 forced.  Same bits either way.
- * "gemm_waves": the pipeline of those 256-row tiles: 8 waves (each a 128 x 64
- * block) or 4 waves (each a 128 x 128 block, accumulators in AGPRs; tiles of
- * at least two K stages); 0 automatic.  Same bits either way. */
+ * "gemm_waves": the pipeline of those 256-row tiles, plain and routed: 8 waves
+ * (each a 128 x 64 block) or 4 waves (each a 128 x 128 block, accumulators in
+ * AGPRs; tiles of at least two K stages); 0 automatic (4 where it applies).
+ * Same bits either way. */
 int ee_engine_set_option(ee_engine* eng, const char* key, int64_t value);
 int ee_engine_device(const ee_engine* eng);
 /* Name of the last kernel the calling thread launched through an ee_* entry

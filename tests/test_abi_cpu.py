@@ -83,6 +83,7 @@ def test_engine_create_errors(L, tmp_path):
 # kernel name prefix -> the argument struct its entry takes (csrc/kernels/*.hip)
 _ARG_STRUCTS = [
     ("eek_gemm256_routed", "EeRoutedGemmArgs"), ("eek_gemm256n128_routed", "EeRoutedGemmArgs"),
+    ("eek_gemm4w_routed", "EeRoutedGemmArgs"),
     ("eek_gemm_routed", "EeRoutedGemmArgs"), ("eek_gemm", "EeGemmArgs"),
     ("eek_softmax_entropy", "EeSoftmaxArgs"), ("eek_quant", "EeQuantArgs"), ("eek_absmax_partial", "EeAbsmaxArgs"),
     ("eek_route", "EeRouteArgs"), ("eek_transpose_i8", "EeWeightArgs"), ("eek_pack_b", "EeWeightArgs"),

@@ -205,3 +205,85 @@ def test_gemm4w_seeded_sweep(ee, orc, M, K, N, grid):
 def test_gemm4w_option_rejects_bad_value(ee):
     from entropy_engine import _lib
     assert _lib.lib().ee_engine_set_option(_lib.engine(), b"gemm_waves", 6) == _lib.EE_ERR_INVALID_ARG
+
+
+# ---------------------------------------------------------------------------- routed
+
+@pytest.mark.parametrize("M,K,N,H_hi,grid", [(300, 512, 520, 3.0, 0), (700, 1024, 384, 3.0, 8), (700, 256, 264, 3.0, 3),
+                                             (129, 256, 128, 10.0, 0), (257, 512, 256, 0.3, 0), (1500, 384, 1100, 3.0, 13)])
+def test_gemm4w_routed_equals_8wave_and_per_tier(ee, orc, M, K, N, H_hi, grid):
+    """The four-wave routed grid (phases FP16, INT8, FP8 per workgroup): every
+    row equals the 8-wave routed grid's and the un-routed GEMM of its tier bit
+    for bit.  Entropy ranges make tiers empty (H_hi 0.3: INT8 only; 10: mostly
+    FP16)."""
+    rng = np.random.default_rng(M * 5 + K + N)
+    X = rng.standard_normal((M, K)).astype(np.float16)
+    B, bs = weights(orc, rng, N, K)
+    H = (rng.random(M) * H_hi).astype(np.float32)
+    pw = ee.prepare_weight(cuda(B), cuda(bs)).materialize()
+    x = cuda(X)
+    tier, idx, counts = ee.route(cuda(H), 0.41, 1.68)
+    with _Options(gemm_tile=256, gemm_persist=grid):
+        out = host(ee.routed_linear(x, pw, idx, counts)).view(np.uint16)
+        assert _last_kernel() == "eek_gemm4w_routed"
+    with _Options(gemm_tile=256, gemm_persist=grid, gemm_waves=8):
+        ref8 = host(ee.routed_linear(x, pw, idx, counts)).view(np.uint16)
+        assert _last_kernel() == "eek_gemm256_routed"
+    assert np.array_equal(out, ref8)
+    t = host(tier)
+    full = [ee.triton_int8_gemm(x, cuda(B), cuda(bs)), ee.triton_fp8_gemm(x, cuda(B), cuda(bs)),
+            ee.triton_fp16_gemm(x, cuda(B), cuda(bs))]
+    for k in range(3):
+        if (t == k).any():
+            assert np.array_equal(out[t == k], host(full[k]).view(np.uint16)[t == k]), f"tier {k}"
+
+
+@pytest.mark.parametrize("N,sw", [(2048, False), (2560, False), (1024, True)])
+def test_gemm4w_routed_sparse_fp16_halves(ee, orc, N, sw):
+    """Config 4's mix (2.3 / 95.8 / 1.9 % of 4096 rows): one sparse FP16 M-tile per
+    column, run as 256 x 128 halves; rows equal the 8-wave routed grid's and, per
+    tier, the un-routed GEMMs'."""
+    M, K = 4096, 512
+    rng = np.random.default_rng(N + 3 * sw)
+    u = rng.random(M)
+    H = np.where(u < 0.023, 0.1, np.where(u < 0.981, 1.0, 9.0)).astype(np.float32)
+    if sw:
+        W = (rng.standard_normal((2 * N, K)) / np.sqrt(K)).astype(np.float16)
+        codes, scale = ee.quantize_weight_codes(cuda(W))
+        pw = ee.PackedWeight(ee.interleave_gate_up(codes), ee.interleave_gate_up(scale)).materialize()
+    else:
+        B, bs = weights(orc, rng, N, K)
+        pw = ee.prepare_weight(cuda(B), cuda(bs)).materialize()
+    x = cuda(rng.standard_normal((M, K)).astype(np.float16))
+    tier, idx, counts = ee.route(cuda(H), 0.5, 5.0)
+    assert all(c > 0 for c in counts.tolist())
+    with _Options(gemm_tile=256):
+        out = host(ee.routed_linear(x, pw, idx, counts, swiglu=sw)).view(np.uint16)
+        assert _last_kernel().startswith("eek_gemm4w_routed")
+    with _Options(gemm_tile=256, gemm_waves=8):
+        ref8 = host(ee.routed_linear(x, pw, idx, counts, swiglu=sw)).view(np.uint16)
+    assert np.array_equal(out, ref8)
+    if not sw:
+        t = host(tier)
+        full = [ee.triton_int8_gemm(x, cuda(B), cuda(bs)), ee.triton_fp8_gemm(x, cuda(B), cuda(bs)),
+                ee.triton_fp16_gemm(x, cuda(B), cuda(bs))]
+        for k in range(3):
+            assert np.array_equal(out[t == k], host(full[k]).view(np.uint16)[t == k]), f"tier {k}"
+
+
+@pytest.mark.parametrize("M,K,F", [(4096, 2048, 1408), (600, 256, 320)])
+def test_gemm4w_routed_swiglu(ee, orc, M, K, F):
+    """SwiGLU epilogue of the four-wave routed grid: the bits of the 8-wave one."""
+    rng = np.random.default_rng(M + 11 * F)
+    W = (rng.standard_normal((2 * F, K)) / np.sqrt(K)).astype(np.float16)
+    codes, scale = ee.quantize_weight_codes(cuda(W))
+    pw = ee.PackedWeight(ee.interleave_gate_up(codes), ee.interleave_gate_up(scale)).materialize()
+    x = cuda(rng.standard_normal((M, K)).astype(np.float16))
+    h = cuda((rng.random(M) * 3).astype(np.float32))
+    _, idx, counts = ee.route(h, 0.41, 1.68)
+    with _Options(gemm_tile=256):
+        fused = ee.routed_linear(x, pw, idx, counts, swiglu=True)
+        assert _last_kernel() == "eek_gemm4w_routed_swiglu"
+    with _Options(gemm_tile=256, gemm_waves=8):
+        ref = ee.routed_linear(x, pw, idx, counts, swiglu=True)
+    assert torch.equal(fused.view(torch.int16), ref.view(torch.int16))

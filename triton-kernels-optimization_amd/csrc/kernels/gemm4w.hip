@@ -556,6 +556,69 @@ EE_DEV void gemm4w(const EeGemmArgs& g) {
     k.run();
 }
 
+// ---------------------------------------------------------------- routed
+// The routed linear's three tier GEMMs as one persistent grid of 256 x 256
+// tiles on the four-wave pipeline: the deal of gemm256.hip's routed grid
+// (tier t owns ceil(counts[t] / 256) M-tiles of its partition slots; FP16
+// tiles, twice a 1-byte tile's work, dealt first round robin, as 256 x 128
+// halves where that shortens the estimated makespan; then the INT8 and FP8
+// tiles in TileDeal rounds), each phase one G4 pipeline.  Every tile sums K in
+// the order of the un-routed kernels, so routed rows equal ee_gemm's rows of
+// their tier bit for bit.
+template <int SW>
+EE_DEV void gemm4w_routed(const EeRoutedGemmArgs& r) {
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[G4Geom<256>::LDS];
+    const int32_t* counts = r.t[0].counts;
+    const int c0 = counts[0], c1 = counts[1], c2 = counts[2];
+    const int T0 = (c0 + T2M - 1) / T2M, T1 = (c1 + T2M - 1) / T2M, T2 = (c2 + T2M - 1) / T2M;
+    const int N = r.t[0].N;
+    const int nN = (N + 255) / 256;
+    const int b = (int)blockIdx.x, G = (int)gridDim.x;
+    // W8A16 tiles: 256 x 256, or 256 x 128 halves where that shortens the estimated
+    // makespan (in 1-byte-tile units: a full W8A16 tile costs 2, a half ~1.15).
+    // Every workgroup reads the same counts, so every workgroup makes the same choice.
+    int nF = T2 * nN, skip = 2;
+    bool half = false;
+    {
+        const int nFh = T2 * ((N + 127) / 128), nA = (T0 + T1) * nN;
+        const int full20 = 20 * max(2 * ((nF + G - 1) / G), (2 * nF + nA + G - 1) / G);
+        const int half20 = max(23 * ((nFh + G - 1) / G), 20 * (((23 * nFh + 19) / 20 + nA + G - 1) / G));
+        if (nF > 0 && half20 < full20) {
+            half = true;
+            nF = nFh;
+            skip = 1;
+        }
+    }
+    const TileDeal d(T0 + T1, nN, nF, b, G, skip);
+    // phase FP16
+    const SeqRF sf{b, G, b < nF ? (nF - b + G - 1) / G : 0, T2};
+    if (sf.n > 0) {
+        if (half) {
+            G4<EE_GEMM_F16, SW, SeqRF, 128> k(r.t[2], smem, sf, c2, (int64_t)c0 + c1);
+            k.run();
+        } else {
+            G4<EE_GEMM_F16, SW, SeqRF, 256> k(r.t[2], smem, sf, c2, (int64_t)c0 + c1);
+            k.run();
+        }
+    }
+    // the 1-byte tiles: the INT8 ones come first (logical index < T0 * nN)
+    const int n1 = d.count();
+    int ni8 = 0;
+    while (ni8 < n1 && d.tile_index(d.first_round + ni8) < T0 * nN) ++ni8;
+    if (ni8 > 0) {
+        if (sf.n > 0) __syncthreads();                // the previous phase's LDS reads and DMA are done
+        const SeqR1 s8{d, 0, ni8, T0, T1, nN};
+        G4<EE_GEMM_I8, SW, SeqR1, 256> k(r.t[0], smem, s8, c0, 0);
+        k.run();
+    }
+    if (n1 > ni8) {
+        if (sf.n > 0 || ni8 > 0) __syncthreads();
+        const SeqR1 s8{d, ni8, n1 - ni8, T0, T1, nN};
+        G4<EE_GEMM_F8, SW, SeqR1, 256> k(r.t[1], smem, s8, c1, c0);
+        k.run();
+    }
+}
+
 #define EE_G4_ENTRY(NAME, KIND, TN)                                                                        \
     extern "C" __global__ void __launch_bounds__(G4_THREADS) __attribute__((amdgpu_waves_per_eu(1, 1)))   \
     NAME(EeGemmArgs g) { gemm4w<KIND, 0, TN>(g); }                                                        \
@@ -568,3 +631,8 @@ EE_G4_ENTRY(eek_gemm4w_f16, EE_GEMM_F16, 256)
 EE_G4_ENTRY(eek_gemm4wn128_i8, EE_GEMM_I8, 128)
 EE_G4_ENTRY(eek_gemm4wn128_f8, EE_GEMM_F8, 128)
 EE_G4_ENTRY(eek_gemm4wn128_f16, EE_GEMM_F16, 128)
+// the routed grid
+extern "C" __global__ void __launch_bounds__(G4_THREADS) __attribute__((amdgpu_waves_per_eu(1, 1)))
+eek_gemm4w_routed(EeRoutedGemmArgs r) { gemm4w_routed<0>(r); }
+extern "C" __global__ void __launch_bounds__(G4_THREADS) __attribute__((amdgpu_waves_per_eu(1, 1)))
+eek_gemm4w_routed_swiglu(EeRoutedGemmArgs r) { gemm4w_routed<1>(r); }

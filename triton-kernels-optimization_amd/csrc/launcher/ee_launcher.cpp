@@ -721,11 +721,14 @@ static int gemm_impl(ee_engine* eng, int32_t kind, const void* a, int64_t lda, c
         std::string n256 = std::string(narrow ? names128[kind] : names256[kind]) + (sw ? "_swiglu" : "");
         // Four waves per workgroup, each a 128 x (tile width / 2) quarter of the tile
         // (eek_gemm4w*: the same tiles, deal and K order, so the same bits), where a
-        // tile has at least two K stages.  Option "gemm_waves": 0 auto, 4 or 8.
+        // tile has at least two K stages.  Measured on MI355X (same inputs, alternating
+        // launches), 8 against 4 waves: 4096^3 INT8 55.7 / 54.0 us, FP8 54.2 / 54.0,
+        // FP16 106.8 / 99.5; 4096 x 4096 x 14336 INT8 196 / 185, FP8 187 / 186, FP16
+        // 379 / 349.  Option "gemm_waves": 0 auto (4), 4 or 8.
         static const char* names4w[3] = {"eek_gemm4w_i8", "eek_gemm4w_f8", "eek_gemm4w_f16"};
         static const char* names4w128[3] = {"eek_gemm4wn128_i8", "eek_gemm4wn128_f8", "eek_gemm4wn128_f16"};
         const int64_t waves_opt = opt(eng, "gemm_waves");
-        if (waves_opt == 4 && K * esz >= 256) {
+        if (waves_opt != 8 && K * esz >= 256) {
             const std::string n4 = std::string(narrow ? names4w128[kind] : names4w[kind]) + (sw ? "_swiglu" : "");
             if (find_kernel(eng, n4) != nullptr) n256 = n4;
         }
@@ -902,6 +905,9 @@ static int routed_impl(ee_engine* eng, const void* x, int64_t ld_x, int32_t M, i
             // (256 x 256 tiles unless option gemm_tile_n = 128: the tiers' row counts, which
             // decide the rounds, are on the device)
             std::string n256 = opt(eng, "gemm_tile_n") == 128 ? "eek_gemm256n128_routed" : "eek_gemm256_routed";
+            // the four-wave routed grid (same deal, same bits) where every tier's tiles
+            // have at least two K stages; option gemm_waves = 8 keeps the 8-wave one
+            if (opt(eng, "gemm_tile_n") != 128 && opt(eng, "gemm_waves") != 8 && K >= 256) n256 = "eek_gemm4w_routed";
             if (sw) n256 += "_swiglu";
             const Kernel* k256 = find_kernel(eng, n256);
             if (k256 != nullptr) {
