@@ -529,19 +529,6 @@ def main():
                      "32000), random N(0,0.02) weights, batch 8 x seq 512 uniform token ids; every linear "
                      "routed per token row at (2.34, 6.03); all-FP16 run = hipBLASLt fp16 on the original weights",
         }
-    if not only or "probes" in only:
-        # the rates that bound the GEMMs, measured on this box (probe.hip)
-        pr = {k: ee.probe(k) for k in ("stream", "lds", "mfma_i8", "mfma_f8", "frag_i8_32x32", "frag_i8_16x16",
-                                       "frag_f16_32x32", "frag_f16_16x16")}
-        kernels["probes"] = {k: {"value": v["value"], "unit": v["unit"], "sclk_mhz": v["sclk_mhz"]}
-                             for k, v in pr.items()}
-        kernels["probes"]["c0_int8_bound"] = {
-            "stream_clocks_per_cu": round((1 << 20) / pr["stream"]["value"]),
-            "mfma_clocks_per_simd": round(512 * pr["mfma_i8"]["value"]),
-            "basis": "one 128x128 tile per CU: (128 + 128) x 4096 operand bytes through the CU's vector memory "
-                     "path, and 128 x 128 x 4096 MACs = 512 32x32x32 MFMAs (or 1024 16x16x64, the same clocks) "
-                     "per SIMD",
-        }
     for k, r in results.items():                                       # both timings of every kernel, in us
         kernels.setdefault("timings_us", {})[k] = {
             "eager": r["ms_eager"] * 1e3, "graph": None if r["ms_graph"] is None else r["ms_graph"] * 1e3,

@@ -386,34 +386,6 @@ int ee_routed_gemm_swiglu(ee_engine* eng, const void* x, int64_t ld_x, int32_t M
 int ee_interleave_gate_up(ee_engine* eng, const void* src, int64_t ld_src_bytes, void* dst, int64_t ld_dst_bytes,
                           int64_t F, int64_t row_bytes, ee_stream_t stream);
 
-/* ---- hardware probes ----------------------------------------------------------
- * No counterpart in the reference: diagnostics that measure, on the running
- * GPU, the rates that bound the GEMM kernels.  One launch of `grid`
- * workgroups of 512 threads; workgroup b writes times[4b .. 4b+3] = s_memtime
- * (shader clock) at the start and end of its timed loop, then s_memrealtime
- * (100 MHz) at both, and sink[512 b + t] keeps each thread's result.
- *   EE_PROBE_STREAM: iters stages of 32 KB streamed into LDS with direct-to-LDS
- *     loads from src, window % 32768 == 0: 8 windows of `window` bytes
- *     (workgroup b reads window b % 8, which its XCD's L2 keeps) or, with
- *     kind EE_PROBE_STREAM_OWN, `grid` windows (workgroup b reads window b);
- *   EE_PROBE_LDS: iters rounds of 8 conflict-free ds_read_b128 per thread;
- *   EE_PROBE_MFMA_I8 / _F8: iters rounds of 4 independent 32x32 MFMAs per wave
- *     (i8 32x32x32, e4m3 32x32x64);
- *   EE_PROBE_FRAG_*: the GEMM inner loop without its memory stream: per
- *     iteration each wave reads 8 fragments (16 bytes per lane) of a 64 x 64
- *     block from LDS and runs that block's MFMAs, as 32x32 MFMAs (_32: i8
- *     32x32x32, f16 32x32x16) or as 16x16 MFMAs of the same work (_16: i8
- *     16x16x64, f16 16x16x32); the operands are src's bytes (window >= 1 MiB:
- *     workgroup b copies 64 KB block b % 16 to LDS), so a caller passes data of
- *     the GEMMs' statistics.
- * src may be NULL for the other probes. */
-enum {
-    EE_PROBE_STREAM = 0, EE_PROBE_LDS = 1, EE_PROBE_MFMA_I8 = 2, EE_PROBE_MFMA_F8 = 3, EE_PROBE_STREAM_OWN = 4,
-    EE_PROBE_FRAG_I8_32 = 5, EE_PROBE_FRAG_I8_16 = 6, EE_PROBE_FRAG_F16_32 = 7, EE_PROBE_FRAG_F16_16 = 8
-};
-int ee_probe(ee_engine* eng, int32_t kind, const void* src, int64_t window, int32_t iters, int32_t grid,
-             uint64_t* times, uint32_t* sink, ee_stream_t stream);
-
 /* ---- CubinEngine counterpart (EE/csrc/engine.cpp:64-216) --------------------
  * One code object + one GEMM function, launched on the caller's stream (the
  * reference launched on the NULL stream, engine.cpp:160).  create mirrors the

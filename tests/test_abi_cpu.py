@@ -90,7 +90,6 @@ _ARG_STRUCTS = [
     ("eek_quant_weight", "EeWeightArgs"), ("eek_row_copy", "EeRowCopyArgs"), ("eek_silu_mul", "EeSiluMulArgs"),
     ("eek_interleave_rows", "EeInterleaveArgs"), ("eek_add_rmsnorm_route", "EeRmsNormRouteArgs"),
     ("eek_add_rmsnorm", "EeRmsNormArgs"), ("eek_qkv_rope", "EeQkvRopeArgs"), ("eek_attn", "EeAttnArgs"),
-    ("eek_probe", "EeProbeArgs"),
 ]
 
 
@@ -146,7 +145,6 @@ def test_null_engine_rejected(L):
                      None) == _lib.EE_ERR_INVALID_ARG
     assert L.ee_softmax_entropy(None, None, None, None, 1, 1, 1, 1, 0, None, 0.0, 0.0, None) == _lib.EE_ERR_INVALID_ARG
     assert L.ee_route(None, None, 1, 0.0, 0.0, None, None, None, None) == _lib.EE_ERR_INVALID_ARG
-    assert L.ee_probe(None, 0, None, 32768, 1, 1, None, None, None) == _lib.EE_ERR_INVALID_ARG
     assert L.ee_engine_set_option(None, b"se_wpr", 1) == _lib.EE_ERR_INVALID_ARG
     assert L.ee_silu_mul(None, None, 16, None, 8, 1, 8, None) == _lib.EE_ERR_INVALID_ARG
     assert L.ee_mlp_forward(None, None, 16, 1, 16, 16, *([None] * 8), 1.0, None, 1.5, 2.5, None, 16, None, 0,

@@ -95,8 +95,8 @@ template <> struct Pipe<EE_GEMM_I8> : PipeI8x64 {};
 // forms.  Fragment half h holds rows 16h + (l & 15) of the block, K bytes
 // 16 (l >> 4) .. +15 of the slice, for A and B alike; accumulator quarter q is
 // the 16 x 16 sub-block of A half q & 1 and B half q >> 1, lane l holding its
-// row l & 15 and columns 4 (l >> 4) .. +3.  Measured on MI355X (probe.hip's
-// fragment loops: the same clocks per iteration either way), the 16x16 forms
+// row l & 15 and columns 4 (l >> 4) .. +3.  Measured on MI355X (timing-only
+// fragment-read + MFMA loops: the same clocks per iteration either way), the 16x16 forms
 // run at a 9-13% higher shader clock under the power limit than the 32x32
 // forms of the same work.
 struct Lay16 {

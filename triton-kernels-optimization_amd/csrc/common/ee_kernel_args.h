@@ -206,14 +206,3 @@ struct EeAttnArgs {
     int32_t W;              // query heads (waves) per workgroup: 2 or 4, dividing Hq / Hkv
 };
 
-// Hardware probes (probe.hip): each workgroup records its s_memtime (shader
-// clock) and s_memrealtime (100 MHz) counters before and after its timed loop.
-struct EeProbeArgs {
-    const uint8_t* src;     // EE_PROBE_STREAM: windows of `window` bytes: 8 (workgroup b reads window b % 8,
-                            // which stays in its XCD's L2) or, with own_window, one per workgroup
-    uint64_t* times;        // [gridDim.x][4]: memtime start, memtime end, realtime start, realtime end
-    uint32_t* sink;         // [gridDim.x * 512]: each thread's result, so that nothing is optimised away
-    int64_t window;         // bytes per window, a multiple of 32768
-    int32_t iters;          // timed loop trips
-    int32_t own_window;     // EE_PROBE_STREAM: 1 = workgroup b reads window b (L2 misses: MALL / HBM)
-};

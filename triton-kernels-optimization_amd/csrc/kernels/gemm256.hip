@@ -14,7 +14,8 @@
 // Why a 256 x 256 tile.  A CU computing a T x T tile streams 2T bytes of
 // operands per K byte for 2T^2 ops: at the MFMA rate of 8192 int8/fp8 ops per
 // clock a 128 x 128 tile needs 64 B/clk per CU from L2, a 256 x 256 tile 32.
-// A gfx950 CU streams at most ~58 B/clk from L2 with every CU streaming (probe.hip),
+// A gfx950 CU streams at most ~58 B/clk from L2 with every CU streaming (a
+// timing-only direct-to-LDS stream kernel measured on MI355X),
 // and the GEMM loops reach ~38 of it beside their fragment reads, so 128-wide
 // tiles are operand-stream bound and 256-wide tiles can be MFMA bound.
 //

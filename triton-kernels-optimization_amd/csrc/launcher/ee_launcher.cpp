@@ -806,29 +806,6 @@ EE_EXPORT int ee_route_heads(ee_engine* eng, const float* h, int32_t B, int32_t 
     return launch(eng, "eek_route", 1, 1, 1024, a, stream);
 }
 
-EE_EXPORT int ee_probe(ee_engine* eng, int32_t kind, const void* src, int64_t window, int32_t iters, int32_t grid,
-                       uint64_t* times, uint32_t* sink, ee_stream_t stream) {
-    static const char* names[9] = {"eek_probe_stream",     "eek_probe_lds",        "eek_probe_mfma_i8",
-                                   "eek_probe_mfma_f8",    "eek_probe_stream",     "eek_probe_frag_i8_32",
-                                   "eek_probe_frag_i8_16", "eek_probe_frag_f16_32", "eek_probe_frag_f16_16"};
-    if (eng == nullptr || times == nullptr || sink == nullptr) return fail(EE_ERR_INVALID_ARG, "NULL argument");
-    if (kind < 0 || kind > 8) return fail(EE_ERR_INVALID_ARG, "probe kind must be 0..8");
-    if (iters < 1 || iters > (1 << 24) || grid < 1 || grid > 65535)
-        return fail(EE_ERR_INVALID_ARG, "iters must be 1..2^24 and grid 1..65535");
-    if (!aligned(times, 8) || !aligned(sink, 4)) return fail(EE_ERR_INVALID_ARG, "misaligned pointer");
-    if (kind == EE_PROBE_STREAM || kind == EE_PROBE_STREAM_OWN) {
-        if (src == nullptr || !aligned(src, 16)) return fail(EE_ERR_INVALID_ARG, "the stream probe needs a 16-byte aligned src");
-        if (window < 32768 || window % 32768 != 0 || window > (int64_t(1) << 30))
-            return fail(EE_ERR_INVALID_ARG, "window must be a multiple of 32768 bytes (at most 1 GiB)");
-    }
-    if (kind >= EE_PROBE_FRAG_I8_32) {
-        if (src == nullptr || !aligned(src, 16)) return fail(EE_ERR_INVALID_ARG, "the fragment probes need a 16-byte aligned src");
-        if (window < 16 * 65536) return fail(EE_ERR_INVALID_ARG, "the fragment probes read 16 blocks of 64 KB of src (window)");
-    }
-    EeProbeArgs a{(const uint8_t*)src, times, sink, window, iters, kind == EE_PROBE_STREAM_OWN ? 1 : 0};
-    return launch(eng, names[kind], grid, 1, 512, a, stream);
-}
-
 EE_EXPORT int ee_row_copy(ee_engine* eng, const void* src, int64_t ld_src_bytes, void* dst, int64_t ld_dst_bytes,
                           int64_t rows, int64_t row_bytes, const int32_t* idx, const int32_t* counts, int32_t tier,
                           int32_t scatter, ee_stream_t stream) {

@@ -11,7 +11,7 @@ from .dispatch import (TINYLLAMA_1B, EntropyDispatchedLinear, EntropyDispatchedL
                        quantize_weights_int8, tier_of)
 from .engine import CubinEngine, EntropyMLPEngine, HsacoEngine
 from .kernels import (VT_ORDER, PackedWeight, add_rmsnorm, add_rmsnorm_route, attention_causal, fp8_tensor_gemm, interleave_gate_up,
-                      fused_softmax_entropy, gemm, prepare_weight, probe,
+                      fused_softmax_entropy, gemm, prepare_weight,
                       qkv_rope, quantize_activations, quantize_tensor_fp8, quantize_weight_codes, route, route_heads,
                       routed_linear,
                       row_copy,
@@ -24,6 +24,6 @@ __all__ = [
     "gemm", "prepare_weight", "quantize_activations", "quantize_weight_codes", "route", "route_heads", "routed_linear", "row_copy",
     "fp8_tensor_gemm", "quantize_tensor_fp8",
     "silu_mul", "add_rmsnorm", "add_rmsnorm_route", "qkv_rope", "attention_causal", "VT_ORDER", "interleave_gate_up", "softmax_entropy",
-    "transpose_i8", "probe",
+    "transpose_i8",
     "triton_fp8_gemm", "triton_fp16_gemm", "triton_int8_gemm",
 ]

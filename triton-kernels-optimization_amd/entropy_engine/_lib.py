@@ -64,7 +64,6 @@ SIGNATURES = {
                                 ctypes.c_int),
     "ee_interleave_gate_up": ([_p, _p, _i64, _p, _i64, _i64, _i64, _p], ctypes.c_int),
     "ee_route": ([_p, _p, _i64, _f64, _f64, _p, _p, _p, _p], ctypes.c_int),
-    "ee_probe": ([_p, _i32, _p, _i64, _i32, _i32, _p, _p, _p], ctypes.c_int),
     "ee_route_heads": ([_p, _p, _i32, _i32, _i32, _f64, _f64, _p, _p, _p, _p], ctypes.c_int),
     "ee_row_copy": ([_p, _p, _i64, _p, _i64, _i64, _i64, _p, _p, _i32, _i32, _p], ctypes.c_int),
     "ee_routed_linear_noalloc": ([_p, _p, _i64, _i32, _i32, _i32, _p, _p, _p, _p, _p, _p, _p, _i64, _p],

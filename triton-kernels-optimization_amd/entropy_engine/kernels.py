@@ -552,70 +552,3 @@ def attention_causal(q: torch.Tensor, k: torch.Tensor, vt: torch.Tensor, out: to
         check(_lib.lib().ee_attention_causal(engine(), ptr(q), ptr(k), ptr(vt), ptr(out), ld_out, ptr(h), B, S, Hq,
                                              Hkv, d, stream_handle()))
     return out, h
-
-
-# ---------------------------------------------------------------- hardware probes
-
-PROBE_KINDS = {"stream": 0, "lds": 1, "mfma_i8": 2, "mfma_f8": 3, "stream_own": 4,
-               "frag_i8_32x32": 5, "frag_i8_16x16": 6, "frag_f16_32x32": 7, "frag_f16_16x16": 8}
-_PROBE_ITERS = {"stream": 2048, "lds": 4096, "mfma_i8": 4096, "mfma_f8": 2048, "stream_own": 256,
-                "frag_i8_32x32": 8000, "frag_i8_16x16": 8000, "frag_f16_32x32": 8000, "frag_f16_16x16": 8000}
-_PROBE_UNITS = {"stream": "bytes/clock/CU", "lds": "bytes/clock/CU", "mfma_i8": "clocks/MFMA",
-                "mfma_f8": "clocks/MFMA", "stream_own": "bytes/clock/CU", "frag_i8_32x32": "clocks/iteration",
-                "frag_i8_16x16": "clocks/iteration", "frag_f16_32x32": "clocks/iteration",
-                "frag_f16_16x16": "clocks/iteration"}
-
-
-def probe(kind: str, iters: int | None = None, grid: int | None = None, window: int | None = None) -> dict:
-    """One hardware rate of the current GPU, measured by probe.hip (ee_probe):
-    "stream" -- direct-to-LDS load bytes per clock per CU from L2-resident data
-    (each XCD's workgroups share one `window`-byte window); "stream_own" -- the
-    same with a window per workgroup (default 8 MiB: nothing shared, so the
-    stream comes from the MALL or HBM); "lds" -- ds_read_b128
-    bytes per clock per CU; "mfma_i8" / "mfma_f8" -- clocks per 32x32 MFMA per
-    SIMD with two waves on it; "frag_{i8,f16}_{32x32,16x16}" -- clocks per
-    iteration of a GEMM-like loop of fragment reads and MFMAs (the same work in
-    32x32 or in 16x16 MFMAs) on random operands of the GEMMs' statistics (int8
-    codes of Gaussian data, fp16 N(0, 0.5)), timed after enough launches (~25 ms)
-    for the power limit to settle, so that "sclk_mhz" is the clock each shape
-    holds.  One workgroup of 512 threads per CU by default.  Returns the median
-    over workgroups of the rate and of the shader clock (MHz, s_memtime against
-    the 100 MHz s_memrealtime), after one untimed launch (frag kinds: eight)."""
-    if kind not in PROBE_KINDS:
-        raise ValueError(f"probe kind must be one of {sorted(PROBE_KINDS)}")
-    dev = torch.device("cuda", torch.cuda.current_device())
-    k = PROBE_KINDS[kind]
-    grid = grid or torch.cuda.get_device_properties(dev).multi_processor_count
-    iters = iters or _PROBE_ITERS[kind]
-    window = window or (8 << 20 if kind == "stream_own" else 1 << 19)
-    nwin = grid if kind == "stream_own" else 8
-    src = torch.ones(nwin * window, dtype=torch.uint8, device=dev) if kind.startswith("stream") else None
-    warm = 1
-    if kind.startswith("frag"):
-        window, warm = 16 * 65536, 8
-        g = torch.Generator().manual_seed(5)
-        if "_i8_" in kind:
-            src = (torch.randn(window, generator=g) * 40.0).round().clamp(-127, 127).to(torch.int8)
-        else:
-            src = (torch.randn(window // 2, generator=g) * 0.5).half()
-        src = src.view(torch.uint8).to(dev)
-    times = torch.zeros(grid * 4, dtype=torch.int64, device=dev)
-    sink = torch.empty(grid * 512, dtype=torch.int32, device=dev)
-    with torch.cuda.device(dev):
-        for _ in range(warm + 1):                # the first launches warm L2 and the clock
-            check(_lib.lib().ee_probe(engine(), k, ptr(src), window, iters, grid, ptr(times), ptr(sink),
-                                      stream_handle()))
-        torch.cuda.synchronize()
-    t = times.view(grid, 4).cpu().double()
-    clk = t[:, 1] - t[:, 0]
-    us = (t[:, 3] - t[:, 2]) / 100.0
-    if kind.startswith("stream"):
-        rate = iters * 32768.0 / clk
-    elif kind == "lds":
-        rate = 512 * 16 * 8.0 * iters / clk
-    elif kind.startswith("frag"):
-        rate = clk / iters
-    else:
-        rate = clk / (iters * 4 * 2.0)
-    return {"kind": kind, "value": round(float(rate.median()), 2), "unit": _PROBE_UNITS[kind],
-            "sclk_mhz": round(float((clk / us).median()), 0), "grid": grid, "iters": iters}
