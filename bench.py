@@ -269,6 +269,12 @@ def main():
                 ee.softmax_entropy(big_in[i], out_probs=big_out[i])
 
             run("softmax_entropy_c2_cold", ent_c2, steps=3 * max(1, args.steps // 6), warmup=6)
+            # the same with non-temporal logits loads forced (option se_nt = 2: faster from
+            # HBM, slower on logits a producer has just written; automatic leaves them off here)
+            from entropy_engine import _lib as eel
+            eel.check(eel.lib().ee_engine_set_option(eel.engine(), b"se_nt", 2))
+            run("softmax_entropy_c2_cold_nt", ent_c2, steps=3 * max(1, args.steps // 6), warmup=6)
+            eel.check(eel.lib().ee_engine_set_option(eel.engine(), b"se_nt", 0))
             del big_in, big_out
         run("quant_i8", lambda: ee.quantize_activations(a, "dispatcher", out_codes=a_i8, out_scale=s_i8))
         run("quant_f8", lambda: ee.quantize_activations(a, "fp8", out_codes=a_f8, out_scale=s_f8))
@@ -291,7 +297,8 @@ def main():
         # kernels) -- config 1 [4096, 4096, 4096] with FP8 per-tensor scaling and 0.1% outliers of
         # magnitude 20 in A; config 2 [4096, 4096, 14336]; the FP16 baseline is torch.matmul (hipBLASLt)
         big = {}
-        big_names = ("c1_int8", "c1_fp8_tensor", "c1_fp16_torch", "c2_int8", "c2_fp8", "c2_fp16_torch")
+        big_names = ("c1_int8", "c1_fp8", "c1_fp8_tensor", "c1_fp16_torch", "c1_w8a16", "c2_int8", "c2_fp8",
+                     "c2_fp16_torch")
         if not only or any(n in only for n in big_names):
             for cfg, (Mb, Kb, Nb) in (("c1", (4096, 4096, 4096)), ("c2", (4096, 4096, 14336))):
                 if only and not any(n.startswith(cfg) for n in only):
@@ -308,13 +315,15 @@ def main():
                 ai_b, si_b = ee.quantize_activations(ab, "dispatcher")
                 cb = torch.empty((Mb, Nb), dtype=torch.float16, device=dev)
                 run(f"{cfg}_int8", lambda: ee.gemm("int8", ai_b, pwb.i8, si_b, pwb.scale, out=cb), primary="eager")
+                # FP8 in the reference's scheme (kernels.py:354-373: per-row e4m3 codes of A,
+                # the int8 weight codes as e4m3, per-channel scales) at both configs, and at
+                # config 1 also with per-tensor amax scales of A and W
+                af_b, sf_b = ee.quantize_activations(ab, "fp8")
+                run(f"{cfg}_fp8", lambda: ee.gemm("fp8", af_b, pwb.f8, sf_b, pwb.scale, out=cb), primary="eager")
                 if cfg == "c1":
                     ca, sa = ee.quantize_tensor_fp8(ab)
                     cw, sw = ee.quantize_tensor_fp8(Wb)
                     run("c1_fp8_tensor", lambda: ee.gemm("fp8", ca, cw, sa, sw, out=cb), primary="eager")
-                else:
-                    af_b, sf_b = ee.quantize_activations(ab, "fp8")
-                    run("c2_fp8", lambda: ee.gemm("fp8", af_b, pwb.f8, sf_b, pwb.scale, out=cb), primary="eager")
                 run(f"{cfg}_fp16_torch", lambda: torch.matmul(ab, Wb.t(), out=cb), primary="eager")
                 if cfg == "c1":                                        # this build's own FP16 (W8A16) tier
                     run("c1_w8a16", lambda: ee.gemm("fp16", ab, pwb.f16, out=cb), primary="eager")
@@ -457,7 +466,9 @@ def main():
                                / (results["softmax_entropy_c2_cold"]["ms"] * 1e-3) / 1e9,
                                "frac_of_hbm_cold": (4096 * 14336 * 4 + 4096 * 4)
                                / (results["softmax_entropy_c2_cold"]["ms"] * 1e-3) / 1e9 / PEAK_HBM_GBS,
-                               "shape": "config 2: fp16 [4096, 14336], row scales log-uniform in [0.1, 30]"},
+                               "shape": "config 2: fp16 [4096, 14336], row scales log-uniform in [0.1, 30]",
+                               "us_cold_nt_loads": results["softmax_entropy_c2_cold_nt"]["ms"] * 1e3
+                               if "softmax_entropy_c2_cold_nt" in results else None},
         "quant_i8": {"us": results["quant_i8"]["ms"] * 1e3,
                      "GBps": q_bytes / (results["quant_i8"]["ms"] * 1e-3) / 1e9},
         "quant_f8": {"us": results["quant_f8"]["ms"] * 1e3,
@@ -490,7 +501,7 @@ def main():
                 "note": "routed GEMM launch alone (codes from its quantiser) vs the three tiers' own GEMMs on the "
                         "same partitioned rows, each a separate launch"})
     for cfg, ops_b in big.items():
-        legs = ("int8", "fp8_tensor", "w8a16", "fp16_torch") if cfg == "c1" else ("int8", "fp8", "fp16_torch")
+        legs = ("int8", "fp8", "fp8_tensor", "w8a16", "fp16_torch") if cfg == "c1" else ("int8", "fp8", "fp16_torch")
         peak = {"int8": PEAK_I8_TOPS, "fp8_tensor": PEAK_F8_TFLOPS, "fp8": PEAK_F8_TFLOPS, "w8a16": PEAK_F16_TFLOPS,
                 "fp16_torch": PEAK_F16_TFLOPS}
         kernels[f"gemm_{cfg}"] = {
@@ -498,8 +509,9 @@ def main():
                   "TOPS": ops_b / (results[f"{cfg}_{leg}"]["ms"] * 1e-3) / 1e12,
                   "frac_of_peak": ops_b / (results[f"{cfg}_{leg}"]["ms"] * 1e-3) / 1e12 / peak[leg]}
             for leg in legs}
-        kernels[f"gemm_{cfg}"]["shape"] = ("M, K, N = 4096, 4096, 4096; A with 0.1% outliers of 20; FP8 per-tensor "
-                                           "scales; w8a16 = this build's FP16 tier (fp16 A, W8A16 weights)"
+        kernels[f"gemm_{cfg}"]["shape"] = ("M, K, N = 4096, 4096, 4096; A with 0.1% outliers of 20; fp8 = the "
+                                           "reference's per-row e4m3 scheme, fp8_tensor = per-tensor amax scales; "
+                                           "w8a16 = this build's FP16 tier (fp16 A, W8A16 weights)"
                                            if cfg == "c1" else "M, K, N = 4096, 4096, 14336")
     if "c1_softmax_entropy" in results:
         b1 = 4096 * 4096 * 4 + 4096 * 4
@@ -546,17 +558,16 @@ def main():
             ee.softmax_entropy(logits[i], out_probs=probs[i])
 
         ent_launch_ms = time_launches(ent_one, n_rot * max(1, args.steps // n_rot), n_rot, stream)
-    # The roofline figures divide by the average launch duration over a timed
-    # region of K launches (events on the launch stream): the smaller of the
-    # eager loop's and the replayed graph's.  Each is an upper bound on the
-    # kernel's own duration (each includes the launch-to-launch gaps: host-side
-    # ones for eager loops, ~1.6 us per node for a graph), and which one is
-    # lower varies from box to box for the INT8 GEMM.  The events bracketing each
-    # launch separately inflate a 7 us kernel by several us, so they are kept
-    # for reference only.
+    # The roofline figures divide by the average launch duration over the timed
+    # region of one replayed HIP graph of K launches (events on the launch
+    # stream), the basis rocprofv3's per-dispatch durations agree with; the eager
+    # figure is reported beside it (us_per_launch_eager).  Without graphs
+    # (--no-graph) the eager figure is the basis.  The events bracketing each
+    # launch separately inflate a 7 us kernel by several us, so they are kept for
+    # reference only.
     def roof_ms(name):
         r = results[name]
-        return min(t for t in (r["ms_eager"], r["ms_graph"]) if t)
+        return r["ms_graph"] if r["ms_graph"] else r["ms_eager"]
 
     i8_roof_ms = roof_ms("gemm_i8")
     ent_roof_ms = roof_ms("softmax_entropy_cold")
@@ -599,74 +610,99 @@ def main():
                    "M": M, "K": K, "N": N, "entropy_rows": ER, "entropy_cols": ES},
         "value_timing": "eager launches back to back, events on the launch stream (the reference's loop)",
         "roofline": {"bound": "mfma", "achieved": round(i8_launch_tops, 2), "peak": PEAK_I8_TOPS, "unit": "TOPS",
-                     "timing": "average launch over K back-to-back launches: the lower of eager and HIP-graph replay",
+                     "timing": "average launch over the replay of one HIP graph of K back-to-back launches",
                      "frac": round(i8_launch_tops / PEAK_I8_TOPS, 4), "traffic": traffic,
-                     "kernel": "eek_gemm_i8_w8 (8-wave INT8 pipeline, 1024x4096x4096)", "us_per_launch": round(i8_roof_ms * 1e3, 3)},
+                     "kernel": "eek_gemm_i8_w8 (8-wave INT8 pipeline, 1024x4096x4096)", "us_per_launch": round(i8_roof_ms * 1e3, 3),
+                     "us_per_launch_eager": round(results["gemm_i8"]["ms_eager"] * 1e3, 3)},
         "roofline_entropy": {"bound": "hbm", "achieved": round(ent_launch_gbs, 1), "peak": PEAK_HBM_GBS,
-                             "unit": "GB/s", "timing": "average launch over K back-to-back launches (lower of eager and graph replay), cold", "frac": round(ent_launch_gbs / PEAK_HBM_GBS, 4), "traffic": ent_traffic,
-                             "kernel": "eek_softmax_entropy_v4_w2 (cold, [1024,4096])", "us_per_launch": round(ent_roof_ms * 1e3, 3)},
+                             "unit": "GB/s", "timing": "average launch over the replay of one HIP graph of K back-to-back launches, cold",
+                             "frac": round(ent_launch_gbs / PEAK_HBM_GBS, 4), "traffic": ent_traffic,
+                             "kernel": "eek_softmax_entropy_v4_w2 (cold, [1024,4096])", "us_per_launch": round(ent_roof_ms * 1e3, 3),
+                             "us_per_launch_eager": round(results["softmax_entropy_cold"]["ms_eager"] * 1e3, 3)},
         "kernels": kernels,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line))
 
 
+def cpu_threads():
+    """(threads, affinity, quota): the CPUs this process may run on
+    (len(os.sched_getaffinity(0))), capped by the cgroup CPU quota when one is
+    set (the GPU box grants each GPU a share of a larger host)."""
+    aff = len(os.sched_getaffinity(0))
+    quota = None
+    try:
+        q, period = open("/sys/fs/cgroup/cpu.max").read().split()[:2]
+        if q != "max":
+            quota = max(1, int(int(q) // int(period)))
+    except (OSError, ValueError):
+        pass
+    return (min(aff, quota) if quota else aff), aff, quota
+
+
+def cpu_model():
+    try:
+        return [l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo") if l.startswith("model name")][0]
+    except (OSError, IndexError):
+        return "unknown"
+
+
 def cpu_baseline(A, W, L):
-    """The reference path's arithmetic on this host's cores, over a bounded
-    sample of the config-0 workload (~15-25 s of CPU work):
-      * oracle/torch_cpu.py, PyTorch CPU ops (the reference's own CPU path): INT8 =
-        the dispatcher quantiser + torch._int_mm + epilogue at the full
-        1024x4096x4096 shape (`value`); FP8 = e4m3 codes decoded to f32 + an f32
-        matmul on a 256-row slice; softmax+entropy in f32 on all 1024 rows;
-      * the repository's C oracle (OpenMP) on the INT8 path, beside it.
-    Threads: torch's (OMP_NUM_THREADS: the host's CPU share)."""
+    """The reference path's arithmetic on this host's cores, on the config-0
+    workload (BASELINE.md's CPU plan): oracle/torch_cpu.py, PyTorch CPU ops --
+    INT8 = the dispatcher quantiser + torch._int_mm + epilogue (`value`), FP8 =
+    e4m3 codes decoded to f32 + an f32 matmul, softmax+entropy in f32, each at
+    the full 1024x4096x4096 / [1024, 4096] shape -- and the repository's C
+    oracle (OpenMP) on the INT8 path beside it.  torch.set_num_threads(the
+    process's CPUs); time.perf_counter around each call, 3 warmup calls, then
+    the median of 10."""
     import numpy as np
     import torch
     sys.path.insert(0, ROOT)
     import oracle
     from oracle import torch_cpu as tc
-    threads = torch.get_num_threads()
+    threads, affinity, quota = cpu_threads()
+    torch.set_num_threads(threads)
 
-    def rate(fn, seconds, cap=30.0):
-        fn()                                                           # warm
-        reps, t0 = 0, time.perf_counter()
-        while True:
+    def median_s(fn, warm=3, reps=10):
+        for _ in range(warm):
             fn()
-            reps += 1
-            el = time.perf_counter() - t0
-            if el >= seconds or (el / reps) * (reps + 1) > cap:
-                return reps, el
+        ts = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        ts.sort()
+        return 0.5 * (ts[reps // 2 - 1] + ts[reps // 2])
 
     a, w, lg = torch.from_numpy(A), torch.from_numpy(W), torch.from_numpy(L)
     B, bs = oracle.quantize_weights_int8(W)
     b, bst = torch.from_numpy(B), torch.from_numpy(bs)
-    reps_i8, el_i8 = rate(lambda: tc.triton_int8_gemm(a, b, bst), 8.0)
-    i8_tops = 2.0 * M * N * K * reps_i8 / el_i8 / 1e12
+    ops = 2.0 * M * N * K
+    t_i8 = median_s(lambda: tc.triton_int8_gemm(a, b, bst))
     b8 = tc.weight_f8(b)
-    a_s = a[:256]
-    reps_f8, el_f8 = rate(lambda: tc.triton_fp8_gemm(a_s, b, bst, b8), 4.0)
-    f8_tflops = 2.0 * 256 * N * K * reps_f8 / el_f8 / 1e12
-    reps_e, el_e = rate(lambda: tc.softmax_entropy(lg), 2.0)
-    ent_gbs = (ER * ES * 4 + ER * 4) * reps_e / el_e / 1e9
+    t_f8 = median_s(lambda: tc.triton_fp8_gemm(a, b, bst, b8))
+    t_e = median_s(lambda: tc.softmax_entropy(lg))
+    ent_b = ER * ES * 4 + ER * 4
+
     def c_int8():
         codes, s = oracle.quant_act_i8(A, "dispatcher")
         return oracle.epilogue_i8(oracle.gemm_i8_acc(codes, B), s, bs)
 
-    reps_c, el_c = rate(c_int8, 5.0)
-    c_tops = 2.0 * M * N * K * reps_c / el_c / 1e12
-    try:
-        model = [l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo") if l.startswith("model name")][0]
-    except Exception:
-        model = "unknown"
-    return {"value": round(i8_tops, 4), "unit": "TOPS", "cores": threads, "kind": "port",
-            "int8_tops": round(i8_tops, 4), "fp8_tflops": round(f8_tflops, 4),
-            "entropy_gbps": round(ent_gbs, 3), "c_oracle_int8_tops": round(c_tops, 4),
-            "c_oracle_threads": oracle.num_threads(),
+    t_c = median_s(c_int8, warm=1, reps=4)
+    model = cpu_model()
+    return {"value": round(ops / t_i8 / 1e12, 4), "unit": "TOPS", "cores": threads, "kind": "port",
+            "cpu_model": model, "cpus_affinity": affinity, "cpu_quota": quota,
+            "int8_tops": round(ops / t_i8 / 1e12, 4), "int8_ms": round(t_i8 * 1e3, 3),
+            "fp8_tflops": round(ops / t_f8 / 1e12, 4), "fp8_ms": round(t_f8 * 1e3, 3),
+            "entropy_gbps": round(ent_b / t_e / 1e9, 3), "entropy_ms": round(t_e * 1e3, 3),
+            "c_oracle_int8_tops": round(ops / t_c / 1e12, 4), "c_oracle_threads": oracle.num_threads(),
+            "timing": "time.perf_counter per call; 3 warmup calls, median of 10 (C oracle: 1 warmup, median of 4)",
             "sample": f"PyTorch-CPU restatement (oracle/torch_cpu.py), {threads} threads on {model}: INT8 dispatcher "
-                      f"quantiser + torch._int_mm + epilogue at 1024x4096x4096, {reps_i8} reps in {el_i8:.1f} s; "
-                      f"FP8 codes -> f32 matmul on 256x4096x4096, {reps_f8} reps in {el_f8:.1f} s; f32 "
-                      f"softmax+entropy [1024,4096], {reps_e} reps in {el_e:.1f} s; C oracle INT8 path "
-                      f"{reps_c} reps in {el_c:.1f} s"}
+                      f"quantiser + torch._int_mm + epilogue at 1024x4096x4096 ({t_i8 * 1e3:.1f} ms); FP8 codes -> f32 "
+                      f"matmul at 1024x4096x4096 ({t_f8 * 1e3:.1f} ms); f32 softmax+entropy [1024,4096] "
+                      f"({t_e * 1e3:.1f} ms); C oracle INT8 path ({t_c * 1e3:.1f} ms)"}
+
 
 if __name__ == "__main__":
     main()

@@ -80,7 +80,8 @@ int ee_engine_destroy(ee_engine* eng);
 /* Tuning knobs (0 = automatic): "se_wpr" waves per softmax row (1..8),
  * "se_rpw" softmax rows per wave for short rows (1, 2, 4),
  * "se_nt" non-temporal loads of the softmax logits in the 2-, 4- and 8-wave
- * row layouts (1 off, 2 on; automatic: on when the logits span 64 MiB or more),
+ * row layouts (1 off, 2 on; automatic: on where the logits and probabilities
+ * together exceed the 256 MiB Infinity Cache),
  * "quant_wpr" waves per quantiser row (1,2,4);
  * "routed_unfused" = 1 makes ee_routed_linear use its five-launch sequence for
  * every K (for comparisons); "gemm_variant" = 1 runs every GEMM on the

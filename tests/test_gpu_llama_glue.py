@@ -302,7 +302,10 @@ def test_routed_gemm_on_prepared_codes(ee, T, tl, th, swiglu):
     pw = ee.PackedWeight(codes_w, scale_w).materialize()
     idx, counts = _partition(ee, T, tl, th, T + 1)
     _, n_ref = ee.add_rmsnorm(x, w, 1e-5, y)
-    _, n, codes, scale = ee.add_rmsnorm_route(x, w, 1e-5, y, idx, counts)
+    none = ee.add_rmsnorm_route(x, w, 1e-5, y, idx, counts)[1]
+    assert none is None                                   # n is only returned into n_out
+    n = torch.empty_like(x)
+    _, n, codes, scale = ee.add_rmsnorm_route(x, w, 1e-5, y, idx, counts, n_out=n)
     ref = ee.routed_linear(n_ref, pw, idx, counts, swiglu=swiglu)
     got = ee.routed_linear(n, pw, idx, counts, swiglu=swiglu, quantized=(codes, scale))
     assert torch.equal(got.view(torch.int16), ref.view(torch.int16))

@@ -508,11 +508,14 @@ EE_EXPORT int ee_softmax_entropy(ee_engine* eng, const void* x, void* p, float* 
     if (rows == 0) return EE_OK;
     EeSoftmaxArgs a{(const uint16_t*)x, (uint16_t*)p, h, tier, rows, ld_x, ld_p, S, causal, tau_low, tau_high};
     // Non-temporal loads of the logits (the _nt kernels of the multi-wave layouts; option
-    // "se_nt": 0 auto, 1 off, 2 on): from HBM they are 3-5% faster, from the caches ~13%
-    // slower (measured at configs 0-2), so automatic takes them where the logits alone are
-    // 64 MiB or more, too large to have stayed in the 256 MB MALL beside the probabilities.
+    // "se_nt": 0 auto, 1 off, 2 on).  Measured on MI355X at [4096, 14336]: logits read
+    // from HBM (rotating buffers) 3-5% faster; logits just written by a producer kernel
+    // (the pipeline's case) 2% slower; the same buffer again 11% slower.  Automatic takes
+    // them only where the logits and probabilities together exceed the 256 MiB Infinity
+    // Cache, so that logits cannot have stayed there ([8192, 8192]: a tie after a producer).
     const int64_t nt_opt = opt(eng, "se_nt");
-    const bool nt = nt_opt == 2 || (nt_opt == 0 && rows * ld_x * 2 >= (int64_t(64) << 20));
+    const int64_t se_bytes = rows * S * 2 * (p != nullptr ? 2 : 1);
+    const bool nt = nt_opt == 2 || (nt_opt == 0 && se_bytes > (int64_t(256) << 20));
     const bool vec_ok = aligned(x, 16) && aligned(p, 16) && ld_x % 8 == 0 && (p == nullptr || ld_p % 8 == 0);
     int vpt = 0, wpr = 0;
     if (vec_ok && pick_se_cfg(S, rows, opt(eng, "se_wpr"), vpt, wpr)) {

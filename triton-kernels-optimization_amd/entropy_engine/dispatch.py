@@ -517,7 +517,8 @@ class EntropyGatedLlama:
         if (gated and route is not None and self.fused_norm_quant and self.linear_impl is None
                 and self.linear_probe is None and x.shape[-1] % 128 == 0):
             idx, counts = route
-            x, xn, codes, scale = K.add_rmsnorm_route(x, w, self.cfg["eps"], res, idx, counts)
+            xn = torch.empty((x.numel() // x.shape[-1], x.shape[-1]), dtype=torch.float16, device=x.device)
+            x, xn, codes, scale = K.add_rmsnorm_route(x, w, self.cfg["eps"], res, idx, counts, n_out=xn)
             return x, xn, (codes, scale)
         x, xn = K.add_rmsnorm(x, w, self.cfg["eps"], res)
         return x, xn, None

@@ -485,10 +485,13 @@ def add_rmsnorm_route(x: torch.Tensor, w: torch.Tensor, eps: float, y: torch.Ten
     """(s, n, codes, scale): add_rmsnorm's s, plus the routed linear's INT8
     and FP8 operands of the rows of the partition idx/counts (from route or
     route_heads): codes uint8 [T, D] and scale f32 [T] in slot order, the bits
-    routed_linear's quantiser writes from add_rmsnorm's n.  n holds add_rmsnorm's
-    rows for the FP16 slots only (the others are not written; n_out, fp16 [T, D]
-    contiguous, receives them when given).  Pass (codes, scale) to
-    routed_linear(..., quantized=...) to skip that quantiser."""
+    routed_linear's quantiser writes from add_rmsnorm's n.  The normalised rows
+    are written for the FP16 slots only (the INT8 and FP8 slots' rows reach the
+    GEMM as codes): n is n_out (fp16 [T, D] contiguous), holding add_rmsnorm's
+    rows at the FP16 slots' source rows and nothing elsewhere, when the caller
+    passes it, and None otherwise.  Pass (codes, scale) to
+    routed_linear(..., quantized=...) to skip that quantiser, with n_out as its
+    input (its FP16 rows are the only ones it reads)."""
     dev = _require_cuda(x, w, y, idx, counts, n_out)
     x2, y2, s, n, w, T, D = _rmsnorm_operands(x, w, y)
     if idx.dtype != torch.int32 or counts.dtype != torch.int32 or idx.numel() != T:
@@ -504,7 +507,7 @@ def add_rmsnorm_route(x: torch.Tensor, w: torch.Tensor, eps: float, y: torch.Ten
                                               _rowmajor(y2, "y") if y2 is not None else D, ptr(w),
                                               ptr(s) if y is not None else None, D, ptr(n), D, T, D, float(eps),
                                               ptr(idx), ptr(counts), ptr(codes), D, ptr(scale), stream_handle()))
-    return s.view(x.shape), n.view(x.shape), codes, scale
+    return s.view(x.shape), (n.view(x.shape) if n_out is not None else None), codes, scale
 
 
 def qkv_rope(qkv: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, B: int, S: int, Hq: int, Hkv: int, d: int,
