@@ -183,6 +183,7 @@ def main():
     import torch
 
     import entropy_engine as ee
+    from entropy_engine import _lib as eel
 
     torch.cuda.set_device(0)
     dev = torch.device("cuda", 0)
@@ -233,6 +234,7 @@ def main():
         # GEMMs (26-50 us each) keep the queue full from eager launches, as in the
         # reference's own timing loop; graph replay adds per-node overhead on top.
         run("gemm_i8", lambda: ee.gemm("int8", a_i8, pw.i8, s_i8, pw.scale, out=c), primary="eager")
+        i8_kernel = eel.lib().ee_last_kernel().decode()
         run("gemm_f8", lambda: ee.gemm("fp8", a_f8, pw.f8, s_f8, pw.scale, out=c), primary="eager")
         run("gemm_f16w8", lambda: ee.gemm("fp16", a, w16, out=c), primary="eager")
         rot = {"i": 0}
@@ -243,6 +245,7 @@ def main():
             ee.softmax_entropy(logits[i], out_probs=probs[i])
 
         run("softmax_entropy_cold", ent_cold, steps=n_rot * max(1, args.steps // n_rot), warmup=n_rot)
+        ent_kernel = eel.lib().ee_last_kernel().decode()
         run("softmax_entropy_hot", lambda: ee.softmax_entropy(logits[0], out_probs=probs[0]))
         # Context for the C0 entropy figure: the runtime's plain copy of the same
         # 8 MiB -> 8 MiB, cold; and the entropy kernel cold at config 2's
@@ -271,7 +274,6 @@ def main():
             run("softmax_entropy_c2_cold", ent_c2, steps=3 * max(1, args.steps // 6), warmup=6)
             # the same with non-temporal logits loads forced (option se_nt = 2: faster from
             # HBM, slower on logits a producer has just written; automatic leaves them off here)
-            from entropy_engine import _lib as eel
             eel.check(eel.lib().ee_engine_set_option(eel.engine(), b"se_nt", 2))
             run("softmax_entropy_c2_cold_nt", ent_c2, steps=3 * max(1, args.steps // 6), warmup=6)
             eel.check(eel.lib().ee_engine_set_option(eel.engine(), b"se_nt", 0))
@@ -612,12 +614,12 @@ def main():
         "roofline": {"bound": "mfma", "achieved": round(i8_launch_tops, 2), "peak": PEAK_I8_TOPS, "unit": "TOPS",
                      "timing": "average launch over the replay of one HIP graph of K back-to-back launches",
                      "frac": round(i8_launch_tops / PEAK_I8_TOPS, 4), "traffic": traffic,
-                     "kernel": "eek_gemm_i8_w8 (8-wave INT8 pipeline, 1024x4096x4096)", "us_per_launch": round(i8_roof_ms * 1e3, 3),
+                     "kernel": f"{i8_kernel} (INT8, 1024x4096x4096)", "us_per_launch": round(i8_roof_ms * 1e3, 3),
                      "us_per_launch_eager": round(results["gemm_i8"]["ms_eager"] * 1e3, 3)},
         "roofline_entropy": {"bound": "hbm", "achieved": round(ent_launch_gbs, 1), "peak": PEAK_HBM_GBS,
                              "unit": "GB/s", "timing": "average launch over the replay of one HIP graph of K back-to-back launches, cold",
                              "frac": round(ent_launch_gbs / PEAK_HBM_GBS, 4), "traffic": ent_traffic,
-                             "kernel": "eek_softmax_entropy_v4_w2 (cold, [1024,4096])", "us_per_launch": round(ent_roof_ms * 1e3, 3),
+                             "kernel": f"{ent_kernel} (cold, [1024,4096])", "us_per_launch": round(ent_roof_ms * 1e3, 3),
                              "us_per_launch_eager": round(results["softmax_entropy_cold"]["ms_eager"] * 1e3, 3)},
         "kernels": kernels,
         "cpu_baseline": cpu,

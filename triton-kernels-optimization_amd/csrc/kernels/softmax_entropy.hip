@@ -17,6 +17,7 @@
 #include "../common/ee_device.h"
 
 #define LOG2E 1.4426950408889634f
+#define LN2 0.69314718055994531f
 
 // Rows per block for WPR waves per row (the block holds RPB * WPR waves).
 template <int WPR>
@@ -48,6 +49,28 @@ EE_DEV float sub_hi(uint32_t u, float negm) {
     asm("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(u), "v"(negm));
     return r;
 }
+// (x - m) log2 e in one v_fma_mix_f32: x * log2e + (-m log2e), one rounding.
+// The waves of a row that hold no entry equal to the max take this form (one
+// instruction per element instead of two); it is within 2^-24 |m log2 e| of
+// the two-step value, so e changes by at most a few f32 ulps.
+EE_DEV float sub2_lo(uint32_t u, float l2e, float negml) {
+    float r;
+    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(u), "s"(l2e), "v"(negml));
+    return r;
+}
+EE_DEV float sub2_hi(uint32_t u, float l2e, float negml) {
+    float r;
+    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(u), "s"(l2e), "v"(negml));
+    return r;
+}
+// fp16(e0 * s) | fp16(e1 * s) << 16, each product rounded once to fp16
+// (v_fma_mixlo_f16 / v_fma_mixhi_f16 with a zero addend).
+EE_DEV uint32_t scale_pack_f16x2(float e0, float e1, float s) {
+    uint32_t r;
+    asm("v_fma_mixlo_f16 %0, %1, %2, 0" : "=v"(r) : "v"(e0), "v"(s));
+    asm("v_fma_mixhi_f16 %0, %1, %2, 0" : "+v"(r) : "v"(e1), "v"(s));
+    return r;
+}
 
 // Row kernel: WPR wave64s per row (one to eight), VPT 16-byte vectors per lane
 // (S <= VPT * WPR * 512).  Passes over the registers:
@@ -59,7 +82,9 @@ EE_DEV float sub_hi(uint32_t u, float negm) {
 //     hold an entry equal to the row max (one wave of the row, typically) needs
 //     the per-element test that keeps those entries out of Z' and counts them
 //     (c0); the others take the test-free loop;
-//  4. probabilities p = fp16(e / Z) from the kept e (VPT <= 4) or recomputed e.
+//  4. probabilities p = fp16(e / Z) from the kept e (VPT <= 4) or recomputed e,
+//     stored before
+//  5. H, which only the row's first wave evaluates (its stores drain meanwhile).
 // The row's registers: lane l of wave wr of the row holds 16-byte vectors
 // j = 0 .. VPT-1 at column ((j * WPR + wr) * 64 + l) * 8; entries past the row
 // (or past the causal limit) read as -inf and are not loaded.
@@ -85,7 +110,16 @@ EE_DEV void se_load(const EeSoftmaxArgs& a, int64_t r, int wr, int lane, u32x4 (
     }
 }
 
-// Steps 1-4 for one row held in v (red: the block's cross-wave partials when WPR > 1).
+// H of a row from its reduced sums, and its tier, written by lane 0.
+EE_DEV void se_entropy_out(const EeSoftmaxArgs& a, int64_t row, bool dead, float cz, float z, float t, int lane) {
+    const float H = dead ? NAN : entropy_from(cz, z, t);
+    if (lane == 0) {
+        a.h[row] = H;
+        if (a.tier) a.tier[row] = tier_of(H, a.tau_low, a.tau_high);
+    }
+}
+
+// Steps 1-5 for one row held in v (red: the block's cross-wave partials when WPR > 1).
 template <int VPT, int WPR>
 EE_DEV void se_process(const EeSoftmaxArgs& a, u32x4 (&v)[VPT], int64_t row, bool valid, int w, int wr, int lane,
                        float (*red)[4]) {
@@ -124,16 +158,18 @@ EE_DEV void se_process(const EeSoftmaxArgs& a, u32x4 (&v)[VPT], int64_t row, boo
     float ek[KEEP_E ? VPT * 8 : 1];
     float z0 = 0.f, z1 = 0.f, t0 = 0.f, t1 = 0.f;
     int cnt = 0;
+    const float negml = negm * LOG2E;
     if (!has_max) {
+        // s2 = (x - m) log2 e; T accumulates e * s2 and is scaled by ln 2 below
 #pragma unroll
         for (int j = 0; j < VPT; ++j)
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
                 const uint32_t u = v[j][i >> 1];
-                const float s = (i & 1) ? sub_hi(u, negm) : sub_lo(u, negm);
-                const float e = __builtin_amdgcn_exp2f(s * LOG2E);
-                if (i & 1) { z1 += e; t1 = fmaf(e, s, t1); }
-                else       { z0 += e; t0 = fmaf(e, s, t0); }
+                const float s2 = (i & 1) ? sub2_hi(u, LOG2E, negml) : sub2_lo(u, LOG2E, negml);
+                const float e = __builtin_amdgcn_exp2f(s2);
+                if (i & 1) { z1 += e; t1 = fmaf(e, s2, t1); }
+                else       { z0 += e; t0 = fmaf(e, s2, t0); }
                 if (KEEP_E) ek[j * 8 + i] = e;
             }
     } else {
@@ -153,6 +189,7 @@ EE_DEV void se_process(const EeSoftmaxArgs& a, u32x4 (&v)[VPT], int64_t row, boo
     }
     float z = wave_sum(z0 + z1);
     float t = wave_sum(t0 + t1);
+    if (!has_max) t *= LN2;
     float cz = (float)wave_sum_i32(cnt);
     if constexpr (WPR > 1) {
         if (lane == 0) { red[w][1] = z; red[w][2] = t; red[w][3] = cz; }
@@ -162,44 +199,48 @@ EE_DEV void se_process(const EeSoftmaxArgs& a, u32x4 (&v)[VPT], int64_t row, boo
 #pragma unroll
         for (int i = 1; i < WPR; ++i) { z += red[base + i][1]; t += red[base + i][2]; cz += red[base + i][3]; }
     }
-    const float H = dead ? NAN : entropy_from(cz, z, t);
-    if (valid && wr == 0 && lane == 0) {
-        a.h[row] = H;
-        if (a.tier) a.tier[row] = tier_of(H, a.tau_low, a.tau_high);
-    }
-    if (a.p == nullptr || !valid) return;
+    if (!valid) return;
+    // One wave x 4 vectors (eight waves per SIMD, 64 VGPRs) has no registers to keep
+    // the row sums through the stores: it evaluates H first.
+    constexpr bool H_FIRST = WPR == 1 && VPT == 4;
+    if constexpr (H_FIRST) se_entropy_out(a, row, dead, cz, z, t, lane);
 
-    // ---- 4. one write of the probabilities
-    const float invZ = dead ? NAN : 1.0f / (cz + z);
-    uint16_t* pr = a.p + row * a.ld_p;
-#pragma unroll
-    for (int j = 0; j < VPT; ++j) {
-        const int c0 = ((j * WPR + wr) * 64 + lane) * 8;
-        if (c0 >= S) continue;
-        float pv[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            float e;
-            if (KEEP_E) {
-                e = ek[j * 8 + i];
-            } else {
-                const uint32_t u = v[j][i >> 1];
-                e = __builtin_amdgcn_exp2f(((i & 1) ? sub_hi(u, negm) : sub_lo(u, negm)) * LOG2E);
+    // ---- 4. one write of the probabilities, issued before H is evaluated so that
+    // the stores drain while the row's first wave computes it (1/Z from v_rcp_f32,
+    // within 1 ulp; Z >= 1)
+    if (a.p != nullptr) {
+        const float invZ = dead ? NAN : __builtin_amdgcn_rcpf(cz + z);
+        uint16_t* pr = a.p + row * a.ld_p;
+    #pragma unroll
+        for (int j = 0; j < VPT; ++j) {
+            const int c0 = ((j * WPR + wr) * 64 + lane) * 8;
+            if (c0 >= S) continue;
+            float ev[8];
+    #pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                if (KEEP_E) {
+                    ev[i] = ek[j * 8 + i];
+                } else {                                  // the e of step 3, recomputed
+                    const uint32_t u = v[j][i >> 1];
+                    ev[i] = __builtin_amdgcn_exp2f(has_max ? ((i & 1) ? sub_hi(u, negm) : sub_lo(u, negm)) * LOG2E
+                                                           : ((i & 1) ? sub2_hi(u, LOG2E, negml) : sub2_lo(u, LOG2E, negml)));
+                }
             }
-            pv[i] = e * invZ;
-        }
-        const u32x4 o{pack_f16x2(pv[0], pv[1]), pack_f16x2(pv[2], pv[3]),
-                      pack_f16x2(pv[4], pv[5]), pack_f16x2(pv[6], pv[7])};
-        if (c0 + 8 <= S) {
-            // written once, read by a later kernel: non-temporal (measured 5% faster
-            // at [4096, 14336], where the kernel runs at ~93% of a plain copy)
-            __builtin_nontemporal_store(o, (u32x4*)(pr + c0));
-        } else {
-#pragma unroll
-            for (int i = 0; i < 8; ++i)
-                if (c0 + i < S) pr[c0 + i] = (uint16_t)(o[i >> 1] >> ((i & 1) * 16));
+            const u32x4 o{scale_pack_f16x2(ev[0], ev[1], invZ), scale_pack_f16x2(ev[2], ev[3], invZ),
+                          scale_pack_f16x2(ev[4], ev[5], invZ), scale_pack_f16x2(ev[6], ev[7], invZ)};
+            if (c0 + 8 <= S) {
+                // written once, read by a later kernel: non-temporal (measured 5% faster
+                // at [4096, 14336], where the kernel runs at ~93% of a plain copy)
+                __builtin_nontemporal_store(o, (u32x4*)(pr + c0));
+            } else {
+    #pragma unroll
+                for (int i = 0; i < 8; ++i)
+                    if (c0 + i < S) pr[c0 + i] = (uint16_t)(o[i >> 1] >> ((i & 1) * 16));
+            }
         }
     }
+    // ---- 5. H and the tier, by the row's first wave
+    if (!H_FIRST && wr == 0) se_entropy_out(a, row, dead, cz, z, t, lane);
 }
 
 template <int VPT, int WPR, bool NT = false>

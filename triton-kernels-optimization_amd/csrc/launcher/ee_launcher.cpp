@@ -277,9 +277,10 @@ bool pick_row_cfg(int64_t len, int64_t rows, int64_t forced_wpr, int& vpt, int& 
 
 // (VPT, WPR) for the softmax row kernel: WPR = 1..8 waves per row holding
 // VPT <= 4 vectors per lane (the kernel keeps e in registers up to 4), with
-// VPT * WPR * 512 >= len.  Among the layouts that cover the row with the
-// least padding, the fewest waves per row that still put >= 4096 waves on the
-// chip.  Rows longer than 4 * 8 * 512 take eight waves and VPT 5..8.
+// VPT * WPR * 512 >= len.  Among the layouts that cover the row: the one that
+// fills the chip best (4096 waves of two or more vectors, else 2048 waves), then
+// the least padding, then the fewest waves per row.  Rows longer than 4 * 8 * 512
+// take eight waves and VPT 5..8.
 bool pick_se_cfg(int64_t len, int64_t rows, int64_t forced_wpr, int& vpt, int& wpr) {
     int best_w = -1, best_v = 0;
     int64_t best_pad = 0;
@@ -288,13 +289,16 @@ bool pick_se_cfg(int64_t len, int64_t rows, int64_t forced_wpr, int& vpt, int& w
         const int v = (int)std::max<int64_t>(1, cdiv(len, 512LL * w));
         if (v > 4 && !(w == 8 && v <= 8)) continue;
         const int64_t pad = (int64_t)v * w * 512 - len;
-        // 2048 waves (8 per CU) keep HBM busy; fewer, fuller waves shorten each row's
-        // reduction chain: at [1024, 4096], 2 waves x 4 vectors beat 4 x 2 by 5% (cold)
-        const bool fills = rows * w >= 2048;
+        // 2048 waves (8 per CU) keep HBM busy; 4096 waves of two or more vectors also
+        // halve each wave's share of the row's exponentials, which at [1024, 4096]
+        // (2048 waves of 4 vectors otherwise) is the longest phase of a wave's life:
+        // 4 waves x 2 vectors 6.01 us cold against 2 x 4 6.20 us.  At [4096, 4096]
+        // 2 x 4 already gives 8192 waves (13.45 us against 4 x 2's 14.44 us).
+        auto fill = [&](int ww, int vv) { return rows * ww >= 4096 && vv >= 2 ? 2 : rows * ww >= 2048 ? 1 : 0; };
         if (best_w < 0) { best_w = w; best_v = v; best_pad = pad; continue; }
-        const bool best_fills = rows * best_w >= 2048;
+        const int f = fill(w, v), best_f = fill(best_w, best_v);
         // prefer filling the chip, then least padding, then fewer waves per row
-        if ((fills && !best_fills) || (fills == best_fills && pad < best_pad)) {
+        if (f > best_f || (f == best_f && pad < best_pad)) {
             best_w = w; best_v = v; best_pad = pad;
         }
     }
