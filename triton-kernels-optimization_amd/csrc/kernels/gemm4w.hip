@@ -349,6 +349,19 @@ struct G4 {
                 if (g.c_idx) return *(const int32_t*)(sc + GE::SC + (wm * 128 + r) * 4);
             return m;
         };
+        // A tile wholly inside C whose rows are C's rows in order (no c_idx) and
+        // 16-byte aligned stores without per-row tests: a wave-uniform base (the
+        // wave's first output) plus a 32-bit byte offset per lane.
+        const bool fast = !(Seq::ROUTED && g.c_idx != nullptr) && m0 + T2M <= M && n0 + TN <= N &&
+                          ((uintptr_t)g.c & 15) == 0 && (g.ldc & 7) == 0;
+        const int64_t ldc = g.ldc;
+        const uint8_t* cwave = (const uint8_t*)(g.c + (int64_t)(m0 + wm * 128) * ldc + (SW ? (nb >> 1) : nb));
+        constexpr int SCPR = SW ? NJ * 2 : 8;         // 16-byte chunks per stored row of a pass
+        const uint32_t lofs = (uint32_t)(((lane / SCPR) * ldc + (lane % SCPR) * 8) * 2);
+        auto fast_store = [&](int row, int col, const u32x4& v) {   // row, col: uniform, from the wave's origin
+            const uint8_t* b = cwave + ((int64_t)row * ldc + col) * 2;
+            __builtin_nontemporal_store(v, (u32x4*)(b + lofs));
+        };
         auto bsc = [&](int j, int c) -> f32x4 {       // b_scale of column group c of block j
             if constexpr (KIND == EE_GEMM_F16) return f32x4{1.f, 1.f, 1.f, 1.f};
             else return *(const f32x4*)(sc + GE::SB + (wn * WC + j * 32 + P::col_of(q_of_cq(c), lane)) * 4);
@@ -406,9 +419,13 @@ struct G4 {
                 for (int k = 0; k < 32 / RPR; ++k) {
                     const int rl = k * RPR + lane / CPR, ch = lane % CPR;
                     const u32x4 v = *(const u32x4*)(slot + lds_off(rl, ch));
-                    const int n = (nb >> 1) + ch * 8;
-                    const int32_t crow = crow_of(i * 32 + rl);
-                    if (crow >= 0 && n < na) store_row16(g.c + (int64_t)crow * g.ldc + n, v, true);
+                    if (fast) {
+                        fast_store(i * 32 + k * RPR, 0, v);
+                    } else {
+                        const int n = (nb >> 1) + ch * 8;
+                        const int32_t crow = crow_of(i * 32 + rl);
+                        if (crow >= 0 && n < na) store_row16(g.c + (int64_t)crow * g.ldc + n, v, true);
+                    }
                 }
             } else {
 #pragma unroll
@@ -437,9 +454,13 @@ struct G4 {
                     for (int k = 0; k < 4; ++k) {
                         const int rl = k * 8 + (lane >> 3), ch = lane & 7;
                         const u32x4 v = *(const u32x4*)(slot + lds_off(rl, ch));
-                        const int n = nb + jp * 64 + ch * 8;
-                        const int32_t crow = crow_of(i * 32 + rl);
-                        if (crow >= 0 && n < N) store_row16(g.c + (int64_t)crow * g.ldc + n, v, n + 8 <= N);
+                        if (fast) {
+                            fast_store(i * 32 + k * 8, jp * 64, v);
+                        } else {
+                            const int n = nb + jp * 64 + ch * 8;
+                            const int32_t crow = crow_of(i * 32 + rl);
+                            if (crow >= 0 && n < N) store_row16(g.c + (int64_t)crow * g.ldc + n, v, n + 8 <= N);
+                        }
                     }
                 }
             }
