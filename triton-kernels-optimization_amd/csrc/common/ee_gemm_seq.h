@@ -53,6 +53,16 @@ struct SeqR1 {
         else band_coords(a - T0 * nN, T1, nN, tm, tn);
     }
 };
+// One routed 256 x 128 half of a 1-byte tile (tm, tn in 128-column units), or none.
+struct SeqR1Half {
+    static constexpr bool ROUTED = true, GATHER = false;
+    int n, tm, tn;
+    __device__ __forceinline__ int count() const { return n; }
+    __device__ __forceinline__ void coords(int, int& tm_, int& tn_) const {
+        tm_ = tm;
+        tn_ = tn;
+    }
+};
 // The FP16 tiles f = b, b + G, ... < nF: M-tile f % T2, N-tile f / T2.
 struct SeqRF {
     static constexpr bool ROUTED = true, GATHER = true;    // fp16 rows gathered from x through a_idx

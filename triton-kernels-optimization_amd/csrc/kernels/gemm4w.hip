@@ -349,11 +349,11 @@ struct G4 {
                 if (g.c_idx) return *(const int32_t*)(sc + GE::SC + (wm * 128 + r) * 4);
             return m;
         };
-        // A tile wholly inside C whose rows are C's rows in order (no c_idx) and
-        // 16-byte aligned stores without per-row tests: a wave-uniform base (the
-        // wave's first output) plus a 32-bit byte offset per lane.
-        const bool fast = !(Seq::ROUTED && g.c_idx != nullptr) && m0 + T2M <= M && n0 + TN <= N &&
-                          ((uintptr_t)g.c & 15) == 0 && (g.ldc & 7) == 0;
+        // An un-routed tile wholly inside C with 16-byte aligned rows stores without
+        // per-row tests: a wave-uniform base (the wave's first output) plus a 32-bit
+        // byte offset per lane.
+        const bool fast = !Seq::ROUTED && m0 + T2M <= M && n0 + TN <= N && ((uintptr_t)g.c & 15) == 0 &&
+                          (g.ldc & 7) == 0;
         const int64_t ldc = g.ldc;
         const uint8_t* cwave = (const uint8_t*)(g.c + (int64_t)(m0 + wm * 128) * ldc + (SW ? (nb >> 1) : nb));
         constexpr int SCPR = SW ? NJ * 2 : 8;         // 16-byte chunks per stored row of a pass
@@ -586,6 +586,22 @@ EE_DEV void gemm4w(const EeGemmArgs& g) {
 // tiles in TileDeal rounds), each phase one G4 pipeline.  Every tile sums K in
 // the order of the un-routed kernels, so routed rows equal ee_gemm's rows of
 // their tier bit for bit.
+// The last round R of a deal's 1-byte tiles and its first logical tile, when that
+// round is at most half full (it then runs as 256 x 128 halves).
+EE_DEV bool half_last_round(const TileDeal& d, int G, int& R, int& base) {
+    R = -1;
+    base = 0;
+    if (d.rF == 0) {
+        R = (d.nA + G - 1) / G - 1;
+        base = R * G;
+    } else if (d.nA > d.skip * d.P) {
+        const int q = (d.nA - d.skip * d.P + G - 1) / G - 1;
+        R = d.skip + q;
+        base = d.skip * d.P + q * G;
+    }
+    return R >= 0 && d.nA > base && 2 * (d.nA - base) <= G;
+}
+
 template <int SW>
 EE_DEV void gemm4w_routed(const EeRoutedGemmArgs& r) {
     __shared__ __attribute__((aligned(1024))) uint8_t smem[G4Geom<256>::LDS];
@@ -622,18 +638,49 @@ EE_DEV void gemm4w_routed(const EeRoutedGemmArgs& r) {
             k.run();
         }
     }
-    // the 1-byte tiles: the INT8 ones come first (logical index < T0 * nN)
-    const int n1 = d.count();
+    // The 1-byte tiles: the INT8 ones come first (logical index < T0 * nN).  A last
+    // round at most half full runs as 256 x 128 halves, one per workgroup (both
+    // halves of a tile on one XCD), as gemm4w does: halves sum K in the same order,
+    // so their rows do not change.  (Config 4's per-token gate|up grid: 836 units of
+    // work on 256 workgroups, a fourth round of 68 tiles.)  The halves run first.
+    bool had_half = false;
+    int R, last_base;
+    if (half_last_round(d, G, R, last_base)) {
+        const int rem = d.nA - last_base;
+        const int h = d.pos_all();                    // positions 0 .. G-1, one per workgroup
+        if (h < 2 * rem) {
+            const int a = last_base + (h >> 1);
+            const bool i8 = a < T0 * nN;
+            int tm, tn;
+            if (i8) band_coords(a, T0, nN, tm, tn);
+            else band_coords(a - T0 * nN, T1, nN, tm, tn);
+            const int tn2 = 2 * tn + (h & 1);
+            if (tn2 * 128 < N) {
+                if (sf.n > 0) __syncthreads();        // the previous phase's LDS reads and DMA are done
+                const SeqR1Half sh{1, tm, tn2};
+                if (i8) {
+                    G4<EE_GEMM_I8, SW, SeqR1Half, 128> k(r.t[0], smem, sh, c0, 0);
+                    k.run();
+                } else {
+                    G4<EE_GEMM_F8, SW, SeqR1Half, 128> k(r.t[1], smem, sh, c1, c0);
+                    k.run();
+                }
+                had_half = true;
+            }
+        }
+    }
+    int n1 = d.count();
+    if (half_last_round(d, G, R, last_base)) n1 = max(0, min(n1, R - d.first_round));   // tiles before it
     int ni8 = 0;
     while (ni8 < n1 && d.tile_index(d.first_round + ni8) < T0 * nN) ++ni8;
     if (ni8 > 0) {
-        if (sf.n > 0) __syncthreads();                // the previous phase's LDS reads and DMA are done
+        if (sf.n > 0 || had_half) __syncthreads();
         const SeqR1 s8{d, 0, ni8, T0, T1, nN};
         G4<EE_GEMM_I8, SW, SeqR1, 256> k(r.t[0], smem, s8, c0, 0);
         k.run();
     }
     if (n1 > ni8) {
-        if (sf.n > 0 || ni8 > 0) __syncthreads();
+        if (sf.n > 0 || had_half || ni8 > 0) __syncthreads();
         const SeqR1 s8{d, ni8, n1 - ni8, T0, T1, nN};
         G4<EE_GEMM_F8, SW, SeqR1, 256> k(r.t[1], smem, s8, c1, c0);
         k.run();
