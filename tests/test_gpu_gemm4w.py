@@ -271,6 +271,43 @@ def test_gemm4w_routed_sparse_fp16_halves(ee, orc, N, sw):
             assert np.array_equal(out[t == k], host(full[k]).view(np.uint16)[t == k]), f"tier {k}"
 
 
+@pytest.mark.parametrize("mix,N,sw", [("c4", 11264, True), ("c4", 11264, False), ("int8", 5120, False),
+                                      ("c3", 11264, True), ("int8", 1536, True)])
+def test_gemm4w_routed_last_round_halves(ee, orc, mix, N, sw):
+    """A last round of 1-byte tiles at most half full runs as 256 x 128 halves on
+    twice the workgroups (config 4's gate|up: 748 1-byte tiles, a fourth round of
+    68; INT8 only at N = 5120: 320 tiles, a second round of 64 INT8 halves; N =
+    1536: one round of 96 tiles, all halves): rows equal the 8-wave routed grid's
+    and, per tier, the un-routed GEMMs'."""
+    M, K = 4096, 256
+    rng = np.random.default_rng(N + 7 * sw + len(mix))
+    u = rng.random(M)
+    lo, hi = {"c4": (0.023, 0.981), "c3": (0.2, 0.6), "int8": (1.0, 1.0)}[mix]
+    H = np.where(u < lo, 0.1, np.where(u < hi, 1.0, 9.0)).astype(np.float32)
+    if sw:
+        W = (rng.standard_normal((2 * (N // 2), K)) / np.sqrt(K)).astype(np.float16)
+        codes, scale = ee.quantize_weight_codes(cuda(W))
+        pw = ee.PackedWeight(ee.interleave_gate_up(codes), ee.interleave_gate_up(scale)).materialize()
+    else:
+        B, bs = weights(orc, rng, N, K)
+        pw = ee.prepare_weight(cuda(B), cuda(bs)).materialize()
+    x = cuda(rng.standard_normal((M, K)).astype(np.float16))
+    tier, idx, counts = ee.route(cuda(H), 0.5, 5.0)
+    with _Options(gemm_tile=256):
+        out = host(ee.routed_linear(x, pw, idx, counts, swiglu=sw)).view(np.uint16)
+        assert _last_kernel().startswith("eek_gemm4w_routed")
+    with _Options(gemm_tile=256, gemm_waves=8):
+        ref8 = host(ee.routed_linear(x, pw, idx, counts, swiglu=sw)).view(np.uint16)
+    assert np.array_equal(out, ref8)
+    if not sw:
+        t = host(tier)
+        full = [ee.triton_int8_gemm(x, cuda(B), cuda(bs)), ee.triton_fp8_gemm(x, cuda(B), cuda(bs)),
+                ee.triton_fp16_gemm(x, cuda(B), cuda(bs))]
+        for k in range(3):
+            if (t == k).any():
+                assert np.array_equal(out[t == k], host(full[k]).view(np.uint16)[t == k]), f"tier {k}"
+
+
 @pytest.mark.parametrize("M,K,F", [(4096, 2048, 1408), (600, 256, 320)])
 def test_gemm4w_routed_swiglu(ee, orc, M, K, F):
     """SwiGLU epilogue of the four-wave routed grid: the bits of the 8-wave one."""
