@@ -11,6 +11,11 @@ tiles of two to twelve K stages, several tiles per workgroup on forced grids
 re-issued stages past a workgroup's last tile), grids whose last round runs as
 256 x 128 halves, and the SwiGLU epilogue.  Each case asserts, through
 ee_last_kernel, that the four-wave kernel is the one that ran.
+
+The W8A16 kind (int8 codes + f32 scales, dequantised in registers) on the
+four-wave kernels gives the bits of the FP16 kind on eek_pack_b_f16's weights
+(the same MFMAs on the same weight values in the same order), on the same
+shapes, grids and epilogues.
 """
 import numpy as np
 import pytest
@@ -200,6 +205,90 @@ def test_gemm4w_seeded_sweep(ee, orc, M, K, N, grid):
     assert np.array_equal(o_i8.view(np.uint16), r_i8.view(np.uint16))
     assert np.array_equal(o_f8.view(np.uint16), r_f8.view(np.uint16))
     assert np.array_equal(o_f16.view(np.uint16), r_f16.view(np.uint16))
+
+
+# ---------------------------------------------------------------------------- W8A16 from int8 codes
+
+def _w8a16_and_f16(ee, A, pw, swiglu=False, **opts):
+    """The W8A16 kind on the int8 codes + scales and the FP16 kind on the
+    pre-dequantised weights under opts, with the names of the kernels that ran."""
+    with _Options(**opts):
+        o_w8 = host(ee.gemm("w8a16", cuda(A), pw.i8, None, pw.scale, swiglu=swiglu))
+        n_w8 = _last_kernel()
+        o_f16 = host(ee.gemm("fp16", cuda(A), pw.f16, swiglu=swiglu))
+        n_f16 = _last_kernel()
+    return o_w8, o_f16, n_w8, n_f16
+
+
+@pytest.mark.parametrize("tn", [256, 128])
+@pytest.mark.parametrize("M,K,N,grid", SHAPES + [(520, 128, 1028, 3), (257, 192, 516, 0)])
+def test_gemm4w_w8a16_small(ee, orc, M, K, N, grid, tn):
+    """eek_gemm4w[n128]_w8a16 dequantises the int8 codes in registers to exactly
+    eek_pack_b_f16's weights and runs the FP16 kernel's MFMAs on them: its outputs
+    equal eek_gemm4w[n128]_f16's on the pre-dequantised weights bit for bit (K of
+    two stages of 64 elements and up, ragged M and N, several tiles per workgroup,
+    half last rounds) and lie within 1e-2 of float64."""
+    A, B, bs, pw = _operands(ee, orc, M, K, N, M * 11 + K + N)
+    o_w8, o_f16, n_w8, n_f16 = _w8a16_and_f16(ee, A, pw, gemm_tile=256, gemm_tile_n=tn, gemm_persist=grid,
+                                              gemm_waves=4)
+    assert "gemm4w" in n_w8 and n_w8.endswith("w8a16"), n_w8
+    assert n_f16 == n_w8.replace("w8a16", "f16"), n_f16
+    assert np.array_equal(o_w8.view(np.uint16), o_f16.view(np.uint16))
+    check_close_f64(o_w8, orc.gemm_w8a16_f64(A, B, bs))
+
+
+@pytest.mark.parametrize("M,K,N", [(4096, 4096, 4096), (4096, 4096, 14336), (1024, 4096, 4096)],
+                         ids=["config1", "config2", "config0"])
+def test_gemm4w_w8a16_full_size(ee, orc, M, K, N):
+    """Configs 0-2 at full size on the automatic choice of kernel: where the FP16
+    kind runs the four-wave kernel the W8A16 kind does too, with the same bits;
+    sampled rows within 1e-2 of float64."""
+    A, B, bs, pw = _operands(ee, orc, M, K, N, 5 + N + M)
+    o_w8, o_f16, n_w8, n_f16 = _w8a16_and_f16(ee, A, pw)
+    if "gemm4w" in n_f16:
+        assert n_w8 == n_f16.replace("f16", "w8a16"), (n_w8, n_f16)
+        assert np.array_equal(o_w8.view(np.uint16), o_f16.view(np.uint16))
+    rows = np.array([0, 1, 255, 256, 257, 700, M // 2 - 1, M // 2, M - 2, M - 1])
+    check_close_f64(o_w8[rows], orc.gemm_w8a16_f64(A[rows], B, bs))
+
+
+@pytest.mark.parametrize("tn", [256, 128])
+@pytest.mark.parametrize("M,K,F,grid", [(4096, 2048, 5632, 0), (600, 256, 640, 0), (512, 256, 1216, 8),
+                                        (300, 128, 320, 3)])
+def test_gemm4w_w8a16_swiglu(ee, orc, M, K, F, grid, tn):
+    """The SwiGLU epilogue on int8 gate|up codes: the bits of the FP16 kind's
+    four-wave SwiGLU GEMM on the pre-dequantised interleaved weights."""
+    rng = np.random.default_rng(M + 3 * F)
+    W = (rng.standard_normal((2 * F, K)) / np.sqrt(K)).astype(np.float16)
+    codes, scale = ee.quantize_weight_codes(cuda(W))
+    pw = ee.PackedWeight(ee.interleave_gate_up(codes), ee.interleave_gate_up(scale)).materialize()
+    x = rng.standard_normal((M, K)).astype(np.float16)
+    o_w8, o_f16, n_w8, n_f16 = _w8a16_and_f16(ee, x, pw, swiglu=True, gemm_tile=256, gemm_tile_n=tn,
+                                              gemm_persist=grid, gemm_waves=4)
+    assert "gemm4w" in n_w8 and n_w8.endswith("w8a16_swiglu"), n_w8
+    assert n_f16 == n_w8.replace("w8a16", "f16"), n_f16
+    assert np.array_equal(o_w8.view(np.uint16), o_f16.view(np.uint16))
+
+
+def _w8_sweep_cases(n=16, seed=808):
+    """Seeded shapes and forced grids for the W8A16 kind: K of 2-24 stages of 64."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(n):
+        M = int(rng.integers(1, 1300))
+        N = int(rng.integers(1, 700)) * 4
+        K = int(rng.integers(2, 25)) * 64
+        grid = int(rng.choice([1, 2, 3, 5, 8, 13, 16, 37]))
+        out.append((M, K, N, grid))
+    return out
+
+
+@pytest.mark.parametrize("M,K,N,grid", _w8_sweep_cases())
+def test_gemm4w_w8a16_seeded_sweep(ee, orc, M, K, N, grid):
+    A, B, bs, pw = _operands(ee, orc, M, K, N, M * 13 + K + N + grid)
+    o_w8, o_f16, n_w8, n_f16 = _w8a16_and_f16(ee, A, pw, gemm_tile=256, gemm_persist=grid, gemm_waves=4)
+    assert "gemm4w" in n_w8 and n_f16 == n_w8.replace("w8a16", "f16"), (n_w8, n_f16)
+    assert np.array_equal(o_w8.view(np.uint16), o_f16.view(np.uint16))
 
 
 def test_gemm4w_option_rejects_bad_value(ee):

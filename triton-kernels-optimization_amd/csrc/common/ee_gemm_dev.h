@@ -18,6 +18,12 @@
 EE_DEV int swz(int row) { return (row >> 1) & 7; }
 EE_DEV uint32_t lds_off(int row, int chunk) { return (uint32_t)(row * BKB + ((chunk ^ swz(row)) << 4)); }
 
+// 64-byte LDS rows (int8 W8A16 weight codes, 64 K elements per stage): chunk c
+// of row r at chunk c ^ ((r >> 2) & 3), so that 16 rows x two 8-byte halves of
+// a chunk pair (a ds_read_b64 pass of 32 lanes) fall on 32 distinct bank pairs,
+// as do 16 rows of one chunk for a ds_read_b128 pass.
+EE_DEV int swz64(int row) { return (row >> 2) & 3; }
+
 EE_DEV i32x4 as_i32x4(u32x4 v) { return __builtin_bit_cast(i32x4, v); }
 EE_DEV f16x8 as_f16x8(u32x4 v) { return __builtin_bit_cast(f16x8, v); }
 
@@ -166,6 +172,20 @@ template <> struct Pipe<EE_GEMM_F8> : Lay32 {    // 32x32x64 e4m3: 64 K bytes pe
         return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(b, a, c, 0, 0, 0, 0, 0, 0);
     }
 };
+
+// 4 int8 weight codes (one dword) -> 4 fp16 w = fp16(fp16(b) * s) as two f16x2
+// words (EE/python/kernels.py:215,233): byte b -> fp16 bits 0x6400 | (b ^ 0x80)
+// is 1024 + (b + 128) exactly, minus 1152 is fp16(b); times fp16(scale) in one
+// RNE fp16 multiply, which rounds the exact product as eek_pack_b_f16's f32
+// product (exact: 8 x 11 significant bits) rounded to fp16 does.
+EE_DEV void dq4(uint32_t w, f16x2 s2, uint32_t& lo, uint32_t& hi) {
+    const uint32_t x = w ^ 0x80808080u;
+    const f16x2 bias = {(f16)1152.0f, (f16)1152.0f};
+    const f16x2 a = f16x2_from_bits(__builtin_amdgcn_perm(0x64646464u, x, 0x04010400u)) - bias;
+    const f16x2 b = f16x2_from_bits(__builtin_amdgcn_perm(0x64646464u, x, 0x04030402u)) - bias;
+    lo = bits_of(a * s2);
+    hi = bits_of(b * s2);
+}
 
 // Dequantised value of one accumulator, as the fp16 epilogues compute it
 // (left-to-right f32 multiplies; W8A16 accumulators are the value).

@@ -619,17 +619,7 @@ EE_DEV void gemm_tile(const EeGemmArgs& g, int tm, int tn, uint8_t* smem) {
 #define W8_EPI (W8_NSTAGE * W8_STAGE)             // 120 KB: the epilogue tiles, 4 x 8 KB
 #define W8_LDS (W8_EPI + 4 * 64 * BKB)            // 152 KB
 
-EE_DEV uint32_t w8_boff(int r, int c) { return (uint32_t)(BM * 128 + r * 64 + ((c ^ ((r >> 2) & 3)) << 4)); }
-
-// 4 int8 codes (one dword) -> 4 fp16 w = fp16(fp16(b) * s), as two f16x2 words
-EE_DEV void dq4(uint32_t w, f16x2 s2, uint32_t& lo, uint32_t& hi) {
-    const uint32_t x = w ^ 0x80808080u;
-    const f16x2 bias = {(f16)1152.0f, (f16)1152.0f};
-    const f16x2 a = f16x2_from_bits(__builtin_amdgcn_perm(0x64646464u, x, 0x04010400u)) - bias;
-    const f16x2 b = f16x2_from_bits(__builtin_amdgcn_perm(0x64646464u, x, 0x04030402u)) - bias;
-    lo = bits_of(a * s2);
-    hi = bits_of(b * s2);
-}
+EE_DEV uint32_t w8_boff(int r, int c) { return (uint32_t)(BM * 128 + r * 64 + ((c ^ swz64(r)) << 4)); }
 
 template <int SW>
 EE_DEV void gemm_tile_w8a16(const EeGemmArgs& g, int tm, int tn, uint8_t* smem) {

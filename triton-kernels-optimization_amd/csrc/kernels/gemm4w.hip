@@ -10,6 +10,11 @@
 //   EE_GEMM_F16: fp16 x fp16 -> f32 (v_mfma_f32_16x16x32_f16, four per 32x32 block
 //                and 64-byte K slice); C = fp16(acc)
 //                (EE/python/kernels.py:192-246, W8A16 weights pre-dequantised)
+//   EE_GEMM_W8A16: the same GEMM from the int8 weight codes and f32 column
+//                scales, dequantised in registers to exactly the pre-dequantised
+//                weights (dq4): the same MFMAs on the same fragment values in the
+//                same order, so the same bits as EE_GEMM_F16 on those weights,
+//                with B streamed at 1 byte per element.
 //
 // Why four waves.  The eight-wave 256-tile pipeline (gemm256.hip) gives each
 // wave a 128 x 64 block, so every A row of a stage is read from LDS by four
@@ -53,36 +58,47 @@
 
 #define G4_THREADS 256
 
-// Tile 256 x TN (TN = 256 or 128).  Wave w owns rows 128 (w >> 1) .. +127 and
-// columns (TN / 2) (w & 1) .. + TN / 2 - 1 as 4 x NJ blocks of 32 x 32.
-template <int TN>
+// Tile 256 x TN (TN = 256 or 128).  The waves form a WM x WN grid over the tile:
+// wave w owns rows WR (w / WN) .. + WR - 1 and columns WC (w % WN) .. + WC - 1
+// as NI x NJ blocks of 32 x 32.  A stage holds 128 K bytes of each A row and BRB
+// K bytes of each B row: 128, or 64 for int8 W8A16 codes (64 K elements, as the
+// fp16 A rows' 128 bytes).  2 x 2 waves of 128 x (TN / 2), except W8A16 256 x 256
+// tiles: 1 x 4 waves of 256 x 64, so that each B column's codes are dequantised
+// by one wave of the workgroup instead of two.
+template <int TN, int BRB = BKB, int WN_ = 2>
 struct G4Geom {
-    static constexpr int STAGE = (T2M + TN) * BKB;    // 64 KB or 48 KB
+    static constexpr int STAGE = T2M * BKB + TN * BRB;   // 64, 48, 48 or 40 KB
     static constexpr int SLOTS = 2 * STAGE;           // after the ring of two stages
     static constexpr int SLOT = 32 * 64 * 2;          // 32 rows x 64 fp16 columns per wave
     static constexpr int SCALES = SLOTS + 4 * SLOT;   // two scale areas (tile parity)
     static constexpr int SA = 0, SB = T2M * 4, SC = SB + TN * 4;   // a_scale, b_scale, C rows
     static constexpr int SCALE_SZ = SC + T2M * 4;
-    static constexpr int LDS = SCALES + 2 * SCALE_SZ; // 150 KB or 117 KB
-    static constexpr int WC = TN / 2;                 // columns of a wave's block
-    static constexpr int NJ = WC / 32;                // its 32-column blocks
+    static constexpr int LDS = SCALES + 2 * SCALE_SZ; // 150, 117, 118 or 101 KB
+    static constexpr int WN = WN_, WM = 4 / WN_;     // the wave grid
+    static constexpr int WR = T2M / WM, WC = TN / WN; // rows and columns of a wave's block
+    static constexpr int NI = WR / 32, NJ = WC / 32;  // its 32-row and 32-column blocks
     static constexpr int AG = 8;                      // A row groups (of 8 rows) per wave and stage
-    static constexpr int BG = TN / 32;                // B row groups per wave and stage
+    static constexpr int BROWS = 1024 / BRB;          // B rows per DMA instruction (8 or 16)
+    static constexpr int BG = TN / BROWS / 4;         // B row groups per wave and stage
+    static constexpr int BRB_ = BRB;
     static constexpr int PARTS = AG + BG;             // DMA instructions per wave and stage
 };
 
 template <int KIND, int SW, class Seq, int TN = 256>
 struct G4 {
-    typedef G4Geom<TN> GE;
-    static constexpr int NJ = GE::NJ, WC = GE::WC;
-    typedef std::conditional_t<KIND == EE_GEMM_I8, PipeI8x16, Pipe<KIND>> P;
+    static constexpr bool W8 = KIND == EE_GEMM_W8A16;       // int8 B codes, dequantised in registers
+    static constexpr bool F16T = KIND == EE_GEMM_F16 || W8;  // the FP16 tier: fp16 A, no scales in the epilogue
+    typedef G4Geom<TN, W8 ? 64 : BKB, W8 && TN == 256 ? 4 : 2> GE;
+    static constexpr int NI = GE::NI, NJ = GE::NJ, WR = GE::WR, WC = GE::WC;
+    typedef std::conditional_t<KIND == EE_GEMM_I8, PipeI8x16, std::conditional_t<W8, PipeF16x16, Pipe<KIND>>> P;
     typedef typename P::acc_t acc_t;
     typedef typename P::frag_t frag_t;
-    static constexpr int ESZ = (KIND == EE_GEMM_F16) ? 2 : 1;
+    static constexpr int ESZ = F16T ? 2 : 1;                 // bytes per A element
+    static constexpr int ESZB = KIND == EE_GEMM_F16 ? 2 : 1; // bytes per B element
     static_assert(BKB / P::SB == 2, "two K slices per stage");
     static_assert(NJ % 2 == 0, "the epilogue stores pairs of 32-column blocks");
-    static constexpr int NBLK = 4 * NJ;               // 32 x 32 blocks per wave
-    static constexpr int NFR = 4 + NJ;                // fragments per slice
+    static constexpr int NBLK = NI * NJ;              // 32 x 32 blocks per wave
+    static constexpr int NFR = NI + NJ;               // fragments per slice
 
     const EeGemmArgs& g;
     uint8_t* smem;
@@ -97,10 +113,17 @@ struct G4 {
     const uint8_t* abase;
     const uint8_t* bbase;
     uint32_t aoff[GE::AG], boff[GE::BG];
-    acc_t acc[4][NJ];
+    acc_t acc[NI][NJ];
+    struct RawB {                                     // W8: 8 codes of each of the lane's two B rows
+        u32x2 h[2];
+    };
+    typedef std::conditional_t<W8, RawB, frag_t> bfrag_t;
     struct Frags {
-        frag_t a[4], b[NJ];
+        frag_t a[NI];
+        bfrag_t b[NJ];
     } fr[2];
+    frag_t wb[W8 ? NJ : 1];                           // W8: the slice's dequantised B fragments
+    f16x2 bs2[W8 ? NJ : 1][2];                        // W8: {s, s}, s = fp16(b_scale) of the lane's B rows
 
     __device__ __forceinline__ G4(const EeGemmArgs& g_, uint8_t* smem_, const Seq& seq_, int M_, int64_t off_)
         : g(g_), smem(smem_), seq(seq_), M(M_), off(off_) {}
@@ -114,8 +137,10 @@ struct G4 {
 
     // DMA rows of tile i: one global_load_lds_dwordx4 fills 8 LDS rows (1 KB);
     // lane l lands at row 8 * grp + l / 8, physical chunk l % 8, which holds
-    // logical chunk (l % 8) ^ swz(row).  Wave w fills A row groups 8w .. 8w+7
-    // and B row groups BG w .. BG w + BG-1 (rows clamped to the operand: rows
+    // logical chunk (l % 8) ^ swz(row) (W8 B: 16 rows of 64 bytes, row 16 * grp
+    // + l / 4, physical chunk l % 4 holding (l % 4) ^ swz64(row)).  Wave w fills
+    // A row groups 8w .. 8w+7 and B row groups BG w .. BG w + BG-1 (rows clamped
+    // to the operand: rows
     // beyond it load a valid row whose results are never stored).  Un-routed:
     // offsets from the tile's first row; routed: A row m is a[a_idx[off + m]] or
     // a[off + m], offsets from the operand's start (the launcher checks that
@@ -129,7 +154,7 @@ struct G4 {
         asm volatile("" : "+v"(lane));                // lane-dependent offsets computed here, not hoisted
         constexpr bool routed = Seq::ROUTED;
         abase = (const uint8_t*)g.a + (routed ? 0 : (int64_t)m0 * g.lda * ESZ);
-        bbase = (const uint8_t*)g.b + (int64_t)n0 * g.ldb * ESZ;
+        bbase = (const uint8_t*)g.b + (int64_t)n0 * g.ldb * ESZB;
 #pragma unroll
         for (int q = 0; q < GE::AG; ++q) {
             const int r = (wave * GE::AG + q) * 8 + (lane >> 3);
@@ -142,19 +167,18 @@ struct G4 {
         }
 #pragma unroll
         for (int q = 0; q < GE::BG; ++q) {
-            const int r = (wave * GE::BG + q) * 8 + (lane >> 3);
-            const int lchunk = (lane & 7) ^ swz(r);   // swz(T2M + r) == swz(r)
+            const int r = W8 ? (wave * GE::BG + q) * 16 + (lane >> 2) : (wave * GE::BG + q) * 8 + (lane >> 3);
+            const int lchunk = W8 ? (lane & 3) ^ swz64(r) : (lane & 7) ^ swz(r);   // swz(T2M + r) == swz(r)
             const int n = min(n0 + r, g.N - 1) - n0;
-            uint32_t pr = (uint32_t)n * (uint32_t)(g.ldb * ESZ);
+            uint32_t pr = (uint32_t)n * (uint32_t)(g.ldb * ESZB);
             asm volatile("" : "+v"(pr));
             boff[q] = pr + (uint32_t)(lchunk * 16);
         }
         const uint32_t sa = lds0 + (uint32_t)(GE::SCALES + (i & 1) * GE::SCALE_SZ);
         const int mr = min(m0 + wave * 64 + lane, M - 1);
-        if constexpr (KIND != EE_GEMM_F16) {
-            dma4(g.a_scale + off + mr, sa + GE::SA + wave * 256);
+        if constexpr (!F16T) dma4(g.a_scale + off + mr, sa + GE::SA + wave * 256);
+        if constexpr (KIND != EE_GEMM_F16)
             if (wave < TN / 64) dma4(g.b_scale + min(n0 + wave * 64 + lane, g.N - 1), sa + GE::SB + wave * 256);
-        }
         if constexpr (routed)
             if (g.c_idx) dma4(g.c_idx + off + mr, sa + GE::SC + wave * 256);
     }
@@ -177,11 +201,11 @@ struct G4 {
             }
         }
         const uint32_t s = lds0 + (uint32_t)((iss & 1) * GE::STAGE);
-        const uint32_t kb = (uint32_t)ikt * BKB;
         if constexpr (PT < GE::AG)
-            dma16_at<PT * 8 * BKB>(abase + kb, aoff[PT], s + wave * (GE::AG * 8 * BKB));
+            dma16_at<PT * 8 * BKB>(abase + (uint32_t)ikt * BKB, aoff[PT], s + wave * (GE::AG * 8 * BKB));
         else
-            dma16_at<(PT - GE::AG) * 8 * BKB>(bbase + kb, boff[PT - GE::AG], s + (T2M + wave * GE::BG * 8) * BKB);
+            dma16_at<(PT - GE::AG) * 1024>(bbase + (uint32_t)ikt * GE::BRB_, boff[PT - GE::AG],
+                                           s + T2M * BKB + wave * GE::BG * 1024);
         if constexpr (PT == GE::PARTS - 1) {
             ++ikt;
             ++iss;
@@ -207,21 +231,31 @@ struct G4 {
     // (swz(row0 + x) == swz(x) for row0 % 32 == 0);
     // 32x32 forms: row row0 + (l & 31), chunk SL * SB/16 + (l >> 5) * LSTEP and
     // the chunk CSTEP after it (offsets x = 0, 1).
-    // Fragment K: 0..3 A row block K (rows 128 wm + 32 K), 4.. B row block K - 4
-    // (rows 256 + WC wn + 32 (K - 4)); each read takes the block's offset as its
-    // immediate.
+    // Fragment K: 0..NI-1 A row block K (rows WR wm + 32 K), NI.. B row block K - NI
+    // (rows 256 + WC wn + 32 (K - NI)); each read takes the block's offset as its
+    // immediate.  W8 B: the 8 codes of K elements 32 SL + 8 (l >> 4) .. +7 of rows
+    // (l & 15) and 16 + (l & 15), two ds_read_b64 (byte 32 SL + 8 (l >> 4) of the
+    // 64-byte row: chunk 2 SL + (l >> 5), half (l >> 4) & 1).
     static constexpr int XR = P::SUB16 ? 1 : 2;
     uint32_t offA[2][XR], offB[2][XR];
     template <int SL, int K>
     __device__ __forceinline__ void rd_frag(const uint8_t* st, Frags& f) {
-        constexpr int rel = (K < 4 ? K : K - 4) * 32 * BKB;
+        constexpr int rel = K < NI ? K * 32 * BKB : (K - NI) * 32 * GE::BRB_;
         uint32_t o0, o1 = 0;
-        if constexpr (K < 4) {
+        if constexpr (K < NI) {
             o0 = offA[SL][0];
             if constexpr (XR == 2) o1 = offA[SL][XR - 1];
         } else {
             o0 = offB[SL][0];
             if constexpr (XR == 2) o1 = offB[SL][XR - 1];
+        }
+        if constexpr (W8 && K >= NI) {
+            const uint8_t* q = st + o0 + rel;
+            RawB v;
+            v.h[0] = *(const u32x2*)q;
+            v.h[1] = *(const u32x2*)(q + 16 * 64);
+            f.b[K - NI] = v;
+            return;
         }
         frag_t v;
         if constexpr (P::SUB16) {
@@ -232,8 +266,8 @@ struct G4 {
             const u32x4 x0 = *(const u32x4*)(st + o0 + rel), x1 = *(const u32x4*)(st + o1 + rel);
             v = i32x8{(int)x0[0], (int)x0[1], (int)x0[2], (int)x0[3], (int)x1[0], (int)x1[1], (int)x1[2], (int)x1[3]};
         }
-        if constexpr (K < 4) f.a[K] = v;
-        else f.b[K - 4] = v;
+        if constexpr (K < NI) f.a[K] = v;
+        else if constexpr (!W8) f.b[K - NI] = v;
     }
     template <int SL, int K = 0>
     __device__ __forceinline__ void rd_all(const uint8_t* st, Frags& f) {
@@ -246,7 +280,7 @@ struct G4 {
 #define G4_SB() __builtin_amdgcn_sched_barrier(0)
     // MFMA Q of block (I, J) on fragments f: SUB16 blocks are four 16x16 MFMAs
     // (quarter Q: B half Q >> 1, A half Q & 1), exactly PipeI8x16 / PipeF16x16's
-    // mma; the 32x32 forms are one.
+    // mma; the 32x32 forms are one.  W8 takes B from the dequantised wb[J].
     static constexpr int NQ = P::SUB16 ? 4 : 1;       // MFMAs per block
     static constexpr int NM = NBLK * NQ;              // MFMAs per slice
     template <int I, int J, int Q>
@@ -255,16 +289,30 @@ struct G4 {
             acc[I][J] = P::mma(f.b[J], f.a[I], acc[I][J]);
         } else if constexpr (KIND == EE_GEMM_I8) {
             acc[I][J].q[Q] = __builtin_amdgcn_mfma_i32_16x16x64_i8(f.b[J].h[Q >> 1], f.a[I].h[Q & 1], acc[I][J].q[Q], 0, 0, 0);
+        } else if constexpr (W8) {
+            acc[I][J].q[Q] = P::m16(wb[J].h[Q >> 1], f.a[I].h[Q & 1], acc[I][J].q[Q]);
         } else {
             acc[I][J].q[Q] = P::m16(f.b[J].h[Q >> 1], f.a[I].h[Q & 1], acc[I][J].q[Q]);
         }
     }
-    // Fragment read order: by first use in the next slice (a0 b0 .. b3, then a1 .. a3).
-    static constexpr int rd_order(int r) { return r == 0 ? 0 : r <= NJ ? 3 + r : r - NJ; }
+    // Block order within a slice: by block rows (I outer), or for W8 by block
+    // columns (J outer), so that each dequantised B fragment is dead after its
+    // column's 16 MFMAs and one set of wb registers serves every slice.  Either
+    // order gives every accumulator the same MFMAs in the same K order.
+    static constexpr bool JMAJ = W8;
+    static constexpr int blk_i(int b) { return JMAJ ? b % NI : b / NJ; }
+    static constexpr int blk_j(int b) { return JMAJ ? b / NI : b % NJ; }
+    // Fragment read order: by first use in the next slice (a0 b0 .. b3, then
+    // a1 .. a3; W8: b0, whose dequantisation comes first, then a0 .. a3, b1 ..).
+    static constexpr int rd_order(int r) {
+        return W8 ? (r == 0 ? NI : r <= NI ? r - 1 : r) : (r == 0 ? 0 : r <= NJ ? NI - 1 + r : r - NJ);
+    }
     // The ops of a slice: RD: the NFR fragment reads of the next slice; DMA: the
-    // PARTS parts of the stage being issued.  With both, two parts then one
-    // read, repeated; op o goes after MFMA (o * span) / n, span = 3/4 of the
-    // slice's MFMAs when reading (the last reads land before the next slice).
+    // PARTS parts of the stage being issued.  With both, reads and parts
+    // interleaved evenly (op o is a read where (o + 1) NFR / n passes an integer:
+    // two parts then one read, repeated, where PARTS = 2 NFR); op o goes after
+    // MFMA (o * span) / n, span = 3/4 of the slice's MFMAs when reading (the last
+    // reads land before the next slice).
     static constexpr int n_ops(bool rd, bool dma) { return (rd ? NFR : 0) + (dma ? GE::PARTS : 0); }
     static constexpr int op_at(int m, bool rd, bool dma) {   // first op after MFMA m (m may be NM: the end)
         const int n = n_ops(rd, dma), span = rd ? (NM * 3) / 4 : NM;
@@ -274,10 +322,10 @@ struct G4 {
     template <int SL, bool RD, bool DMA, int O>
     __device__ __forceinline__ void op(const uint8_t* rs, Frags& nf) {
         if constexpr (RD && DMA) {
-            constexpr int g = O / 3, k = O % 3;           // groups of (part, part, read)
-            static_assert(GE::PARTS == 2 * NFR, "two parts per fragment read");
-            if constexpr (k < 2) issue_part<2 * g + k>();
-            else rd_frag<SL, rd_order(g)>(rs, nf);
+            constexpr int n = NFR + GE::PARTS;
+            constexpr int r0 = (O * NFR) / n, r1 = ((O + 1) * NFR) / n;   // reads before op O, through it
+            if constexpr (r1 > r0) rd_frag<SL, rd_order(r1 - 1)>(rs, nf);
+            else issue_part<O - r0>();
         } else if constexpr (RD) {
             rd_frag<SL, rd_order(O)>(rs, nf);
         } else if constexpr (DMA) {
@@ -291,15 +339,88 @@ struct G4 {
             ops<SL, RD, DMA, O + 1, OE>(rs, nf);
         }
     }
-    // The MFMAs of one K slice on fragments fr[C], block row by block row, one
-    // MFMA at a time with the slice's ops between them (RD: slice SL of the stage
-    // at rs into fr[1 - C]).
+    // W8 dequantisation: unit U (0..3) of B fragment J from raw codes f.b[J]:
+    // half U >> 1, codes 4 (U & 1) .. +3 -> fp16 words 2 (U & 1), +1 of wb[J].
+    template <int J, int U>
+    __device__ __forceinline__ void dq_unit(const Frags& f) {
+        constexpr int h = U >> 1, d = U & 1;
+        uint32_t lo, hi;
+        dq4(f.b[J].h[h][d], bs2[J][h], lo, hi);
+        asm volatile("" : "+v"(lo), "+v"(hi));        // computed here, not sunk past the stage barrier
+        wb[J].h[h][2 * d] = (int)lo;
+        wb[J].h[h][2 * d + 1] = (int)hi;
+    }
+    template <int J, int U = 0>
+    __device__ __forceinline__ void dq_frag(const Frags& f) {
+        if constexpr (U < 4) {
+            dq_unit<J, U>(f);
+            dq_frag<J, U + 1>(f);
+        }
+    }
+    // The units in flight, one step per MFMA: dq4's four dependent steps (xor;
+    // the two perms; the two bias subtracts; the two scale multiplies), each a
+    // full MFMA after the one before, so that no VALU op waits on its operand
+    // and at most two issue between two MFMAs (the matrix core is never left
+    // without a queued MFMA).
+    uint32_t dq_x[1], dq_p[2];                        // W8: the unit in flight
+    template <int J, int U, int S>
+    __device__ __forceinline__ void dq_part(const Frags& f) {
+        constexpr int h = U >> 1, d = U & 1;
+        if constexpr (S == 0) {
+            dq_x[0] = f.b[J].h[h][d] ^ 0x80808080u;
+        } else if constexpr (S == 1) {
+            dq_p[0] = __builtin_amdgcn_perm(0x64646464u, dq_x[0], 0x04010400u);
+            dq_p[1] = __builtin_amdgcn_perm(0x64646464u, dq_x[0], 0x04030402u);
+        } else if constexpr (S == 2) {
+            const f16x2 bias = {(f16)1152.0f, (f16)1152.0f};
+            dq_p[0] = bits_of(f16x2_from_bits(dq_p[0]) - bias);
+            dq_p[1] = bits_of(f16x2_from_bits(dq_p[1]) - bias);
+        } else {
+            uint32_t lo = bits_of(f16x2_from_bits(dq_p[0]) * bs2[J][h]);
+            uint32_t hi = bits_of(f16x2_from_bits(dq_p[1]) * bs2[J][h]);
+            asm volatile("" : "+v"(lo), "+v"(hi));    // computed here, not sunk past the stage barrier
+            wb[J].h[h][2 * d] = (int)lo;
+            wb[J].h[h][2 * d + 1] = (int)hi;
+        }
+    }
+    // Block column c's CM MFMAs carry the 16 steps of fragment c + 1 of this
+    // slice, or after the last column, of fragment 0 of the next slice (NEXT: its
+    // codes were read during this slice): step 4 u + s (unit u, step s) after
+    // MFMA c CM + (4 u + s) CM / 16.  Unit u writes half u >> 1; the next column's
+    // first MFMAs read half 0, so the last unit (half 1) is read at least two
+    // MFMAs after its last step.
+    static constexpr int CM = NI * NQ;                // MFMAs per block column (16 or 32)
+    template <int C, bool NEXT, int MI>
+    __device__ __forceinline__ void dq_step() {
+        constexpr int c = MI / CM, p = MI % CM, SP = CM / 16;
+        if constexpr (p % SP == 0) {
+            constexpr int k = p / SP, u = k / 4, st = k % 4;
+            if constexpr (c + 1 < NJ) dq_part<c + 1, u, st>(fr[C]);
+            else if constexpr (NEXT) dq_part<0, u, st>(fr[1 - C]);
+        }
+    }
+    // The lane's b_scale pairs of tile t, from its scale area.
+    __device__ __forceinline__ void load_bscales(int t) {
+        const uint8_t* sb = smem + GE::SCALES + (t & 1) * GE::SCALE_SZ + GE::SB;
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const f16 v = (f16)f32_rn(*(const float*)(sb + (wn * WC + j * 32 + h * 16 + (lane & 15)) * 4));
+                bs2[j][h] = f16x2{v, v};
+            }
+    }
+
+    // The MFMAs of one K slice on fragments fr[C], block by block (blk_i, blk_j),
+    // one MFMA at a time with the slice's ops between them (RD: slice SL of the
+    // stage at rs into fr[1 - C]).
     template <int C, int SL, bool RD, bool DMA, int MI = 0>
     __device__ __forceinline__ void slice(const uint8_t* rs) {
         if constexpr (MI < NM) {
             constexpr int b = MI / NQ, q = MI % NQ;
-            mma_q<b / NJ, b % NJ, q>(fr[C]);
+            mma_q<blk_i(b), blk_j(b), q>(fr[C]);
             G4_SB();
+            if constexpr (W8) dq_step<C, RD, MI>();
             ops<SL, RD, DMA, op_at(MI, RD, DMA), op_at(MI + 1, RD, DMA)>(rs, fr[1 - C]);
             G4_SB();
             slice<C, SL, RD, DMA, MI + 1>(rs);
@@ -343,10 +464,10 @@ struct G4 {
         const uint8_t* sc = smem + GE::SCALES + (t & 1) * GE::SCALE_SZ;
         uint8_t* slot = smem + GE::SLOTS + wave * GE::SLOT;
         auto crow_of = [&](int r) -> int32_t {        // C row of wave row r (0..127), -1 beyond M
-            const int m = m0 + wm * 128 + r;
+            const int m = m0 + wm * WR + r;
             if (m >= M) return -1;
             if constexpr (Seq::ROUTED)
-                if (g.c_idx) return *(const int32_t*)(sc + GE::SC + (wm * 128 + r) * 4);
+                if (g.c_idx) return *(const int32_t*)(sc + GE::SC + (wm * WR + r) * 4);
             return m;
         };
         // An un-routed tile wholly inside C with 16-byte aligned rows stores without
@@ -355,7 +476,7 @@ struct G4 {
         const bool fast = !Seq::ROUTED && m0 + T2M <= M && n0 + TN <= N && ((uintptr_t)g.c & 15) == 0 &&
                           (g.ldc & 7) == 0;
         const int64_t ldc = g.ldc;
-        const uint8_t* cwave = (const uint8_t*)(g.c + (int64_t)(m0 + wm * 128) * ldc + (SW ? (nb >> 1) : nb));
+        const uint8_t* cwave = (const uint8_t*)(g.c + (int64_t)(m0 + wm * WR) * ldc + (SW ? (nb >> 1) : nb));
         constexpr int SCPR = SW ? NJ * 2 : 8;         // 16-byte chunks per stored row of a pass
         const uint32_t lofs = (uint32_t)(((lane / SCPR) * ldc + (lane % SCPR) * 8) * 2);
         auto fast_store = [&](int row, int col, const u32x4& v) {   // row, col: uniform, from the wave's origin
@@ -363,18 +484,18 @@ struct G4 {
             __builtin_nontemporal_store(v, (u32x4*)(b + lofs));
         };
         auto bsc = [&](int j, int c) -> f32x4 {       // b_scale of column group c of block j
-            if constexpr (KIND == EE_GEMM_F16) return f32x4{1.f, 1.f, 1.f, 1.f};
+            if constexpr (F16T) return f32x4{1.f, 1.f, 1.f, 1.f};
             else return *(const f32x4*)(sc + GE::SB + (wn * WC + j * 32 + P::col_of(q_of_cq(c), lane)) * 4);
         };
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < NI; ++i) {
             G4_SB();                                  // one block row's accumulators at a time
-            const int mb = m0 + wm * 128 + i * 32;    // first row of this 32-row block
+            const int mb = m0 + wm * WR + i * 32;     // first row of this 32-row block
             float as[P::NRQ] = {};
-            if constexpr (KIND != EE_GEMM_F16)
+            if constexpr (!F16T)
 #pragma unroll
                 for (int h = 0; h < P::NRQ; ++h)
-                    as[h] = *(const float*)(sc + GE::SA + (wm * 128 + i * 32 + P::row_of(h, lane)) * 4);
+                    as[h] = *(const float*)(sc + GE::SA + (wm * WR + i * 32 + P::row_of(h, lane)) * 4);
             if constexpr (KIND == EE_GEMM_I8) {
                 if (!Seq::ROUTED && g.acc) {          // debug output: int32 accumulators, direct stores
 #pragma unroll
@@ -443,7 +564,7 @@ struct G4 {
                             float o[4];
 #pragma unroll
                             for (int r = 0; r < 4; ++r) {
-                                if constexpr (KIND == EE_GEMM_F16) o[r] = acc[i][j][4 * q + r];
+                                if constexpr (F16T) o[r] = acc[i][j][4 * q + r];
                                 else o[r] = deq<KIND>(acc[i][j][4 * q + r], as[P::rq(q)], bs[P::cq(q)][r]);
                             }
                             *(u32x2*)(slot + lds_off(P::row_of(q, lane), cl >> 3) + ((cl >> 2) & 1) * 8) =
@@ -479,7 +600,7 @@ struct G4 {
     }
     __device__ __forceinline__ void zero() {
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < NI; ++i)
 #pragma unroll
             for (int j = 0; j < NJ; ++j) {
                 if constexpr (P::SUB16) {
@@ -495,8 +616,8 @@ struct G4 {
         const int tid = threadIdx.x;
         lane = tid & 63;
         wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-        wm = wave >> 1;
-        wn = wave & 1;
+        wm = wave / GE::WN;
+        wn = wave % GE::WN;
 #pragma unroll
         for (int sl = 0; sl < 2; ++sl)
 #pragma unroll
@@ -504,7 +625,12 @@ struct G4 {
                 uint32_t o;
                 if constexpr (P::SUB16) o = lds_off(lane & 15, lane >> 4) ^ (uint32_t)(sl << 6);
                 else o = lds_off(lane & 31, sl * (P::SB / 16) + (lane >> 5) * P::LSTEP + x * P::CSTEP);
-                uint32_t oa = (uint32_t)(wm * 128 * BKB) + o, ob = (uint32_t)((T2M + wn * WC) * BKB) + o;
+                uint32_t oa = (uint32_t)(wm * WR * BKB) + o, ob = (uint32_t)((T2M + wn * WC) * BKB) + o;
+                if constexpr (W8) {
+                    const int r = lane & 15, g4 = lane >> 4;
+                    ob = (uint32_t)(T2M * BKB + (wn * WC + r) * 64 + (((2 * sl + (g4 >> 1)) ^ swz64(r)) << 4) +
+                                    (g4 & 1) * 8);
+                }
                 asm volatile("" : "+v"(oa), "+v"(ob));
                 offA[sl][x] = oa;
                 offB[sl][x] = ob;
@@ -523,6 +649,10 @@ struct G4 {
         __builtin_amdgcn_s_barrier();                 // barrier 0
         asm volatile("" ::: "memory");
         rd_all<0>(smem, fr[0]);
+        if constexpr (W8) {
+            load_bscales(0);
+            dq_frag<0>(fr[0]);
+        }
         int cs = 0;
         for (int t = 0; t < ntiles; ++t) {
             zero();
@@ -533,6 +663,10 @@ struct G4 {
             if (t + 1 < ntiles) {                     // slice 0 of the next tile's first stage (landed)
                 G4_SB();
                 rd_all<0>(smem + (cs & 1) * GE::STAGE, fr[0]);
+                if constexpr (W8) {
+                    load_bscales(t + 1);
+                    dq_frag<0>(fr[0]);
+                }
             }
         }
         WAITCNT_VM(0);                                // the re-issued stages have landed
@@ -546,7 +680,7 @@ struct G4 {
 // order, so the output bits do not change.
 template <int KIND, int SW, int TN>
 EE_DEV void gemm4w(const EeGemmArgs& g) {
-    __shared__ __attribute__((aligned(1024))) uint8_t smem[G4Geom<TN>::LDS];
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[G4<KIND, SW, Seq256<TN>, TN>::GE::LDS];
     const int b = (int)blockIdx.x, G = (int)gridDim.x;
     const Seq256<TN> seq(g, b, G);
     if constexpr (TN == 256) {
@@ -695,10 +829,12 @@ EE_DEV void gemm4w_routed(const EeRoutedGemmArgs& r) {
 EE_G4_ENTRY(eek_gemm4w_i8, EE_GEMM_I8, 256)
 EE_G4_ENTRY(eek_gemm4w_f8, EE_GEMM_F8, 256)
 EE_G4_ENTRY(eek_gemm4w_f16, EE_GEMM_F16, 256)
+EE_G4_ENTRY(eek_gemm4w_w8a16, EE_GEMM_W8A16, 256)
 // 256 x 128 tiles
 EE_G4_ENTRY(eek_gemm4wn128_i8, EE_GEMM_I8, 128)
 EE_G4_ENTRY(eek_gemm4wn128_f8, EE_GEMM_F8, 128)
 EE_G4_ENTRY(eek_gemm4wn128_f16, EE_GEMM_F16, 128)
+EE_G4_ENTRY(eek_gemm4wn128_w8a16, EE_GEMM_W8A16, 128)
 // the routed grid
 extern "C" __global__ void __launch_bounds__(G4_THREADS) __attribute__((amdgpu_waves_per_eu(1, 1)))
 eek_gemm4w_routed(EeRoutedGemmArgs r) { gemm4w_routed<0>(r); }

@@ -659,6 +659,31 @@ static int gemm_impl(ee_engine* eng, int32_t kind, const void* a, int64_t lda, c
         if (M == 0) return EE_OK;
         EeGemmArgs g{a, b_nk, (uint16_t*)c, nullptr, nullptr, b_scale, a_idx, c_idx, counts, lda, ldb, ldc,
                      M, N, K, counts ? tier : 0, sw};
+        // The four-wave 256-row tiles (eek_gemm4w[n128]_w8a16) wherever EE_GEMM_F16 on
+        // eek_pack_b_f16's weights would run eek_gemm4w[n128]_f16 (the conditions
+        // below): the same MFMAs on the same weight values in the same K order, so
+        // the same bits, with B streamed at 1 byte per element.
+        {
+            const int64_t tiles = cdiv(M, 128) * cdiv(N, 128);
+            const bool off32 = 255 * std::max(lda * 2, ldb) + K * 2 < (int64_t(1) << 32);
+            const int64_t tile_opt = opt(eng, "gemm_tile"), tn_opt = opt(eng, "gemm_tile_n");
+            if (counts == nullptr && K >= 128 && tile_opt != 128 && off32 && opt(eng, "gemm_variant") != 2 &&
+                opt(eng, "gemm_waves") != 8 && (tile_opt == 256 || tiles > eng->cus)) {
+                const int64_t gcu = eng->cus >= 8 ? (eng->cus & ~7) : eng->cus;
+                const int64_t t256 = cdiv(M, 256) * cdiv(N, 256), t128 = cdiv(M, 256) * cdiv(N, 128);
+                const bool narrow = tn_opt == 128 || (tn_opt == 0 && 2 * t256 <= gcu);
+                const std::string n4 = std::string(narrow ? "eek_gemm4wn128_w8a16" : "eek_gemm4w_w8a16") +
+                                       (sw ? "_swiglu" : "");
+                const Kernel* k4 = find_kernel(eng, n4);
+                if (k4 != nullptr) {
+                    const int64_t tt = narrow ? t128 : t256;
+                    int64_t g4 = persist_grid(eng, tt);
+                    if (g4 <= 0) g4 = std::min<int64_t>(tt, gcu);
+                    if (g4 <= 0) g4 = tt;
+                    return launch(eng, n4, g4, 1, k4->block, g, stream);
+                }
+            }
+        }
         const std::string name = sw ? "eek_gemm_w8a16_swiglu" : "eek_gemm_w8a16";
         const Kernel* k = find_kernel(eng, name);
         return launch(eng, name, cdiv(M, 128) * cdiv(N, 128), 1, k ? k->block : EE_BLOCK, g, stream);
