@@ -31,9 +31,20 @@ EE_DEV int tier_of(float h, double tl, double th) {
     return d < tl ? 0 : (d < th ? 1 : 2);
 }
 
-// Entropy from the reduced partial sums (see header comment).
+// ln x for x >= 1: v_log_f32 (log2, within 1 ulp of the result) times ln 2.
+EE_DEV float ln_ge1(float x) { return __builtin_amdgcn_logf(x) * LN2; }
+// log1p(x) for x >= 0 (Goldberg): u = 1 + x; x ln(u) / (u - 1) with u - 1 exact,
+// which cancels u's rounding, or x where u rounds to 1.  A few ulps relative.
+EE_DEV float log1p_ge0(float x) {
+    const float u = 1.0f + x;
+    return u == 1.0f ? x : ln_ge1(u) * (x * __builtin_amdgcn_rcpf(u - 1.0f));
+}
+// Entropy from the reduced partial sums (see header comment): c0 >= 1 counts the
+// entries at the max, z >= 0, t <= 0, so every term is >= 0; the quotients take
+// v_rcp_f32 (1 ulp).  Within ~1e-6 relative of the libm form (logf, log1pf and
+// IEEE divisions: ~120 dependent instructions, evaluated once per row).
 EE_DEV float entropy_from(float c0, float z, float t) {
-    return logf(c0) + log1pf(z / c0) - t / (c0 + z);
+    return ln_ge1(c0) + log1p_ge0(z * __builtin_amdgcn_rcpf(c0)) - t * __builtin_amdgcn_rcpf(c0 + z);
 }
 
 // s = x - m for the low / high fp16 half of a packed word: one v_fma_mix_f32
@@ -190,7 +201,7 @@ EE_DEV void se_process(const EeSoftmaxArgs& a, u32x4 (&v)[VPT], int64_t row, boo
     float z = wave_sum(z0 + z1);
     float t = wave_sum(t0 + t1);
     if (!has_max) t *= LN2;
-    float cz = (float)wave_sum_i32(cnt);
+    float cz = has_max ? (float)wave_sum_i32(cnt) : 0.0f;   // cnt is 0 in every lane elsewhere
     if constexpr (WPR > 1) {
         if (lane == 0) { red[w][1] = z; red[w][2] = t; red[w][3] = cz; }
         __syncthreads();
