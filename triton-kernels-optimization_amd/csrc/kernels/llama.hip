@@ -128,75 +128,83 @@ EE_RMSNORM(8)
 // half, x2 = the same positions of the second half (h = d/2):
 //   out[j]   = fp16( fp16(x[j] * cos[j])     + fp16(-x[j+h] * sin[j]) )
 //   out[j+h] = fp16( fp16(x[j+h] * cos[j+h]) + fp16( x[j]   * sin[j+h]) )
-// which is torch's x * cos + rotate_half(x) * sin, each op rounded to fp16
-// (products of two fp16 values are exact in f32; the sum is rounded from f32,
-// as torch's fp16 add).  q_scale != 1 then stores fp16(out * q_scale).
-EE_DEV uint32_t rope2(uint32_t xa, uint32_t xb, uint32_t c, uint32_t s, bool first, float scale) {
-    float o[2];
+// which is torch's x * cos + rotate_half(x) * sin, each op rounded to fp16.
+// Packed fp16 multiplies and adds give exactly those roundings: a product of
+// two fp16 values is exact in f32, so rounding it once to fp16 is the RNE fp16
+// product; the f32 sum of two fp16 values is exact whenever it can matter (an
+// addend more than 2^13 below the other is under an eighth of the result's
+// fp16 ulp), so its fp16 rounding is the RNE fp16 sum.
+EE_DEV void rope8(const u32x4& x1, const u32x4& x2, const u32x4& c1, const u32x4& s1, const u32x4& c2,
+                  const u32x4& s2, u32x4& o1, u32x4& o2) {
 #pragma unroll
-    for (int e = 0; e < 2; ++e) {
-        const float a = e ? f16_hi(xa) : f16_lo(xa);  // this element
-        const float b = e ? f16_hi(xb) : f16_lo(xb);  // its partner in the other half
-        const float cc = e ? f16_hi(c) : f16_lo(c), sn = e ? f16_hi(s) : f16_lo(s);
-        const float t1 = f16_round(a * cc);
-        const float t2 = f16_round((first ? -b : b) * sn);
-        float v = f16_round(t1 + t2);
-        if (scale != 1.0f) v = v * scale;
-        o[e] = v;
+    for (int j = 0; j < 4; ++j) {
+        const f16x2 a = f16x2_from_bits(x1[j]), b = f16x2_from_bits(x2[j]);
+        o1[j] = bits_of(a * f16x2_from_bits(c1[j]) - b * f16x2_from_bits(s1[j]));
+        o2[j] = bits_of(b * f16x2_from_bits(c2[j]) + a * f16x2_from_bits(s2[j]));
     }
-    return pack_f16x2(o[0], o[1]);
+}
+// fp16(v * scale) for packed fp16 v: torch's f32 product rounded to fp16.  A power
+// of two (1/sqrt(d) for d = 4^k) is one exact packed fp16 multiply.
+EE_DEV void scale8(u32x4& o, float scale, bool pow2) {
+    if (pow2) {
+        const f16x2 s2 = {(f16)scale, (f16)scale};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o[j] = bits_of(f16x2_from_bits(o[j]) * s2);
+    } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o[j] = pack_f16x2(f16_lo(o[j]) * scale, f16_hi(o[j]) * scale);
+    }
 }
 
+// Work items (32-bit indices: the launcher checks that they fit): the v_t units
+// first (each moves 16 rows, the longest items, so they start with the first
+// workgroups), then the q/k chunk pairs, then the plain v chunks.
 extern "C" __global__ void __launch_bounds__(EE_BLOCK) eek_qkv_rope(EeQkvRopeArgs a) {
-    const int d = a.d, h = d >> 1;
-    const int cpr = d >> 4;                           // 8-element chunk pairs per head row
-    const int64_t T = (int64_t)a.B * a.S;
-    const int64_t n_qk = T * (a.Hq + a.Hkv) * cpr;
+    const uint32_t d = (uint32_t)a.d, h = d >> 1;
+    const uint32_t cpr = d >> 4;                      // 8-element chunk pairs per head row
+    const uint32_t HH = (uint32_t)(a.Hq + a.Hkv), S = (uint32_t)a.S;
+    const uint32_t T = (uint32_t)a.B * S;
+    const uint32_t n_qk = T * HH * cpr;
     // v: 16-byte chunks of each token's heads, or with v_t one unit per 16 tokens x
     // 8 d of a kv head, transposed in registers
-    const int64_t n_v = a.v_t ? (int64_t)a.B * a.Hkv * (a.S >> 4) * (d >> 3) : T * a.Hkv * (d >> 3);
-    const int64_t stride = (int64_t)gridDim.x * EE_BLOCK;
-    // Work items: the v_t units first (each moves 16 rows, the longest items, so
-    // they start with the first workgroups), then the q/k chunk pairs, then the
-    // plain v chunks.
-    const int64_t n_vt = a.v_t ? n_v : 0;
-    for (int64_t i0 = (int64_t)blockIdx.x * EE_BLOCK + threadIdx.x; i0 < n_qk + n_v; i0 += stride) {
-        const int64_t i = i0 < n_vt ? i0 + n_qk : i0 - n_vt;   // index in the order q/k, v
+    const uint32_t n_v = a.v_t ? (uint32_t)a.B * a.Hkv * (S >> 4) * (d >> 3) : T * a.Hkv * (d >> 3);
+    const uint32_t stride = gridDim.x * EE_BLOCK;
+    const uint32_t n_vt = a.v_t ? n_v : 0;
+    const float q_scale = a.q_scale;
+    const bool pow2 = q_scale > 0.0f && (__float_as_uint(q_scale) & 0x007fffffu) == 0 && q_scale >= 0x1p-14f &&
+                      q_scale <= 0x1p15f;        // an exact fp16 power of two
+    for (uint32_t i0 = blockIdx.x * EE_BLOCK + threadIdx.x; i0 < n_qk + n_v; i0 += stride) {
+        const uint32_t i = i0 < n_vt ? i0 + n_qk : i0 - n_vt;   // index in the order q/k, v
         if (i < n_qk) {
-            const int c = (int)(i % cpr);
-            const int64_t th = i / cpr;
-            const int head = (int)(th % (a.Hq + a.Hkv));
-            const int64_t t = th / (a.Hq + a.Hkv);
-            const int b = (int)(t / a.S), s = (int)(t % a.S);
-            const uint16_t* src = a.qkv + t * a.ld + (int64_t)head * d + 8 * c;
+            const uint32_t c = i % cpr, th = i / cpr;
+            const uint32_t head = th % HH, t = th / HH;
+            const uint32_t b = t / S, sp = t - b * S;
+            const uint16_t* src = a.qkv + (int64_t)t * a.ld + head * d + 8 * c;
             const u32x4 x1 = *(const u32x4*)src, x2 = *(const u32x4*)(src + h);
-            const uint16_t* cr = a.cos_t + (int64_t)s * d + 8 * c;
-            const uint16_t* sr = a.sin_t + (int64_t)s * d + 8 * c;
+            const uint16_t* cr = a.cos_t + sp * d + 8 * c;
+            const uint16_t* sr = a.sin_t + sp * d + 8 * c;
             const u32x4 c1 = *(const u32x4*)cr, c2 = *(const u32x4*)(cr + h);
             const u32x4 s1 = *(const u32x4*)sr, s2 = *(const u32x4*)(sr + h);
-            const bool isq = head < a.Hq;
-            const float scale = isq ? a.q_scale : 1.0f;
+            const bool isq = head < (uint32_t)a.Hq;
             u32x4 o1, o2;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                o1[j] = rope2(x1[j], x2[j], c1[j], s1[j], true, scale);
-                o2[j] = rope2(x2[j], x1[j], c2[j], s2[j], false, scale);
+            rope8(x1, x2, c1, s1, c2, s2, o1, o2);
+            if (isq && q_scale != 1.0f) {
+                scale8(o1, q_scale, pow2);
+                scale8(o2, q_scale, pow2);
             }
-            uint16_t* dst = isq ? a.q + (((int64_t)b * a.Hq + head) * a.S + s) * d
-                                : a.k + (((int64_t)b * a.Hkv + (head - a.Hq)) * a.S + s) * d;
+            uint16_t* dst = isq ? a.q + ((int64_t)(b * a.Hq + head) * S + sp) * d
+                                : a.k + ((int64_t)(b * a.Hkv + (head - a.Hq)) * S + sp) * d;
             *(u32x4*)(dst + 8 * c) = o1;
             *(u32x4*)(dst + h + 8 * c) = o2;
         } else if (a.v_t) {
             // V^T [B, Hkv, d, S]: row dd holds v[.., dd] of every token; within each
             // group of 16 tokens the stored order is 0-3, 8-11, 4-7, 12-15 (the
             // K-slot order of the attention kernel's probability fragments).
-            const int64_t iv = i - n_qk;
-            const int c = (int)(iv % (d >> 3));
-            const int64_t r1 = iv / (d >> 3);
-            const int g = (int)(r1 % (a.S >> 4));
-            const int64_t bh = r1 / (a.S >> 4);
-            const int head = (int)(bh % a.Hkv), b = (int)(bh / a.Hkv);
-            const uint16_t* src = a.qkv + ((int64_t)b * a.S + 16 * g) * a.ld + (int64_t)(a.Hq + a.Hkv + head) * d + 8 * c;
+            const uint32_t iv = i - n_qk;
+            const uint32_t c = iv % (d >> 3), r1 = iv / (d >> 3);
+            const uint32_t g = r1 % (S >> 4), bh = r1 / (S >> 4);
+            const uint32_t head = bh % (uint32_t)a.Hkv, b = bh / (uint32_t)a.Hkv;
+            const uint16_t* src = a.qkv + (int64_t)(b * S + 16 * g) * a.ld + (HH + head) * d + 8 * c;
             u32x4 x[16];
 #pragma unroll
             for (int j = 0; j < 16; ++j) x[j] = *(const u32x4*)(src + (int64_t)j * a.ld);
@@ -209,19 +217,17 @@ extern "C" __global__ void __launch_bounds__(EE_BLOCK) eek_qkv_rope(EeQkvRopeArg
 #pragma unroll
                 for (int k = 0; k < 8; ++k)
                     w[k] = __builtin_amdgcn_perm(x[perm[2 * k + 1]][e >> 1], x[perm[2 * k]][e >> 1], sel);
-                uint16_t* dst = a.v + (((int64_t)b * a.Hkv + head) * d + 8 * c + e) * a.S + 16 * g;
+                uint16_t* dst = a.v + ((int64_t)(b * a.Hkv + head) * d + 8 * c + e) * S + 16 * g;
                 *(u32x4*)dst = u32x4{w[0], w[1], w[2], w[3]};
                 *(u32x4*)(dst + 8) = u32x4{w[4], w[5], w[6], w[7]};
             }
         } else {
-            const int64_t iv = i - n_qk;
-            const int c = (int)(iv % (d >> 3));
-            const int64_t th = iv / (d >> 3);
-            const int head = (int)(th % a.Hkv);
-            const int64_t t = th / a.Hkv;
-            const int b = (int)(t / a.S), s = (int)(t % a.S);
-            const u32x4 v = *(const u32x4*)(a.qkv + t * a.ld + (int64_t)(a.Hq + a.Hkv + head) * d + 8 * c);
-            *(u32x4*)(a.v + (((int64_t)b * a.Hkv + head) * a.S + s) * d + 8 * c) = v;
+            const uint32_t iv = i - n_qk;
+            const uint32_t c = iv % (d >> 3), th = iv / (d >> 3);
+            const uint32_t head = th % (uint32_t)a.Hkv, t = th / (uint32_t)a.Hkv;
+            const uint32_t b = t / S, sp = t - b * S;
+            const u32x4 v = *(const u32x4*)(a.qkv + (int64_t)t * a.ld + (HH + head) * d + 8 * c);
+            *(u32x4*)(a.v + ((int64_t)(b * a.Hkv + head) * S + sp) * d + 8 * c) = v;
         }
     }
 }

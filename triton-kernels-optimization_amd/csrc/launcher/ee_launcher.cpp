@@ -1115,6 +1115,7 @@ static int qkv_rope_impl(ee_engine* eng, const void* qkv, int64_t ld, const void
     EeQkvRopeArgs a{(const uint16_t*)qkv, (const uint16_t*)cos_t, (const uint16_t*)sin_t, (uint16_t*)q, (uint16_t*)k,
                     (uint16_t*)v, ld, B, S, Hq, Hkv, d, q_scale, v_t};
     const int64_t work = T * (Hq + Hkv) * (d / 16) + (v_t ? T / 16 : T) * Hkv * (d / 8);
+    if (work >= (int64_t(1) << 31)) return fail(EE_ERR_UNSUPPORTED, "qkv_rope: more than 2^31 work items");
     return launch(eng, "eek_qkv_rope", std::min<int64_t>(cdiv(work, EE_BLOCK), 16384), 1, EE_BLOCK, a, stream);
 }
 
