@@ -32,9 +32,10 @@ EE_DEV void rmsnorm_row(const EeRmsNormArgs& a, int64_t row, int lane, u32x4 (&o
             u32x4 v = *(const u32x4*)(xr + 8 * c);
             if (a.y) {
                 const u32x4 yv = *(const u32x4*)(a.y + row * a.ld_y + 8 * c);
+                // torch's fp16 add (f32 sum rounded to fp16) is the RNE fp16 sum: one
+                // packed add per two elements
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    v[j] = pack_f16x2(f16_lo(v[j]) + f16_lo(yv[j]), f16_hi(v[j]) + f16_hi(yv[j]));
+                for (int j = 0; j < 4; ++j) v[j] = bits_of(f16x2_from_bits(v[j]) + f16x2_from_bits(yv[j]));
                 *(u32x4*)(a.x_out + row * a.ld_xo + 8 * c) = v;
             }
             s[i] = v;
@@ -52,10 +53,12 @@ EE_DEV void rmsnorm_row(const EeRmsNormArgs& a, int64_t row, int lane, u32x4 (&o
         const int c = lane + 64 * i;
         if (c < nc) {
             const u32x4 w = *(const u32x4*)(a.w + 8 * c);
+            // n = fp16(xf * r) from the f32 product; w * n, a product of two fp16
+            // values, is exact in f32, so its fp16 rounding is one packed fp16 multiply
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const float n0 = f16_round(f16_lo(s[i][j]) * r), n1 = f16_round(f16_hi(s[i][j]) * r);
-                o[i][j] = pack_f16x2(f16_lo(w[j]) * n0, f16_hi(w[j]) * n1);
+                const uint32_t n = pack_f16x2(f16_lo(s[i][j]) * r, f16_hi(s[i][j]) * r);
+                o[i][j] = bits_of(f16x2_from_bits(w[j]) * f16x2_from_bits(n));
             }
             if (store_n) *(u32x4*)(a.n_out + row * a.ld_n + 8 * c) = o[i];
         }

@@ -158,12 +158,14 @@ EE_DEV void se_process(const EeSoftmaxArgs& a, u32x4 (&v)[VPT], int64_t row, boo
     if (dead) m = 0.0f;
     const float negm = -m;
 
-    // ---- 2. -inf -> -65504 (after the max, so NaN rows stay dead)
+    // ---- 2. -inf -> -65504 (after the max, so NaN rows stay dead).  IEEE maximum
+    // (NaN-propagating) needs no canonicalising max of its input first, as maxnum
+    // does: one v_pk_maximum3_f16 per two elements.
     const f16x2 lowest = f16x2_from_bits(0xFBFFFBFFu);
 #pragma unroll
     for (int j = 0; j < VPT; ++j)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) v[j][i] = bits_of(__builtin_elementwise_max(f16x2_from_bits(v[j][i]), lowest));
+        for (int i = 0; i < 4; ++i) v[j][i] = bits_of(__builtin_elementwise_maximum(f16x2_from_bits(v[j][i]), lowest));
 
     // ---- 3. sums
     float ek[KEEP_E ? VPT * 8 : 1];
