@@ -58,38 +58,37 @@
 
 #define G4_THREADS 256
 
-// Tile TM x TN (TM = 256, or 128 for the routed FP16 tier's small partitions;
-// TN = 256 or 128).  The waves form a WM x WN grid over the tile:
+// Tile 256 x TN (TN = 256 or 128).  The waves form a WM x WN grid over the tile:
 // wave w owns rows WR (w / WN) .. + WR - 1 and columns WC (w % WN) .. + WC - 1
 // as NI x NJ blocks of 32 x 32.  A stage holds 128 K bytes of each A row and BRB
 // K bytes of each B row: 128, or 64 for int8 W8A16 codes (64 K elements, as the
 // fp16 A rows' 128 bytes).  2 x 2 waves of 128 x (TN / 2), except W8A16 256 x 256
 // tiles: 1 x 4 waves of 256 x 64, so that each B column's codes are dequantised
 // by one wave of the workgroup instead of two.
-template <int TM, int TN, int BRB = BKB, int WN_ = 2>
+template <int TN, int BRB = BKB, int WN_ = 2>
 struct G4Geom {
-    static constexpr int STAGE = TM * BKB + TN * BRB;    // 64, 48, 48, 40 or 32 KB
+    static constexpr int STAGE = T2M * BKB + TN * BRB;   // 64, 48, 48 or 40 KB
     static constexpr int SLOTS = 2 * STAGE;           // after the ring of two stages
     static constexpr int SLOT = 32 * 64 * 2;          // 32 rows x 64 fp16 columns per wave
     static constexpr int SCALES = SLOTS + 4 * SLOT;   // two scale areas (tile parity)
-    static constexpr int SA = 0, SB = TM * 4, SC = SB + TN * 4;    // a_scale, b_scale, C rows
-    static constexpr int SCALE_SZ = SC + TM * 4;
-    static constexpr int LDS = SCALES + 2 * SCALE_SZ; // 150, 117, 118, 101 or 83 KB
+    static constexpr int SA = 0, SB = T2M * 4, SC = SB + TN * 4;   // a_scale, b_scale, C rows
+    static constexpr int SCALE_SZ = SC + T2M * 4;
+    static constexpr int LDS = SCALES + 2 * SCALE_SZ; // 150, 117, 118 or 101 KB
     static constexpr int WN = WN_, WM = 4 / WN_;     // the wave grid
-    static constexpr int WR = TM / WM, WC = TN / WN;  // rows and columns of a wave's block
+    static constexpr int WR = T2M / WM, WC = TN / WN; // rows and columns of a wave's block
     static constexpr int NI = WR / 32, NJ = WC / 32;  // its 32-row and 32-column blocks
-    static constexpr int AG = TM / 32;                // A row groups (of 8 rows) per wave and stage
+    static constexpr int AG = 8;                      // A row groups (of 8 rows) per wave and stage
     static constexpr int BROWS = 1024 / BRB;          // B rows per DMA instruction (8 or 16)
     static constexpr int BG = TN / BROWS / 4;         // B row groups per wave and stage
     static constexpr int BRB_ = BRB;
     static constexpr int PARTS = AG + BG;             // DMA instructions per wave and stage
 };
 
-template <int KIND, int SW, class Seq, int TN = 256, int TM = T2M>
+template <int KIND, int SW, class Seq, int TN = 256>
 struct G4 {
     static constexpr bool W8 = KIND == EE_GEMM_W8A16;       // int8 B codes, dequantised in registers
     static constexpr bool F16T = KIND == EE_GEMM_F16 || W8;  // the FP16 tier: fp16 A, no scales in the epilogue
-    typedef G4Geom<TM, TN, W8 ? 64 : BKB, W8 && TN == 256 ? 4 : 2> GE;
+    typedef G4Geom<TN, W8 ? 64 : BKB, W8 && TN == 256 ? 4 : 2> GE;
     static constexpr int NI = GE::NI, NJ = GE::NJ, WR = GE::WR, WC = GE::WC;
     typedef std::conditional_t<KIND == EE_GEMM_I8, PipeI8x16, std::conditional_t<W8, PipeF16x16, Pipe<KIND>>> P;
     typedef typename P::acc_t acc_t;
@@ -132,7 +131,7 @@ struct G4 {
     __device__ __forceinline__ void coords(int i, int& m0, int& n0) const {
         int tm, tn;
         seq.coords(i, tm, tn);
-        m0 = tm * TM;
+        m0 = tm * T2M;
         n0 = tn * TN;
     }
 
@@ -169,7 +168,7 @@ struct G4 {
 #pragma unroll
         for (int q = 0; q < GE::BG; ++q) {
             const int r = W8 ? (wave * GE::BG + q) * 16 + (lane >> 2) : (wave * GE::BG + q) * 8 + (lane >> 3);
-            const int lchunk = W8 ? (lane & 3) ^ swz64(r) : (lane & 7) ^ swz(r);   // swz(TM + r) == swz(r)
+            const int lchunk = W8 ? (lane & 3) ^ swz64(r) : (lane & 7) ^ swz(r);   // swz(T2M + r) == swz(r)
             const int n = min(n0 + r, g.N - 1) - n0;
             uint32_t pr = (uint32_t)n * (uint32_t)(g.ldb * ESZB);
             asm volatile("" : "+v"(pr));
@@ -177,12 +176,11 @@ struct G4 {
         }
         const uint32_t sa = lds0 + (uint32_t)(GE::SCALES + (i & 1) * GE::SCALE_SZ);
         const int mr = min(m0 + wave * 64 + lane, M - 1);
-        if constexpr (!F16T)
-            if (wave < TM / 64) dma4(g.a_scale + off + mr, sa + GE::SA + wave * 256);
+        if constexpr (!F16T) dma4(g.a_scale + off + mr, sa + GE::SA + wave * 256);
         if constexpr (KIND != EE_GEMM_F16)
             if (wave < TN / 64) dma4(g.b_scale + min(n0 + wave * 64 + lane, g.N - 1), sa + GE::SB + wave * 256);
         if constexpr (routed)
-            if (g.c_idx && wave < TM / 64) dma4(g.c_idx + off + mr, sa + GE::SC + wave * 256);
+            if (g.c_idx) dma4(g.c_idx + off + mr, sa + GE::SC + wave * 256);
     }
     // Part P (0 .. PARTS-1) of the next stage: A row group 8w + P, then B row
     // group BG w + P - 8: one s_add writing m0 (the part's LDS rows) and the
@@ -207,7 +205,7 @@ struct G4 {
             dma16_at<PT * 8 * BKB>(abase + (uint32_t)ikt * BKB, aoff[PT], s + wave * (GE::AG * 8 * BKB));
         else
             dma16_at<(PT - GE::AG) * 1024>(bbase + (uint32_t)ikt * GE::BRB_, boff[PT - GE::AG],
-                                           s + TM * BKB + wave * GE::BG * 1024);
+                                           s + T2M * BKB + wave * GE::BG * 1024);
         if constexpr (PT == GE::PARTS - 1) {
             ++ikt;
             ++iss;
@@ -482,7 +480,7 @@ struct G4 {
         // An un-routed tile wholly inside C with 16-byte aligned rows stores without
         // per-row tests: a wave-uniform base (the wave's first output) plus a 32-bit
         // byte offset per lane.
-        const bool fast = !Seq::ROUTED && m0 + TM <= M && n0 + TN <= N && ((uintptr_t)g.c & 15) == 0 &&
+        const bool fast = !Seq::ROUTED && m0 + T2M <= M && n0 + TN <= N && ((uintptr_t)g.c & 15) == 0 &&
                           (g.ldc & 7) == 0;
         const int64_t ldc = g.ldc;
         const uint8_t* cwave = (const uint8_t*)(g.c + (int64_t)(m0 + wm * WR) * ldc + (SW ? (nb >> 1) : nb));
@@ -634,10 +632,10 @@ struct G4 {
                 uint32_t o;
                 if constexpr (P::SUB16) o = lds_off(lane & 15, lane >> 4) ^ (uint32_t)(sl << 6);
                 else o = lds_off(lane & 31, sl * (P::SB / 16) + (lane >> 5) * P::LSTEP + x * P::CSTEP);
-                uint32_t oa = (uint32_t)(wm * WR * BKB) + o, ob = (uint32_t)((TM + wn * WC) * BKB) + o;
+                uint32_t oa = (uint32_t)(wm * WR * BKB) + o, ob = (uint32_t)((T2M + wn * WC) * BKB) + o;
                 if constexpr (W8) {
                     const int r = lane & 15, g4 = lane >> 4;
-                    ob = (uint32_t)(TM * BKB + (wn * WC + r) * 64 + (((2 * sl + (g4 >> 1)) ^ swz64(r)) << 4) +
+                    ob = (uint32_t)(T2M * BKB + (wn * WC + r) * 64 + (((2 * sl + (g4 >> 1)) ^ swz64(r)) << 4) +
                                     (g4 & 1) * 8);
                 }
                 asm volatile("" : "+v"(oa), "+v"(ob));
@@ -747,45 +745,33 @@ EE_DEV bool half_last_round(const TileDeal& d, int G, int& R, int& base) {
 
 template <int SW>
 EE_DEV void gemm4w_routed(const EeRoutedGemmArgs& r) {
-    __shared__ __attribute__((aligned(1024))) uint8_t smem[G4Geom<T2M, 256>::LDS];
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[G4Geom<256>::LDS];
     const int32_t* counts = r.t[0].counts;
     const int c0 = counts[0], c1 = counts[1], c2 = counts[2];
     const int T0 = (c0 + T2M - 1) / T2M, T1 = (c1 + T2M - 1) / T2M, T2 = (c2 + T2M - 1) / T2M;
     const int N = r.t[0].N;
     const int nN = (N + 255) / 256;
     const int b = (int)blockIdx.x, G = (int)gridDim.x;
-    // W8A16 tiles: 256 x 256, 256 x 128 halves or 128 x 128 quarters, whichever
-    // gives the shortest estimated makespan (in 1-byte-tile units: a full W8A16
-    // tile costs 2, a half ~1.15, a quarter ~Q20 / 20).  Quarters pay where the
-    // tier's rows fill a fraction of a 256-row tile (config 4's 1.9% FP16 rows:
-    // 78 of 256).  Every workgroup reads the same counts, so every workgroup
-    // makes the same choice.
-    int nF = T2 * nN, skip = 2, form = 0;            // form 0 full, 1 half, 2 quarter
-    const int T2q = (c2 + 127) / 128;
+    // W8A16 tiles: 256 x 256, or 256 x 128 halves where that shortens the estimated
+    // makespan (in 1-byte-tile units: a full W8A16 tile costs 2, a half ~1.15).
+    // Every workgroup reads the same counts, so every workgroup makes the same choice.
+    int nF = T2 * nN, skip = 2;
+    bool half = false;
     {
-        constexpr int Q20 = 13;
-        const int nFh = T2 * ((N + 127) / 128), nFq = T2q * ((N + 127) / 128), nA = (T0 + T1) * nN;
+        const int nFh = T2 * ((N + 127) / 128), nA = (T0 + T1) * nN;
         const int full20 = 20 * max(2 * ((nF + G - 1) / G), (2 * nF + nA + G - 1) / G);
         const int half20 = max(23 * ((nFh + G - 1) / G), 20 * (((23 * nFh + 19) / 20 + nA + G - 1) / G));
-        const int quarter20 = max(Q20 * ((nFq + G - 1) / G), 20 * (((Q20 * nFq + 19) / 20 + nA + G - 1) / G));
-        if (nF > 0 && quarter20 < full20 && quarter20 < half20) {
-            form = 2;
-            nF = nFq;
-            skip = 1;
-        } else if (nF > 0 && half20 < full20) {
-            form = 1;
+        if (nF > 0 && half20 < full20) {
+            half = true;
             nF = nFh;
             skip = 1;
         }
     }
     const TileDeal d(T0 + T1, nN, nF, b, G, skip);
     // phase FP16
-    const SeqRF sf{b, G, b < nF ? (nF - b + G - 1) / G : 0, form == 2 ? T2q : T2};
+    const SeqRF sf{b, G, b < nF ? (nF - b + G - 1) / G : 0, T2};
     if (sf.n > 0) {
-        if (form == 2) {
-            G4<EE_GEMM_F16, SW, SeqRF, 128, 128> k(r.t[2], smem, sf, c2, (int64_t)c0 + c1);
-            k.run();
-        } else if (form == 1) {
+        if (half) {
             G4<EE_GEMM_F16, SW, SeqRF, 128> k(r.t[2], smem, sf, c2, (int64_t)c0 + c1);
             k.run();
         } else {
