@@ -270,7 +270,9 @@ int ee_add_rmsnorm_route(ee_engine* eng, const void* x, int64_t ld_x, const void
  * ([B*S, (Hq + 2*Hkv)*d], row stride ld) into head-major q [B, Hq, S, d],
  * k and v [B, Hkv, S, d]: x*cos + rotate_half(x)*sin with each op rounded to
  * fp16, as the HF Llama attention the reference wraps computes it; cos/sin
- * fp16 [S, d].  q is stored scaled by q_scale (1: unscaled).  d % 16 == 0. */
+ * fp16 [S, d].  q is stored scaled by q_scale (1: unscaled).  d % 16 == 0;
+ * B*S*(Hq + Hkv)*d/16 work items plus the v chunks must stay below 2^31
+ * (EE_ERR_UNSUPPORTED otherwise). */
 int ee_qkv_rope(ee_engine* eng, const void* qkv, int64_t ld, const void* cos_t, const void* sin_t, void* q, void* k,
                 void* v, int32_t B, int32_t S, int32_t Hq, int32_t Hkv, int32_t d, float q_scale,
                 ee_stream_t stream);
