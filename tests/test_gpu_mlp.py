@@ -145,6 +145,25 @@ def test_silu_mul_every_fp16_gate(ee, orc, up):
     check_act(act, gu, orc, ref=ref_torch)
 
 
+@pytest.mark.parametrize("up", [1.0, -3.0, 0.001])
+def test_silu_mul_equals_the_f32_formula_on_every_gate(ee, up):
+    """All 65,536 fp16 gates, bit for bit: act == fp16(fp16(g / (1 + exp(-g))) * up)
+    with each op a torch f32 op on the GPU (exp, add and divide each rounded to
+    f32, as the kernels' f32 evaluation).  The kernels reach it by a fast form
+    (hardware exp2 and reciprocal) wherever a bracket of its error bound fixes the
+    fp16 value, and by the f32 formula elsewhere; this checks that the two agree
+    on every input the fp16 silu can see.  NaN gates only need a NaN."""
+    g = torch.arange(65536, dtype=torch.int32).to(torch.int16).view(torch.float16).reshape(256, 256).cuda()
+    gu = torch.cat([g, torch.full_like(g, up)], dim=1)
+    act = ee.silu_mul(gu)
+    gf = g.float()
+    s16 = (gf / (1.0 + torch.exp(-gf))).half()
+    ref = (s16.float() * gu[:, 256:].float()).half()             # up as the fp16 value the kernel reads
+    nan = torch.isnan(g)
+    assert torch.equal(torch.isnan(act), torch.isnan(ref))
+    assert torch.equal(act.view(torch.int16)[~nan], ref.view(torch.int16)[~nan])
+
+
 def test_silu_mul_rejects_bad_input(ee):
     with pytest.raises(ValueError):
         ee.silu_mul(torch.zeros((4, 7), dtype=torch.float16, device="cuda"))

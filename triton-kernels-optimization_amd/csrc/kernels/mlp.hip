@@ -30,14 +30,14 @@ extern "C" __global__ void __launch_bounds__(EE_BLOCK) eek_silu_mul(EeSiluMulArg
             const u32x4 g = *(const u32x4*)row;
             const u32x4 u = *(const u32x4*)(row + (a.interleave ? 32 : a.F));
             *(u32x4*)(a.act + m * a.ld_act + j) =
-                u32x4{silu_mul2(g[0], u[0]), silu_mul2(g[1], u[1]), silu_mul2(g[2], u[2]), silu_mul2(g[3], u[3])};
+                u32x4{silu_mul2_fast(g[0], u[0]), silu_mul2_fast(g[1], u[1]), silu_mul2_fast(g[2], u[2]), silu_mul2_fast(g[3], u[3])};
         }
     } else {
         const int64_t total = a.M * a.F;
         for (int64_t i = (int64_t)blockIdx.x * EE_BLOCK + threadIdx.x; i < total; i += stride) {
             const int64_t m = i / a.F, j = i - m * a.F;
             const uint16_t* row = a.gu + m * a.ld_gu + gate_col(j, a.F, a.interleave);
-            a.act[m * a.ld_act + j] = (uint16_t)silu_mul2(row[0], row[a.interleave ? 32 : a.F]);
+            a.act[m * a.ld_act + j] = (uint16_t)silu_mul2_fast(row[0], row[a.interleave ? 32 : a.F]);
         }
     }
 }
