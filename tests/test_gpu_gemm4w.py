@@ -362,18 +362,21 @@ def test_gemm4w_routed_sparse_fp16_halves(ee, orc, N, sw):
 
 @pytest.mark.parametrize("mix,N,sw", [("c4", 11264, True), ("c4", 11264, False), ("int8", 5120, False),
                                       ("c3", 11264, True), ("int8", 1536, True), ("c4", 2048, False),
-                                      ("c4", 2560, True), ("c4", 520, False)])
+                                      ("c4", 2560, True), ("c4", 520, False), ("i8f8", 2048, False),
+                                      ("i8f8", 2560, False), ("i8f8", 2560, True)])
 def test_gemm4w_routed_last_round_halves(ee, orc, mix, N, sw):
     """A last round of 1-byte tiles at most half full runs as 256 x 128 halves on
     twice the workgroups (config 4's gate|up: 748 1-byte tiles, a fourth round of
     68; INT8 only at N = 5120: 320 tiles, a second round of 64 INT8 halves; N =
     1536: one round of 96 tiles, all halves; config 4's one-round grids at N =
-    2048 / 2560 / 520 with FP16 halves beside them): rows equal the 8-wave routed
+    2048 / 2560 / 520 with FP16 halves beside them); one-round grids without
+    FP16 rows (config 4's INT8 + FP8 mix at N = 2048 / 2560: 136 / 170 tiles,
+    ~17 per XCD) spread their tiles over the XCDs: rows equal the 8-wave routed
     grid's and, per tier, the un-routed GEMMs'."""
     M, K = 4096, 256
     rng = np.random.default_rng(N + 7 * sw + len(mix))
     u = rng.random(M)
-    lo, hi = {"c4": (0.023, 0.981), "c3": (0.2, 0.6), "int8": (1.0, 1.0)}[mix]
+    lo, hi = {"c4": (0.023, 0.981), "c3": (0.2, 0.6), "int8": (1.0, 1.0), "i8f8": (0.023, 1.0)}[mix]
     H = np.where(u < lo, 0.1, np.where(u < hi, 1.0, 9.0)).astype(np.float32)
     if sw:
         W = (rng.standard_normal((2 * (N // 2), K)) / np.sqrt(K)).astype(np.float16)

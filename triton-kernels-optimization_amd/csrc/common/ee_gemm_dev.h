@@ -226,36 +226,63 @@ EE_DEV void store_row16(uint16_t* dst, const u32x4& v, bool full) {
 // first, round robin: workgroups b < rF get qF + 1, the others qF.  The first
 // `skip` rounds of 1-byte tiles then go only to workgroups b >= rF, which levels
 // the load (a static version of what the hardware dispatcher does for one-tile
-// grids).
+// grids).  A grid of one partial round (fewer tiles than workgroups, no W8A16
+// tiles) gives each XCD ceil(n / 8) consecutive tiles instead, so that its
+// tiles load every XCD's L2 and CUs alike rather than filling the first XCDs
+// and leaving the others idle (config 4's routed q/k/v, o and down projections,
+// 160-170, 136 and 136 tiles of 256 x 256: 31.7 -> 28.4, 33.4 -> 30.5 and
+// 69.4 -> 57.5 us).  The last, partial round of a longer grid keeps the full rounds'
+// positions: spread there, config 4's gate|up grids measured 2-5% slower.
 struct TileDeal {
-    int tiles_m, tiles_n, nA, b, G, per, rF, P, first_round, skip;
+    int tiles_m, tiles_n, nA, b, G, rF, P, first_round, skip;
+    // the rounds of G from logical tile r0 on: `full` full ones, then a partial
+    // one of `rem` tiles; this workgroup's position in a full round and in that one
+    // (spread over the XCDs where it is the grid's only round)
+    int r0, full, rem, pfull, plast;
     __device__ __forceinline__ TileDeal(int tm_count, int tn_count, int nF, int bb, int GG, int sk = 2)
         : tiles_m(tm_count), tiles_n(tn_count), nA(tm_count * tn_count), b(bb), G(GG), skip(sk) {
-        per = (G & 7) == 0 ? G >> 3 : 0;
         rF = nF % G;
         P = G - rF;                                   // workgroups in the first `skip` rounds
         first_round = (rF != 0 && b < rF) ? skip : 0; // heavier workgroups skip those rounds
+        r0 = rF == 0 ? 0 : skip * P;
+        const int left = max(nA - r0, 0);
+        full = left / G;
+        rem = left - full * G;
+        pfull = pos_in(G);
+        plast = rF == 0 && full == 0 ? pos_in(rem) : pfull;
     }
-    // position of this workgroup in a round in which all G take part
-    __device__ __forceinline__ int pos_all() const { return per ? (b & 7) * per + (b >> 3) : b; }
+    // Position of this workgroup in a round of n tiles in which all G take part
+    // (n >= G: a full round): 0 .. n-1 for the workgroups that take a tile, G for
+    // the others.  A full round gives XCD x positions x * G/8 .. +G/8-1; a
+    // partial one q = ceil(n / 8) positions per XCD (pairs: q rounded up to even
+    // where G/8 allows, so that positions 2i and 2i + 1 -- the two halves of a
+    // tile -- share an XCD).
+    __device__ __forceinline__ int pos_in(int n, bool pairs = false) const {
+        const int per = G >> 3;
+        if ((G & 7) != 0) return b;
+        int q = n >= G ? per : (max(n, 0) + 7) >> 3;
+        if (pairs && (q & 1) && q < per) ++q;
+        const int j = b >> 3, p = (b & 7) * q + j;
+        return j < q && p < n ? p : G;
+    }
+    // Position for a halved last round of n2 = 2 rem halves (one per workgroup,
+    // positions 0 .. G-1): spread where that round is the grid's only one.
+    __device__ __forceinline__ int half_pos(int n2, bool only) const { return only ? pos_in(n2, true) : pfull; }
     __device__ __forceinline__ int tile_index(int round) const {
-        if (rF == 0) return round * G + pos_all();
-        if (round < skip) return round * P + (b - rF);
-        return skip * P + (round - skip) * G + pos_all();
+        if (rF != 0 && round < skip) return round * P + (b - rF);
+        const int r = rF == 0 ? round : round - skip;
+        return r0 + r * G + (r < full ? pfull : plast);
     }
     __device__ __forceinline__ int count() const {
         // rounds first_round, first_round+1, ... while tile_index(round) < nA
-        if (rF == 0) {
-            const int p = pos_all();
-            return p < nA ? (nA - p + G - 1) / G : 0;
-        }
-        int n = 0;
+        const int n = full + (plast < rem ? 1 : 0);   // rem == 0: plast == G
+        if (rF == 0) return n;
+        int k = 0;
         if (first_round == 0) {
-            for (int r = 0; r < skip; ++r) n += tile_index(r) < nA;
-            if (n < skip) return n;
+            for (int r = 0; r < skip; ++r) k += tile_index(r) < nA;
+            if (k < skip) return k;
         }
-        const int p = skip * P + pos_all();
-        return n + (p < nA ? (nA - p + G - 1) / G : 0);
+        return k + n;
     }
     // logical tile a -> (tm, tn): bands of 8 M-tiles, M fastest within a band
     __device__ __forceinline__ void coords(int a, int& tm, int& tn) const {

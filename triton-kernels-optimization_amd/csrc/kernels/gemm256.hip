@@ -737,7 +737,7 @@ EE_DEV void gemm256(const EeGemmArgs& g) {
                 k.run();
                 __syncthreads();                      // every wave's reads of the ring and its slot are done
             }
-            const int h = seq.d.pos_all();            // positions 0 .. G-1, one per workgroup
+            const int h = seq.d.half_pos(2 * rem, full == 0);   // one position per workgroup
             Seq256Half sh{0, 0, 0};
             if (h < 2 * rem) {
                 int tm, tn;

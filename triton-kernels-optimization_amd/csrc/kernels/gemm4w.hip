@@ -699,7 +699,7 @@ EE_DEV void gemm4w(const EeGemmArgs& g) {
                 k.run();
                 __syncthreads();                      // every wave's reads of the ring, slots and scales are done
             }
-            const int h = seq.d.pos_all();            // positions 0 .. G-1, one per workgroup
+            const int h = seq.d.half_pos(2 * rem, full == 0);   // one position per workgroup
             Seq256Half sh{0, 0, 0};
             if (h < 2 * rem) {
                 int tm, tn;
@@ -788,7 +788,7 @@ EE_DEV void gemm4w_routed(const EeRoutedGemmArgs& r) {
     int R, last_base;
     if (half_last_round(d, G, R, last_base)) {
         const int rem = d.nA - last_base;
-        const int h = d.pos_all();                    // positions 0 .. G-1, one per workgroup
+        const int h = d.half_pos(2 * rem, d.rF == 0 && last_base == 0);   // one position per workgroup
         if (h < 2 * rem) {
             const int a = last_base + (h >> 1);
             const bool i8 = a < T0 * nN;
