@@ -369,10 +369,10 @@ def test_gemm4w_routed_last_round_halves(ee, orc, mix, N, sw):
     twice the workgroups (config 4's gate|up: 748 1-byte tiles, a fourth round of
     68; INT8 only at N = 5120: 320 tiles, a second round of 64 INT8 halves; N =
     1536: one round of 96 tiles, all halves; config 4's one-round grids at N =
-    2048 / 2560 / 520 with FP16 halves beside them); one-round grids without
-    FP16 rows (config 4's INT8 + FP8 mix at N = 2048 / 2560: 136 / 170 tiles,
-    ~17 per XCD) spread their tiles over the XCDs: rows equal the 8-wave routed
-    grid's and, per tier, the un-routed GEMMs'."""
+    2048 / 2560 / 520 with FP16 halves beside them); config 4's INT8 + FP8 mix
+    at N = 2048 / 2560 (one round, an INT8 tier of one tile row: its tiles run
+    as halves beside the FP8 tiles): rows equal the 8-wave routed grid's and,
+    per tier, the un-routed GEMMs'."""
     M, K = 4096, 256
     rng = np.random.default_rng(N + 7 * sw + len(mix))
     u = rng.random(M)
@@ -400,6 +400,34 @@ def test_gemm4w_routed_last_round_halves(ee, orc, mix, N, sw):
         for k in range(3):
             if (t == k).any():
                 assert np.array_equal(out[t == k], host(full[k]).view(np.uint16)[t == k]), f"tier {k}"
+
+
+@pytest.mark.parametrize("lo,hi,N", [(0.0, 1.0, 2048), (0.1, 1.0, 2048), (0.0, 1.0, 2560), (0.1, 0.99, 2048)])
+def test_gemm4w_routed_one_round_spread(ee, orc, lo, hi, N):
+    """One round of 1-byte tiles (4352 rows: 17 tile rows, 136-170 tiles) spread
+    over the XCDs: all FP8, INT8 over two tile rows beside FP8, and with a few
+    FP16 rows (the W8A16 deal): rows equal the 8-wave routed grid's and, per
+    tier, the un-routed GEMMs'."""
+    M, K = 4352, 256
+    rng = np.random.default_rng(N + int(100 * lo) + int(1000 * hi))
+    u = rng.random(M)
+    H = np.where(u < lo, 0.1, np.where(u < hi, 1.0, 9.0)).astype(np.float32)
+    B, bs = weights(orc, rng, N, K)
+    pw = ee.prepare_weight(cuda(B), cuda(bs)).materialize()
+    x = cuda(rng.standard_normal((M, K)).astype(np.float16))
+    tier, idx, counts = ee.route(cuda(H), 0.5, 5.0)
+    with _Options(gemm_tile=256):
+        out = host(ee.routed_linear(x, pw, idx, counts)).view(np.uint16)
+        assert _last_kernel() == "eek_gemm4w_routed"
+    with _Options(gemm_tile=256, gemm_waves=8):
+        ref8 = host(ee.routed_linear(x, pw, idx, counts)).view(np.uint16)
+    assert np.array_equal(out, ref8)
+    t = host(tier)
+    full = [ee.triton_int8_gemm(x, cuda(B), cuda(bs)), ee.triton_fp8_gemm(x, cuda(B), cuda(bs)),
+            ee.triton_fp16_gemm(x, cuda(B), cuda(bs))]
+    for k in range(3):
+        if (t == k).any():
+            assert np.array_equal(out[t == k], host(full[k]).view(np.uint16)[t == k]), f"tier {k}"
 
 
 @pytest.mark.parametrize("M,K,F", [(4096, 2048, 1408), (600, 256, 320)])

@@ -229,9 +229,9 @@ EE_DEV void store_row16(uint16_t* dst, const u32x4& v, bool full) {
 // grids).  A grid of one partial round (fewer tiles than workgroups, no W8A16
 // tiles) gives each XCD ceil(n / 8) consecutive tiles instead, so that its
 // tiles load every XCD's L2 and CUs alike rather than filling the first XCDs
-// and leaving the others idle (config 4's routed q/k/v, o and down projections,
-// 160-170, 136 and 136 tiles of 256 x 256: 31.7 -> 28.4, 33.4 -> 30.5 and
-// 69.4 -> 57.5 us).  The last, partial round of a longer grid keeps the full rounds'
+// and leaving the others idle (the routed q/k/v, o and down projections at config
+// 4's shapes with INT8 + FP8 rows, 160-170, 136 and 136 tiles of 256 x 256:
+// 31.7 -> 28.4, 33.4 -> 30.5 and 69.4 -> 57.5 us).  The last, partial round of a longer grid keeps the full rounds'
 // positions: spread there, config 4's gate|up grids measured 2-5% slower.
 struct TileDeal {
     int tiles_m, tiles_n, nA, b, G, rF, P, first_round, skip;

@@ -767,6 +767,29 @@ EE_DEV void gemm4w_routed(const EeRoutedGemmArgs& r) {
             skip = 1;
         }
     }
+    // One round of 1-byte tiles, no W8A16 tiles, and an INT8 tier of one tile row
+    // (config 4's ~95 INT8 rows per 4096): each INT8 tile streams all of its B
+    // columns for a few rows, with no other tile sharing them in L2, so it sets the
+    // makespan where B comes from HBM.  The INT8 tiles then run as 256 x 128
+    // halves on the last 2 nN workgroups and the FP8 tiles on the others, spread
+    // over the XCDs (same tiles, same K order, so the same bits).
+    if (nF == 0 && T0 == 1 && T1 > 0 && 2 * (T0 + T1) * nN > G && (T1 + 2) * nN <= G) {
+        const int G8 = G - 2 * nN;
+        if (b >= G8) {
+            const int h = b - G8, tn2 = h;           // half h: columns 128 h ..
+            if (tn2 * 128 < N) {
+                const SeqR1Half sh{1, 0, tn2};
+                G4<EE_GEMM_I8, SW, SeqR1Half, 128> k(r.t[0], smem, sh, c0, 0);
+                k.run();
+            }
+        } else {
+            const TileDeal d8(T1, nN, 0, b, G8);
+            const SeqR1 s8{d8, 0, d8.count(), 0, T1, nN};
+            G4<EE_GEMM_F8, SW, SeqR1, 256> k(r.t[1], smem, s8, c1, c0);
+            k.run();
+        }
+        return;
+    }
     const TileDeal d(T0 + T1, nN, nF, b, G, skip);
     // phase FP16
     const SeqRF sf{b, G, b < nF ? (nF - b + G - 1) / G : 0, T2};
