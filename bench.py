@@ -347,6 +347,11 @@ def main():
                 ee.softmax_entropy(c1_in[i], out_probs=c1_out[i])
 
             run("c1_softmax_entropy", ent_c1, steps=9 * max(1, args.steps // 9), warmup=9)
+            # non-temporal logits loads forced (the automatic choice keeps them for logits
+            # and probabilities beyond the MALL; these buffers are cold by construction)
+            eel.check(eel.lib().ee_engine_set_option(eel.engine(), b"se_nt", 2))
+            run("c1_softmax_entropy_nt", ent_c1, steps=9 * max(1, args.steps // 9), warmup=9)
+            eel.check(eel.lib().ee_engine_set_option(eel.engine(), b"se_nt", 0))
             del c1_in, c1_out, L1
         # ---- config 3: the dispatcher end to end on a mixed batch (M = K = N = 4096)
         c3 = None
@@ -520,6 +525,8 @@ def main():
         g1 = b1 / (results["c1_softmax_entropy"]["ms"] * 1e-3) / 1e9
         kernels["softmax_entropy_c1"] = {"us_cold": results["c1_softmax_entropy"]["ms"] * 1e3, "GBps_cold": g1,
                                          "frac_of_hbm_cold": g1 / PEAK_HBM_GBS, "bytes_per_launch": b1,
+                                         "us_cold_nt_loads": results["c1_softmax_entropy_nt"]["ms"] * 1e3
+                                         if "c1_softmax_entropy_nt" in results else None,
                                          "shape": "config 1: fp16 [4096, 4096] with probabilities, rows as config 0"}
     if mlp is not None:
         kernels["mlp_engine"] = {
