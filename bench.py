@@ -300,7 +300,7 @@ def main():
         # magnitude 20 in A; config 2 [4096, 4096, 14336]; the FP16 baseline is torch.matmul (hipBLASLt)
         big = {}
         big_names = ("c1_int8", "c1_fp8", "c1_fp8_tensor", "c1_fp16_torch", "c1_w8a16", "c2_int8", "c2_fp8",
-                     "c2_fp16_torch")
+                     "c2_fp16_torch", "c2_w8a16")
         if not only or any(n in only for n in big_names):
             for cfg, (Mb, Kb, Nb) in (("c1", (4096, 4096, 4096)), ("c2", (4096, 4096, 14336))):
                 if only and not any(n.startswith(cfg) for n in only):
@@ -327,8 +327,7 @@ def main():
                     cw, sw = ee.quantize_tensor_fp8(Wb)
                     run("c1_fp8_tensor", lambda: ee.gemm("fp8", ca, cw, sa, sw, out=cb), primary="eager")
                 run(f"{cfg}_fp16_torch", lambda: torch.matmul(ab, Wb.t(), out=cb), primary="eager")
-                if cfg == "c1":                                        # this build's own FP16 (W8A16) tier
-                    run("c1_w8a16", lambda: ee.gemm("fp16", ab, pwb.f16, out=cb), primary="eager")
+                run(f"{cfg}_w8a16", lambda: ee.gemm("fp16", ab, pwb.f16, out=cb), primary="eager")   # own FP16 tier
                 big[cfg] = 2.0 * Mb * Nb * Kb
                 del ab, Wb, Bb, pwb, ai_b, cb
         # config 1's softmax + entropy: fp16 [4096, 4096] rows drawn as in config 0, with
@@ -508,7 +507,8 @@ def main():
                 "note": "routed GEMM launch alone (codes from its quantiser) vs the three tiers' own GEMMs on the "
                         "same partitioned rows, each a separate launch"})
     for cfg, ops_b in big.items():
-        legs = ("int8", "fp8", "fp8_tensor", "w8a16", "fp16_torch") if cfg == "c1" else ("int8", "fp8", "fp16_torch")
+        legs = ("int8", "fp8", "fp8_tensor", "w8a16", "fp16_torch") if cfg == "c1" else ("int8", "fp8", "w8a16",
+                                                                                          "fp16_torch")
         peak = {"int8": PEAK_I8_TOPS, "fp8_tensor": PEAK_F8_TFLOPS, "fp8": PEAK_F8_TFLOPS, "w8a16": PEAK_F16_TFLOPS,
                 "fp16_torch": PEAK_F16_TFLOPS}
         kernels[f"gemm_{cfg}"] = {
@@ -519,7 +519,8 @@ def main():
         kernels[f"gemm_{cfg}"]["shape"] = ("M, K, N = 4096, 4096, 4096; A with 0.1% outliers of 20; fp8 = the "
                                            "reference's per-row e4m3 scheme, fp8_tensor = per-tensor amax scales; "
                                            "w8a16 = this build's FP16 tier (fp16 A, W8A16 weights)"
-                                           if cfg == "c1" else "M, K, N = 4096, 4096, 14336")
+                                           if cfg == "c1" else "M, K, N = 4096, 4096, 14336; w8a16 = this build's "
+                                           "FP16 tier")
     if "c1_softmax_entropy" in results:
         b1 = 4096 * 4096 * 4 + 4096 * 4
         g1 = b1 / (results["c1_softmax_entropy"]["ms"] * 1e-3) / 1e9
