@@ -430,6 +430,33 @@ def test_gemm4w_routed_one_round_spread(ee, orc, lo, hi, N):
             assert np.array_equal(out[t == k], host(full[k]).view(np.uint16)[t == k]), f"tier {k}"
 
 
+@pytest.mark.parametrize("n_i8,grid", [(100, 24), (100, 32), (0, 24), (300, 32)])
+def test_gemm4w_routed_one_round_forced_grid(ee, orc, n_i8, grid):
+    """One-round routed grids on forced workgroup counts (gemm_persist): 2000 rows,
+    N = 512 (2 tile columns), INT8 rows first.  100 INT8 rows on 24 or 32 workgroups
+    take the INT8-halves deal on 20 or 28 FP8 workgroups (not a multiple of 8);
+    all-FP8 and two INT8 tile rows take the spread deal.  Rows equal the 8-wave
+    routed grid's and, per tier, the un-routed GEMMs'."""
+    M, K, N = 2000, 256, 512
+    rng = np.random.default_rng(n_i8 + grid)
+    H = np.where(rng.permutation(M) < n_i8, 0.1, 1.0).astype(np.float32)
+    B, bs = weights(orc, rng, N, K)
+    pw = ee.prepare_weight(cuda(B), cuda(bs)).materialize()
+    x = cuda(rng.standard_normal((M, K)).astype(np.float16))
+    tier, idx, counts = ee.route(cuda(H), 0.5, 5.0)
+    with _Options(gemm_tile=256, gemm_persist=grid):
+        out = host(ee.routed_linear(x, pw, idx, counts)).view(np.uint16)
+        assert _last_kernel() == "eek_gemm4w_routed"
+    with _Options(gemm_tile=256, gemm_waves=8):
+        ref8 = host(ee.routed_linear(x, pw, idx, counts)).view(np.uint16)
+    assert np.array_equal(out, ref8)
+    t = host(tier)
+    full = [ee.triton_int8_gemm(x, cuda(B), cuda(bs)), ee.triton_fp8_gemm(x, cuda(B), cuda(bs))]
+    for k in range(2):
+        if (t == k).any():
+            assert np.array_equal(out[t == k], host(full[k]).view(np.uint16)[t == k]), f"tier {k}"
+
+
 @pytest.mark.parametrize("M,K,F", [(4096, 2048, 1408), (600, 256, 320)])
 def test_gemm4w_routed_swiglu(ee, orc, M, K, F):
     """SwiGLU epilogue of the four-wave routed grid: the bits of the 8-wave one."""
