@@ -86,8 +86,8 @@ int ee_engine_destroy(ee_engine* eng);
  * "routed_unfused" = 1 makes ee_routed_linear use its five-launch sequence for
  * every K (for comparisons); "gemm_variant" = 1 runs every GEMM on the
  * loader-wave pipeline, 2 on the 8-wave pipeline where one exists (INT8 and
- * W8A16); automatic: 8-wave for INT8 grids of at most one tile per CU.  INT8
- * results are identical either way.  Every FP16-tier kernel sums K in one f32
+ * W8A16); automatic: the loader-wave pipeline.  INT8 results are identical
+ * either way.  Every FP16-tier kernel sums K in one f32
  * order (slice after slice), whatever the shape, tile size or routing, except
  * the 8-wave form (gemm_variant = 2), which splits K between wave pairs; the
  * routed linear follows ee_gemm's choice.

@@ -75,27 +75,6 @@ struct Lay32 {
     static EE_DEV int row_of(int, int lane) { return lane & 31; }
     static EE_DEV int col_of(int q, int lane) { return 8 * q + 4 * (lane >> 5); }
 };
-// INT8 slices are 64 K bytes deep by default, as FP8's: two 32x32x32 i8 MFMAs
-// per block, on the first and second 16 bytes of each lane's 32 (lanes 0-31
-// hold K bytes 0-31 of the slice, lanes 32-63 bytes 32-63; A and B fragments
-// pair up the same K bytes, and int32 sums are exact in any order).  64 clocks
-// of MFMA per block and slice, against 32 for one 32-byte slice, cover each
-// batch of fragment reads twice as long.  (The 8-wave and 256-tile kernels run
-// the same slices as 16x16x64 MFMAs: PipeI8x16 below.)
-// Fragment chunks: lane l reads 16-byte chunk sl * SB/16 + (l >> 5) * LSTEP of its
-// row and, when CPF == 2, the chunk CSTEP after it.
-struct PipeI8x64 : Lay32 {                       // 2 x 32x32x32 i8: 64 K bytes per slice, 32 B per lane
-    static constexpr int SB = 64, CPF = 2, LSTEP = 2, CSTEP = 1;
-    typedef i32x8 frag_t;
-    typedef i32x16 acc_t;
-    static EE_DEV acc_t mma(const frag_t& b, const frag_t& a, const acc_t& c) {
-        const i32x4 b0{b[0], b[1], b[2], b[3]}, b1{b[4], b[5], b[6], b[7]};
-        const i32x4 a0{a[0], a[1], a[2], a[3]}, a1{a[4], a[5], a[6], a[7]};
-        return __builtin_amdgcn_mfma_i32_32x32x32_i8(b1, a1, __builtin_amdgcn_mfma_i32_32x32x32_i8(b0, a0, c, 0, 0, 0),
-                                                     0, 0, 0);
-    }
-};
-template <> struct Pipe<EE_GEMM_I8> : PipeI8x64 {};
 // 16x16 MFMAs on 64-byte K slices (INT8 16x16x64 i8, FP16 16x16x32 f16): a
 // 32x32 block of a slice is four of them, the same MFMA time as the 32x32
 // forms.  Fragment half h holds rows 16h + (l & 15) of the block, K bytes
@@ -139,6 +118,9 @@ struct PipeI8x16 : Lay16 {
         return r;
     }
 };
+// INT8 slices are 64 K bytes deep, as FP8's, on four 16x16x64 MFMAs per block
+// (int32 sums are exact in any order, so every INT8 kernel has the same bits).
+template <> struct Pipe<EE_GEMM_I8> : PipeI8x16 {};
 struct PipeF16x16 : Lay16 {                       // 16x16x32 f16: 64 K bytes (32 elements) per slice
     static constexpr int SB = 64, CPF = 2, LSTEP = 0, CSTEP = 0;
     typedef I32x4x2 frag_t;
@@ -164,6 +146,8 @@ struct PipeF16x32 : Lay32 {                      // 32x32x16 f16: 32 K bytes per
     }
 };
 template <> struct Pipe<EE_GEMM_F16> : PipeF16x16 {};
+// 32x32 pipes' fragment chunks: lane l reads 16-byte chunk sl * SB/16 + (l >> 5) *
+// LSTEP of its row and, when CPF == 2, the chunk CSTEP after it.
 template <> struct Pipe<EE_GEMM_F8> : Lay32 {    // 32x32x64 e4m3: 64 K bytes per slice, 32 B per lane
     static constexpr int SB = 64, CPF = 2, LSTEP = 2, CSTEP = 1;
     typedef i32x8 frag_t;

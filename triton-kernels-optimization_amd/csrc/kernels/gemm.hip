@@ -19,8 +19,7 @@
 // (global_load_lds_dwordx4, no VGPR staging) stream into a ring of LDS stages;
 // LDS rows are 128 bytes, 16-byte chunk c of row r at chunk c ^ ((r >> 1) & 7).
 // Per block and K slice the MFMAs are the pipes of ee_gemm_dev.h: INT8 four
-// 16x16x64 (8-wave) or two 32x32x32 (loader-wave, persistent) per 64-byte
-// slice, FP8 one 32x32x64, FP16 four 16x16x32.
+// 16x16x64 per 64-byte slice, FP8 one 32x32x64, FP16 four 16x16x32.
 //   eek_gemm_{i8,f8,f16}: loader waves (4 compute waves + 4 DMA waves);
 //   eek_gemm_{i8,f16}_w8: 8 waves that each compute and load (Gemm8);
 //   eek_gemm_{i8,f8}_persist, eek_gemm_routed[_persist]: persistent and routed grids;
@@ -223,8 +222,8 @@ EE_DEV void interleave() {
 template <int KIND, class P = Pipe<KIND>>
 EE_DEV void epilogue32(const EeGemmArgs& g, const typename P::acc_t (&acc)[2][2], int m0, int n0, int M,
                        int64_t off, int wm, int wn, int lane) {
-    if constexpr (P::SUB16) {                         // (FP16: no scales) quarter q at row_of(q), col_of(q)
-        static_assert(KIND == EE_GEMM_F16, "16x16 loader-wave epilogues are FP16's");
+    if constexpr (P::SUB16) {                         // quarter q at row_of(q), col_of(q)
+        static_assert(KIND != EE_GEMM_F8, "FP8 runs 32x32 MFMAs");
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -235,8 +234,17 @@ EE_DEV void epilogue32(const EeGemmArgs& g, const typename P::acc_t (&acc)[2][2]
                     const int n = n0 + wn * 64 + j * 32 + P::col_of(q, lane);
                     if (m >= M || n >= g.N) continue;
                     const int64_t crow = g.c_idx ? (int64_t)g.c_idx[off + m] : (int64_t)m;
-                    *(u32x2*)(g.c + crow * g.ldc + n) = u32x2{pack_f16x2(acc[i][j][4 * q], acc[i][j][4 * q + 1]),
-                                                              pack_f16x2(acc[i][j][4 * q + 2], acc[i][j][4 * q + 3])};
+                    const float as = (KIND == EE_GEMM_F16) ? 0.0f : g.a_scale[off + m];
+                    float o[4];
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        o[r] = deq<KIND>(acc[i][j][4 * q + r], as, KIND == EE_GEMM_F16 ? 0.0f : g.b_scale[n + r]);
+                    *(u32x2*)(g.c + crow * g.ldc + n) = u32x2{pack_f16x2(o[0], o[1]), pack_f16x2(o[2], o[3])};
+                    if constexpr (KIND == EE_GEMM_I8) {
+                        if (g.acc)
+                            *(i32x4*)(g.acc + crow * g.ldc + n) = i32x4{acc[i][j][4 * q], acc[i][j][4 * q + 1],
+                                                                        acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+                    }
                 }
         return;
     } else {
@@ -292,11 +300,35 @@ struct TileScales {
     f32x4 bs[2][4];
     float as[2];
 };
+// The same for the 16x16 layout (Lay16): lane l needs, per 32-column block j, the
+// scales of columns j*32 + col_of(0 | 2, l) + 0..3 and, per 32-row block i, of rows
+// i*32 + row_of(0 | 1, l).
+struct TileScalesL16 {
+    f32x4 bs[2][2];
+    float as[2][2];
+};
+template <class P>
+using TileScalesOf = std::conditional_t<P::SUB16, TileScalesL16, TileScales>;
 
-template <int KIND>
+template <int KIND, class P = Pipe<KIND>>
 EE_DEV void load_scales(const EeGemmArgs& g, int m0, int n0, int M, int64_t off, int wm, int wn, int lane,
-                        TileScales& sc) {
-    if constexpr (KIND != EE_GEMM_F16) {
+                        TileScalesOf<P>& sc) {
+    if constexpr (KIND != EE_GEMM_F16 && P::SUB16) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int c = 0; c < 2; ++c) {
+                const int n = n0 + wn * 64 + j * 32 + P::col_of(2 * c, lane);
+                sc.bs[j][c] = (n < g.N) ? *(const f32x4*)(g.b_scale + n) : f32x4{0.f, 0.f, 0.f, 0.f};
+            }
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int m = m0 + wm * 64 + i * 32 + P::row_of(h, lane);
+                sc.as[i][h] = (m < M) ? g.a_scale[off + m] : 0.0f;
+            }
+    } else if constexpr (KIND != EE_GEMM_F16) {
 #pragma unroll
         for (int j = 0; j < 2; ++j)
 #pragma unroll
@@ -320,20 +352,28 @@ EE_DEV void load_scales(const EeGemmArgs& g, int m0, int n0, int M, int64_t off,
 // through the wave's LDS region to act columns (n0 + 64 wn) / 2 ...
 template <int KIND, class P = Pipe<KIND>>
 EE_DEV void epilogue32_lds_swiglu(const EeGemmArgs& g, const typename P::acc_t (&acc)[2][2],
-                                  const TileScales& sc, uint8_t* tile, int m0, int n0, int M, int64_t off, int wm,
-                                  int wn, int lane) {
-    if constexpr (P::SUB16) {                         // FP16: act column col_of(q) of row row_of(q)
-        static_assert(KIND == EE_GEMM_F16, "16x16 loader-wave epilogues are FP16's");
+                                  const TileScalesOf<P>& sc, uint8_t* tile, int m0, int n0, int M, int64_t off,
+                                  int wm, int wn, int lane) {
+    if constexpr (P::SUB16) {                         // act column col_of(q) of row row_of(q)
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
+                float gv[4], uv[4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    if constexpr (KIND == EE_GEMM_F16) {
+                        gv[r] = acc[i][0][4 * q + r];
+                        uv[r] = acc[i][1][4 * q + r];
+                    } else {
+                        gv[r] = deq<KIND>(acc[i][0][4 * q + r], sc.as[i][P::rq(q)], sc.bs[0][P::cq(q)][r]);
+                        uv[r] = deq<KIND>(acc[i][1][4 * q + r], sc.as[i][P::rq(q)], sc.bs[1][P::cq(q)][r]);
+                    }
+                }
                 const int rl = i * 32 + P::row_of(q, lane), ca = P::col_of(q, lane);
                 *(u32x2*)(tile + lds_off(rl, ca >> 3) + ((ca >> 2) & 1) * 8) =
-                    u32x2{silu_mul2(pack_f16x2(acc[i][0][4 * q], acc[i][0][4 * q + 1]),
-                                    pack_f16x2(acc[i][1][4 * q], acc[i][1][4 * q + 1])),
-                          silu_mul2(pack_f16x2(acc[i][0][4 * q + 2], acc[i][0][4 * q + 3]),
-                                    pack_f16x2(acc[i][1][4 * q + 2], acc[i][1][4 * q + 3]))};
+                    u32x2{silu_mul2(pack_f16x2(gv[0], gv[1]), pack_f16x2(uv[0], uv[1])),
+                          silu_mul2(pack_f16x2(gv[2], gv[3]), pack_f16x2(uv[2], uv[3]))};
             }
     } else {
 #pragma unroll
@@ -369,15 +409,14 @@ EE_DEV void epilogue32_lds_swiglu(const EeGemmArgs& g, const typename P::acc_t (
 
 // JB = 1: the wave's 64 x 32 block of a 64-wide FP16 tile (columns n0 + 32 wn ..).
 template <int KIND, int SW, class P = Pipe<KIND>, int JB = 2>
-EE_DEV void epilogue32_lds(const EeGemmArgs& g, const typename P::acc_t (&acc)[2][2], const TileScales& sc,
+EE_DEV void epilogue32_lds(const EeGemmArgs& g, const typename P::acc_t (&acc)[2][2], const TileScalesOf<P>& sc,
                            uint8_t* tile, int m0, int n0, int M, int64_t off, int wm, int wn, int lane) {
-    static_assert(JB == 2 || (P::SUB16 && SW == 0), "one-block waves: 16x16 FP16, no SwiGLU");
+    static_assert(JB == 2 || (P::SUB16 && SW == 0 && KIND == EE_GEMM_F16), "one-block waves: 16x16 FP16, no SwiGLU");
     if constexpr (SW) {
         epilogue32_lds_swiglu<KIND, P>(g, acc, sc, tile, m0, n0, M, off, wm, wn, lane);
         return;
     }
-    if constexpr (P::SUB16) {                         // FP16: quarter q at row_of(q), col_of(q)
-        static_assert(KIND == EE_GEMM_F16, "16x16 loader-wave epilogues are FP16's");
+    if constexpr (P::SUB16) {                         // quarter q at row_of(q), col_of(q)
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -385,9 +424,14 @@ EE_DEV void epilogue32_lds(const EeGemmArgs& g, const typename P::acc_t (&acc)[2
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     const int rl = i * 32 + P::row_of(q, lane), cl = j * 32 + P::col_of(q, lane);
+                    float o[4];
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        if constexpr (KIND == EE_GEMM_F16) o[r] = acc[i][j][4 * q + r];
+                        else o[r] = deq<KIND>(acc[i][j][4 * q + r], sc.as[i][P::rq(q)], sc.bs[j][P::cq(q)][r]);
+                    }
                     *(u32x2*)(tile + lds_off(rl, cl >> 3) + ((cl >> 2) & 1) * 8) =
-                        u32x2{pack_f16x2(acc[i][j][4 * q], acc[i][j][4 * q + 1]),
-                              pack_f16x2(acc[i][j][4 * q + 2], acc[i][j][4 * q + 3])};
+                        u32x2{pack_f16x2(o[0], o[1]), pack_f16x2(o[2], o[3])};
                 }
     } else {
     // 1. dequantise and write: lane l holds rows i*32 + (l & 31), columns j*32 + 8q + 4(l >> 5) + 0..3.
@@ -554,7 +598,7 @@ EE_DEV void gemm_tile(const EeGemmArgs& g, int tm, int tn, uint8_t* smem) {
     // The last stage is peeled off the loop: were its final slice (whose reads are
     // still in flight) and the steady-state final slice one block, the waitcnt
     // pass would make the steady state wait for the next stage's reads as well.
-    TileScales sc;
+    TileScalesOf<P> sc;
     if (!g.acc) load_scales<KIND>(g, m0, n0, M, off, wm, wn, lane, sc);
     Frags<KIND> f0, f1;
     auto stage = [&](int kt, bool more) {
@@ -1517,7 +1561,7 @@ EE_DEV void persist_compute(const PTile& t, int nk, int s0, uint8_t* smem, int w
     for (int i = 0; i < 2; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j) acc[i][j] = acc_t{};
-    TileScales sc;
+    TileScalesOf<P> sc;
     if (!g.acc) load_scales<KIND>(g, m0, n0, t.M, t.off, wm, wn, lane, sc);
     Frags<KIND> f0, f1;
     auto stage = [&](int kt, bool more) {

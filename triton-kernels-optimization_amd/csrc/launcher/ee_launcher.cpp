@@ -715,9 +715,10 @@ static int gemm_impl(ee_engine* eng, int32_t kind, const void* a, int64_t lda, c
     // The pipelined kernels stream whole 128-byte K stages; other K take the fallback.
     // Two pipelines: loader waves + MFMA waves (eek_gemm_*), and eight waves that
     // each load and compute (eek_gemm_*_w8).  Measured on MI355X (identical data,
-    // interleaved runs): the 8-wave form is faster for INT8 when the grid is at
-    // most one tile per CU (1024 x 4096 x 4096: 22.9 vs 24.9 us); with several
-    // tiles per CU the loader-wave form is ~5% faster.  FP8 keeps the loader-wave
+    // interleaved runs), both on 16x16x64 MFMAs for INT8: the loader-wave form is
+    // 3-4.5% faster for INT8 grids of at most one tile per CU (1024 x 4096 x 4096:
+    // 18.8 against 19.4 us; 821 and 256 rows alike) and level at 2048^3; with
+    // several tiles per CU it was ~5% faster already.  FP8 keeps the loader-wave
     // form (its 8-wave form spills).  The FP16 tier takes the loader-wave form
     // unless gemm_variant = 2: its 8-wave form splits K between wave pairs, an f32
     // order no other kernel (the 256 tiles, the routed grids) shares, and every
@@ -775,7 +776,7 @@ static int gemm_impl(ee_engine* eng, int32_t kind, const void* a, int64_t lda, c
     }
     if ((K * esz) % 128 == 0) {
         const int64_t v = variant;
-        const bool w8 = v == 2 || (v == 0 && kind == EE_GEMM_I8 && tiles <= 256);
+        const bool w8 = v == 2;
         if (w8 && find_kernel(eng, name + "_w8")) {
             name += "_w8";
         } else if (kind != EE_GEMM_F16 && counts == nullptr) {
