@@ -659,7 +659,7 @@ def cpu_model():
 
 def cpu_baseline(A, W, L):
     """The reference path's arithmetic on this host's cores, on the config-0
-    workload (BASELINE.md's CPU plan): oracle/torch_cpu.py, PyTorch CPU ops --
+    workload, as PyTorch's CPU ops run it: oracle/torch_cpu.py --
     INT8 = the dispatcher quantiser + torch._int_mm + epilogue (`value`), FP8 =
     e4m3 codes decoded to f32 + an f32 matmul, softmax+entropy in f32, each at
     the full 1024x4096x4096 / [1024, 4096] shape -- and the repository's C
